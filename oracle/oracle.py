@@ -1,0 +1,189 @@
+"""CPU oracle for the fused group-wise expert dequant+GEMV path (numpy front end).
+
+TEST INFRASTRUCTURE ONLY: the checker the HIP kernels are compared against. Only
+``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg may
+import it; the product package never does.
+
+The arithmetic lives in ``wisp_oracle.c`` (built to ``liboracle_wisp.so`` by
+``oracle/Makefile``); this module wraps it with numpy arrays and adds the
+routing step of the caller. Each function names the reference lines it restates.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_wisp.so")
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compile the C oracle with its Makefile (gcc); returns the .so path."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-B" if force else "-s", "-C", _HERE], check=True, capture_output=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        i64, i32, vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+        L.wo_f32_to_f16.restype, L.wo_f32_to_f16.argtypes = ctypes.c_uint16, [ctypes.c_float]
+        L.wo_f16_to_f32.restype, L.wo_f16_to_f32.argtypes = ctypes.c_float, [ctypes.c_uint16]
+        L.wo_f32_to_bf16.restype, L.wo_f32_to_bf16.argtypes = ctypes.c_uint16, [ctypes.c_float]
+        L.wo_expert_nbytes.restype, L.wo_expert_nbytes.argtypes = i64, [i64, i32, i64]
+        L.wo_pack.restype, L.wo_pack.argtypes = i32, [vp, i64, i32, vp]
+        L.wo_unpack.restype, L.wo_unpack.argtypes = i32, [vp, i64, i32, vp]
+        L.wo_q3_field.restype, L.wo_q3_field.argtypes = i32, [vp, i64]
+        L.wo_quantize.restype, L.wo_quantize.argtypes = i32, [vp, i64, i32, i64, vp, vp]
+        L.wo_dequant.restype, L.wo_dequant.argtypes = i32, [vp, i64, i32, i64, vp]
+        L.wo_moe_layer_f64.restype = i32
+        L.wo_moe_layer_f64.argtypes = [vp, i64, i64, vp, vp, i32, vp, i64, i64, i32, i64, vp, vp, vp]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---------------------------------------------------------------- scalar conversions
+def f32_to_f16_bits(a) -> np.ndarray:
+    """binary32 -> binary16 bits, RTNE (torch .half(); quant.py:70)."""
+    a = np.ascontiguousarray(a, dtype=np.float32).ravel()
+    f = lib().wo_f32_to_f16
+    return np.fromiter((f(float(v)) for v in a), dtype=np.uint16, count=a.size)
+
+
+def f32_to_bf16_bits(a) -> np.ndarray:
+    """binary32 -> bf16 bits, RTNE (torch .to(bfloat16); quant.py:87). Vectorised
+    integer-add form of round-to-nearest-even, identical to wo_f32_to_bf16."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ---------------------------------------------------------------- layout / packing
+def expert_nbytes(n: int, bits: int, group: int) -> int:
+    """quant.py:17-22. Raises ValueError where the reference asserts."""
+    v = lib().wo_expert_nbytes(n, bits, group)
+    if v < 0:
+        raise ValueError((n, bits, group))
+    return int(v)
+
+
+def pack(q: np.ndarray, bits: int) -> np.ndarray:
+    """quant.py:25-41."""
+    q = np.ascontiguousarray(q, dtype=np.uint8).ravel()
+    out = np.empty(q.size * bits // 8, dtype=np.uint8)
+    if lib().wo_pack(_p(q), q.size, bits, _p(out)) != 0:
+        raise ValueError(bits)
+    return out
+
+
+def unpack(c: np.ndarray, bits: int, m: int | None = None) -> np.ndarray:
+    """quant.py:44-57 (m codes out of packed bytes)."""
+    c = np.ascontiguousarray(c, dtype=np.uint8).ravel()
+    m = c.size * 8 // bits if m is None else m
+    out = np.empty(m, dtype=np.uint8)
+    if lib().wo_unpack(_p(c), m, bits, _p(out)) != 0:
+        raise ValueError(bits)
+    return out
+
+
+def q3_field(buf: np.ndarray, e: int) -> int:
+    """kernels.py:209-217: the kernels' own statement of the 3-bit read."""
+    buf = np.ascontiguousarray(buf, dtype=np.uint8)
+    return int(lib().wo_q3_field(_p(buf), e))
+
+
+# ---------------------------------------------------------------- quantize / dequant
+def quantize(w3: np.ndarray, bits: int, group: int = 128) -> np.ndarray:
+    """quant.py:60-73. w3: [3, n] (or flat 3n) float32 -> flat uint8 buffer."""
+    w = np.ascontiguousarray(w3, dtype=np.float32).ravel()
+    assert w.size % 3 == 0
+    n = w.size // 3
+    out = np.empty(expert_nbytes(n, bits, group), dtype=np.uint8)
+    scratch = np.empty(w.size, dtype=np.uint8)
+    if lib().wo_quantize(_p(w), n, bits, group, _p(out), _p(scratch)) != 0:
+        raise ValueError((n, bits, group))
+    return out
+
+
+def dequant(buf: np.ndarray, n: int, bits: int, group: int = 128) -> np.ndarray:
+    """quant.py:76-87. buf: [B, >=nbytes] uint8 -> [B, 3, n] bf16 bit patterns (uint16)."""
+    buf = np.ascontiguousarray(buf, dtype=np.uint8)
+    if buf.ndim == 1:
+        buf = buf[None]
+    nb = expert_nbytes(n, bits, group)
+    out = np.empty((buf.shape[0], 3, n), dtype=np.uint16)
+    for b in range(buf.shape[0]):
+        row = np.ascontiguousarray(buf[b, :nb])
+        o = out[b]
+        if lib().wo_dequant(_p(row), n, bits, group, _p(o)) != 0:
+            raise ValueError((n, bits, group))
+    return out
+
+
+# ---------------------------------------------------------------- fused layer
+def moe_layer_f64(pool: np.ndarray, slots, w, x_bf16: np.ndarray, H: int, I: int, bits: int, group: int = 128):
+    """Binary64 statement of one batch-1 MoE layer with the fused kernels' semantics
+    (kernels.py:12, 20-69, 72-112, 140-185, 220-307): returns (a [k,I], y [k,H], out [H]),
+    all float64 and unrounded. `w` are the routing weights the kernels read (float32 values)."""
+    pool = np.ascontiguousarray(pool, dtype=np.uint8)
+    slots = np.ascontiguousarray(slots, dtype=np.int64).ravel()
+    w = np.ascontiguousarray(w, dtype=np.float32).ravel()
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16).ravel()
+    k = slots.size
+    assert w.size == k and x.size == H
+    a = np.empty((k, I), dtype=np.float64)
+    y = np.empty((k, H), dtype=np.float64)
+    out = np.empty(H, dtype=np.float64)
+    rc = lib().wo_moe_layer_f64(
+        _p(pool), pool.shape[1], pool.shape[0], _p(slots), _p(w), k, _p(x), H, I, bits, group, _p(a), _p(y), _p(out)
+    )
+    if rc != 0:
+        raise ValueError("bad arguments to moe_layer_f64")
+    return a, y, out
+
+
+# ---------------------------------------------------------------- routing (caller side)
+def route(logits: np.ndarray, k: int, norm_topk: bool = True):
+    """moe.py:67-72 / graphdec.py:177-181: softmax in float32 -> top-k -> renormalise ->
+    round the weights to bf16. Returns (experts int64 [N,k], weights float32 [N,k] holding
+    the bf16-rounded values, i.e. what the meta buffer carries)."""
+    lg = np.asarray(logits, dtype=np.float32)
+    if lg.ndim == 1:
+        lg = lg[None]
+    m = lg.max(axis=1, keepdims=True)
+    e = np.exp((lg - m).astype(np.float64))
+    p = (e / e.sum(axis=1, keepdims=True)).astype(np.float32)
+    sel = np.argsort(-p, axis=1, kind="stable")[:, :k]
+    rw = np.take_along_axis(p, sel, axis=1)
+    if norm_topk:
+        rw = (rw / rw.sum(axis=1, keepdims=True)).astype(np.float32)
+    rw_b = bf16_bits_to_f32(f32_to_bf16_bits(rw)).reshape(rw.shape)
+    return sel.astype(np.int64), rw_b
+
+
+def meta(slots, weights) -> np.ndarray:
+    """The packed routing buffer the fast kernels read (kernels.py:189-190, 167-168;
+    moe.py:190-197): float32 [2k] = [slot ids as float32 ..., weights ...]."""
+    s = np.asarray(slots, dtype=np.int64).ravel()
+    assert np.all(s < (1 << 24)), "slot ids must be exact in float32"
+    return np.concatenate([s.astype(np.float32), np.asarray(weights, dtype=np.float32).ravel()])

@@ -1,0 +1,140 @@
+"""CPU checks of the C-ABI library and the host logic around it (no kernel launches).
+
+The library is loaded here without a GPU: every symbol include/wisp_hip.h declares must
+be exported, and argument validation must reject bad calls before anything reaches HIP.
+"""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from wisp import _lib, kernels, quant
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "wisp_hip.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(wisp_\w+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = _declared()
+    assert len(names) >= 14
+    for name in names:
+        assert hasattr(L, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_abi_version_matches_header():
+    m = re.search(r"#define WISP_ABI_VERSION (\d+)", open(HEADER).read())
+    assert _lib.lib().wisp_abi_version() == int(m.group(1)) == _lib.ABI_VERSION
+
+
+@pytest.mark.parametrize("bits", [16, 8, 4, 3, 2])
+@pytest.mark.parametrize("n,group", [(1572864, 128), (2048, 32), (32768, 128), (100, 128), (96, 96)])
+def test_expert_nbytes_agrees(bits, n, group):
+    L = _lib.lib()
+    try:
+        want = O.expert_nbytes(n, bits, group)
+    except ValueError:
+        want = -1
+    assert L.wisp_expert_nbytes(n, bits, group) == want
+    if want >= 0:
+        assert quant.expert_nbytes(n, bits, group) == want
+
+
+def test_act_bytes():
+    L = _lib.lib()
+    assert L.wisp_act_bytes(8, 768) == 8 * 768 * 4
+    assert L.wisp_act_bytes(0, 768) == -1
+
+
+def test_tuning_validation():
+    L = _lib.lib()
+    assert L.wisp_set_tuning(3, 0, 0) == _lib.WISP_EINVAL
+    assert b"gu_rows" in L.wisp_last_error()
+    assert L.wisp_set_tuning(0, 0, 5) == _lib.WISP_EINVAL
+    assert L.wisp_set_tuning(0, 0, 0) == _lib.WISP_OK
+    with pytest.raises(ValueError):
+        kernels.set_tuning(gu_rows=6)
+
+
+FAKE = ctypes.c_void_p(0x100000)  # never dereferenced: every call below fails validation first
+
+
+@pytest.mark.parametrize(
+    "args,needle",
+    [
+        (dict(bits=5), b"bits"),
+        (dict(k=0), b"k must"),
+        (dict(k=17), b"k must"),
+        (dict(H=2000), b"multiples of group"),
+        (dict(group=64 + 16, H=2080 // 1, I=80 * 9), b"multiple of 32"),
+        (dict(slot_bytes=1000), b"smaller than one expert"),
+        (dict(nslots=0), b"nslots"),
+        (dict(pool=None), b"null"),
+    ],
+)
+def test_layer_argument_validation(args, needle):
+    L = _lib.lib()
+    a = dict(pool=FAKE, slot_bytes=2506752, nslots=128, meta=FAKE, k=8, x=FAKE, H=2048, I=768, bits=4, group=128,
+             act=FAKE, stream=None)
+    a.update(args)
+    rc = L.wisp_moe_gate_up(*a.values())
+    assert rc == _lib.WISP_EINVAL, rc
+    assert needle in L.wisp_last_error()
+    d = (a["pool"], a["slot_bytes"], a["nslots"], a["meta"], a["k"], FAKE, a["H"], a["I"], a["bits"], a["group"])
+    assert L.wisp_moe_down_sum(*d, FAKE, None) == _lib.WISP_EINVAL
+    assert L.wisp_moe_down(*d, FAKE, None) == _lib.WISP_EINVAL
+
+
+def test_alignment_validation():
+    L = _lib.lib()
+    rc = L.wisp_moe_gate_up(ctypes.c_void_p(0x100004), 2506752, 128, FAKE, 8, FAKE, 2048, 768, 4, 128, FAKE, None)
+    assert rc == _lib.WISP_EALIGN
+    rc = L.wisp_moe_gate_up(FAKE, 2506752 + 4, 128, FAKE, 8, FAKE, 2048, 768, 4, 128, FAKE, None)
+    assert rc == _lib.WISP_EALIGN
+
+
+def test_format_entry_validation():
+    L = _lib.lib()
+    assert L.wisp_dequant(FAKE, 100, None, 1, 1, 1572864, 4, 128, FAKE, None) == _lib.WISP_EINVAL  # stride < nbytes
+    assert L.wisp_dequant(FAKE, 2506752, None, 1, 1, 1572864, 5, 128, FAKE, None) == _lib.WISP_EINVAL
+    assert L.wisp_quantize(FAKE, 2, 1572864, 4, 128, FAKE, None) == _lib.WISP_EINVAL  # dtype code
+    assert L.wisp_pack(FAKE, 7, 4, FAKE, None) == _lib.WISP_EINVAL
+    assert L.wisp_unpack(FAKE, 9, 3, FAKE, None) == _lib.WISP_EINVAL
+    assert L.wisp_act_read(FAKE, 8, 100, 4, FAKE, None) == _lib.WISP_EINVAL
+    # empty work is a no-op that succeeds without touching the device
+    assert L.wisp_pack(FAKE, 0, 4, FAKE, None) == _lib.WISP_OK
+    assert L.wisp_dequant(FAKE, 2506752, None, 0, 1, 1572864, 4, 128, FAKE, None) == _lib.WISP_OK
+
+
+def test_no_cpu_fallback():
+    """The product path raises on CPU tensors instead of computing on the host."""
+    w3 = torch.randn(3, 2048)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        quant.quantize(w3, 4, 128)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        quant.dequant(torch.zeros(1, 7680, dtype=torch.uint8), 2048, 4, 128)
+    pool = torch.zeros(2, quant.expert_nbytes(256 * 128, 4, 128), dtype=torch.uint8)
+    meta = torch.tensor([0.0, 1.0, 0.5, 0.5])
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        kernels.moe_decode_q4_fast(pool, meta, torch.zeros(256, dtype=torch.bfloat16), 2, 256 * 128, 256, 128)
+    # the reference's shape assertion (kernels.py:191) comes first
+    with pytest.raises(AssertionError):
+        kernels.moe_decode_q4_fast(pool, meta, torch.zeros(256, dtype=torch.bfloat16), 2, 256 * 128, 250, 128)
+
+
+def test_meta_layout_helpers():
+    m = O.meta(np.array([5, 0, 3]), np.array([0.5, 0.25, 0.25], np.float32))
+    assert m.tolist() == [5.0, 0.0, 3.0, 0.5, 0.25, 0.25]

@@ -1,0 +1,268 @@
+"""GPU parity of the HIP path against the CPU oracle (oracle/), through the C ABI.
+
+Bars (set by the task): dequant, quantize and packing bit-exact; layer outputs within
+1e-3 relative L2 of the binary64 oracle of the fused semantics rounded to bf16 (the
+kernels accumulate in fp32 and store bf16 once). The reference's own looser criterion
+(tests/test_kernels.py:33: max|d|/max|ref| < 2e-2 against dequant->bf16->matmul) is
+checked too.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from wisp import kernels, quant
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 1e-3  # rel-L2 vs the oracle
+
+
+def _weights(rng, n, scale=0.02):
+    return (rng.standard_normal(3 * n) * scale).astype(np.float32)
+
+
+def _pool(E, H, I, bits, group, seed, pad=0):
+    rng = np.random.default_rng(seed)
+    n = H * I
+    rows = [O.quantize(_weights(rng, n), bits, group) for _ in range(E)]
+    nb = rows[0].size
+    pool = np.zeros((E, nb + pad), np.uint8)
+    for e, r in enumerate(rows):
+        pool[e, :nb] = r
+    return pool
+
+
+def _x(rng, H):
+    return O.f32_to_bf16_bits(rng.standard_normal(H).astype(np.float32))
+
+
+def _bf16(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _rel_l2(got, ref):
+    return float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+
+
+def _route(rng, E, k):
+    sel, rw = O.route(rng.standard_normal((1, E)).astype(np.float32), k)
+    return sel[0], rw[0]
+
+
+# ---------------------------------------------------------------- format kernels
+@pytest.mark.parametrize(
+    "bits,n,group,pad",
+    [(4, 256 * 128, 128, 0), (3, 256 * 128, 128, 16), (2, 256 * 128, 128, 0), (8, 256 * 128, 128, 0),
+     (4, 2048 * 768, 128, 0), (3, 2048 * 768, 128, 0), (2, 2048 * 768, 128, 0),
+     (4, 64 * 32, 32, 0), (3, 64 * 32, 32, 4), (2, 64 * 32, 32, 0), (8, 64 * 32, 32, 0),
+     (4, 3072, 96, 0), (3, 3072, 96, 0), (2, 3072, 96, 2)],
+)
+def test_dequant_bit_exact(bits, n, group, pad):
+    rng = np.random.default_rng(bits * 7 + group)
+    rows = np.stack([O.quantize(_weights(rng, n, 0.05), bits, group) for _ in range(2)])
+    if pad:
+        rows = np.concatenate([rows, np.full((2, pad), 0xAB, np.uint8)], 1)
+    ref = O.dequant(rows, n, bits, group)
+    got = quant.dequant(torch.from_numpy(rows).to(DEV), n, bits, group)
+    assert got.shape == (2, 3, n) and got.dtype == torch.bfloat16
+    assert np.array_equal(_bf16(got), ref)
+
+
+def test_dequant_rows_gather_and_bounds():
+    H, I, bits, group = 256, 128, 4, 128
+    n = H * I
+    pool = _pool(5, H, I, bits, group, seed=3, pad=32)
+    idx = torch.tensor([4, 0, 2, 7, -1], device=DEV)  # last two out of range
+    got = _bf16(quant.dequant_rows(torch.from_numpy(pool).to(DEV), idx, n, bits, group))
+    ref = O.dequant(pool[[4, 0, 2]], n, bits, group)
+    assert np.array_equal(got[:3], ref)
+    assert np.all((got[3:] & 0x7F80) == 0x7F80) and np.all(got[3:] & 0x7F)  # NaN rows, nothing read
+
+
+@pytest.mark.parametrize("bits", [8, 4, 3, 2])
+@pytest.mark.parametrize("group,n", [(128, 256 * 128), (32, 64 * 32), (128, 2048 * 768)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_quantize_bit_exact(bits, group, n, dtype):
+    rng = np.random.default_rng(bits + group)
+    w = _weights(rng, n, 0.05)
+    w[:group] = 0.3  # a constant group: scale clamps to 1e-5 (an fp16 subnormal)
+    w[group : 2 * group] = np.arange(group) % 16  # integer levels with exact ties
+    if dtype == "bf16":
+        w = O.bf16_bits_to_f32(O.f32_to_bf16_bits(w))
+        t = torch.from_numpy(w).to(torch.bfloat16)
+    else:
+        t = torch.from_numpy(w)
+    got = quant.quantize(t.reshape(3, n).to(DEV), bits, group).cpu().numpy()
+    assert np.array_equal(got, O.quantize(w, bits, group))
+
+
+@pytest.mark.parametrize("bits", [8, 4, 3, 2])
+def test_pack_unpack(bits):
+    q = np.random.default_rng(bits).integers(0, 2**bits, 3 * 4096).astype(np.uint8)
+    packed = quant._pack(torch.from_numpy(q).to(DEV), bits)
+    assert np.array_equal(packed.cpu().numpy(), O.pack(q, bits))
+    back = quant._unpack(packed.reshape(1, -1), bits)
+    assert np.array_equal(back.cpu().numpy()[0], q)
+
+
+# ---------------------------------------------------------------- fused layer
+LAYER_SHAPES = [
+    # (H, I, group, E, k): reference test shapes, the BASELINE layer, the tiny-model shape,
+    # and shapes that take the generic (H/32 > 64 or I/32 > 64) kernels
+    (256, 128, 128, 6, 3),
+    (2048, 768, 128, 10, 8),
+    (64, 32, 32, 8, 2),
+    (4096, 256, 128, 3, 2),
+    (256, 4096, 128, 3, 2),
+    (512, 384, 128, 4, 4),
+]
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("H,I,group,E,k", LAYER_SHAPES)
+def test_moe_decode_fast_parity(bits, H, I, group, E, k):
+    rng = np.random.default_rng(1000 * bits + H + I)
+    n = H * I
+    pool = _pool(E, H, I, bits, group, seed=H + bits)
+    sel, rw = _route(rng, E, k)
+    x = _x(rng, H)
+    _, _, ref = O.moe_layer_f64(pool, sel, rw, x, H, I, bits, group)
+    fn = {4: kernels.moe_decode_q4_fast, 3: kernels.moe_decode_q3_fast, 2: kernels.moe_decode_q2_fast}[bits]
+    meta = torch.from_numpy(O.meta(sel, rw)).to(DEV)
+    got = fn(torch.from_numpy(pool).to(DEV), meta, torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV),
+             k, n, H, I, group)
+    torch.cuda.synchronize()
+    g = O.bf16_bits_to_f32(_bf16(got)).astype(np.float64)
+    r = O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.astype(np.float32))).astype(np.float64)
+    err = _rel_l2(g, r)
+    print(f"bits={bits} H={H} I={I} G={group} k={k}: rel-L2 {err:.3e}")
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("H,I,group", [(2048, 768, 128), (256, 128, 128), (4096, 256, 128), (64, 32, 32)])
+def test_gate_up_activation(bits, H, I, group):
+    rng = np.random.default_rng(bits + H)
+    n, E, k = H * I, 4, 3
+    pool = _pool(E, H, I, bits, group, seed=bits * 3 + I)
+    sel, rw = _route(rng, E, k)
+    x = _x(rng, H)
+    a_ref, _, _ = O.moe_layer_f64(pool, sel, rw, x, H, I, bits, group)
+    meta = torch.from_numpy(O.meta(sel, rw)).to(DEV)
+    a = kernels.gate_up_act(torch.from_numpy(pool).to(DEV), meta,
+                            torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV), k, n, H, I, bits, group)
+    err = _rel_l2(a.cpu().numpy().astype(np.float64), a_ref)
+    print(f"gate_up bits={bits} H={H}: rel-L2 {err:.3e}")
+    assert err <= 2e-5, err
+
+
+@pytest.mark.parametrize("H,I,group,E,k", [(256, 128, 128, 6, 3), (2048, 768, 128, 10, 8)])
+def test_moe_decode_q4_per_expert_path(H, I, group, E, k):
+    """kernels.py:115-137: slots int64 + weight tensor, per-expert y then torch weighted sum."""
+    rng = np.random.default_rng(H)
+    n = H * I
+    pool = _pool(E, H, I, 4, group, seed=E)
+    sel, rw = _route(rng, E, k)
+    x = _x(rng, H)
+    _, y_ref, ref = O.moe_layer_f64(pool, sel, rw, x, H, I, 4, group)
+    got = kernels.moe_decode_q4(torch.from_numpy(pool).to(DEV), torch.from_numpy(sel).to(DEV),
+                                torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV),
+                                torch.from_numpy(rw).to(torch.bfloat16).to(DEV), n, H, I, group)
+    g = O.bf16_bits_to_f32(_bf16(got)).astype(np.float64)
+    assert _rel_l2(g, ref) <= TOL
+
+
+@pytest.mark.parametrize("bits", [4, 3])
+def test_reference_test_criterion(bits):
+    """The reference's own check (tests/test_kernels.py:10-33): ref = dequant -> bf16 ->
+    fp32 matmul, SiLU, weighted sum; max|d| / max|ref| < 2e-2. Seeds/shapes as there."""
+    rng = np.random.default_rng(bits)
+    H, I, E, k, group = 256, 128, 6, 3, 128
+    n = H * I
+    w3 = (rng.standard_normal((E, 3 * n)) * 0.05).astype(np.float32)
+    w3 = O.bf16_bits_to_f32(O.f32_to_bf16_bits(w3)).reshape(E, 3 * n)
+    pool = np.stack([O.quantize(w3[e], bits, group) for e in range(E)])
+    slots = np.array([4, 1, 2])
+    x = _x(rng, H)
+    w = torch.softmax(torch.from_numpy(rng.standard_normal(k).astype(np.float32)), 0).numpy()
+    W = O.bf16_bits_to_f32(O.dequant(pool[slots], n, bits, group)).astype(np.float32).reshape(k, 3, n)
+    xf = O.bf16_bits_to_f32(x)
+    g = W[:, 0].reshape(k, I, H) @ xf
+    u = W[:, 1].reshape(k, I, H) @ xf
+    a = g / (1 + np.exp(-g)) * u
+    y = np.einsum("khi,ki->kh", W[:, 2].reshape(k, H, I), a)
+    exp = (y * w[:, None]).sum(0)
+    meta = torch.from_numpy(O.meta(slots, w)).to(DEV)
+    fn = kernels.moe_decode_q4_fast if bits == 4 else kernels.moe_decode_q3_fast
+    got = fn(torch.from_numpy(pool).to(DEV), meta, torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV),
+             k, n, H, I)
+    d = O.bf16_bits_to_f32(_bf16(got))
+    assert np.abs(d - exp).max() / np.abs(exp).max() < 2e-2
+
+
+def test_invalid_slot_gives_nan_not_a_fault():
+    H, I, group, E, k = 256, 128, 128, 3, 2
+    pool = torch.from_numpy(_pool(E, H, I, 4, group, seed=1)).to(DEV)
+    x = torch.randn(H, device=DEV).to(torch.bfloat16)
+    for bad in (3.0, -1.0, 1.5, float("nan")):
+        meta = torch.tensor([0.0, bad, 0.5, 0.5], device=DEV)
+        out = kernels.moe_decode_q4_fast(pool, meta, x, k, H * I, H, I, group)
+        assert torch.isnan(out.float()).all()
+    ok = kernels.moe_decode_q4_fast(pool, torch.tensor([0.0, 2.0, 0.5, 0.5], device=DEV), x, k, H * I, H, I, group)
+    assert torch.isfinite(ok.float()).all()
+
+
+@pytest.mark.parametrize("gu", [(4, 4), (2, 4), (8, 4), (1, 4), (4, 2), (2, 8), (4, 1), (8, 1)])
+@pytest.mark.parametrize("dn", [1, 2, 4, 8])
+def test_tuning_variants_agree(gu, dn):
+    H, I, group, E, k, bits = 2048, 768, 128, 9, 8, 4
+    rng = np.random.default_rng(42)
+    pool = _pool(E, H, I, bits, group, seed=42)
+    sel, rw = _route(rng, E, k)
+    x = _x(rng, H)
+    _, _, ref = O.moe_layer_f64(pool, sel, rw, x, H, I, bits, group)
+    try:
+        kernels.set_tuning(gu[0], gu[1], dn)
+        got = kernels.moe_decode_q4_fast(torch.from_numpy(pool).to(DEV), torch.from_numpy(O.meta(sel, rw)).to(DEV),
+                                         torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV),
+                                         k, H * I, H, I)
+        torch.cuda.synchronize()
+    finally:
+        kernels.set_tuning(4, 4, 4)
+    assert _rel_l2(O.bf16_bits_to_f32(_bf16(got)), ref) <= TOL
+
+
+def test_graph_capture_with_meta_updates():
+    """graphdec.py capture contract: kernel arguments frozen, slots/weights read from the
+    device meta buffer at replay time (updated by an H2D copy between replays)."""
+    H, I, group, E, k, bits = 2048, 768, 128, 12, 8, 4
+    n = H * I
+    rng = np.random.default_rng(9)
+    pool_np = _pool(E, H, I, bits, group, seed=9)
+    pool = torch.from_numpy(pool_np).to(DEV)
+    x_np = _x(rng, H)
+    x = torch.from_numpy(x_np.view(np.int16)).view(torch.bfloat16).to(DEV)
+    meta_dev = torch.zeros(2 * k, device=DEV)
+    meta_host = torch.zeros(2 * k).pin_memory()
+    meta_dev.copy_(torch.from_numpy(O.meta(np.arange(k), np.full(k, 1.0 / k, np.float32))))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        kernels.moe_decode_q4_fast(pool, meta_dev, x, k, n, H, I)  # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = kernels.moe_decode_q4_fast(pool, meta_dev, x, k, n, H, I)
+    for it in range(4):
+        sel, rw = _route(rng, E, k)
+        meta_host.copy_(torch.from_numpy(O.meta(sel, rw)))
+        meta_dev.copy_(meta_host, non_blocking=True)
+        g.replay()
+        eager = kernels.moe_decode_q4_fast(pool, meta_dev, x, k, n, H, I)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), it
+        _, _, ref = O.moe_layer_f64(pool_np, sel, rw, x_np, H, I, bits, group)
+        assert _rel_l2(O.bf16_bits_to_f32(_bf16(out)), ref) <= TOL

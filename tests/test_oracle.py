@@ -1,0 +1,255 @@
+"""Pins for the CPU oracle (oracle/wisp_oracle.c) before it is trusted as the checker.
+
+Each check is chosen so that a plausible mistake in the oracle fails it: known-answer
+tests derived by hand from the reference's stated layout, the reference's own KATs and
+bounds (tests/test_quant.py of imronpuji/wisp-runtime), a second independent statement
+of the 3-bit layout (the kernels' `_q3`, kernels.py:209-217), conversions compared with
+torch's own (library routines), and the fused layer compared with a dense numpy matvec.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+
+# ---------------------------------------------------------------- sizes (quant.py:17-22)
+def test_expert_nbytes_kats():
+    # test_quant.py:37-40
+    n = 1572864
+    assert O.expert_nbytes(n, 16, 128) == 9437184
+    assert abs(O.expert_nbytes(n, 4, 128) / O.expert_nbytes(n, 16, 128) - 0.265) < 0.01
+    # docs/architecture.md:82: 4/3/2-bit experts are 2.39/1.83/1.27 MiB
+    for bits, mib in ((4, 2.39), (3, 1.83), (2, 1.27)):
+        assert round(O.expert_nbytes(n, bits, 128) / 2**20, 2) == mib
+    # exact byte counts: codes + 2 fp16 per group
+    assert O.expert_nbytes(n, 4, 128) == 2359296 + 73728 + 73728
+    assert O.expert_nbytes(n, 3, 128) == 1769472 + 2 * 36864 * 2
+    assert O.expert_nbytes(n, 2, 128) == 1179648 + 2 * 36864 * 2
+    with pytest.raises(ValueError):
+        O.expert_nbytes(100, 4, 128)  # 3n not a multiple of the group
+    with pytest.raises(ValueError):
+        O.expert_nbytes(2048, 5, 32)
+
+
+# ---------------------------------------------------------------- packing (quant.py:25-57)
+def test_pack_known_answers():
+    # 4-bit: element e is the low nibble of byte e/2 when e is even (architecture.md:79)
+    assert O.pack(np.array([1, 2, 3, 4], np.uint8), 4).tolist() == [0x21, 0x43]
+    # 2-bit: 4 codes per byte, LSB first
+    assert O.pack(np.array([1, 2, 3, 0], np.uint8), 2).tolist() == [0x39]
+    # 3-bit: 8 codes -> 24-bit little endian, code i at bit 3i (hand-computed: 0x1F58D1)
+    assert O.pack(np.array([1, 2, 3, 4, 5, 6, 7, 0], np.uint8), 3).tolist() == [0xD1, 0x58, 0x1F]
+    assert O.pack(np.array([7] * 8, np.uint8), 3).tolist() == [0xFF, 0xFF, 0xFF]
+    assert O.pack(np.array([200, 3], np.uint8), 8).tolist() == [200, 3]
+
+
+@pytest.mark.parametrize("bits", [8, 4, 3, 2])
+def test_pack_roundtrip(bits):
+    # test_quant.py:9-12
+    q = np.random.default_rng(bits).integers(0, 2**bits, 4096).astype(np.uint8)
+    assert np.array_equal(O.unpack(O.pack(q, bits), bits, q.size), q)
+
+
+def test_q3_layout_matches_kernel_statement():
+    # unpack (quant.py:53-56) against the kernels' own 3-bit read (kernels.py:209-217)
+    rng = np.random.default_rng(3)
+    q = rng.integers(0, 8, 3 * 4096).astype(np.uint8)
+    buf = np.concatenate([O.pack(q, 3), np.zeros(8, np.uint8)])  # trailing bytes stand in for the scales
+    got = np.array([O.q3_field(buf, e) for e in range(q.size)], dtype=np.uint8)
+    assert np.array_equal(got, q)
+
+
+# ---------------------------------------------------------------- scalar conversions
+def _f16_cases():
+    rng = np.random.default_rng(0)
+    specials = np.array(
+        [0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0, 70000.0, 1e-5, 6.1e-5, 5.96e-8, 2.98e-8, 2.99e-8,
+         1e-10, np.inf, -np.inf, 0.1, 0.3, 1.00048828125, 1.000732421875],
+        dtype=np.float32,
+    )
+    mags = 10.0 ** rng.uniform(-9, 5, 20000)
+    rnd = (mags * rng.choice([-1, 1], mags.size)).astype(np.float32)
+    # exact halfway points between fp16 neighbours (ties)
+    h = rng.integers(0, 0x7BFF, 2000).astype(np.uint16)
+    lo = h.view(np.float16).astype(np.float32)
+    hi = (h + 1).view(np.float16).astype(np.float32)
+    ties = ((lo.astype(np.float64) + hi.astype(np.float64)) / 2).astype(np.float32)
+    return np.concatenate([specials, rnd, ties])
+
+
+def test_f32_to_f16_matches_torch():
+    v = _f16_cases()
+    ref = torch.from_numpy(v).half().view(torch.int16).numpy().view(np.uint16)
+    got = O.f32_to_f16_bits(v)
+    assert np.array_equal(got, ref)
+
+
+def test_f32_to_bf16_matches_torch():
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32)
+    v = bits.view(np.float32)
+    v = v[~np.isnan(v)]
+    ties = (rng.integers(0, 2**16, 5000).astype(np.uint32) << 16 | 0x8000).view(np.float32)
+    v = np.concatenate([v, ties[~np.isnan(ties)]])
+    ref = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.f32_to_bf16_bits(v), ref)
+
+
+# ---------------------------------------------------------------- quantize (quant.py:60-73)
+def _split(buf, n, bits, group):
+    N = 3 * n
+    ncode = N * bits // 8
+    ng = N // group
+    codes = O.unpack(buf[:ncode], bits, N)
+    s = buf[ncode : ncode + 2 * ng].view(np.uint16)
+    m = buf[ncode + 2 * ng : ncode + 4 * ng].view(np.uint16)
+    return codes, s, m
+
+
+def test_quantize_known_answer_round_half_even():
+    # one group of 32 with min 0 and max 15: scale (15-0)/15 = 1 exactly, min 0
+    n, group = 32, 32  # 3n = 96 values = 3 groups
+    g0 = np.array([0, 15, 2.5, 3.5, 7.5, 0.49, 14.5, 8.5] + [1.0] * 24, np.float32)
+    w = np.concatenate([g0, g0 * 2, np.full(32, 0.3, np.float32)])
+    buf = O.quantize(w, 4, group)
+    codes, s, m = _split(buf, n, 4, group)
+    # round half to even: 2.5->2, 3.5->4, 7.5->8, 14.5->14, 8.5->8
+    assert codes[:8].tolist() == [0, 15, 2, 4, 8, 0, 14, 8]
+    assert s[0] == 0x3C00 and m[0] == 0x0000  # 1.0, 0.0
+    # group 1: scale 2 (0x4000), identical codes
+    assert s[1] == 0x4000 and codes[32:40].tolist() == [0, 15, 2, 4, 8, 0, 14, 8]
+    # constant group: scale clamps to 1e-5 -> fp16 subnormal 168 * 2^-24 (0x00A8);
+    # min 0.3 -> fp16 0x34CD (0.300048828125) > 0.3, so every code is clamp(round(-4.9)) = 0
+    assert s[2] == 0x00A8 and m[2] == 0x34CD
+    assert codes[64:].tolist() == [0] * 32
+
+
+@pytest.mark.parametrize("bits", [8, 4, 3, 2])
+def test_quantize_codes_are_nearest_level(bits):
+    # every code is round((v - m)/s) clamped: within 1/2 level of the exact quotient
+    rng = np.random.default_rng(bits)
+    n, group = 2048, 32
+    w = (rng.standard_normal(3 * n) * 0.02).astype(np.float32)
+    buf = O.quantize(w, bits, group)
+    codes, s, m = _split(buf, n, bits, group)
+    sf = np.repeat(s.view(np.float16).astype(np.float64), group)
+    mf = np.repeat(m.view(np.float16).astype(np.float64), group)
+    r = (w.astype(np.float64) - mf) / sf
+    lv = 2**bits - 1
+    inside = (r > 0.5) & (r < lv - 0.5)
+    assert np.all(np.abs(codes[inside] - r[inside]) <= 0.5 + 1e-4)
+    assert np.all(codes <= lv)
+
+
+@pytest.mark.parametrize("bits", [16, 8, 4, 3, 2])
+def test_sizes_and_error_bounds(bits):
+    # test_quant.py:15-24
+    rng = np.random.default_rng(bits)
+    n, group = 2048, 32
+    w = (rng.standard_normal(3 * n) * 0.02).astype(np.float32)
+    buf = O.quantize(w, bits, group)
+    assert buf.size == O.expert_nbytes(n, bits, group)
+    r = O.bf16_bits_to_f32(O.dequant(buf, n, bits, group)[0]).reshape(-1)
+    rel = np.linalg.norm(r - w) / np.linalg.norm(w)
+    assert rel < {16: 0.01, 8: 0.01, 4: 0.12, 3: 0.25, 2: 0.6}[bits], rel
+
+
+def test_error_monotonic():
+    # test_quant.py:27-34
+    rng = np.random.default_rng(7)
+    n, group = 4096, 32
+    w = rng.standard_normal(3 * n).astype(np.float32)
+    errs = []
+    for b in (8, 4, 3, 2):
+        r = O.bf16_bits_to_f32(O.dequant(O.quantize(w, b, group), n, b, group)[0]).reshape(-1)
+        errs.append(np.linalg.norm(r - w) / np.linalg.norm(w))
+    assert errs == sorted(errs)
+
+
+# ---------------------------------------------------------------- dequant (quant.py:76-87)
+def _hand_buffer(code4, s16, m16, n=32, group=32):
+    """4-bit expert with every code of group g equal to code4[g] and the given fp16 bits."""
+    N = 3 * n
+    q = np.repeat(np.array(code4, np.uint8), group)
+    return np.concatenate(
+        [O.pack(q, 4), np.array(s16, np.uint16).view(np.uint8), np.array(m16, np.uint16).view(np.uint8)]
+    ), N
+
+
+def test_dequant_known_answers():
+    # group 0: 5*0.5 - 1 = 1.5 (bf16 0x3FC0); group 1: 15*2 + 0 = 30 (0x41F0);
+    # group 2: 1*(1+2^-8) + 2^-24 -> fp32 tie rounds to 1+2^-8, whose bf16 tie rounds to
+    # 1.0 (0x3F80). A single rounding of the exact sum would give 0x3F81: this pins the
+    # binary32 add before the bf16 cast (quant.py:86-87).
+    buf, N = _hand_buffer([5, 15, 1], [0x3800, 0x4000, 0x3C04], [0xBC00, 0x0000, 0x0001])
+    out = O.dequant(buf, 32, 4, 32)[0].reshape(-1)
+    assert set(out[:32].tolist()) == {0x3FC0}
+    assert set(out[32:64].tolist()) == {0x41F0}
+    assert set(out[64:].tolist()) == {0x3F80}
+
+
+def test_dequant_matches_numpy_float32_semantics():
+    # separately-rounded float32 mul and add, then RTNE bf16 (numpy float32 ops are IEEE)
+    rng = np.random.default_rng(11)
+    for bits in (8, 4, 3, 2):
+        n, group = 1024, 128
+        buf = O.quantize((rng.standard_normal(3 * n) * 0.05).astype(np.float32), bits, group)
+        codes, s, m = _split(buf, n, bits, group)
+        sf = np.repeat(s.view(np.float16).astype(np.float32), group)
+        mf = np.repeat(m.view(np.float16).astype(np.float32), group)
+        ref = O.f32_to_bf16_bits(codes.astype(np.float32) * sf + mf)
+        assert np.array_equal(O.dequant(buf, n, bits, group)[0].reshape(-1), ref)
+
+
+# ---------------------------------------------------------------- fused layer semantics
+def _dense_layer(pool, slots, w, x_bits, H, I, bits, group):
+    n = H * I
+    xf = O.bf16_bits_to_f32(x_bits).astype(np.float64)
+    out = np.zeros(H)
+    a_all, y_all = [], []
+    for s, wj in zip(slots, w):
+        buf = pool[s]
+        codes, sc, mn = _split(buf[: O.expert_nbytes(n, bits, group)], n, bits, group)
+        W = codes.astype(np.float64) * np.repeat(sc.view(np.float16).astype(np.float64), group) + np.repeat(
+            mn.view(np.float16).astype(np.float64), group
+        )
+        g = W[:n].reshape(I, H) @ xf
+        u = W[n : 2 * n].reshape(I, H) @ xf
+        a = g / (1 + np.exp(-g)) * u
+        y = W[2 * n :].reshape(H, I) @ a
+        a_all.append(a)
+        y_all.append(y)
+        out += float(wj) * y
+    return np.array(a_all), np.array(y_all), out
+
+
+@pytest.mark.parametrize("bits,H,I,group", [(4, 256, 128, 128), (3, 256, 128, 128), (2, 128, 64, 32)])
+def test_fused_oracle_matches_dense_matvec(bits, H, I, group):
+    rng = np.random.default_rng(bits)
+    n, E, k = H * I, 5, 3
+    pool = np.stack([O.quantize((rng.standard_normal(3 * n) * 0.05).astype(np.float32), bits, group) for _ in range(E)])
+    slots = [4, 0, 2]
+    w = np.array([0.5, 0.3, 0.2], np.float32)
+    x = O.f32_to_bf16_bits(rng.standard_normal(H).astype(np.float32))
+    a, y, out = O.moe_layer_f64(pool, slots, w, x, H, I, bits, group)
+    a2, y2, out2 = _dense_layer(pool, slots, w, x, H, I, bits, group)
+    assert np.allclose(a, a2, rtol=1e-10, atol=1e-12)
+    assert np.allclose(y, y2, rtol=1e-10, atol=1e-12)
+    assert np.allclose(out, out2, rtol=1e-10, atol=1e-12)
+
+
+# ---------------------------------------------------------------- routing (moe.py:67-72)
+def test_route_matches_torch():
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((16, 128)).astype(np.float32)
+    sel, rw = O.route(logits, 8)
+    t = torch.from_numpy(logits)
+    p = torch.softmax(t, dim=1, dtype=torch.float32)
+    tw, ts = torch.topk(p, 8, dim=-1)
+    tw = (tw / tw.sum(-1, keepdim=True)).to(torch.bfloat16).float()
+    assert np.array_equal(sel, ts.numpy())
+    assert np.allclose(rw, tw.numpy(), rtol=0, atol=0)
+    m = O.meta([3, 1], [0.25, 0.75])
+    assert m.dtype == np.float32 and m.tolist() == [3.0, 1.0, 0.25, 0.75]

@@ -1,0 +1,610 @@
+// Batch-1 MoE layer kernels for gfx950: gate_up+SiLU (kernel 1) and down with
+// the routing-weighted expert sum (kernel 2), reading packed 4/3/2-bit experts
+// straight out of the slot pool.
+//
+// Reference semantics: wisp/kernels.py:12 (folded dequant
+// sum_i (q_i s + m) v_i = s (q.v) + m sum(v)), 20-69 (_gate_up_kernel),
+// 72-112 (_down_kernel), 140-185 (_down_sum_kernel), 206-307 (3-bit twins).
+//
+// Work decomposition (MI355X: 256 CUs, wave64):
+//  * A lane owns one 32-code chunk of a row (16/12/8 bytes for 4/3/2-bit) and
+//    keeps the matching 32 operand values in registers as 16 bf16 pairs, so
+//    the codes stream through 128/96/64-bit loads that are contiguous across
+//    the wave, and each chunk dot is 16 v_and_or_b32 + 16 v_dot2c_f32_bf16
+//    (+ window shifts). All loads of a wave are issued before any math.
+//  * Kernel 1: one wave = one expert x T*RPI rows (gate and up), RPI = rows
+//    per wave-wide load (1 when H = 2048). Per-lane partials are summed per
+//    row through LDS; SiLU(gate)*up is formed by the lane holding the row.
+//  * Kernel 2: one workgroup = k waves (wave j = expert j) over T*RPI output
+//    rows; per-lane partials are summed per row through LDS, then the k
+//    expert sums are combined in expert order and stored once as bf16.
+//  * The activation between the kernels is kept at ~17-bit precision as a
+//    bf16 hi/lo split (a = hi + lo), pre-arranged in the down kernel's pair
+//    order, so kernel 2 uses the same dot2 path (two dot2 per code pair).
+#include "wisp_device.hpp"
+#include "wisp_internal.hpp"
+
+namespace wisp {
+
+// Layer constants, computed once on the host (no divisions in the kernels).
+struct Layer {
+    const uint8_t* pool;
+    const float* meta;
+    int64_t slot_bytes;
+    int64_t nmb;  // code bytes of one matrix, n*BITS/8
+    int nslots, k;
+    int H, I, G;
+    int rowb_gu;  // code bytes of one gate/up row, H*BITS/8
+    int rowb_dn;  // code bytes of one down row, I*BITS/8
+    int gpr_gu;   // groups per gate/up row, H/G
+    int gpr_dn;   // groups per down row, I/G
+    int NGM;      // groups per matrix, n/G
+    int gsh;      // log2(G/32) when G/32 is a power of two, else -1
+    int spr_gu;   // chunks per gate/up row, H/32
+    int spr_dn;   // chunks per down row, I/32
+};
+
+// slot id from the meta buffer: -1 unless an exact integer in [0, nslots)
+__device__ __forceinline__ int slot_of(const float* meta, int j, int nslots) {
+    const float f = meta[j];
+    const int s = (int)f;
+    return (f >= 0.f && f < (float)nslots && (float)s == f) ? s : -1;
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Store a[j, r] into the activation workspace: segment r/32, pair slot of
+// r%32, as bf16 hi and lo parts of a * 2^-e.
+// Workspace layout: act[(j*(I/32) + s)*32 + P] = hi pair P, [+16+P] = lo pair P.
+template <int BITS>
+__device__ __forceinline__ void write_act(uint32_t* act, int j, int I, int r, float a) {
+    const int info = pair_slot<BITS>(r & 31);
+    const int P = info & 15, half = (info >> 4) & 1, e = info >> 5;
+    const float av = scale_pow2(a, e);
+    const uint16_t hi = f32_to_bf16(av);
+    const uint16_t lo = f32_to_bf16(av - bf16_to_f32(hi));
+    uint16_t* a16 = reinterpret_cast<uint16_t*>(act + ((int64_t)j * (I >> 5) + (r >> 5)) * 32);
+    a16[2 * P + half] = hi;
+    a16[2 * (16 + P) + half] = lo;
+}
+
+// x operand of chunk c: pairs, sum of stored values, sum of true values
+template <int BITS>
+__device__ __forceinline__ void load_x_operand(const uint16_t* x, int c, uint32_t* xp, float& vsum, float& xsum) {
+    const uint4* xq = reinterpret_cast<const uint4*>(x + 32 * c);
+    uint32_t w[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint4 q = xq[i];
+        w[4 * i] = q.x; w[4 * i + 1] = q.y; w[4 * i + 2] = q.z; w[4 * i + 3] = q.w;
+    }
+    operand_pairs<BITS>(w, xp);
+    operand_sums<BITS>(xp, vsum, xsum);
+}
+
+// activation operand of segment s of expert j: hi and lo pairs and their sums
+template <int BITS>
+__device__ __forceinline__ void load_act_operand(const uint32_t* act, int j, int I, int s, uint32_t* AH, uint32_t* AL,
+                                                 float& vsum, float& asum) {
+    const uint4* ap = reinterpret_cast<const uint4*>(act + ((int64_t)j * (I >> 5) + s) * 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint4 h = ap[i], l = ap[4 + i];
+        AH[4 * i] = h.x; AH[4 * i + 1] = h.y; AH[4 * i + 2] = h.z; AH[4 * i + 3] = h.w;
+        AL[4 * i] = l.x; AL[4 * i + 1] = l.y; AL[4 * i + 2] = l.z; AL[4 * i + 3] = l.w;
+    }
+    float vh, th, vl, tl;
+    operand_sums<BITS>(AH, vh, th);
+    operand_sums<BITS>(AL, vl, tl);
+    vsum = vh + vl;
+    asum = th + tl;
+}
+
+// dot of one chunk of codes against one operand, bias removed: sum q*v
+template <int BITS>
+__device__ __forceinline__ float chunk_dot(const uint32_t* codes, const uint32_t* opr, float bias, uint32_t B) {
+    uint32_t p[16];
+    code_pairs<BITS>(codes, p, B);
+    float a0 = bias, a1 = 0.f;
+#pragma unroll
+    for (int P = 0; P < 16; P += 2) {
+        a0 = dot2(p[P], opr[P], a0);
+        a1 = dot2(p[P + 1], opr[P + 1], a1);
+    }
+    return a0 + a1;
+}
+// same against a hi/lo split operand
+template <int BITS>
+__device__ __forceinline__ float chunk_dot_hl(const uint32_t* codes, const uint32_t* oh, const uint32_t* ol,
+                                              float bias, uint32_t B) {
+    uint32_t p[16];
+    code_pairs<BITS>(codes, p, B);
+    float a0 = bias, a1 = 0.f;
+#pragma unroll
+    for (int P = 0; P < 16; ++P) {
+        a0 = dot2(p[P], oh[P], a0);
+        a1 = dot2(p[P], ol[P], a1);
+    }
+    return a0 + a1;
+}
+
+// Sum the SPR partials of row-set q (LDS floats src[0..SPR)) across the LPS
+// lanes of its lane group; every lane of the group gets the total.
+template <int SPR_T>
+__device__ __forceinline__ float group_sum(const float* src, int SPR, int sub, int LPS) {
+    float v = 0.f;
+    if (SPR_T) {
+        const int VPL = SPR_T / LPS;  // SPR_T and LPS are powers of two, LPS <= SPR_T
+        const float* p = src + sub * VPL;
+        for (int i = 0; i < VPL; ++i) v += p[i];
+    } else {
+        for (int i = sub; i < SPR; i += LPS) v += src[i];
+    }
+    for (int o = LPS >> 1; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ===========================================================================
+// Kernel 1 (fast path): H/32 <= 64 chunks per row, G/32 a power of two.
+// SPR_T = H/32 when known at compile time (64 for H = 2048), 0 = runtime.
+// grid = (ceil(I / (NW*T*RPI)), k), block = 64*NW.
+// ===========================================================================
+template <int BITS, int SPR_T, int T, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16_t* __restrict__ x,
+                                                      uint32_t* __restrict__ act) {
+    __shared__ float part[NW][T][2][64];
+    const int SPR = SPR_T ? SPR_T : L.spr_gu;
+    const int RPI = 64 / SPR;
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = blockIdx.y;
+    int rr = lane / SPR;
+    const int seg = lane - rr * SPR;
+    const bool lane_on = rr < RPI;
+    rr = lane_on ? rr : RPI - 1;  // idle lanes repeat an active lane's addresses
+    const int r0 = (blockIdx.x * NW + wv) * (T * RPI);
+    const int slot = __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots));
+    if (slot < 0) {  // the whole workgroup shares j: nobody reaches a barrier
+        for (int t = 0; t < T; ++t) {
+            const int r = r0 + t * RPI + rr;
+            if (lane_on && seg == 0 && r < L.I) write_act<BITS>(act, j, L.I, r, __builtin_nanf(""));
+        }
+        return;
+    }
+    const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb);
+    const uint16_t* mn = sc + 3 * L.NGM;
+    const int gi = seg >> L.gsh;
+
+    uint32_t cg[T][BITS], cu[T][BITS];
+    uint32_t sg[T], mg[T], su[T], mu[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int r = min(r0 + t * RPI + rr, L.I - 1);
+        const uint8_t* rp = base + (int64_t)r * L.rowb_gu + seg * (4 * BITS);
+        load_chunk<BITS>(rp, cg[t]);
+        load_chunk<BITS>(rp + L.nmb, cu[t]);
+        const int gidx = r * L.gpr_gu + gi;
+        sg[t] = sc[gidx];
+        mg[t] = mn[gidx];
+        su[t] = sc[L.NGM + gidx];
+        mu[t] = mn[L.NGM + gidx];
+    }
+    uint32_t xp[16];
+    float vs, xs;
+    load_x_operand<BITS>(x, seg, xp, vs, xs);
+    const float bias = -kBiasF * vs;
+    const uint32_t B = bias_vgpr();
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const bool ok = lane_on && (r0 + t * RPI + rr < L.I);
+        const float dg = chunk_dot<BITS>(cg[t], xp, bias, B);
+        const float du = chunk_dot<BITS>(cu[t], xp, bias, B);
+        const float pg = h2f((uint16_t)sg[t]) * dg + h2f((uint16_t)mg[t]) * xs;
+        const float pu = h2f((uint16_t)su[t]) * du + h2f((uint16_t)mu[t]) * xs;
+        part[wv][t][0][lane] = ok ? pg : 0.f;
+        part[wv][t][1][lane] = ok ? pu : 0.f;
+    }
+    wave_sync_lds();
+
+    // row sums: NQ = 2*T*RPI sums (gate/up interleaved) of SPR partials each
+    const int NQ = 2 * T * RPI;
+    int LPS = 1;
+    while (LPS * 2 * NQ <= 64) LPS <<= 1;
+    const int QPR = 64 / LPS;
+    for (int q0 = 0; q0 < NQ; q0 += QPR) {
+        const int q = q0 + lane / LPS;
+        const int sub = lane & (LPS - 1);
+        const int qq = q < NQ ? q : NQ - 1;
+        const int m = qq & 1, row = qq >> 1, t = row / RPI, rq = row - t * RPI;
+        const float v = group_sum<SPR_T>(&part[wv][t][m][rq * SPR], SPR, sub, LPS);
+        const float u = __shfl_down(v, LPS, 64);
+        if (q < NQ && sub == 0 && m == 0) {
+            const int r = r0 + t * RPI + rq;
+            if (r < L.I) write_act<BITS>(act, j, L.I, r, silu_mul(v, u));
+        }
+    }
+}
+
+// Kernel 1 (generic): any H, G; one wave per (row, expert).
+template <int BITS>
+__global__ __launch_bounds__(64) void k_gate_up_generic(const Layer L, const uint16_t* __restrict__ x,
+                                                        uint32_t* __restrict__ act) {
+    const int lane = threadIdx.x;
+    const int r = blockIdx.x, j = blockIdx.y;
+    const int slot = __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots));
+    float pg = 0.f, pu = 0.f;
+    if (slot >= 0) {
+        const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
+        const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb);
+        const uint16_t* mn = sc + 3 * L.NGM;
+        const uint32_t B = bias_vgpr();
+        for (int c = lane; c < L.spr_gu; c += 64) {
+            uint32_t cg[BITS], cu[BITS], xp[16];
+            const uint8_t* rp = base + (int64_t)r * L.rowb_gu + c * (4 * BITS);
+            load_chunk<BITS>(rp, cg);
+            load_chunk<BITS>(rp + L.nmb, cu);
+            float vs, xs;
+            load_x_operand<BITS>(x, c, xp, vs, xs);
+            const float bias = -kBiasF * vs;
+            const int gidx = r * L.gpr_gu + (c * 32) / L.G;
+            pg += h2f(sc[gidx]) * chunk_dot<BITS>(cg, xp, bias, B) + h2f(mn[gidx]) * xs;
+            pu += h2f(sc[L.NGM + gidx]) * chunk_dot<BITS>(cu, xp, bias, B) + h2f(mn[L.NGM + gidx]) * xs;
+        }
+        pg = wave_sum(pg);
+        pu = wave_sum(pu);
+    } else {
+        pg = pu = __builtin_nanf("");
+    }
+    if (lane == 0) write_act<BITS>(act, j, L.I, r, silu_mul(pg, pu));
+}
+
+// ===========================================================================
+// Kernel 2 (fast path): I/32 <= 64 chunks per row, G/32 a power of two.
+// SPR_T = I/32 when known at compile time (24 for I = 768), 0 = runtime.
+// grid = ceil(H / (T*RPI)), block = 64*k (wave j = expert j),
+// dynamic LDS = (k*T*64 + k*T*RPI) floats.
+// WSUM: out[h] = bf16(sum_j w_j y_j[h]); else y[j*H + h] = y_j[h].
+// ===========================================================================
+template <int BITS, int SPR_T, int T, bool WSUM>
+__global__ __launch_bounds__(1024) void k_down(const Layer L, const uint32_t* __restrict__ act,
+                                               uint16_t* __restrict__ out, float* __restrict__ y) {
+    extern __shared__ float lds[];
+    const int SPR = SPR_T ? SPR_T : L.spr_dn;
+    const int RPI = 64 / SPR;
+    const int RW = T * RPI;
+    const int lane = threadIdx.x & 63;
+    const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int rr = lane / SPR;
+    const int seg = lane - rr * SPR;
+    const bool lane_on = rr < RPI;
+    rr = lane_on ? rr : RPI - 1;
+    const int h0 = blockIdx.x * RW;
+    float* part = lds + j * (T * 64);  // [T][64], this wave's partials
+    float* rows = lds + L.k * (T * 64);  // [k][RW]
+    const int slot = __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots));
+
+    float p[T];
+    if (slot >= 0) {
+        const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
+        const uint8_t* dcodes = base + 2 * L.nmb;
+        const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb) + 2 * L.NGM;
+        const uint16_t* mn = sc + 3 * L.NGM;
+        const int gi = seg >> L.gsh;
+        uint32_t cd[T][BITS], sd[T], md[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int h = min(h0 + t * RPI + rr, L.H - 1);
+            load_chunk<BITS>(dcodes + (int64_t)h * L.rowb_dn + seg * (4 * BITS), cd[t]);
+            sd[t] = sc[h * L.gpr_dn + gi];
+            md[t] = mn[h * L.gpr_dn + gi];
+        }
+        uint32_t AH[16], AL[16];
+        float vs, as;
+        load_act_operand<BITS>(act, j, L.I, seg, AH, AL, vs, as);
+        const float bias = -kBiasF * vs;
+        const uint32_t B = bias_vgpr();
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const bool ok = lane_on && (h0 + t * RPI + rr < L.H);
+            const float d = chunk_dot_hl<BITS>(cd[t], AH, AL, bias, B);
+            const float v = h2f((uint16_t)sd[t]) * d + h2f((uint16_t)md[t]) * as;
+            p[t] = ok ? v : 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < T; ++t) p[t] = __builtin_nanf("");
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) part[t * 64 + lane] = p[t];
+    wave_sync_lds();
+
+    // per-wave row sums: RW sums of SPR partials each
+    int LPS = 1;
+    while (LPS * 2 * RW <= 64) LPS <<= 1;
+    const int QPR = 64 / LPS;
+    for (int q0 = 0; q0 < RW; q0 += QPR) {
+        const int q = q0 + lane / LPS;
+        const int sub = lane & (LPS - 1);
+        const int qq = q < RW ? q : RW - 1;
+        const int t = qq / RPI, rq = qq - t * RPI;
+        const float v = group_sum<SPR_T>(part + t * 64 + rq * SPR, SPR, sub, LPS);
+        if (q < RW && sub == 0) {
+            if (WSUM) {
+                rows[j * RW + q] = v;
+            } else {
+                const int h = h0 + q;
+                if (h < L.H) y[(int64_t)j * L.H + h] = v;
+            }
+        }
+    }
+    if (WSUM) {
+        __syncthreads();
+        for (int q = threadIdx.x; q < RW; q += blockDim.x) {
+            const int h = h0 + q;
+            if (h < L.H) {
+                float acc = 0.f;
+                for (int jj = 0; jj < L.k; ++jj) acc += L.meta[L.k + jj] * rows[jj * RW + q];
+                out[h] = f32_to_bf16(acc);
+            }
+        }
+    }
+}
+
+// Kernel 2 (generic): any I, G; one workgroup (k waves) per output row.
+template <int BITS, bool WSUM>
+__global__ __launch_bounds__(1024) void k_down_generic(const Layer L, const uint32_t* __restrict__ act,
+                                                       uint16_t* __restrict__ out, float* __restrict__ y) {
+    __shared__ float rows[16];
+    const int lane = threadIdx.x & 63;
+    const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = blockIdx.x;
+    const int slot = __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots));
+    float v = 0.f;
+    if (slot >= 0) {
+        const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
+        const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb) + 2 * L.NGM;
+        const uint16_t* mn = sc + 3 * L.NGM;
+        const uint32_t B = bias_vgpr();
+        for (int c = lane; c < L.spr_dn; c += 64) {
+            uint32_t cd[BITS], AH[16], AL[16];
+            load_chunk<BITS>(base + 2 * L.nmb + (int64_t)h * L.rowb_dn + c * (4 * BITS), cd);
+            float vs, as;
+            load_act_operand<BITS>(act, j, L.I, c, AH, AL, vs, as);
+            const int gidx = h * L.gpr_dn + (c * 32) / L.G;
+            v += h2f(sc[gidx]) * chunk_dot_hl<BITS>(cd, AH, AL, -kBiasF * vs, B) + h2f(mn[gidx]) * as;
+        }
+        v = wave_sum(v);
+    } else {
+        v = __builtin_nanf("");
+    }
+    if (WSUM) {
+        if (lane == 0) rows[j] = v;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float acc = 0.f;
+            for (int jj = 0; jj < L.k; ++jj) acc += L.meta[L.k + jj] * rows[jj];
+            out[h] = f32_to_bf16(acc);
+        }
+    } else if (lane == 0) {
+        y[(int64_t)j * L.H + h] = v;
+    }
+}
+
+// Workspace decode: a[j, r] = (hi + lo) * 2^e
+template <int BITS>
+__global__ void k_act_read(const uint32_t* __restrict__ act, int k, int I, float* __restrict__ a) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)k * I) return;
+    const int j = (int)(i / I), r = (int)(i - (int64_t)j * I);
+    const int info = pair_slot<BITS>(r & 31);
+    const int P = info & 15, half = (info >> 4) & 1, e = info >> 5;
+    const uint16_t* a16 = reinterpret_cast<const uint16_t*>(act + ((int64_t)j * (I >> 5) + (r >> 5)) * 32);
+    const float v = bf16_to_f32(a16[2 * P + half]) + bf16_to_f32(a16[2 * (16 + P) + half]);
+    a[i] = v * (float)(1 << e);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+static int make_layer(Layer& L, const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
+                      int64_t H, int64_t I, int bits, int64_t group) {
+    if (!pool || !meta) return fail_inval("null pool or meta");
+    if (!(bits == 4 || bits == 3 || bits == 2)) return fail_inval("bits must be 4, 3 or 2 for the fused kernels");
+    if (k < 1 || k > 16) return fail_inval("k must be in [1, 16]");
+    if (H <= 0 || I <= 0 || group <= 0 || H % group || I % group)
+        return fail_inval("H and I must be positive multiples of group (kernels.py:118)");
+    if (group % 32) return fail_inval("group must be a multiple of 32");
+    if (H > (1 << 16) || I > (1 << 16)) return fail_inval("H, I must be <= 65536");
+    const int64_t n = H * I;
+    const int64_t nb = wisp_expert_nbytes(n, bits, group);
+    if (nb < 0 || slot_bytes < nb) return fail_inval("slot_bytes is smaller than one expert");
+    if (nslots < 1 || nslots > (1 << 24)) return fail_inval("nslots must be in [1, 2^24] (exact float ids)");
+    const int al = bits == 3 ? 4 : 4 * bits;
+    if (!aligned(pool, al) || slot_bytes % al) {
+        set_error("pool base and slot_bytes must be %d-byte aligned for %d-bit experts", al, bits);
+        return WISP_EALIGN;
+    }
+    L.pool = pool;
+    L.meta = meta;
+    L.slot_bytes = slot_bytes;
+    L.nmb = n * bits / 8;
+    L.nslots = (int)nslots;
+    L.k = k;
+    L.H = (int)H;
+    L.I = (int)I;
+    L.G = (int)group;
+    L.rowb_gu = (int)(H * bits / 8);
+    L.rowb_dn = (int)(I * bits / 8);
+    L.gpr_gu = (int)(H / group);
+    L.gpr_dn = (int)(I / group);
+    L.NGM = (int)(n / group);
+    const int cpg = (int)(group / 32);
+    L.gsh = (cpg & (cpg - 1)) ? -1 : __builtin_ctz(cpg);
+    L.spr_gu = (int)(H / 32);
+    L.spr_dn = (int)(I / 32);
+    return WISP_OK;
+}
+
+template <int BITS, int SPR, int T, int NW>
+static void launch_gu(const Layer& L, const uint16_t* x, uint32_t* act, hipStream_t st) {
+    const int RPI = 64 / L.spr_gu;
+    const int rows_wg = NW * T * RPI;
+    const dim3 grid((L.I + rows_wg - 1) / rows_wg, L.k);
+    hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW>), grid, dim3(64 * NW), 0, st, L, x, act);
+}
+
+template <int BITS>
+static int gate_up_bits(const Layer& L, const uint16_t* x, uint32_t* act, hipStream_t st) {
+    if (L.spr_gu > 64 || L.gsh < 0) {
+        hipLaunchKernelGGL((k_gate_up_generic<BITS>), dim3(L.I, L.k), dim3(64), 0, st, L, x, act);
+        return check_launch("k_gate_up_generic");
+    }
+    if (L.spr_gu != 64) {
+        launch_gu<BITS, 0, 2, 4>(L, x, act, st);
+        return check_launch("k_gate_up");
+    }
+    const Tuning& tu = tuning();
+#define WISP_GU(TT, WW)                                   \
+    if (tu.gu_rows == TT && tu.gu_waves == WW) {          \
+        launch_gu<BITS, 64, TT, WW>(L, x, act, st);       \
+        return check_launch("k_gate_up");                 \
+    }
+    WISP_GU(4, 4)
+    WISP_GU(2, 4)
+    WISP_GU(8, 4)
+    WISP_GU(1, 4)
+    WISP_GU(4, 2)
+    WISP_GU(2, 8)
+    WISP_GU(4, 1)
+    WISP_GU(8, 1)
+#undef WISP_GU
+    return fail_inval("unsupported tuning (gu_rows, gu_waves)");
+}
+
+template <int BITS, int SPR, int T, bool WSUM>
+static void launch_dn(const Layer& L, const uint32_t* act, uint16_t* out, float* y, hipStream_t st) {
+    const int RPI = 64 / L.spr_dn;
+    const int RW = T * RPI;
+    const size_t lds = sizeof(float) * ((size_t)L.k * T * 64 + (size_t)L.k * RW);
+    hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM>), dim3((L.H + RW - 1) / RW), dim3(64 * L.k), lds, st, L, act,
+                       out, y);
+}
+
+template <int BITS, bool WSUM>
+static int down_bits(const Layer& L, const uint32_t* act, uint16_t* out, float* y, hipStream_t st) {
+    if (L.spr_dn > 64 || L.gsh < 0) {
+        hipLaunchKernelGGL((k_down_generic<BITS, WSUM>), dim3(L.H), dim3(64 * L.k), 0, st, L, act, out, y);
+        return check_launch("k_down_generic");
+    }
+    if (L.spr_dn != 24) {
+        launch_dn<BITS, 0, 4, WSUM>(L, act, out, y, st);
+        return check_launch("k_down");
+    }
+    switch (tuning().dn_iters) {
+    case 1: launch_dn<BITS, 24, 1, WSUM>(L, act, out, y, st); break;
+    case 2: launch_dn<BITS, 24, 2, WSUM>(L, act, out, y, st); break;
+    case 4: launch_dn<BITS, 24, 4, WSUM>(L, act, out, y, st); break;
+    case 8: launch_dn<BITS, 24, 8, WSUM>(L, act, out, y, st); break;
+    default: return fail_inval("unsupported tuning dn_iters");
+    }
+    return check_launch("k_down");
+}
+
+}  // namespace wisp
+
+using namespace wisp;
+
+extern "C" int64_t wisp_act_bytes(int k, int64_t I) {
+    if (k < 1 || I <= 0) return -1;
+    return (int64_t)k * I * 4;
+}
+
+extern "C" int wisp_moe_gate_up(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
+                                const uint16_t* x, int64_t H, int64_t I, int bits, int64_t group, uint32_t* act,
+                                void* stream) {
+    clear_error();
+    Layer L;
+    const int rc = make_layer(L, pool, slot_bytes, nslots, meta, k, H, I, bits, group);
+    if (rc) return rc;
+    if (!x || !act) return fail_inval("null x or act");
+    if (!aligned(x, 16) || !aligned(act, 16)) {
+        set_error("x and act must be 16-byte aligned");
+        return WISP_EALIGN;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    switch (bits) {
+    case 4: return gate_up_bits<4>(L, x, act, st);
+    case 3: return gate_up_bits<3>(L, x, act, st);
+    default: return gate_up_bits<2>(L, x, act, st);
+    }
+}
+
+static int down_common(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
+                       const uint32_t* act, int64_t H, int64_t I, int bits, int64_t group, uint16_t* out, float* y,
+                       void* stream) {
+    clear_error();
+    Layer L;
+    const int rc = make_layer(L, pool, slot_bytes, nslots, meta, k, H, I, bits, group);
+    if (rc) return rc;
+    if (!act) return fail_inval("null act");
+    if (!aligned(act, 16)) {
+        set_error("act must be 16-byte aligned");
+        return WISP_EALIGN;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    if (out) {
+        switch (bits) {
+        case 4: return down_bits<4, true>(L, act, out, nullptr, st);
+        case 3: return down_bits<3, true>(L, act, out, nullptr, st);
+        default: return down_bits<2, true>(L, act, out, nullptr, st);
+        }
+    }
+    switch (bits) {
+    case 4: return down_bits<4, false>(L, act, nullptr, y, st);
+    case 3: return down_bits<3, false>(L, act, nullptr, y, st);
+    default: return down_bits<2, false>(L, act, nullptr, y, st);
+    }
+}
+
+extern "C" int wisp_moe_down_sum(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
+                                 const uint32_t* act, int64_t H, int64_t I, int bits, int64_t group, uint16_t* out,
+                                 void* stream) {
+    if (!out) return fail_inval("null out");
+    return down_common(pool, slot_bytes, nslots, meta, k, act, H, I, bits, group, out, nullptr, stream);
+}
+
+extern "C" int wisp_moe_down(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
+                             const uint32_t* act, int64_t H, int64_t I, int bits, int64_t group, float* y,
+                             void* stream) {
+    if (!y) return fail_inval("null y");
+    return down_common(pool, slot_bytes, nslots, meta, k, act, H, I, bits, group, nullptr, y, stream);
+}
+
+extern "C" int wisp_moe_decode(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
+                               const uint16_t* x, int64_t H, int64_t I, int bits, int64_t group, uint32_t* act,
+                               uint16_t* out, void* stream) {
+    const int rc = wisp_moe_gate_up(pool, slot_bytes, nslots, meta, k, x, H, I, bits, group, act, stream);
+    if (rc) return rc;
+    return wisp_moe_down_sum(pool, slot_bytes, nslots, meta, k, act, H, I, bits, group, out, stream);
+}
+
+extern "C" int wisp_act_read(const uint32_t* act, int k, int64_t I, int bits, float* a, void* stream) {
+    clear_error();
+    if (!act || !a) return fail_inval("null pointer");
+    if (k < 1 || I <= 0 || I % 32) return fail_inval("k >= 1 and I a positive multiple of 32");
+    const int64_t total = (int64_t)k * I;
+    const dim3 grid((unsigned)((total + 255) / 256));
+    hipStream_t st = (hipStream_t)stream;
+    switch (bits) {
+    case 4: hipLaunchKernelGGL(k_act_read<4>, grid, dim3(256), 0, st, act, k, (int)I, a); break;
+    case 3: hipLaunchKernelGGL(k_act_read<3>, grid, dim3(256), 0, st, act, k, (int)I, a); break;
+    case 2: hipLaunchKernelGGL(k_act_read<2>, grid, dim3(256), 0, st, act, k, (int)I, a); break;
+    default: return fail_inval("bits must be 4, 3 or 2");
+    }
+    return check_launch("k_act_read");
+}

@@ -1,0 +1,299 @@
+// Device helpers shared by the gfx950 kernels of the dequant+GEMV path.
+//
+// Central trick (used by every GEMV kernel): two b-bit codes are turned into a
+// pair of bf16 values with ONE v_and_or_b32, by OR-ing the code bits into the
+// mantissa of the bf16 constant 128.0 (bits 0x4300):
+//     bf16(0x4300 | (q << e)) = 128 + q * 2^e          (e + b <= 7)
+// A v_dot2c_f32_bf16 against a pair (v_lo, v_hi) of bf16 operands scaled by
+// 2^-e then accumulates 128*(v_lo + v_hi) + q_lo*v_lo' + q_hi*v_hi' in fp32;
+// the constant 128*sum(v) is removed by starting the accumulator at
+// -128*sum(v). Products of a <=15-bit integer with a bf16 are exact in fp32.
+// Which two codes share a pair, and the exponent e of each, is fixed per bit
+// width by PairMap<BITS> below; the operand vector (x for gate/up, the
+// activation for down) is stored pre-arranged in the same pair order.
+//
+// A "chunk" is 32 consecutive codes of one matrix row (BITS*4 bytes); the 16
+// pairs of a chunk are numbered P = 0..15.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wisp {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t kBias2 = 0x43004300u;  // two bf16 128.0
+constexpr float kBiasF = 128.0f;
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                          false);
+}
+
+// round-to-nearest-even float -> bf16 pair (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    bf16x2_t v;
+    v.x = (__bf16)lo;
+    v.y = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    return (uint16_t)(pack_bf16x2(f, 0.f) & 0xFFFFu);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+// (w & m) | bias in ONE v_and_or_b32. Written as inline asm because the
+// compiler otherwise splits it into v_and_b32 + v_or_b32 with literals (a
+// gfx9 VOP3 takes no literal and at most one SGPR): the mask goes in an SGPR,
+// the bias in a VGPR that bias_vgpr() materialises once per kernel.
+__device__ __forceinline__ uint32_t ao(uint32_t w, uint32_t m, uint32_t bias) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(m), "v"(bias));
+    return r;
+}
+__device__ __forceinline__ uint32_t bias_vgpr() {
+    uint32_t b;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(b) : "s"(kBias2));
+    return b;
+}
+__device__ __forceinline__ uint32_t alignbit(uint32_t hi, uint32_t lo, uint32_t s) {
+    return __builtin_amdgcn_alignbit(hi, lo, s);
+}
+
+// ---------------------------------------------------------------------------
+// Pair maps: for pair P of a chunk, the chunk-relative code index of its low
+// and high half and the power-of-two exponent e of each half (the code sits at
+// mantissa bits e..e+BITS-1, so the operand is stored multiplied by 2^-e).
+// ---------------------------------------------------------------------------
+template <int BITS>
+struct PairMap;
+
+// 4-bit: dword d holds codes 8d..8d+7 (nibble i at bits 4i). Window w>>4p puts
+// codes 8d+p and 8d+p+4 at bits 0-3 and 16-19.
+template <>
+struct PairMap<4> {
+    static constexpr int lo(int P) { return 8 * (P >> 2) + (P & 3); }
+    static constexpr int hi(int P) { return lo(P) + 4; }
+    static constexpr int elo(int) { return 0; }
+    static constexpr int ehi(int) { return 0; }
+};
+
+// 3-bit: 32 codes in 96 bits (code c at bit 3c). Pairs (c, c+5) for
+// c in 0..4 and 10..14 with the low code at window bit 1 (e=1) and the high
+// code at bit 16 (e=0); pairs (c, c+6) for c in 20..25 with the low code at
+// bit 0 (e=0) and the high code at bit 18 (e=2).
+template <>
+struct PairMap<3> {
+    static constexpr int lo(int P) { return P < 5 ? P : (P < 10 ? 10 + (P - 5) : 20 + (P - 10)); }
+    static constexpr int hi(int P) { return P < 5 ? P + 5 : (P < 10 ? 15 + (P - 5) : 26 + (P - 10)); }
+    static constexpr int elo(int P) { return P < 10 ? 1 : 0; }
+    static constexpr int ehi(int P) { return P < 10 ? 0 : 2; }
+};
+
+// 2-bit: dword d holds codes 16d..16d+15 (code i at bits 2i). Windows w, w>>6,
+// w>>12 each give up to three pairs (i, i+8) at mantissa bits 0, 2 and 4.
+template <>
+struct PairMap<2> {
+    static constexpr int lo(int P) { return 16 * (P >> 3) + (P & 7); }
+    static constexpr int hi(int P) { return lo(P) + 8; }
+    static constexpr int elo(int P) { return 2 * ((P & 7) % 3); }
+    static constexpr int ehi(int P) { return elo(P); }
+};
+
+// chunk dwords -> 16 biased bf16 code pairs
+template <int BITS>
+__device__ __forceinline__ void code_pairs(const uint32_t* d, uint32_t* p, uint32_t B);
+
+template <>
+__device__ __forceinline__ void code_pairs<4>(const uint32_t* d, uint32_t* p, uint32_t B) {
+    constexpr uint32_t M = 0x000F000Fu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t w = d[i];
+        p[4 * i + 0] = ao(w, M, B);
+        p[4 * i + 1] = ao(w >> 4, M, B);
+        p[4 * i + 2] = ao(w >> 8, M, B);
+        p[4 * i + 3] = ao(w >> 12, M, B);
+    }
+}
+
+template <>
+__device__ __forceinline__ void code_pairs<3>(const uint32_t* d, uint32_t* p, uint32_t B) {
+    constexpr uint32_t MA = 0x0007000Eu;  // low code at bits 1-3, high code at bits 16-18
+    constexpr uint32_t MC = 0x001C0007u;  // low code at bits 0-2, high code at bits 18-20
+    const uint32_t d0 = d[0], d1 = d[1], d2 = d[2];
+    // window start 3c-1 for c = 0..4
+    p[0] = ao(d0 << 1, MA, B);
+    p[1] = ao(alignbit(d1, d0, 2), MA, B);
+    p[2] = ao(alignbit(d1, d0, 5), MA, B);
+    p[3] = ao(alignbit(d1, d0, 8), MA, B);
+    p[4] = ao(alignbit(d1, d0, 11), MA, B);
+    // window start 3c-1 for c = 10..14
+    p[5] = ao(alignbit(d1, d0, 29), MA, B);
+    p[6] = ao(d1, MA, B);
+    p[7] = ao(alignbit(d2, d1, 3), MA, B);
+    p[8] = ao(alignbit(d2, d1, 6), MA, B);
+    p[9] = ao(alignbit(d2, d1, 9), MA, B);
+    // window start 3c for c = 20..25
+    p[10] = ao(alignbit(d2, d1, 28), MC, B);
+    p[11] = ao(alignbit(d2, d1, 31), MC, B);
+    p[12] = ao(d2 >> 2, MC, B);
+    p[13] = ao(d2 >> 5, MC, B);
+    p[14] = ao(d2 >> 8, MC, B);
+    p[15] = ao(d2 >> 11, MC, B);
+}
+
+template <>
+__device__ __forceinline__ void code_pairs<2>(const uint32_t* d, uint32_t* p, uint32_t B) {
+    constexpr uint32_t M0 = 0x00030003u, M2 = 0x000C000Cu, M4 = 0x00300030u;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t w0 = d[i], w6 = d[i] >> 6, w12 = d[i] >> 12;
+        p[8 * i + 0] = ao(w0, M0, B);
+        p[8 * i + 1] = ao(w0, M2, B);
+        p[8 * i + 2] = ao(w0, M4, B);
+        p[8 * i + 3] = ao(w6, M0, B);
+        p[8 * i + 4] = ao(w6, M2, B);
+        p[8 * i + 5] = ao(w6, M4, B);
+        p[8 * i + 6] = ao(w12, M0, B);
+        p[8 * i + 7] = ao(w12, M2, B);
+    }
+}
+
+// Chunk-relative code index c (0..31) -> pair slot: P | half<<4 | e<<5
+// (closed forms of the inverse of PairMap<BITS>).
+template <int BITS>
+__device__ __forceinline__ int pair_slot(int c);
+template <>
+__device__ __forceinline__ int pair_slot<4>(int c) {
+    return (((c >> 3) << 2) | (c & 3)) | (((c >> 2) & 1) << 4);
+}
+template <>
+__device__ __forceinline__ int pair_slot<2>(int c) {
+    const int i = c & 7;
+    const int e = 2 * (i - 3 * ((i * 11) >> 5));  // 2*(i % 3) for i < 8
+    return ((c >> 4) << 3 | i) | (((c >> 3) & 1) << 4) | (e << 5);
+}
+template <>
+__device__ __forceinline__ int pair_slot<3>(int c) {
+    // c: 0-4 -> (c,lo,1) 5-9 -> (c-5,hi,0) 10-14 -> (c-5,lo,1) 15-19 -> (c-10,hi,0)
+    //    20-25 -> (c-10,lo,0) 26-31 -> (c-16,hi,2)
+    if (c < 20) {
+        const int blk = c / 5;  // 0..3
+        const int P = c - 5 * ((blk + 1) >> 1);
+        const int half = blk & 1;
+        return P | (half << 4) | ((half ? 0 : 1) << 5);
+    }
+    return c < 26 ? (c - 10) : ((c - 16) | (1 << 4) | (2 << 5));
+}
+
+// exact multiplication by 2^-e for the small e used here
+__device__ __forceinline__ float scale_pow2(float v, int e) {
+    return v * __uint_as_float((uint32_t)(127 - e) << 23);
+}
+
+// load one chunk (BITS dwords) from a BITS*4-aligned address (4-aligned for
+// 3-bit); non-temporal: every expert byte is read exactly once per layer.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+template <int BITS>
+__device__ __forceinline__ void load_chunk(const uint8_t* p, uint32_t* d);
+template <>
+__device__ __forceinline__ void load_chunk<4>(const uint8_t* p, uint32_t* d) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+}
+template <>
+__device__ __forceinline__ void load_chunk<3>(const uint8_t* p, uint32_t* d) {
+    const u32x3_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x3_t*>(p));
+    d[0] = v.x; d[1] = v.y; d[2] = v.z;
+}
+template <>
+__device__ __forceinline__ void load_chunk<2>(const uint8_t* p, uint32_t* d) {
+    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    d[0] = v.x; d[1] = v.y;
+}
+
+// bf16 pair (2^elo(P), 2^ehi(P)): dot2 of a stored operand pair with it gives
+// the sum of the two true (unscaled) operand values.
+template <int BITS>
+__device__ __forceinline__ constexpr uint32_t unscale_pair(int P) {
+    return ((uint32_t)(0x3F80 + (PairMap<BITS>::ehi(P) << 7)) << 16) | (uint32_t)(0x3F80 + (PairMap<BITS>::elo(P) << 7));
+}
+constexpr uint32_t kOnes2 = 0x3F803F80u;  // bf16 pair (1, 1)
+
+// Operand pairs of one chunk from the 16 dwords w[] holding 32 consecutive
+// bf16 values (value c = half c&1 of w[c>>1]): pair P = (v[lo]*2^-elo,
+// v[hi]*2^-ehi). Exact for bf16 inputs.
+template <int BITS>
+__device__ __forceinline__ void operand_pairs(const uint32_t* w, uint32_t* pr) {
+#pragma unroll
+    for (int P = 0; P < 16; ++P) {
+        const int lo = PairMap<BITS>::lo(P), hi = PairMap<BITS>::hi(P);
+        const uint32_t wl = w[lo >> 1], wh = w[hi >> 1];
+        if (PairMap<BITS>::elo(P) == 0 && PairMap<BITS>::ehi(P) == 0) {
+            // pure 16-bit shuffle: v_perm_b32 / v_bfi_b32
+            const uint32_t l16 = (lo & 1) ? (wl >> 16) : (wl & 0xFFFFu);
+            const uint32_t h16 = (hi & 1) ? (wh & 0xFFFF0000u) : (wh << 16);
+            pr[P] = l16 | h16;
+        } else {
+            const float fl = (lo & 1) ? bf16_hi(wl) : bf16_lo(wl);
+            const float fh = (hi & 1) ? bf16_hi(wh) : bf16_lo(wh);
+            pr[P] = pack_bf16x2(scale_pow2(fl, PairMap<BITS>::elo(P)), scale_pow2(fh, PairMap<BITS>::ehi(P)));
+        }
+    }
+}
+
+// Sum of the stored operand values (for the bias) and of the true values.
+template <int BITS>
+__device__ __forceinline__ void operand_sums(const uint32_t* pr, float& vsum, float& tsum) {
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int P = 0; P < 16; P += 2) {
+        a0 = dot2(pr[P], kOnes2, a0);
+        a1 = dot2(pr[P + 1], kOnes2, a1);
+    }
+    vsum = a0 + a1;
+    if (BITS == 4) {
+        tsum = vsum;
+    } else {
+        float b0 = 0.f, b1 = 0.f;
+#pragma unroll
+        for (int P = 0; P < 16; P += 2) {
+            b0 = dot2(pr[P], unscale_pair<BITS>(P), b0);
+            b1 = dot2(pr[P + 1], unscale_pair<BITS>(P + 1), b1);
+        }
+        tsum = b0 + b1;
+    }
+}
+
+// Wave-wide sum (wave64) with xor shuffles.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    // silu(g) * u = g * sigmoid(g) * u, as kernels.py:68 (fp32)
+    return g * (1.0f / (1.0f + __expf(-g))) * u;
+}
+
+}  // namespace wisp

@@ -1,0 +1,90 @@
+"""Loader for libwisp_hip.so, the gfx950 HIP library of this package.
+
+torch is imported first on purpose: the library then binds to the HIP runtime
+torch already loaded (both carry the SONAME libamdhip64.so.7), so streams and
+device pointers from torch are valid in the library. There is no CPU or
+eager-PyTorch fallback: if the library is missing, every GPU entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_ROOT, "lib", "libwisp_hip.so")
+ABI_VERSION = 1
+
+WISP_OK, WISP_EINVAL, WISP_EALIGN = 0, -1, -2
+
+_i64, _i32, _vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+
+# name -> (restype, argtypes); mirrors include/wisp_hip.h
+SIGNATURES = {
+    "wisp_abi_version": (_i32, []),
+    "wisp_last_error": (ctypes.c_char_p, []),
+    "wisp_expert_nbytes": (_i64, [_i64, _i32, _i64]),
+    "wisp_act_bytes": (_i64, [_i32, _i64]),
+    "wisp_quantize": (_i32, [_vp, _i32, _i64, _i32, _i64, _vp, _vp]),
+    "wisp_pack": (_i32, [_vp, _i64, _i32, _vp, _vp]),
+    "wisp_unpack": (_i32, [_vp, _i64, _i32, _vp, _vp]),
+    "wisp_dequant": (_i32, [_vp, _i64, _vp, _i64, _i64, _i64, _i32, _i64, _vp, _vp]),
+    "wisp_moe_gate_up": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp]),
+    "wisp_moe_down_sum": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp]),
+    "wisp_moe_down": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp]),
+    "wisp_moe_decode": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp, _vp]),
+    "wisp_set_tuning": (_i32, [_i32, _i32, _i32]),
+    "wisp_act_read": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp]),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python wisp-runtime_amd/build_lib.py` "
+                "(or __graft_entry__.build()). There is no fallback path."
+            )
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype, f.argtypes = res, args
+        v = L.wisp_abi_version()
+        if v != ABI_VERSION:
+            raise RuntimeError(f"libwisp_hip ABI {v}, expected {ABI_VERSION}: rebuild the library")
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != WISP_OK:
+        msg = lib().wisp_last_error().decode(errors="replace")
+        if rc in (WISP_EINVAL, WISP_EALIGN):
+            raise ValueError(f"{what}: {msg}")
+        raise RuntimeError(f"{what}: {msg} (hip error {rc})")
+
+
+def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_gpu(*tensors: torch.Tensor, what: str) -> torch.device:
+    dev = None
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(f"{what} needs ROCm device tensors (got a {t.device} tensor); no CPU path is provided")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"{what}: tensors on different devices ({dev}, {t.device})")
+    return dev

@@ -1,0 +1,119 @@
+"""Fused group-wise 4/3/2-bit dequant + GEMV for batch-1 MoE decode, on gfx950.
+
+Same callable surface as the reference's wisp/kernels.py (imronpuji/wisp-runtime),
+so the MoE layer, expert cache and graph decoder call it unchanged. The work is
+done by hand-written HIP kernels in libwisp_hip.so reading the packed experts
+straight out of the GPU slot pool:
+  kernel 1:  a[j, r] = silu(Wg_j[r,:] . x) * (Wu_j[r,:] . x)        every expert j
+  kernel 2:  out[h]  = sum_j w_j * (Wd_j[h,:] . a_j)                 (or per-expert y)
+with the dequant folded into the dot product per group (kernels.py:12):
+  sum_i (q_i*s + m) x_i = s*(q.x) + m*sum(x), accumulated in fp32.
+
+Every call only enqueues kernels on the current torch stream; outputs and the
+workspace come from torch.empty, so the calls can be captured into a graph. The
+`block_*` / `num_warps` keyword arguments are the reference's Triton tiling knobs;
+they are accepted and ignored (launch shapes are set by wisp_set_tuning).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _prep_x(x: torch.Tensor) -> torch.Tensor:
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"x must be bfloat16 (got {x.dtype})")
+    x = x.reshape(-1).contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()
+    return x
+
+
+def _check_pool(pool: torch.Tensor) -> None:
+    assert pool.dtype == torch.uint8 and pool.dim() == 2 and pool.stride(1) == 1, (
+        "pool must be a row-contiguous [nslots, slot_bytes] uint8 tensor"
+    )
+
+
+def _layer(pool, meta, x, k, n, H, I, group, bits):
+    assert H % group == 0 and I % group == 0 and n == H * I
+    _check_pool(pool)
+    dev = _lib.require_gpu(pool, meta, x, what=f"moe_decode (bits={bits})")
+    assert meta.dtype == torch.float32 and meta.numel() >= 2 * k, "meta must be float32 [2k]"
+    meta = meta.contiguous()
+    x = _prep_x(x)
+    assert x.numel() == H
+    act = torch.empty((k, I), dtype=torch.float32, device=dev).view(torch.int32)
+    return dev, meta, x, act
+
+
+def moe_decode_fast(pool, meta, x, k, n, H, I, bits, group=128):
+    """Two launches for one layer: gate_up+SiLU then down + routing-weighted sum.
+    meta: float32 [2k] on the GPU = [slot_0..slot_{k-1}, w_0..w_{k-1}]. Returns [H] in x.dtype."""
+    dev, meta, x, act = _layer(pool, meta, x, k, n, H, I, group, bits)
+    out = torch.empty((H,), dtype=x.dtype, device=dev)
+    _lib.check(
+        _lib.lib().wisp_moe_decode(
+            _lib.ptr(pool), pool.stride(0), pool.shape[0], _lib.ptr(meta), k, _lib.ptr(x), H, I, bits, group,
+            _lib.ptr(act), _lib.ptr(out), _lib.stream(dev),
+        ),
+        "moe_decode",
+    )
+    return out
+
+
+def moe_decode_q4_fast(pool, meta, x, k, n, H, I, group=128, block_gu=32, block_down=8, num_warps=4):
+    """kernels.py:188-203: 4-bit, 2 kernel launches in total, one packed routing buffer.
+    meta: float32 [2k] on the GPU = [slot_0..slot_{k-1}, w_0..w_{k-1}]. Returns [H] in x.dtype."""
+    return moe_decode_fast(pool, meta, x, k, n, H, I, 4, group)
+
+
+def moe_decode_q3_fast(pool, meta, x, k, n, H, I, group=128, block_gu=8, block_down=8, num_warps=4):
+    """kernels.py:310-322: 3-bit twin of moe_decode_q4_fast (same meta layout)."""
+    return moe_decode_fast(pool, meta, x, k, n, H, I, 3, group)
+
+
+def moe_decode_q2_fast(pool, meta, x, k, n, H, I, group=128, block_gu=8, block_down=8, num_warps=4):
+    """2-bit twin of moe_decode_q4_fast. The reference packs 2-bit experts (quant.py:32-34)
+    but has no fused 2-bit kernel; this one follows the same semantics."""
+    return moe_decode_fast(pool, meta, x, k, n, H, I, 2, group)
+
+
+def moe_decode_q4(pool, slots, x, w, n, H, I, group=128, block_r=32, num_warps=4):
+    """kernels.py:115-137. pool: [nslots, nbytes] uint8 (4-bit experts); slots: int64 [k];
+    x: [H] (bf16); w: [k] routing weights. Per-expert y[k, H] from the kernels, then the
+    weighted sum in fp32 and the cast to x.dtype, as the reference does."""
+    k = slots.numel()
+    meta = torch.cat([slots.reshape(-1).to(torch.float32), w.reshape(-1).to(torch.float32)])
+    dev, meta, x, act = _layer(pool, meta, x, k, n, H, I, group, 4)
+    L = _lib.lib()
+    st = _lib.stream(dev)
+    args = (_lib.ptr(pool), pool.stride(0), pool.shape[0], _lib.ptr(meta), k)
+    _lib.check(L.wisp_moe_gate_up(*args, _lib.ptr(x), H, I, 4, group, _lib.ptr(act), st), "moe_decode_q4 gate_up")
+    y = torch.empty((k, H), dtype=torch.float32, device=dev)
+    _lib.check(L.wisp_moe_down(*args, _lib.ptr(act), H, I, 4, group, _lib.ptr(y), st), "moe_decode_q4 down")
+    return (y * w.float().unsqueeze(1)).sum(0).to(x.dtype)
+
+
+def gate_up_act(pool, meta, x, k, n, H, I, bits, group=128) -> torch.Tensor:
+    """Kernel 1 alone, decoded to fp32 a [k, I] (for checks of the first kernel)."""
+    dev, meta, x, act = _layer(pool, meta, x, k, n, H, I, group, bits)
+    L = _lib.lib()
+    st = _lib.stream(dev)
+    _lib.check(
+        L.wisp_moe_gate_up(
+            _lib.ptr(pool), pool.stride(0), pool.shape[0], _lib.ptr(meta), k, _lib.ptr(x), H, I, bits, group,
+            _lib.ptr(act), st,
+        ),
+        "gate_up",
+    )
+    a = torch.empty((k, I), dtype=torch.float32, device=dev)
+    _lib.check(L.wisp_act_read(_lib.ptr(act), k, I, bits, _lib.ptr(a), st), "act_read")
+    return a
+
+
+def set_tuning(gu_rows: int = 0, gu_waves: int = 0, dn_iters: int = 0) -> None:
+    """Launch-shape knobs of the two decode kernels (0 keeps the current value)."""
+    _lib.check(_lib.lib().wisp_set_tuning(gu_rows, gu_waves, dn_iters), "set_tuning")
