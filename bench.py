@@ -23,7 +23,6 @@ import json
 import os
 import platform
 import sys
-import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "wisp-runtime_amd"))
@@ -36,6 +35,7 @@ from wisp.quant import expert_nbytes, quantize  # noqa: E402
 
 H, I, E, K_TOP, G = 2048, 768, 128, 8, 128
 PEAK_HBM_GBS = 8000.0
+ROUNDS = 8  # distinct routings cycled through the graph replays
 
 
 def alg_bytes(bits: int):
@@ -47,6 +47,101 @@ def alg_bytes(bits: int):
     gu = K_TOP * 2 * (mat_codes + mat_sm) + 2 * H + 4 * K_TOP * I + 8 * K_TOP
     dn = K_TOP * (mat_codes + mat_sm) + 4 * K_TOP * I + 2 * H + 8 * K_TOP
     return gu, dn
+
+
+class Layers:
+    """The synthetic C2 workload resident on the GPU: `layers` pools of E experts, routings
+    and inputs, plus capturable launchers for the two kernels of each layer."""
+
+    def __init__(self, dev, bits=4, layers=48, seed=2):
+        self.dev, self.bits, self.layers = dev, bits, layers
+        n = H * I
+        self.nb = nb = expert_nbytes(n, bits, G)
+        print(f"[bench] quantizing {E} experts ({bits}-bit, {nb} B each) on the GPU", file=sys.stderr, flush=True)
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        base = torch.empty((E, nb), dtype=torch.uint8, device=dev)
+        for e in range(E):
+            w3 = torch.randn((3, n), generator=gen, device=dev) * 0.02
+            base[e].copy_(quantize(w3, bits, G))
+        self.pool = torch.empty((layers * E, nb), dtype=torch.uint8, device=dev)
+        for l in range(layers):
+            self.pool[l * E : (l + 1) * E].copy_(base)
+        del base
+        g2 = torch.Generator(device=dev).manual_seed(seed + 1)
+        logits = torch.randn((ROUNDS, layers, E), generator=g2, device=dev)
+        sel, rw = route(logits.reshape(-1, E), K_TOP)
+        slots = sel.reshape(ROUNDS, layers, K_TOP) + (torch.arange(layers, device=dev) * E).view(1, layers, 1)
+        self.metas = pack_meta(slots, rw.reshape(ROUNDS, layers, K_TOP)).contiguous()
+        self.xs = torch.randn((layers, H), generator=g2, device=dev).to(torch.bfloat16)
+        self.meta_live = self.metas[0].clone()
+        self.act = torch.empty((layers, K_TOP, I), dtype=torch.int32, device=dev)
+        self.out = torch.empty((layers, H), dtype=torch.bfloat16, device=dev)
+        self.stream = torch.cuda.Stream(dev)
+        torch.cuda.synchronize()
+        print(f"[bench] slot pool {self.pool.numel() / 2**30:.2f} GiB ({layers} layers x {E} experts)",
+              file=sys.stderr, flush=True)
+
+    def gate_up(self, l, st):
+        L, sp = _lib.lib(), _lib.ptr
+        _lib.check(L.wisp_moe_gate_up(sp(self.pool), self.nb, self.pool.shape[0], sp(self.meta_live[l]), K_TOP,
+                                      sp(self.xs[l]), H, I, self.bits, G, sp(self.act[l]), st), "gate_up")
+
+    def down(self, l, st):
+        L, sp = _lib.lib(), _lib.ptr
+        _lib.check(L.wisp_moe_down_sum(sp(self.pool), self.nb, self.pool.shape[0], sp(self.meta_live[l]), K_TOP,
+                                       sp(self.act[l]), H, I, self.bits, G, sp(self.out[l]), st), "down_sum")
+
+    def layer(self, l, st):
+        self.gate_up(l, st)
+        self.down(l, st)
+
+    def capture(self, body):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(self.stream):
+            st = _lib.stream(self.dev)
+            for l in range(self.layers):  # eager warm-up of the same launches
+                body(l, st)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=self.stream):
+                st = _lib.stream(self.dev)
+                for l in range(self.layers):
+                    body(l, st)
+        torch.cuda.synchronize()
+        return g
+
+    def run(self, g, reps, swap_meta):
+        with torch.cuda.stream(self.stream):
+            for r in range(reps):
+                if swap_meta:
+                    self.meta_live.copy_(self.metas[r % ROUNDS], non_blocking=True)
+                g.replay()
+
+    def timed(self, g, reps, swap_meta):
+        """Seconds for `reps` graph replays, HIP events on the replay stream."""
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(self.stream)
+        self.run(g, reps, swap_meta)
+        e1.record(self.stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3
+
+
+def measure(W: Layers, steps: int, warmup: int):
+    """Per-layer and per-kernel seconds (graph replays over all layers)."""
+    g_layer = W.capture(W.layer)
+    g_gu = W.capture(W.gate_up)
+    g_dn = W.capture(W.down)
+    warm_reps = max(1, -(-warmup // W.layers))
+    reps = max(1, -(-steps // W.layers))
+    W.run(g_layer, warm_reps, True)
+    torch.cuda.synchronize()
+    n = reps * W.layers
+    t_layer = W.timed(g_layer, reps, True) / n
+    t_gu = W.timed(g_gu, reps, False) / n
+    t_dn = W.timed(g_dn, reps, False) / n
+    return dict(steps=n, warmup=warm_reps * W.layers, layer=t_layer, gu=t_gu, dn=t_dn)
 
 
 def main():
@@ -70,114 +165,27 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    L = _lib.lib()
     if a.tune:
         gr, gw, dn = (int(v) for v in a.tune.split(","))
-        _lib.check(L.wisp_set_tuning(gr, gw, dn), "set_tuning")
+        _lib.check(_lib.lib().wisp_set_tuning(gr, gw, dn), "set_tuning")
 
-    bits, layers = a.bits, a.layers
-    n = H * I
-    nb = expert_nbytes(n, bits, G)
-    print(f"[bench] quantizing {E} experts ({bits}-bit, {nb} B each) on the GPU", file=sys.stderr, flush=True)
-    gen = torch.Generator(device=dev).manual_seed(2)
-    base = torch.empty((E, nb), dtype=torch.uint8, device=dev)
-    for e in range(E):
-        w3 = torch.randn((3, n), generator=gen, device=dev) * 0.02
-        base[e].copy_(quantize(w3, bits, G))
-    pool = torch.empty((layers * E, nb), dtype=torch.uint8, device=dev)
-    for l in range(layers):
-        pool[l * E : (l + 1) * E].copy_(base)
-    del base
-    torch.cuda.synchronize()
-    print(f"[bench] slot pool {pool.numel() / 2**30:.2f} GiB ({layers} layers x {E} experts)", file=sys.stderr,
-          flush=True)
-
-    # routing and inputs for `rounds` distinct replays of the layer sequence
-    rounds = 8
-    g2 = torch.Generator(device=dev).manual_seed(3)
-    logits = torch.randn((rounds, layers, E), generator=g2, device=dev)
-    sel, rw = route(logits.reshape(-1, E), K_TOP)
-    slots = sel.reshape(rounds, layers, K_TOP) + (torch.arange(layers, device=dev) * E).view(1, layers, 1)
-    metas = pack_meta(slots, rw.reshape(rounds, layers, K_TOP)).contiguous()  # [rounds, layers, 2k]
-    xs = (torch.randn((layers, H), generator=g2, device=dev)).to(torch.bfloat16)
-    meta_live = torch.empty((layers, 2 * K_TOP), dtype=torch.float32, device=dev)
-    meta_live.copy_(metas[0])
-    act = torch.empty((layers, K_TOP, I), dtype=torch.int32, device=dev)
-    out = torch.empty((layers, H), dtype=torch.bfloat16, device=dev)
-
-    stream = torch.cuda.Stream(dev)
-    sp = _lib.ptr
-
-    def gate_up(l, st):
-        _lib.check(L.wisp_moe_gate_up(sp(pool), nb, pool.shape[0], sp(meta_live[l]), K_TOP, sp(xs[l]), H, I, bits,
-                                      G, sp(act[l]), st), "gate_up")
-
-    def down(l, st):
-        _lib.check(L.wisp_moe_down_sum(sp(pool), nb, pool.shape[0], sp(meta_live[l]), K_TOP, sp(act[l]), H, I,
-                                       bits, G, sp(out[l]), st), "down_sum")
-
-    def capture(body):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(stream):
-            st = _lib.stream(dev)
-            for l in range(layers):  # eager warm-up of the same launches
-                body(l, st)
-            torch.cuda.synchronize()
-            with torch.cuda.graph(g, stream=stream):
-                st = _lib.stream(dev)
-                for l in range(layers):
-                    body(l, st)
-        torch.cuda.synchronize()
-        return g
-
-    g_layer = capture(lambda l, st: (gate_up(l, st), down(l, st)))
-    g_gu = capture(gate_up)
-    g_dn = capture(down)
-
-    def run(g, reps, swap_meta):
-        with torch.cuda.stream(stream):
-            for r in range(reps):
-                if swap_meta:
-                    meta_live.copy_(metas[r % rounds], non_blocking=True)
-                g.replay()
-
-    def timed(g, reps, swap_meta):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record(stream)
-        run(g, reps, swap_meta)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e-3  # seconds
-
-    warm_reps = max(1, -(-a.warmup // layers))
-    reps = max(1, -(-a.steps // layers))
-    steps = reps * layers
-    print(f"[bench] warm-up {warm_reps * layers} layers, timing {steps} layers", file=sys.stderr, flush=True)
-    run(g_layer, warm_reps, True)
-    torch.cuda.synchronize()
-    t_layer = timed(g_layer, reps, True)
-    t_gu = timed(g_gu, reps, False)
-    t_dn = timed(g_dn, reps, False)
-
+    bits = a.bits
+    W = Layers(dev, bits, a.layers)
+    print(f"[bench] timing {a.steps} layers after {a.warmup} warm-up layers", file=sys.stderr, flush=True)
+    m = measure(W, a.steps, a.warmup)
     gu_b, dn_b = alg_bytes(bits)
     layer_b = gu_b + dn_b
-    s_layer = t_layer / steps
-    s_gu = t_gu / steps
-    s_dn = t_dn / steps
-    value = layer_b / s_layer / 1e9
-    ach_gu = gu_b / s_gu / 1e9
+    value = layer_b / m["layer"] / 1e9
+    ach_gu = gu_b / m["gu"] / 1e9
 
     res = {
-        "metric": "us per MoE layer + achieved HBM GB/s (% of peak), 4-bit top-8, batch 1"
-        if bits == 4 else f"us per MoE layer + achieved HBM GB/s (% of peak), {bits}-bit top-8, batch 1",
+        "metric": f"us per MoE layer + achieved HBM GB/s (% of peak), {bits}-bit top-8, batch 1",
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": warm_reps * layers,
-        "ms_per_step": round(s_layer * 1e3, 6),
+        "steps": m["steps"],
+        "warmup": m["warmup"],
+        "ms_per_step": round(m["layer"] * 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -185,21 +193,21 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": f"C2: one Qwen3-30B-A3B MoE layer, decode batch 1, top-{K_TOP} of {E} experts, {bits}-bit "
-                        f"group-{G}, H={H} I={I}, {layers} layer pools rotated",
+                        f"group-{G}, H={H} I={I}, {a.layers} layer pools rotated",
             "weights": f"u{bits} group-{G} fp16 scale+min",
             "accumulate": "fp32 (bf16 x dot2)",
             "bytes_per_layer": layer_b,
         },
-        "us_per_layer": round(s_layer * 1e6, 3),
+        "us_per_layer": round(m["layer"] * 1e6, 3),
         "pct_hbm_peak": round(100.0 * value / PEAK_HBM_GBS, 2),
         "kernels": {
-            "gate_up_us": round(s_gu * 1e6, 3),
-            "down_us": round(s_dn * 1e6, 3),
-            "sum_us": round((s_gu + s_dn) * 1e6, 3),
+            "gate_up_us": round(m["gu"] * 1e6, 3),
+            "down_us": round(m["dn"] * 1e6, 3),
+            "sum_us": round((m["gu"] + m["dn"]) * 1e6, 3),
             "gate_up_bytes": gu_b,
             "down_bytes": dn_b,
             "gate_up_GBs": round(ach_gu, 1),
-            "down_GBs": round(dn_b / s_dn / 1e9, 1),
+            "down_GBs": round(dn_b / m["dn"] / 1e9, 1),
             "timing": "HIP events around graph replays of each kernel alone (per-launch average, incl. "
                       "in-graph launch gaps)",
         },
@@ -216,15 +224,14 @@ def main():
 
     if not a.no_cpu_baseline:
         sys.path.insert(0, ROOT)
-        from oracle import cpu_baseline as CB  # the checker/baseline side only
+        from oracle import cpu_baseline as CB  # the baseline side only
 
         # bounded sample: 96 distinct experts from one layer pool on the host, 8 routed per layer
-        rows = pool[:96].cpu()
-        routes = []
+        rows = W.pool[:96].cpu()
         lg = torch.randn((64, 96), generator=torch.Generator().manual_seed(5))
         s_cpu, w_cpu = route(lg, K_TOP)
         routes = [(s_cpu[i].tolist(), w_cpu[i].float().tolist()) for i in range(64)]
-        xcpu = [xs[i % layers].cpu() for i in range(8)]
+        xcpu = [W.xs[i % W.layers].cpu() for i in range(8)]
         med, cnt, thr = CB.time_layers(rows, routes, xcpu, H, I, bits, G, budget_s=a.cpu_budget)
         res["cpu_baseline"] = {
             "value": round(layer_b / med / 1e9, 3),

@@ -107,7 +107,7 @@ int wisp_moe_decode(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, con
  * kernel 1, gu_waves = waves per workgroup in kernel 1, dn_iters = row
  * iterations per workgroup in kernel 2 (each in {1,2,4,8}; 0 keeps the
  * current value; kernel 1 supports the pairs (4,4) (2,4) (8,4) (1,4) (4,2)
- * (2,8) (4,1) (8,1)). Defaults (4, 4, 4). No reference counterpart: the
+ * (2,8) (4,1) (8,1)). Defaults (2, 4, 4). No reference counterpart: the
  * reference's block_* keyword arguments are Triton tiling knobs of its own
  * kernels (wisp/kernels.py:115, 188, 310). */
 int wisp_set_tuning(int gu_rows, int gu_waves, int dn_iters);

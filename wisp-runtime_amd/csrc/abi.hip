@@ -17,7 +17,7 @@ void set_error(const char* fmt, ...) {
 void clear_error() { g_err[0] = 0; }
 
 Tuning& tuning() {
-    static Tuning t{4, 4, 4};
+    static Tuning t{2, 4, 4};
     return t;
 }
 

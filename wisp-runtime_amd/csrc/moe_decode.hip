@@ -24,6 +24,16 @@
 #include "wisp_device.hpp"
 #include "wisp_internal.hpp"
 
+#ifndef WISP_GU_XLDS
+#define WISP_GU_XLDS 0
+#endif
+#ifndef WISP_DN_ALDS
+#define WISP_DN_ALDS 1
+#endif
+#ifndef WISP_QSC
+#define WISP_QSC 1
+#endif
+
 namespace wisp {
 
 // Layer constants, computed once on the host (no divisions in the kernels).
@@ -133,30 +143,49 @@ __device__ __forceinline__ float chunk_dot_hl(const uint32_t* codes, const uint3
 }
 
 // Sum the SPR partials of row-set q (LDS floats src[0..SPR)) across the LPS
-// lanes of its lane group; every lane of the group gets the total.
+// lanes of its lane group (LPS a power of two <= 16, groups aligned inside a
+// 16-lane DPP row); every lane of the group gets the total. The cross-lane
+// steps are DPP adds (quad_perm xor 1 / xor 2, row_half_mirror, row_mirror).
 template <int SPR_T>
 __device__ __forceinline__ float group_sum(const float* src, int SPR, int sub, int LPS) {
     float v = 0.f;
-    if (SPR_T) {
-        const int VPL = SPR_T / LPS;  // SPR_T and LPS are powers of two, LPS <= SPR_T
+    if (SPR_T && SPR_T % LPS == 0) {  // contiguous VPL values per lane
+        const int VPL = SPR_T / LPS;
         const float* p = src + sub * VPL;
         for (int i = 0; i < VPL; ++i) v += p[i];
-    } else {
+    } else {  // strided; lanes with sub >= SPR add nothing
         for (int i = sub; i < SPR; i += LPS) v += src[i];
     }
-    for (int o = LPS >> 1; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (LPS >= 2) v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    if (LPS >= 4) v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    if (LPS >= 8) v += dpp_f<0x141>(v);  // row_half_mirror
+    if (LPS >= 16) v += dpp_f<0x140>(v); // row_mirror
     return v;
+}
+
+// lanes per row-set sum for NQ sums over 64 lanes: a power of two, at most 16
+__device__ __forceinline__ int lanes_per_sum(int NQ) {
+    int LPS = 1;
+    while (LPS < 16 && LPS * 2 * NQ <= 64) LPS <<= 1;
+    return LPS;
 }
 
 // ===========================================================================
 // Kernel 1 (fast path): H/32 <= 64 chunks per row, G/32 a power of two.
 // SPR_T = H/32 when known at compile time (64 for H = 2048), 0 = runtime.
+// QSC: the 4 lanes of a quad share one (row, group) (G >= 128, H/32 % 4 == 0):
+//      each quad fetches its 4 fp16 values (gate s, gate m, up s, up m) with
+//      one 16-bit load per lane and shares them with DPP broadcasts.
+// x is staged once per workgroup in LDS (H <= 2048 -> 4 KB).
 // grid = (ceil(I / (NW*T*RPI)), k), block = 64*NW.
 // ===========================================================================
-template <int BITS, int SPR_T, int T, int NW>
+template <int BITS, int SPR_T, int T, int NW, bool QSC>
 __global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16_t* __restrict__ x,
                                                       uint32_t* __restrict__ act) {
     __shared__ float part[NW][T][2][64];
+#if WISP_GU_XLDS
+    __shared__ uint4 xlds[320];  // 256 pieces of x, one 16-byte pad after every 4 (bank spread)
+#endif
     const int SPR = SPR_T ? SPR_T : L.spr_gu;
     const int RPI = 64 / SPR;
     const int lane = threadIdx.x & 63;
@@ -180,8 +209,27 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16
     const uint16_t* mn = sc + 3 * L.NGM;
     const int gi = seg >> L.gsh;
 
+#if WISP_GU_XLDS
+    // 1. this thread's piece of x first (so staging it waits for nothing else),
+    //    then the weight codes and fp16 scale/min loads, all before any use
+    const int nx16 = L.H >> 3;  // 16-byte pieces of x
+    constexpr int XPT = (256 + 64 * NW - 1) / (64 * NW);
+    uint4 xpiece[XPT];
+#pragma unroll
+    for (int k2 = 0; k2 < XPT; ++k2)
+        xpiece[k2] = reinterpret_cast<const uint4*>(x)[min((int)threadIdx.x + k2 * 64 * NW, nx16 - 1)];
+#else
+    // 1. this lane's 32 x values first, then the weight codes and fp16 scale/min
+    //    loads, all before any use
+    uint32_t xw[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint4 q = reinterpret_cast<const uint4*>(x + 32 * seg)[i];
+        xw[4 * i] = q.x; xw[4 * i + 1] = q.y; xw[4 * i + 2] = q.z; xw[4 * i + 3] = q.w;
+    }
+#endif
     uint32_t cg[T][BITS], cu[T][BITS];
-    uint32_t sg[T], mg[T], su[T], mu[T];
+    uint32_t sv[T][QSC ? 1 : 4];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const int r = min(r0 + t * RPI + rr, L.I - 1);
@@ -189,14 +237,35 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16
         load_chunk<BITS>(rp, cg[t]);
         load_chunk<BITS>(rp + L.nmb, cu[t]);
         const int gidx = r * L.gpr_gu + gi;
-        sg[t] = sc[gidx];
-        mg[t] = mn[gidx];
-        su[t] = sc[L.NGM + gidx];
-        mu[t] = mn[L.NGM + gidx];
+        if (QSC) {
+            const int w = lane & 3;  // 0 gate s, 1 gate m, 2 up s, 3 up m
+            sv[t][0] = ((w & 1) ? mn : sc)[((w & 2) ? L.NGM : 0) + gidx];
+        } else {
+            sv[t][0] = sc[gidx];
+            sv[t][1 % (QSC ? 1 : 4)] = mn[gidx];
+            sv[t][2 % (QSC ? 1 : 4)] = sc[L.NGM + gidx];
+            sv[t][3 % (QSC ? 1 : 4)] = mn[L.NGM + gidx];
+        }
     }
+#if WISP_GU_XLDS
+    // 2. x -> LDS once per workgroup (one 16-byte pad after every 64 bytes)
+#pragma unroll
+    for (int k2 = 0; k2 < XPT; ++k2) {
+        const int i = min((int)threadIdx.x + k2 * 64 * NW, nx16 - 1);
+        xlds[i + (i >> 2)] = xpiece[k2];
+    }
+    __syncthreads();
+    uint32_t xw[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint4 q = xlds[5 * seg + i];
+        xw[4 * i] = q.x; xw[4 * i + 1] = q.y; xw[4 * i + 2] = q.z; xw[4 * i + 3] = q.w;
+    }
+#endif
     uint32_t xp[16];
+    operand_pairs<BITS>(xw, xp);
     float vs, xs;
-    load_x_operand<BITS>(x, seg, xp, vs, xs);
+    operand_sums<BITS>(xp, vs, xs);
     const float bias = -kBiasF * vs;
     const uint32_t B = bias_vgpr();
 #pragma unroll
@@ -204,8 +273,20 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16
         const bool ok = lane_on && (r0 + t * RPI + rr < L.I);
         const float dg = chunk_dot<BITS>(cg[t], xp, bias, B);
         const float du = chunk_dot<BITS>(cu[t], xp, bias, B);
-        const float pg = h2f((uint16_t)sg[t]) * dg + h2f((uint16_t)mg[t]) * xs;
-        const float pu = h2f((uint16_t)su[t]) * du + h2f((uint16_t)mu[t]) * xs;
+        uint32_t s_g, m_g, s_u, m_u;
+        if (QSC) {
+            s_g = quad_bcast<0>(sv[t][0]);
+            m_g = quad_bcast<1>(sv[t][0]);
+            s_u = quad_bcast<2>(sv[t][0]);
+            m_u = quad_bcast<3>(sv[t][0]);
+        } else {
+            s_g = sv[t][0];
+            m_g = sv[t][1 % (QSC ? 1 : 4)];
+            s_u = sv[t][2 % (QSC ? 1 : 4)];
+            m_u = sv[t][3 % (QSC ? 1 : 4)];
+        }
+        const float pg = h2f((uint16_t)s_g) * dg + h2f((uint16_t)m_g) * xs;
+        const float pu = h2f((uint16_t)s_u) * du + h2f((uint16_t)m_u) * xs;
         part[wv][t][0][lane] = ok ? pg : 0.f;
         part[wv][t][1][lane] = ok ? pu : 0.f;
     }
@@ -213,8 +294,7 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16
 
     // row sums: NQ = 2*T*RPI sums (gate/up interleaved) of SPR partials each
     const int NQ = 2 * T * RPI;
-    int LPS = 1;
-    while (LPS * 2 * NQ <= 64) LPS <<= 1;
+    const int LPS = lanes_per_sum(NQ);
     const int QPR = 64 / LPS;
     for (int q0 = 0; q0 < NQ; q0 += QPR) {
         const int q = q0 + lane / LPS;
@@ -222,7 +302,15 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16
         const int qq = q < NQ ? q : NQ - 1;
         const int m = qq & 1, row = qq >> 1, t = row / RPI, rq = row - t * RPI;
         const float v = group_sum<SPR_T>(&part[wv][t][m][rq * SPR], SPR, sub, LPS);
-        const float u = __shfl_down(v, LPS, 64);
+        // the up sum of the same row sits LPS lanes higher, in the same DPP row when LPS <= 8
+        float u;
+        switch (LPS) {
+        case 1: u = dpp_f<0x101>(v); break;  // row_shl:1
+        case 2: u = dpp_f<0x102>(v); break;
+        case 4: u = dpp_f<0x104>(v); break;
+        case 8: u = dpp_f<0x108>(v); break;
+        default: u = __shfl_down(v, LPS, 64); break;
+        }
         if (q < NQ && sub == 0 && m == 0) {
             const int r = r0 + t * RPI + rq;
             if (r < L.I) write_act<BITS>(act, j, L.I, r, silu_mul(v, u));
@@ -266,13 +354,18 @@ __global__ __launch_bounds__(64) void k_gate_up_generic(const Layer L, const uin
 // ===========================================================================
 // Kernel 2 (fast path): I/32 <= 64 chunks per row, G/32 a power of two.
 // SPR_T = I/32 when known at compile time (24 for I = 768), 0 = runtime.
+// QSC: quads share one (row, group) (G >= 128, I/32 % 4 == 0, T even): lane i
+//      of a quad loads one of (s, m) for rows t and t+1; DPP broadcasts share them.
+// Each wave stages its expert's activation (I dwords) in LDS once, so a lane
+// reads its 128-byte operand from LDS instead of from L2.
 // grid = ceil(H / (T*RPI)), block = 64*k (wave j = expert j),
-// dynamic LDS = (k*T*64 + k*T*RPI) floats.
+// dynamic LDS = (k*T*64 + k*T*RPI + k*I*36/32) floats.
 // WSUM: out[h] = bf16(sum_j w_j y_j[h]); else y[j*H + h] = y_j[h].
 // ===========================================================================
-template <int BITS, int SPR_T, int T, bool WSUM>
+template <int BITS, int SPR_T, int T, bool WSUM, bool QSC>
 __global__ __launch_bounds__(1024) void k_down(const Layer L, const uint32_t* __restrict__ act,
                                                uint16_t* __restrict__ out, float* __restrict__ y) {
+    static_assert(!QSC || T % 2 == 0, "quad-shared scales cover two rows per load");
     extern __shared__ float lds[];
     const int SPR = SPR_T ? SPR_T : L.spr_dn;
     const int RPI = 64 / SPR;
@@ -284,8 +377,12 @@ __global__ __launch_bounds__(1024) void k_down(const Layer L, const uint32_t* __
     const bool lane_on = rr < RPI;
     rr = lane_on ? rr : RPI - 1;
     const int h0 = blockIdx.x * RW;
-    float* part = lds + j * (T * 64);  // [T][64], this wave's partials
-    float* rows = lds + L.k * (T * 64);  // [k][RW]
+    float* part = lds + j * (T * 64);                         // [T][64], this wave's partials
+    float* rows = lds + L.k * (T * 64);                       // [k][RW]
+#if WISP_DN_ALDS
+    // expert j's activation, segment stride 36 dwords (bank spread)
+    uint32_t* stage = reinterpret_cast<uint32_t*>(rows + L.k * RW) + (int64_t)j * (L.I / 32 * 36);
+#endif
     const int slot = __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots));
 
     float p[T];
@@ -295,24 +392,83 @@ __global__ __launch_bounds__(1024) void k_down(const Layer L, const uint32_t* __
         const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb) + 2 * L.NGM;
         const uint16_t* mn = sc + 3 * L.NGM;
         const int gi = seg >> L.gsh;
-        uint32_t cd[T][BITS], sd[T], md[T];
+#if WISP_DN_ALDS
+        // expert j's activation first (so staging it waits for nothing else);
+        // the fast path is used for I <= 2048: at most 8 16-byte pieces per lane
+        const uint4* asrc = reinterpret_cast<const uint4*>(act + (int64_t)j * L.I);
+        const int na16 = L.I >> 2;
+        constexpr int APL = SPR_T ? (SPR_T * 8 + 63) / 64 : 8;
+        uint4 apiece[APL];
+#pragma unroll
+        for (int k2 = 0; k2 < APL; ++k2) apiece[k2] = asrc[min(lane + 64 * k2, na16 - 1)];
+#else
+        uint32_t AH[16], AL[16];
+        {
+            const uint4* ap = reinterpret_cast<const uint4*>(act + ((int64_t)j * (L.I >> 5) + seg) * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint4 hq = ap[i], lq = ap[4 + i];
+                AH[4 * i] = hq.x; AH[4 * i + 1] = hq.y; AH[4 * i + 2] = hq.z; AH[4 * i + 3] = hq.w;
+                AL[4 * i] = lq.x; AL[4 * i + 1] = lq.y; AL[4 * i + 2] = lq.z; AL[4 * i + 3] = lq.w;
+            }
+        }
+#endif
+        uint32_t cd[T][BITS], sv[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int h = min(h0 + t * RPI + rr, L.H - 1);
             load_chunk<BITS>(dcodes + (int64_t)h * L.rowb_dn + seg * (4 * BITS), cd[t]);
-            sd[t] = sc[h * L.gpr_dn + gi];
-            md[t] = mn[h * L.gpr_dn + gi];
+            if (QSC) {
+                if (t % 2 == 0) {
+                    const int w = lane & 3;  // 0 s(t), 1 m(t), 2 s(t+1), 3 m(t+1)
+                    const int hh = (w & 2) ? min(h0 + (t + 1) * RPI + rr, L.H - 1) : h;
+                    sv[t] = ((w & 1) ? mn : sc)[hh * L.gpr_dn + gi];
+                }
+            } else {
+                sv[t] = (uint32_t)sc[h * L.gpr_dn + gi] | ((uint32_t)mn[h * L.gpr_dn + gi] << 16);
+            }
         }
+#if WISP_DN_ALDS
+        // stage expert j's activation (hi/lo pairs) in LDS, segment stride 36 dwords
+#pragma unroll
+        for (int k2 = 0; k2 < APL; ++k2) {
+            const int i = min(lane + 64 * k2, na16 - 1);
+            reinterpret_cast<uint4*>(stage)[i + (i >> 3)] = apiece[k2];
+        }
+        wave_sync_lds();
         uint32_t AH[16], AL[16];
-        float vs, as;
-        load_act_operand<BITS>(act, j, L.I, seg, AH, AL, vs, as);
-        const float bias = -kBiasF * vs;
+        const uint4* ap = reinterpret_cast<const uint4*>(stage + seg * 36);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 hq = ap[i], lq = ap[4 + i];
+            AH[4 * i] = hq.x; AH[4 * i + 1] = hq.y; AH[4 * i + 2] = hq.z; AH[4 * i + 3] = hq.w;
+            AL[4 * i] = lq.x; AL[4 * i + 1] = lq.y; AL[4 * i + 2] = lq.z; AL[4 * i + 3] = lq.w;
+        }
+#endif
+        float vh, th, vl, tl;
+        operand_sums<BITS>(AH, vh, th);
+        operand_sums<BITS>(AL, vl, tl);
+        const float as = th + tl;
+        const float bias = -kBiasF * (vh + vl);
         const uint32_t B = bias_vgpr();
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const bool ok = lane_on && (h0 + t * RPI + rr < L.H);
             const float d = chunk_dot_hl<BITS>(cd[t], AH, AL, bias, B);
-            const float v = h2f((uint16_t)sd[t]) * d + h2f((uint16_t)md[t]) * as;
+            uint32_t s_, m_;
+            if (QSC) {
+                if (t % 2 == 0) {
+                    s_ = quad_bcast<0>(sv[t]);
+                    m_ = quad_bcast<1>(sv[t]);
+                } else {
+                    s_ = quad_bcast<2>(sv[t - 1 + (t == 0)]);
+                    m_ = quad_bcast<3>(sv[t - 1 + (t == 0)]);
+                }
+            } else {
+                s_ = sv[t] & 0xFFFFu;
+                m_ = sv[t] >> 16;
+            }
+            const float v = h2f((uint16_t)s_) * d + h2f((uint16_t)m_) * as;
             p[t] = ok ? v : 0.f;
         }
     } else {
@@ -324,8 +480,7 @@ __global__ __launch_bounds__(1024) void k_down(const Layer L, const uint32_t* __
     wave_sync_lds();
 
     // per-wave row sums: RW sums of SPR partials each
-    int LPS = 1;
-    while (LPS * 2 * RW <= 64) LPS <<= 1;
+    const int LPS = lanes_per_sum(RW);
     const int QPR = 64 / LPS;
     for (int q0 = 0; q0 < RW; q0 += QPR) {
         const int q = q0 + lane / LPS;
@@ -450,12 +605,12 @@ static int make_layer(Layer& L, const uint8_t* pool, int64_t slot_bytes, int64_t
     return WISP_OK;
 }
 
-template <int BITS, int SPR, int T, int NW>
+template <int BITS, int SPR, int T, int NW, bool QSC>
 static void launch_gu(const Layer& L, const uint16_t* x, uint32_t* act, hipStream_t st) {
     const int RPI = 64 / L.spr_gu;
     const int rows_wg = NW * T * RPI;
     const dim3 grid((L.I + rows_wg - 1) / rows_wg, L.k);
-    hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW>), grid, dim3(64 * NW), 0, st, L, x, act);
+    hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW, QSC>), grid, dim3(64 * NW), 0, st, L, x, act);
 }
 
 template <int BITS>
@@ -464,18 +619,18 @@ static int gate_up_bits(const Layer& L, const uint16_t* x, uint32_t* act, hipStr
         hipLaunchKernelGGL((k_gate_up_generic<BITS>), dim3(L.I, L.k), dim3(64), 0, st, L, x, act);
         return check_launch("k_gate_up_generic");
     }
-    if (L.spr_gu != 64) {
-        launch_gu<BITS, 0, 2, 4>(L, x, act, st);
+    if (L.spr_gu != 64 || L.gsh < 2) {
+        launch_gu<BITS, 0, 2, 4, false>(L, x, act, st);
         return check_launch("k_gate_up");
     }
     const Tuning& tu = tuning();
-#define WISP_GU(TT, WW)                                   \
-    if (tu.gu_rows == TT && tu.gu_waves == WW) {          \
-        launch_gu<BITS, 64, TT, WW>(L, x, act, st);       \
-        return check_launch("k_gate_up");                 \
+#define WISP_GU(TT, WW)                                      \
+    if (tu.gu_rows == TT && tu.gu_waves == WW) {             \
+        launch_gu<BITS, 64, TT, WW, (bool)WISP_QSC>(L, x, act, st);    \
+        return check_launch("k_gate_up");                    \
     }
-    WISP_GU(4, 4)
     WISP_GU(2, 4)
+    WISP_GU(4, 4)
     WISP_GU(8, 4)
     WISP_GU(1, 4)
     WISP_GU(4, 2)
@@ -486,30 +641,32 @@ static int gate_up_bits(const Layer& L, const uint16_t* x, uint32_t* act, hipStr
     return fail_inval("unsupported tuning (gu_rows, gu_waves)");
 }
 
-template <int BITS, int SPR, int T, bool WSUM>
+template <int BITS, int SPR, int T, bool WSUM, bool QSC>
 static void launch_dn(const Layer& L, const uint32_t* act, uint16_t* out, float* y, hipStream_t st) {
     const int RPI = 64 / L.spr_dn;
     const int RW = T * RPI;
-    const size_t lds = sizeof(float) * ((size_t)L.k * T * 64 + (size_t)L.k * RW);
-    hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM>), dim3((L.H + RW - 1) / RW), dim3(64 * L.k), lds, st, L, act,
-                       out, y);
+    const size_t lds =
+        sizeof(float) * ((size_t)L.k * T * 64 + (size_t)L.k * RW + (WISP_DN_ALDS ? (size_t)L.k * (L.I / 32 * 36) : 0));
+    hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM, QSC>), dim3((L.H + RW - 1) / RW), dim3(64 * L.k), lds, st, L,
+                       act, out, y);
 }
 
 template <int BITS, bool WSUM>
 static int down_bits(const Layer& L, const uint32_t* act, uint16_t* out, float* y, hipStream_t st) {
-    if (L.spr_dn > 64 || L.gsh < 0) {
+    // the fast path stages k*I activation dwords in LDS: keep it within 64 KB
+    if (L.spr_dn > 64 || L.gsh < 0 || (int64_t)L.k * (L.I / 32 * 36) * 4 > 65536) {
         hipLaunchKernelGGL((k_down_generic<BITS, WSUM>), dim3(L.H), dim3(64 * L.k), 0, st, L, act, out, y);
         return check_launch("k_down_generic");
     }
-    if (L.spr_dn != 24) {
-        launch_dn<BITS, 0, 4, WSUM>(L, act, out, y, st);
+    if (L.spr_dn != 24 || L.gsh < 2) {
+        launch_dn<BITS, 0, 4, WSUM, false>(L, act, out, y, st);
         return check_launch("k_down");
     }
     switch (tuning().dn_iters) {
-    case 1: launch_dn<BITS, 24, 1, WSUM>(L, act, out, y, st); break;
-    case 2: launch_dn<BITS, 24, 2, WSUM>(L, act, out, y, st); break;
-    case 4: launch_dn<BITS, 24, 4, WSUM>(L, act, out, y, st); break;
-    case 8: launch_dn<BITS, 24, 8, WSUM>(L, act, out, y, st); break;
+    case 1: launch_dn<BITS, 24, 1, WSUM, false>(L, act, out, y, st); break;
+    case 2: launch_dn<BITS, 24, 2, WSUM, (bool)WISP_QSC>(L, act, out, y, st); break;
+    case 4: launch_dn<BITS, 24, 4, WSUM, (bool)WISP_QSC>(L, act, out, y, st); break;
+    case 8: launch_dn<BITS, 24, 8, WSUM, (bool)WISP_QSC>(L, act, out, y, st); break;
     default: return fail_inval("unsupported tuning dn_iters");
     }
     return check_launch("k_down");

@@ -274,6 +274,19 @@ __device__ __forceinline__ void operand_sums(const uint32_t* pr, float& vsum, fl
     }
 }
 
+// Broadcast lane I of each quad to the whole quad (DPP quad_perm [I,I,I,I]).
+template <int I>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, I * 0x55, 0xF, 0xF, false);
+}
+
+// v from the lane selected by the DPP control CTRL (0 where the source lane is
+// outside the row, bound_ctrl).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
 // Wave-wide sum (wave64) with xor shuffles.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
