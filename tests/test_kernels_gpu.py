@@ -228,12 +228,13 @@ def test_tuning_variants_agree(gu, dn):
     _, _, ref = O.moe_layer_f64(pool, sel, rw, x, H, I, bits, group)
     try:
         kernels.set_tuning(gu[0], gu[1], dn)
-        got = kernels.moe_decode_q4_fast(torch.from_numpy(pool).to(DEV), torch.from_numpy(O.meta(sel, rw)).to(DEV),
-                                         torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV),
-                                         k, H * I, H, I)
+        got = kernels.moe_decode_fast(torch.from_numpy(pool).to(DEV),
+                                      torch.from_numpy(O.meta(sel, rw)).to(DEV),
+                                      torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV),
+                                      k, H * I, H, I, bits)
         torch.cuda.synchronize()
     finally:
-        kernels.set_tuning(4, 4, 4)
+        kernels.set_tuning(2, 4, 4)
     r = O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.astype(np.float32)))
     assert _rel_l2(O.bf16_bits_to_f32(_bf16(got)), r) <= TOL
 
@@ -271,3 +272,28 @@ def test_graph_capture_with_meta_updates():
         _, _, ref = O.moe_layer_f64(pool_np, sel, rw, x_np, H, I, bits, group)
         r = O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.astype(np.float32)))
         assert _rel_l2(O.bf16_bits_to_f32(_bf16(out)), r) <= TOL
+
+
+# ---------------------------------------------------------------- repeated calls, real shape
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("k", [8, 5, 1])
+def test_layer_parity_repeated_calls(bits, k):
+    """moe_decode_fast at the Qwen3-30B-A3B expert shape, called repeatedly with new routes
+    and inputs on one pool (nothing carried over between calls)."""
+    H, I, group, E = 2048, 768, 128, 12
+    n = H * I
+    rng = np.random.default_rng(77 + bits + k)
+    pool_np = _pool(E, H, I, bits, group, seed=bits * 11 + k)
+    pool = torch.from_numpy(pool_np).to(DEV)
+    for it in range(3):
+        sel, rw = _route(rng, E, k)
+        x = _x(rng, H)
+        _, _, ref = O.moe_layer_f64(pool_np, sel, rw, x, H, I, bits, group)
+        got = kernels.moe_decode_fast(pool, torch.from_numpy(O.meta(sel, rw)).to(DEV),
+                                      torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV),
+                                      k, n, H, I, bits, group)
+        torch.cuda.synchronize()
+        r = O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.astype(np.float32)))
+        err = _rel_l2(O.bf16_bits_to_f32(_bf16(got)), r)
+        print(f"layer bits={bits} k={k} it={it}: rel-L2 {err:.3e}")
+        assert err <= TOL, err

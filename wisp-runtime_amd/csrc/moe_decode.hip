@@ -24,12 +24,6 @@
 #include "wisp_device.hpp"
 #include "wisp_internal.hpp"
 
-#ifndef WISP_GU_XLDS
-#define WISP_GU_XLDS 0
-#endif
-#ifndef WISP_DN_ALDS
-#define WISP_DN_ALDS 1
-#endif
 #ifndef WISP_QSC
 #define WISP_QSC 1
 #endif
@@ -171,63 +165,38 @@ __device__ __forceinline__ int lanes_per_sum(int NQ) {
 }
 
 // ===========================================================================
-// Kernel 1 (fast path): H/32 <= 64 chunks per row, G/32 a power of two.
-// SPR_T = H/32 when known at compile time (64 for H = 2048), 0 = runtime.
+// Kernel 1 body (fast path): H/32 <= 64 chunks per row, G/32 a power of two.
+// One wave computes rows r0 .. r0 + T*RPI - 1 of expert j (slot valid), where
+// RPI = rows per wave-wide load (1 when H = 2048). SPR_T = H/32 when known at
+// compile time (64 for H = 2048), 0 = runtime.
 // QSC: the 4 lanes of a quad share one (row, group) (G >= 128, H/32 % 4 == 0):
-//      each quad fetches its 4 fp16 values (gate s, gate m, up s, up m) with
-//      one 16-bit load per lane and shares them with DPP broadcasts.
-// x is staged once per workgroup in LDS (H <= 2048 -> 4 KB).
-// grid = (ceil(I / (NW*T*RPI)), k), block = 64*NW.
+//      each quad fetches its 4 fp16 values (gate s, gate m, up s, up m) with one
+//      16-bit load per lane and shares them with DPP broadcasts.
+// part: this wave's LDS scratch, T*2*64 floats.
 // ===========================================================================
-template <int BITS, int SPR_T, int T, int NW, bool QSC>
-__global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16_t* __restrict__ x,
-                                                      uint32_t* __restrict__ act) {
-    __shared__ float part[NW][T][2][64];
-#if WISP_GU_XLDS
-    __shared__ uint4 xlds[320];  // 256 pieces of x, one 16-byte pad after every 4 (bank spread)
-#endif
+template <int BITS, int SPR_T, int T, bool QSC>
+__device__ __forceinline__ void gate_up_rows(const Layer& L, const uint16_t* __restrict__ x,
+                                             uint32_t* __restrict__ act, int j, int slot, int r0, float* part) {
     const int SPR = SPR_T ? SPR_T : L.spr_gu;
     const int RPI = 64 / SPR;
     const int lane = threadIdx.x & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int j = blockIdx.y;
     int rr = lane / SPR;
     const int seg = lane - rr * SPR;
     const bool lane_on = rr < RPI;
     rr = lane_on ? rr : RPI - 1;  // idle lanes repeat an active lane's addresses
-    const int r0 = (blockIdx.x * NW + wv) * (T * RPI);
-    const int slot = __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots));
-    if (slot < 0) {  // the whole workgroup shares j: nobody reaches a barrier
-        for (int t = 0; t < T; ++t) {
-            const int r = r0 + t * RPI + rr;
-            if (lane_on && seg == 0 && r < L.I) write_act<BITS>(act, j, L.I, r, __builtin_nanf(""));
-        }
-        return;
-    }
     const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb);
     const uint16_t* mn = sc + 3 * L.NGM;
     const int gi = seg >> L.gsh;
 
-#if WISP_GU_XLDS
-    // 1. this thread's piece of x first (so staging it waits for nothing else),
-    //    then the weight codes and fp16 scale/min loads, all before any use
-    const int nx16 = L.H >> 3;  // 16-byte pieces of x
-    constexpr int XPT = (256 + 64 * NW - 1) / (64 * NW);
-    uint4 xpiece[XPT];
-#pragma unroll
-    for (int k2 = 0; k2 < XPT; ++k2)
-        xpiece[k2] = reinterpret_cast<const uint4*>(x)[min((int)threadIdx.x + k2 * 64 * NW, nx16 - 1)];
-#else
-    // 1. this lane's 32 x values first, then the weight codes and fp16 scale/min
-    //    loads, all before any use
+    // this lane's 32 x values first, then the weight codes and fp16 scale/min
+    // loads, all issued before any use
     uint32_t xw[16];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint4 q = reinterpret_cast<const uint4*>(x + 32 * seg)[i];
         xw[4 * i] = q.x; xw[4 * i + 1] = q.y; xw[4 * i + 2] = q.z; xw[4 * i + 3] = q.w;
     }
-#endif
     uint32_t cg[T][BITS], cu[T][BITS];
     uint32_t sv[T][QSC ? 1 : 4];
 #pragma unroll
@@ -247,21 +216,6 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16
             sv[t][3 % (QSC ? 1 : 4)] = mn[L.NGM + gidx];
         }
     }
-#if WISP_GU_XLDS
-    // 2. x -> LDS once per workgroup (one 16-byte pad after every 64 bytes)
-#pragma unroll
-    for (int k2 = 0; k2 < XPT; ++k2) {
-        const int i = min((int)threadIdx.x + k2 * 64 * NW, nx16 - 1);
-        xlds[i + (i >> 2)] = xpiece[k2];
-    }
-    __syncthreads();
-    uint32_t xw[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint4 q = xlds[5 * seg + i];
-        xw[4 * i] = q.x; xw[4 * i + 1] = q.y; xw[4 * i + 2] = q.z; xw[4 * i + 3] = q.w;
-    }
-#endif
     uint32_t xp[16];
     operand_pairs<BITS>(xw, xp);
     float vs, xs;
@@ -287,8 +241,8 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16
         }
         const float pg = h2f((uint16_t)s_g) * dg + h2f((uint16_t)m_g) * xs;
         const float pu = h2f((uint16_t)s_u) * du + h2f((uint16_t)m_u) * xs;
-        part[wv][t][0][lane] = ok ? pg : 0.f;
-        part[wv][t][1][lane] = ok ? pu : 0.f;
+        part[(2 * t) * 64 + lane] = ok ? pg : 0.f;
+        part[(2 * t + 1) * 64 + lane] = ok ? pu : 0.f;
     }
     wave_sync_lds();
 
@@ -301,7 +255,7 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16
         const int sub = lane & (LPS - 1);
         const int qq = q < NQ ? q : NQ - 1;
         const int m = qq & 1, row = qq >> 1, t = row / RPI, rq = row - t * RPI;
-        const float v = group_sum<SPR_T>(&part[wv][t][m][rq * SPR], SPR, sub, LPS);
+        const float v = group_sum<SPR_T>(part + (2 * t + m) * 64 + rq * SPR, SPR, sub, LPS);
         // the up sum of the same row sits LPS lanes higher, in the same DPP row when LPS <= 8
         float u;
         switch (LPS) {
@@ -316,6 +270,34 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16
             if (r < L.I) write_act<BITS>(act, j, L.I, r, silu_mul(v, u));
         }
     }
+}
+
+// NaN activation rows for an expert whose slot id is invalid (nothing is read)
+template <int BITS>
+__device__ __forceinline__ void gate_up_invalid(const Layer& L, uint32_t* act, int j, int r0, int nrows) {
+    const int lane = threadIdx.x & 63;
+    for (int i = lane; i < nrows; i += 64) {
+        const int r = r0 + i;
+        if (r < L.I) write_act<BITS>(act, j, L.I, r, __builtin_nanf(""));
+    }
+}
+
+// Kernel 1 (fast path), two-kernel form.
+// grid = (ceil(I / (NW*T*RPI)), k), block = 64*NW.
+template <int BITS, int SPR_T, int T, int NW, bool QSC>
+__global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16_t* __restrict__ x,
+                                                      uint32_t* __restrict__ act) {
+    __shared__ float part[NW][T * 2 * 64];
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = blockIdx.y;
+    const int RPI = 64 / (SPR_T ? SPR_T : L.spr_gu);
+    const int r0 = (blockIdx.x * NW + wv) * (T * RPI);
+    const int slot = __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots));
+    if (slot < 0) {
+        gate_up_invalid<BITS>(L, act, j, r0, T * RPI);
+        return;
+    }
+    gate_up_rows<BITS, SPR_T, T, QSC>(L, x, act, j, slot, r0, part[wv]);
 }
 
 // Kernel 1 (generic): any H, G; one wave per (row, expert).
@@ -352,148 +334,129 @@ __global__ __launch_bounds__(64) void k_gate_up_generic(const Layer L, const uin
 }
 
 // ===========================================================================
-// Kernel 2 (fast path): I/32 <= 64 chunks per row, G/32 a power of two.
-// SPR_T = I/32 when known at compile time (24 for I = 768), 0 = runtime.
+// Kernel 2 body (fast path): I/32 <= 64 chunks per row, G/32 a power of two.
+// One workgroup computes output rows h0 .. h0 + T*RPI - 1; wave j handles
+// expert j (waves j >= k idle). SPR_T = I/32 when known at compile time (24
+// for I = 768), 0 = runtime.
 // QSC: quads share one (row, group) (G >= 128, I/32 % 4 == 0, T even): lane i
 //      of a quad loads one of (s, m) for rows t and t+1; DPP broadcasts share them.
-// Each wave stages its expert's activation (I dwords) in LDS once, so a lane
-// reads its 128-byte operand from LDS instead of from L2.
-// grid = ceil(H / (T*RPI)), block = 64*k (wave j = expert j),
-// dynamic LDS = (k*T*64 + k*T*RPI + k*I*36/32) floats.
-// WSUM: out[h] = bf16(sum_j w_j y_j[h]); else y[j*H + h] = y_j[h].
+// Each wave stages its expert's activation (I dwords, segment stride 36 dwords
+// against bank conflicts) in LDS once, so a lane reads its 128-byte operand
+// from LDS instead of from L2.
+// lds: (k*T*64 + k*T*RPI + k*I*36/32) floats.
+// WSUM: out[h] = bf16(sum_j w_j y_j[h]) (wave j scales its row sums by w_j,
+// loaded at the start); else y[j*H + h] = y_j[h].
 // ===========================================================================
 template <int BITS, int SPR_T, int T, bool WSUM, bool QSC>
-__global__ __launch_bounds__(1024) void k_down(const Layer L, const uint32_t* __restrict__ act,
-                                               uint16_t* __restrict__ out, float* __restrict__ y) {
+__device__ __forceinline__ void down_rows(const Layer& L, const uint32_t* __restrict__ act,
+                                          uint16_t* __restrict__ out, float* __restrict__ y, int h0, float* lds) {
     static_assert(!QSC || T % 2 == 0, "quad-shared scales cover two rows per load");
-    extern __shared__ float lds[];
     const int SPR = SPR_T ? SPR_T : L.spr_dn;
     const int RPI = 64 / SPR;
     const int RW = T * RPI;
     const int lane = threadIdx.x & 63;
     const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool active = j < L.k;
     int rr = lane / SPR;
     const int seg = lane - rr * SPR;
     const bool lane_on = rr < RPI;
     rr = lane_on ? rr : RPI - 1;
-    const int h0 = blockIdx.x * RW;
-    float* part = lds + j * (T * 64);                         // [T][64], this wave's partials
-    float* rows = lds + L.k * (T * 64);                       // [k][RW]
-#if WISP_DN_ALDS
-    // expert j's activation, segment stride 36 dwords (bank spread)
+    float* part = lds + j * (T * 64);     // [T][64], this wave's partials (j < k)
+    float* rows = lds + L.k * (T * 64);   // [k][RW]
     uint32_t* stage = reinterpret_cast<uint32_t*>(rows + L.k * RW) + (int64_t)j * (L.I / 32 * 36);
-#endif
-    const int slot = __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots));
+    const int slot = active ? __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots)) : -1;
+    const float wj = (WSUM && active) ? L.meta[L.k + j] : 0.f;  // issued now, used at the end
 
-    float p[T];
-    if (slot >= 0) {
-        const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
-        const uint8_t* dcodes = base + 2 * L.nmb;
-        const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb) + 2 * L.NGM;
-        const uint16_t* mn = sc + 3 * L.NGM;
-        const int gi = seg >> L.gsh;
-#if WISP_DN_ALDS
-        // expert j's activation first (so staging it waits for nothing else);
-        // the fast path is used for I <= 2048: at most 8 16-byte pieces per lane
-        const uint4* asrc = reinterpret_cast<const uint4*>(act + (int64_t)j * L.I);
-        const int na16 = L.I >> 2;
-        constexpr int APL = SPR_T ? (SPR_T * 8 + 63) / 64 : 8;
-        uint4 apiece[APL];
+    if (active) {
+        float p[T];
+        if (slot >= 0) {
+            const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
+            const uint8_t* dcodes = base + 2 * L.nmb;
+            const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb) + 2 * L.NGM;
+            const uint16_t* mn = sc + 3 * L.NGM;
+            const int gi = seg >> L.gsh;
+            const uint4* asrc = reinterpret_cast<const uint4*>(act + (int64_t)j * L.I);
+            const int na16 = L.I >> 2;
+            constexpr int APL = SPR_T ? (SPR_T * 8 + 63) / 64 : 8;
+            uint4 apiece[APL];  // activation first, so staging it waits for nothing else
 #pragma unroll
-        for (int k2 = 0; k2 < APL; ++k2) apiece[k2] = asrc[min(lane + 64 * k2, na16 - 1)];
-#else
-        uint32_t AH[16], AL[16];
-        {
-            const uint4* ap = reinterpret_cast<const uint4*>(act + ((int64_t)j * (L.I >> 5) + seg) * 32);
+            for (int k2 = 0; k2 < APL; ++k2) apiece[k2] = asrc[min(lane + 64 * k2, na16 - 1)];
+            uint32_t cd[T][BITS], sv[T];
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const int h = min(h0 + t * RPI + rr, L.H - 1);
+                load_chunk<BITS>(dcodes + (int64_t)h * L.rowb_dn + seg * (4 * BITS), cd[t]);
+                if (QSC) {
+                    if (t % 2 == 0) {
+                        const int w = lane & 3;  // 0 s(t), 1 m(t), 2 s(t+1), 3 m(t+1)
+                        const int hh = (w & 2) ? min(h0 + (t + 1) * RPI + rr, L.H - 1) : h;
+                        sv[t] = ((w & 1) ? mn : sc)[hh * L.gpr_dn + gi];
+                    }
+                } else {
+                    sv[t] = (uint32_t)sc[h * L.gpr_dn + gi] | ((uint32_t)mn[h * L.gpr_dn + gi] << 16);
+                }
+            }
+            // stage expert j's activation (hi/lo pairs) in LDS, segment stride 36 dwords
+#pragma unroll
+            for (int k2 = 0; k2 < APL; ++k2) {
+                const int i = min(lane + 64 * k2, na16 - 1);
+                reinterpret_cast<uint4*>(stage)[i + (i >> 3)] = apiece[k2];
+            }
+            wave_sync_lds();
+            uint32_t AH[16], AL[16];
+            const uint4* ap = reinterpret_cast<const uint4*>(stage + seg * 36);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint4 hq = ap[i], lq = ap[4 + i];
                 AH[4 * i] = hq.x; AH[4 * i + 1] = hq.y; AH[4 * i + 2] = hq.z; AH[4 * i + 3] = hq.w;
                 AL[4 * i] = lq.x; AL[4 * i + 1] = lq.y; AL[4 * i + 2] = lq.z; AL[4 * i + 3] = lq.w;
             }
-        }
-#endif
-        uint32_t cd[T][BITS], sv[T];
+            float vh, th, vl, tl;
+            operand_sums<BITS>(AH, vh, th);
+            operand_sums<BITS>(AL, vl, tl);
+            const float as = th + tl;
+            const float bias = -kBiasF * (vh + vl);
+            const uint32_t B = bias_vgpr();
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const int h = min(h0 + t * RPI + rr, L.H - 1);
-            load_chunk<BITS>(dcodes + (int64_t)h * L.rowb_dn + seg * (4 * BITS), cd[t]);
-            if (QSC) {
-                if (t % 2 == 0) {
-                    const int w = lane & 3;  // 0 s(t), 1 m(t), 2 s(t+1), 3 m(t+1)
-                    const int hh = (w & 2) ? min(h0 + (t + 1) * RPI + rr, L.H - 1) : h;
-                    sv[t] = ((w & 1) ? mn : sc)[hh * L.gpr_dn + gi];
-                }
-            } else {
-                sv[t] = (uint32_t)sc[h * L.gpr_dn + gi] | ((uint32_t)mn[h * L.gpr_dn + gi] << 16);
-            }
-        }
-#if WISP_DN_ALDS
-        // stage expert j's activation (hi/lo pairs) in LDS, segment stride 36 dwords
-#pragma unroll
-        for (int k2 = 0; k2 < APL; ++k2) {
-            const int i = min(lane + 64 * k2, na16 - 1);
-            reinterpret_cast<uint4*>(stage)[i + (i >> 3)] = apiece[k2];
-        }
-        wave_sync_lds();
-        uint32_t AH[16], AL[16];
-        const uint4* ap = reinterpret_cast<const uint4*>(stage + seg * 36);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint4 hq = ap[i], lq = ap[4 + i];
-            AH[4 * i] = hq.x; AH[4 * i + 1] = hq.y; AH[4 * i + 2] = hq.z; AH[4 * i + 3] = hq.w;
-            AL[4 * i] = lq.x; AL[4 * i + 1] = lq.y; AL[4 * i + 2] = lq.z; AL[4 * i + 3] = lq.w;
-        }
-#endif
-        float vh, th, vl, tl;
-        operand_sums<BITS>(AH, vh, th);
-        operand_sums<BITS>(AL, vl, tl);
-        const float as = th + tl;
-        const float bias = -kBiasF * (vh + vl);
-        const uint32_t B = bias_vgpr();
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const bool ok = lane_on && (h0 + t * RPI + rr < L.H);
-            const float d = chunk_dot_hl<BITS>(cd[t], AH, AL, bias, B);
-            uint32_t s_, m_;
-            if (QSC) {
-                if (t % 2 == 0) {
-                    s_ = quad_bcast<0>(sv[t]);
-                    m_ = quad_bcast<1>(sv[t]);
+            for (int t = 0; t < T; ++t) {
+                const bool ok = lane_on && (h0 + t * RPI + rr < L.H);
+                const float d = chunk_dot_hl<BITS>(cd[t], AH, AL, bias, B);
+                uint32_t s_, m_;
+                if (QSC) {
+                    const uint32_t v2 = sv[t & ~1];
+                    s_ = (t & 1) ? quad_bcast<2>(v2) : quad_bcast<0>(v2);
+                    m_ = (t & 1) ? quad_bcast<3>(v2) : quad_bcast<1>(v2);
                 } else {
-                    s_ = quad_bcast<2>(sv[t - 1 + (t == 0)]);
-                    m_ = quad_bcast<3>(sv[t - 1 + (t == 0)]);
+                    s_ = sv[t] & 0xFFFFu;
+                    m_ = sv[t] >> 16;
                 }
-            } else {
-                s_ = sv[t] & 0xFFFFu;
-                m_ = sv[t] >> 16;
+                const float v = h2f((uint16_t)s_) * d + h2f((uint16_t)m_) * as;
+                p[t] = ok ? v : 0.f;
             }
-            const float v = h2f((uint16_t)s_) * d + h2f((uint16_t)m_) * as;
-            p[t] = ok ? v : 0.f;
+        } else {
+#pragma unroll
+            for (int t = 0; t < T; ++t) p[t] = __builtin_nanf("");
         }
-    } else {
 #pragma unroll
-        for (int t = 0; t < T; ++t) p[t] = __builtin_nanf("");
-    }
-#pragma unroll
-    for (int t = 0; t < T; ++t) part[t * 64 + lane] = p[t];
-    wave_sync_lds();
+        for (int t = 0; t < T; ++t) part[t * 64 + lane] = p[t];
+        wave_sync_lds();
 
-    // per-wave row sums: RW sums of SPR partials each
-    const int LPS = lanes_per_sum(RW);
-    const int QPR = 64 / LPS;
-    for (int q0 = 0; q0 < RW; q0 += QPR) {
-        const int q = q0 + lane / LPS;
-        const int sub = lane & (LPS - 1);
-        const int qq = q < RW ? q : RW - 1;
-        const int t = qq / RPI, rq = qq - t * RPI;
-        const float v = group_sum<SPR_T>(part + t * 64 + rq * SPR, SPR, sub, LPS);
-        if (q < RW && sub == 0) {
-            if (WSUM) {
-                rows[j * RW + q] = v;
-            } else {
-                const int h = h0 + q;
-                if (h < L.H) y[(int64_t)j * L.H + h] = v;
+        // per-wave row sums: RW sums of SPR partials each
+        const int LPS = lanes_per_sum(RW);
+        const int QPR = 64 / LPS;
+        for (int q0 = 0; q0 < RW; q0 += QPR) {
+            const int q = q0 + lane / LPS;
+            const int sub = lane & (LPS - 1);
+            const int qq = q < RW ? q : RW - 1;
+            const int t = qq / RPI, rq = qq - t * RPI;
+            const float v = group_sum<SPR_T>(part + t * 64 + rq * SPR, SPR, sub, LPS);
+            if (q < RW && sub == 0) {
+                if (WSUM) {
+                    rows[j * RW + q] = wj * v;
+                } else {
+                    const int h = h0 + q;
+                    if (h < L.H) y[(int64_t)j * L.H + h] = v;
+                }
             }
         }
     }
@@ -503,11 +466,21 @@ __global__ __launch_bounds__(1024) void k_down(const Layer L, const uint32_t* __
             const int h = h0 + q;
             if (h < L.H) {
                 float acc = 0.f;
-                for (int jj = 0; jj < L.k; ++jj) acc += L.meta[L.k + jj] * rows[jj * RW + q];
+                for (int jj = 0; jj < L.k; ++jj) acc += rows[jj * RW + q];
                 out[h] = f32_to_bf16(acc);
             }
         }
     }
+}
+
+// Kernel 2 (fast path), two-kernel form.
+// grid = ceil(H / (T*RPI)), block = 64*k, dynamic LDS as for down_rows.
+template <int BITS, int SPR_T, int T, bool WSUM, bool QSC>
+__global__ __launch_bounds__(1024) void k_down(const Layer L, const uint32_t* __restrict__ act,
+                                               uint16_t* __restrict__ out, float* __restrict__ y) {
+    extern __shared__ float lds[];
+    const int RW = T * (64 / (SPR_T ? SPR_T : L.spr_dn));
+    down_rows<BITS, SPR_T, T, WSUM, QSC>(L, act, out, y, blockIdx.x * RW, lds);
 }
 
 // Kernel 2 (generic): any I, G; one workgroup (k waves) per output row.
@@ -641,24 +614,29 @@ static int gate_up_bits(const Layer& L, const uint16_t* x, uint32_t* act, hipStr
     return fail_inval("unsupported tuning (gu_rows, gu_waves)");
 }
 
+// dynamic LDS of the fast kernel 2 with T row iterations (see down_rows)
+static size_t dn_lds_bytes(const Layer& L, int T) {
+    const int RW = T * (64 / L.spr_dn);
+    return sizeof(float) * ((size_t)L.k * T * 64 + (size_t)L.k * RW + (size_t)L.k * (L.I / 32 * 36));
+}
+
 template <int BITS, int SPR, int T, bool WSUM, bool QSC>
 static void launch_dn(const Layer& L, const uint32_t* act, uint16_t* out, float* y, hipStream_t st) {
-    const int RPI = 64 / L.spr_dn;
-    const int RW = T * RPI;
-    const size_t lds =
-        sizeof(float) * ((size_t)L.k * T * 64 + (size_t)L.k * RW + (WISP_DN_ALDS ? (size_t)L.k * (L.I / 32 * 36) : 0));
+    const int RW = T * (64 / L.spr_dn);
+    const size_t lds = dn_lds_bytes(L, T);
     hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM, QSC>), dim3((L.H + RW - 1) / RW), dim3(64 * L.k), lds, st, L,
                        act, out, y);
 }
 
 template <int BITS, bool WSUM>
 static int down_bits(const Layer& L, const uint32_t* act, uint16_t* out, float* y, hipStream_t st) {
-    // the fast path stages k*I activation dwords in LDS: keep it within 64 KB
-    if (L.spr_dn > 64 || L.gsh < 0 || (int64_t)L.k * (L.I / 32 * 36) * 4 > 65536) {
+    // the fast path stages k*I activation dwords in LDS: keep the whole LDS within 64 KB
+    const bool tuned = L.spr_dn == 24 && L.gsh >= 2;
+    if (L.spr_dn > 64 || L.gsh < 0 || dn_lds_bytes(L, tuned ? tuning().dn_iters : 4) > 65536) {
         hipLaunchKernelGGL((k_down_generic<BITS, WSUM>), dim3(L.H), dim3(64 * L.k), 0, st, L, act, out, y);
         return check_launch("k_down_generic");
     }
-    if (L.spr_dn != 24 || L.gsh < 2) {
+    if (!tuned) {
         launch_dn<BITS, 0, 4, WSUM, false>(L, act, out, y, st);
         return check_launch("k_down");
     }
@@ -672,6 +650,9 @@ static int down_bits(const Layer& L, const uint32_t* act, uint16_t* out, float* 
     return check_launch("k_down");
 }
 
+// ---------------------------------------------------------------------------
+// single-launch layer
+// ---------------------------------------------------------------------------
 }  // namespace wisp
 
 using namespace wisp;

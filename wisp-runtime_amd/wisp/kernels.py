@@ -50,8 +50,9 @@ def _layer(pool, meta, x, k, n, H, I, group, bits):
 
 
 def moe_decode_fast(pool, meta, x, k, n, H, I, bits, group=128):
-    """Two launches for one layer: gate_up+SiLU then down + routing-weighted sum.
-    meta: float32 [2k] on the GPU = [slot_0..slot_{k-1}, w_0..w_{k-1}]. Returns [H] in x.dtype."""
+    """One batch-1 MoE layer: gate_up+SiLU, then down + routing-weighted sum, as two
+    kernel launches (kernels.py:197-202). meta: float32 [2k] on the GPU =
+    [slot_0..slot_{k-1}, w_0..w_{k-1}]. Returns [H] in x.dtype."""
     dev, meta, x, act = _layer(pool, meta, x, k, n, H, I, group, bits)
     out = torch.empty((H,), dtype=x.dtype, device=dev)
     _lib.check(
