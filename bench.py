@@ -128,6 +128,162 @@ class Layers:
         return e0.elapsed_time(e1) * 1e-3
 
 
+PROFILES = os.path.join(ROOT, "profiles")
+CALIB_BYTES = 256 << 20  # plain device-to-device copy used to calibrate the PMC byte counters
+
+
+def pmc_profile_name(bits: int) -> str:
+    return os.path.join(PROFILES, f"k_gate_up_c2_q{bits}_hbm_traffic.md")
+
+
+def traffic_from_profile(bits: int):
+    """HBM bytes per k_gate_up launch from the committed PMC summary (rocprofv3 FETCH_SIZE
+    and WRITE_SIZE passes, each scaled by the same counter on a copy of known size), or
+    None when no summary exists for this bit width."""
+    path = pmc_profile_name(bits)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    return None
+
+
+def pmc_pass(bits: int) -> None:
+    """Short workload for one rocprofv3 --pmc pass: every layer's two kernels twice (eager,
+    rotating all layer pools), then a plain copy of CALIB_BYTES three times."""
+    dev = torch.device("cuda:0")
+    W = Layers(dev, bits, 48)
+    st = _lib.stream(dev)
+    for _ in range(2):
+        for l in range(W.layers):
+            W.layer(l, st)
+    src = torch.empty(CALIB_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("[bench] pmc pass done", file=sys.stderr, flush=True)
+
+
+def _pmc_rows(csv_path: str, counter: str):
+    """(kernel name, value) per dispatch for `counter` from a rocprofv3 counter_collection.csv."""
+    import csv
+
+    out = []
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            if r.get("Counter_Name") == counter:
+                out.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    out.sort()
+    # the calibration copies are the last three copy dispatches (the pool set-up copies differ in size)
+    copies = [i for i, (_, n, _) in enumerate(out) if "copyBuffer" in n][-3:]
+    return [("CALIBRATION" if i in copies else n, v) for i, (_, n, v) in enumerate(out)]
+
+
+def summarize_pmc(fetch_csv: str, write_csv: str, bits: int, cmd: str) -> str:
+    """Markdown summary of the two PMC passes: mean FETCH_SIZE / WRITE_SIZE (KiB per
+    dispatch) of the decode kernels and of the calibration copy, and the scaled traffic."""
+    fetch = _pmc_rows(fetch_csv, "FETCH_SIZE")
+    write = _pmc_rows(write_csv, "WRITE_SIZE")
+
+    def mean_of(rows, pred):
+        v = [x for n, x in rows if pred(n)]
+        return (sum(v) / len(v), len(v)) if v else (float("nan"), 0)
+
+    is_gu = lambda n: "k_gate_up" in n  # noqa: E731
+    is_dn = lambda n: "k_down" in n  # noqa: E731
+    is_cp = lambda n: n == "CALIBRATION"  # noqa: E731
+    cf, ncf = mean_of(fetch, is_cp)
+    cw, ncw = mean_of(write, is_cp)
+    f_scale = cf * 1024 / CALIB_BYTES
+    w_scale = cw * 1024 / CALIB_BYTES
+    gu_b, dn_b = alg_bytes(bits)
+    lines = [f"# HBM traffic per launch, k_gate_up / k_down, C2 {bits}-bit (rocprofv3 PMC)", ""]
+    lines.append("Commands (from the repository root on the GPU box, one pass each):")
+    lines.append("")
+    lines.append("```")
+    lines.append(cmd)
+    lines.append("```")
+    lines.append("")
+    lines.append(f"Calibration copy: {CALIB_BYTES} B device-to-device; FETCH_SIZE {cf:.0f} KiB (n={ncf}), "
+                 f"WRITE_SIZE {cw:.0f} KiB (n={ncw}); scale fetch {f_scale:.4f}, write {w_scale:.4f} "
+                 "(counter bytes / true bytes).")
+    lines.append("")
+    lines.append("| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic B (scaled) | algorithmic B | ratio |")
+    lines.append("|---|---|---|---|---|---|---|")
+    result = None
+    for name, pred, alg in (("k_gate_up", is_gu, gu_b), ("k_down", is_dn, dn_b)):
+        fk, nf = mean_of(fetch, pred)
+        wk, nw = mean_of(write, pred)
+        t = fk * 1024 / f_scale + wk * 1024 / w_scale
+        lines.append(f"| {name} | {nf}/{nw} | {fk:.1f} | {wk:.1f} | {t:.0f} | {alg} | {t / alg:.3f} |")
+        if name == "k_gate_up":
+            result = int(round(t))
+    lines.append("")
+    lines.append(f"traffic_bytes_per_launch: {result}")
+    return "\n".join(lines) + "\n"
+
+
+def trace_profile_name(bits: int) -> str:
+    return os.path.join(PROFILES, f"moe_decode_c2_q{bits}_kernel_trace.md")
+
+
+def summarize_trace(trace_csv: str, stats_csv: str, bits: int, cmd: str, bench_line: str) -> str:
+    """Markdown summary of a rocprofv3 --kernel-trace --stats run of bench.py: the stats
+    rows of the two decode kernels, and from the trace the start-to-start interval of
+    back-to-back launches of one kernel (its per-launch time inside a graph replay)."""
+    import csv
+    import statistics as stt
+
+    def short(n):
+        return "k_gate_up" if "k_gate_up" in n else "k_down" if "k_down" in n else None
+
+    stats = []
+    with open(stats_csv) as f:
+        for r in csv.DictReader(f):
+            if short(r["Name"]):
+                stats.append(r)
+    seq = []
+    with open(trace_csv) as f:
+        for r in csv.DictReader(f):
+            k = short(r["Kernel_Name"])
+            if k:
+                seq.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), k))
+    seq.sort()
+    same = {"k_gate_up": [], "k_down": []}
+    for a, b in zip(seq, seq[1:]):
+        if a[2] == b[2] and b[0] - a[0] < 50_000:
+            same[a[2]].append(b[0] - a[0])
+    gu_b, dn_b = alg_bytes(bits)
+    lines = [f"# Kernel trace, batch-1 MoE layer, C2 {bits}-bit (rocprofv3)", ""]
+    lines += ["Command (from the repository root on the GPU box):", "", "```", cmd, "```", ""]
+    lines += ["| kernel | calls | avg ns | min ns | max ns | stddev ns | algorithmic B | GB/s at avg |",
+              "|---|---|---|---|---|---|---|---|"]
+    for r in stats:
+        k = short(r["Name"])
+        alg = gu_b if k == "k_gate_up" else dn_b
+        avg = float(r["AverageNs"])
+        lines.append(f"| `{r['Name']}` | {r['Calls']} | {avg:.0f} | {r['MinNs']} | {r['MaxNs']} | "
+                     f"{float(r['StdDev']):.0f} | {alg} | {alg / avg:.0f} |")
+    lines.append("")
+    lines.append("Start-to-start interval of consecutive launches of the same kernel (the single-kernel graph "
+                 "replays, under the profiler):")
+    lines.append("")
+    for k, v in same.items():
+        if v:
+            lines.append(f"- {k}: n={len(v)}, median {stt.median(v):.0f} ns, mean {stt.mean(v):.0f} ns")
+    lines.append("")
+    lines.append("bench.py's own line from the profiled process (its HIP-event times include the profiler's "
+                 "per-dispatch overhead, so they are not the figures of record):")
+    lines.append("")
+    lines.append("```")
+    lines.append(bench_line.strip())
+    lines.append("```")
+    return "\n".join(lines) + "\n"
+
+
 def measure(W: Layers, steps: int, warmup: int):
     """Seconds per layer (both kernels, routing meta refreshed before every replay) and per
     kernel alone: graph replays over all layers, HIP events on the replay stream."""
@@ -155,7 +311,29 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--tune", default="", help="gu_rows,gu_waves,dn_iters")
+    ap.add_argument("--pmc-pass", action="store_true", help="short workload for one rocprofv3 --pmc pass")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write the PMC traffic summary under profiles/ from two counter_collection.csv files")
+    ap.add_argument("--pmc-command", default="", help="command text recorded in the PMC summary")
+    ap.add_argument("--summarize-trace", nargs=3, metavar=("TRACE_CSV", "STATS_CSV", "BENCH_JSON"),
+                    help="write the kernel-trace summary under profiles/ from a rocprofv3 run of bench.py")
     a = ap.parse_args()
+
+    if a.summarize_trace:
+        with open(a.summarize_trace[2]) as f:
+            bench_line = [ln for ln in f if ln.startswith("{")][-1]
+        text = summarize_trace(a.summarize_trace[0], a.summarize_trace[1], a.bits, a.pmc_command, bench_line)
+        with open(trace_profile_name(a.bits), "w") as f:
+            f.write(text)
+        print(text)
+        return
+
+    if a.summarize_pmc:
+        text = summarize_pmc(a.summarize_pmc[0], a.summarize_pmc[1], a.bits, a.pmc_command)
+        with open(pmc_profile_name(a.bits), "w") as f:
+            f.write(text)
+        print(text)
+        return
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (single-GPU path; see DESIGN.md for how it would shard). "
@@ -169,6 +347,9 @@ def main():
     if a.tune:
         gr, gw, dn = (int(v) for v in a.tune.split(","))
         _lib.check(_lib.lib().wisp_set_tuning(gr, gw, dn), "set_tuning")
+    if a.pmc_pass:
+        pmc_pass(a.bits)
+        return
 
     bits = a.bits
     W = Layers(dev, bits, a.layers)
@@ -212,12 +393,12 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_gate_up + k_down (both kernels of the layer)",
-            "achieved": round(value, 1),
+            "kernel": "k_gate_up (kernel 1: gate_up + SiLU, 2/3 of the layer's bytes)",
+            "achieved": round(gu_b / m["gu"] / 1e9, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
-            "frac": round(value / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "frac": round(gu_b / m["gu"] / 1e9 / PEAK_HBM_GBS, 4),
+            "traffic": traffic_from_profile(bits),
         },
         "cpu_baseline": None,
     }
