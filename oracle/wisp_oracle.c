@@ -20,8 +20,22 @@
  * so every float expression rounds exactly where the reference's torch ops
  * round).
  *
- * Pinning status of each function is listed in oracle/README.md and in the
- * tests that pin it (tests/test_oracle_*.py).
+ * Pinning (each function is checked by something other than itself; all in
+ * tests/test_oracle.py):
+ *   wo_f32_to_f16 / wo_f32_to_bf16 / wo_*_to_f32 .. torch's own conversions on
+ *       random, tie, subnormal, overflow and NaN inputs
+ *   wo_expert_nbytes ... reference KATs (test_quant.py:39-40, architecture.md:82)
+ *   wo_pack / wo_unpack  hand-derived byte KATs for 4/3/2-bit, round trips
+ *   wo_q3_field ........ the kernel's 3-bit read formula (kernels.py:206-217)
+ *                        evaluated independently for every element
+ *   wo_quantize ........ hand-derived KATs (half-even ties, constant group,
+ *                        1e-5 clamp), nearest-level property, reference error
+ *                        bounds and monotonicity (test_quant.py:15-34)
+ *   wo_dequant ......... hand KATs incl. the fp32-then-bf16 double rounding,
+ *                        numpy float32 elementwise semantics
+ *   wo_moe_layer_f64 ... dense numpy dequant->matvec (the unfolded form) at
+ *                        several shapes and bit widths
+ * No function is parity-unpinned.
  */
 #include <math.h>
 #include <stdint.h>
