@@ -103,6 +103,16 @@ int wisp_moe_decode(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, con
                     const uint16_t* x, int64_t H, int64_t I, int bits, int64_t group, uint32_t* act, uint16_t* out,
                     void* stream);
 
+/* Rotary embedding of one decode token, q and k heads in one launch:
+ * out[i] = x[i]*cos[i] + sign(i)*x[(i + d/2) mod d]*sin[i], sign = -1 for
+ * i < d/2, else +1; binary32 products and sum rounded separately, one
+ * rounding to the output type. q: hq heads of d elements at q_head_stride
+ * elements apart (unit element stride); k likewise (hk heads, may be 0);
+ * cos, sin: d elements; qo [hq, d], ko [hk, d] contiguous. dtype 0 = float32,
+ * 1 = bfloat16 (all tensors). Replaces wisp/kernels.py:325-371 (rope_decode). */
+int wisp_rope_decode(const void* q, int64_t q_head_stride, const void* k, int64_t k_head_stride, const void* cos,
+                     const void* sin, int hq, int hk, int d, int dtype, void* qo, void* ko, void* stream);
+
 /* Launch-shape tuning, process-wide: gu_rows = rows of one expert per wave in
  * kernel 1, gu_waves = waves per workgroup in kernel 1, dn_iters = row
  * iterations per workgroup in kernel 2 (each in {1,2,4,8}; 0 keeps the

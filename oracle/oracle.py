@@ -47,6 +47,7 @@ def lib() -> ctypes.CDLL:
         L.wo_dequant.restype, L.wo_dequant.argtypes = i32, [vp, i64, i32, i64, vp]
         L.wo_moe_layer_f64.restype = i32
         L.wo_moe_layer_f64.argtypes = [vp, i64, i64, vp, vp, i32, vp, i64, i64, i32, i64, vp, vp, vp]
+        L.wo_rope.restype, L.wo_rope.argtypes = i32, [vp, i64, i32, vp, vp, vp]
         _lib = L
     return _lib
 
@@ -187,3 +188,18 @@ def meta(slots, weights) -> np.ndarray:
     s = np.asarray(slots, dtype=np.int64).ravel()
     assert np.all(s < (1 << 24)), "slot ids must be exact in float32"
     return np.concatenate([s.astype(np.float32), np.asarray(weights, dtype=np.float32).ravel()])
+
+
+# ---------------------------------------------------------------- rotary (decode)
+def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """kernels.py:325-349: rotate head vectors x [nh, d] (float32 values) by cos/sin [d]
+    in binary32 with separately rounded products and sum. Returns float32 [nh, d]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nh, d = x.shape
+    c = np.ascontiguousarray(cos, dtype=np.float32).ravel()
+    s = np.ascontiguousarray(sin, dtype=np.float32).ravel()
+    assert c.size == d and s.size == d
+    out = np.empty_like(x)
+    if lib().wo_rope(_p(x), nh, d, _p(c), _p(s), _p(out)) != 0:
+        raise ValueError("bad arguments to rope")
+    return out

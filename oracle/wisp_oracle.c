@@ -15,6 +15,7 @@
  *   - 3-bit field read used by the kernels . wisp/kernels.py:206-217
  *   - fused MoE decode semantics ........... wisp/kernels.py:12, 20-69,
  *                                            72-112, 137, 140-185, 220-307
+ *   - decode rotary embedding .............. wisp/kernels.py:325-349
  *
  * Build: see oracle/Makefile (gcc -O2 -ffp-contract=off: no FMA contraction,
  * so every float expression rounds exactly where the reference's torch ops
@@ -35,6 +36,9 @@
  *                        numpy float32 elementwise semantics
  *   wo_moe_layer_f64 ... dense numpy dequant->matvec (the unfolded form) at
  *                        several shapes and bit widths
+ *   wo_rope ............ hand KAT (d = 2: complex multiplication), rotation
+ *                        preserves the norm and composes (angle addition),
+ *                        float64 textbook rotate-half formula
  * No function is parity-unpinned.
  */
 #include <math.h>
@@ -364,5 +368,30 @@ WO_EXPORT int wo_moe_layer_f64(const uint8_t* pool, int64_t slot_bytes, int64_t 
     }
     free(xd);
     free(ad);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* rotary embedding of one decode token (kernels.py:325-349)                */
+/* ------------------------------------------------------------------------ */
+
+/* x [nh, d] binary32 head vectors (already widened from their storage type),
+ * cs/sn [d]; out[h, i] = x[i]*cs[i] + sign(i)*x[(i + d/2) % d]*sn[i] with
+ * sign = -1 for i < d/2, else +1 (kernels.py:332-346). Each product and the
+ * sum round separately in binary32 (this file builds with -ffp-contract=off). */
+WO_EXPORT int wo_rope(const float* x, int64_t nh, int d, const float* cs, const float* sn, float* out) {
+    if (nh < 0 || d < 2 || d % 2) return -1;
+    const int half = d / 2;
+    for (int64_t h = 0; h < nh; h++) {
+        const float* xv = x + h * d;
+        float* o = out + h * d;
+        for (int i = 0; i < d; i++) {
+            const int p = (i + half) % d;
+            const float sign = i < half ? -1.0f : 1.0f;
+            const float t1 = xv[i] * cs[i];
+            const float t2 = (sign * xv[p]) * sn[i];
+            o[i] = t1 + t2;
+        }
+    }
     return 0;
 }

@@ -119,6 +119,19 @@ def test_format_entry_validation():
     assert L.wisp_dequant(FAKE, 2506752, None, 0, 1, 1572864, 4, 128, FAKE, None) == _lib.WISP_OK
 
 
+def test_rope_argument_validation():
+    L = _lib.lib()
+    ok = (FAKE, 128, FAKE, 128, FAKE, FAKE, 32, 4, 128, 1, FAKE, FAKE, None)
+    bad_d = (FAKE, 128, FAKE, 128, FAKE, FAKE, 32, 4, 127, 1, FAKE, FAKE, None)
+    assert L.wisp_rope_decode(*bad_d) == _lib.WISP_EINVAL  # odd head dim
+    bad_stride = (FAKE, 64, FAKE, 128, FAKE, FAKE, 32, 4, 128, 1, FAKE, FAKE, None)
+    assert L.wisp_rope_decode(*bad_stride) == _lib.WISP_EINVAL
+    bad_dtype = ok[:9] + (2,) + ok[10:]
+    assert L.wisp_rope_decode(*bad_dtype) == _lib.WISP_EINVAL
+    null_q = (None,) + ok[1:]
+    assert L.wisp_rope_decode(*null_q) == _lib.WISP_EINVAL
+
+
 def test_no_cpu_fallback():
     """The product path raises on CPU tensors instead of computing on the host."""
     w3 = torch.randn(3, 2048)

@@ -297,3 +297,58 @@ def test_layer_parity_repeated_calls(bits, k):
         err = _rel_l2(O.bf16_bits_to_f32(_bf16(got)), r)
         print(f"layer bits={bits} k={k} it={it}: rel-L2 {err:.3e}")
         assert err <= TOL, err
+
+
+# ---------------------------------------------------------------- rotary (kernels.py:325-371)
+def _rope_inputs(seed, Hq, Hk, D, dtype):
+    g = torch.Generator().manual_seed(seed)
+    # HF layout: [1,1,H,D] transposed to a [1,H,1,D] strided view
+    q = torch.randn(1, 1, Hq, D, generator=g).to(dtype).transpose(1, 2)
+    k = torch.randn(1, 1, Hk, D, generator=g).to(dtype).transpose(1, 2)
+    pos = 1 + int(torch.randint(0, 4000, (1,), generator=g))
+    inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float64) / D))
+    ang = torch.cat([inv, inv]) * pos
+    cos = ang.cos().to(dtype).view(1, 1, D)
+    sin = ang.sin().to(dtype).view(1, 1, D)
+    return q, k, cos, sin
+
+
+def _f32(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("Hq,Hk,D", [(32, 4, 128), (16, 2, 64), (8, 8, 256), (4, 0, 128), (3, 1, 2)])
+def test_rope_decode_bit_exact(dtype, Hq, Hk, D):
+    q, k, cos, sin = _rope_inputs(Hq * 7 + D, Hq, Hk, D, dtype)
+    qo, ko = kernels.rope_decode(q.to(DEV), k.to(DEV), cos.to(DEV), sin.to(DEV))
+    torch.cuda.synchronize()
+    assert qo.shape == (1, Hq, 1, D) and ko.shape == (1, Hk, 1, D) and qo.dtype == dtype
+    c, s = _f32(cos).ravel(), _f32(sin).ravel()
+    for got, x, H in ((qo, q, Hq), (ko, k, Hk)):
+        if H == 0:
+            continue
+        ref = O.rope(_f32(x).reshape(H, D), c, s)
+        if dtype == torch.bfloat16:
+            assert np.array_equal(got.view(torch.int16).cpu().numpy().reshape(H, D).view(np.uint16),
+                                  O.f32_to_bf16_bits(ref).reshape(H, D))
+        else:
+            assert np.array_equal(_f32(got).reshape(H, D).view(np.uint32), ref.view(np.uint32))
+
+
+def test_rope_decode_reference_criterion():
+    """tests/test_fastattn.py:12-23 of the reference: against the library's rotate-half formula
+    in bf16 (HF's apply_rotary_pos_emb), max|d| < 3e-2 max|ref|."""
+    D, Hq, Hk = 128, 32, 4
+    q, k, cos, sin = _rope_inputs(0, Hq, Hk, D, torch.bfloat16)
+    try:
+        from transformers.models.qwen3_moe import modeling_qwen3_moe as m
+        qr, kr = m.apply_rotary_pos_emb(q, k, cos, sin)
+    except Exception:  # library missing: the same formula, written out
+        def rot(t):
+            return torch.cat([-t[..., D // 2:], t[..., : D // 2]], dim=-1)
+        qr, kr = q * cos + rot(q) * sin, k * cos + rot(k) * sin
+    qo, ko = kernels.rope_decode(q.to(DEV), k.to(DEV), cos.to(DEV), sin.to(DEV))
+    for got, ref in ((qo.cpu(), qr), (ko.cpu(), kr)):
+        assert got.shape == ref.shape
+        assert (got.float() - ref.float()).abs().max() < 3e-2 * ref.float().abs().max()

@@ -253,3 +253,37 @@ def test_route_matches_torch():
     assert np.allclose(rw, tw.numpy(), rtol=0, atol=0)
     m = O.meta([3, 1], [0.25, 0.75])
     assert m.dtype == np.float32 and m.tolist() == [3.0, 1.0, 0.25, 0.75]
+
+
+# ---------------------------------------------------------------- rotary (kernels.py:325-349)
+def test_rope_known_answer_d2():
+    # d = 2: a plain 2-D rotation, (x0 + i x1) * (c + i s); values chosen so every product
+    # and sum is exact in binary32
+    out = O.rope(np.array([[3.0, 5.0]], np.float32), np.array([0.5, 0.5], np.float32),
+                 np.array([0.25, 0.25], np.float32))
+    assert out.tolist() == [[3.0 * 0.5 - 5.0 * 0.25, 5.0 * 0.5 + 3.0 * 0.25]]
+
+
+def test_rope_rotation_properties():
+    rng = np.random.default_rng(3)
+    d, nh = 128, 6
+    x = rng.standard_normal((nh, d)).astype(np.float32)
+    inv = 1.0 / (10000.0 ** (np.arange(0, d, 2) / d))
+    ang = np.concatenate([inv, inv]) * 7.0  # position 7, HF layout (cos/sin repeated per half)
+    c, s = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    out = O.rope(x, c, s)
+    # the textbook rotate-half statement in float64: x*cos + rotate_half(x)*sin
+    rh = np.concatenate([-x[:, d // 2:], x[:, : d // 2]], axis=1).astype(np.float64)
+    ref = x.astype(np.float64) * c + rh * s
+    assert np.max(np.abs(out - ref)) <= 4 * np.finfo(np.float32).eps * np.max(np.abs(ref))
+    # a rotation keeps each head's norm
+    assert np.allclose(np.linalg.norm(out, axis=1), np.linalg.norm(x, axis=1), rtol=1e-5)
+    # rotating by a then by b equals rotating by a + b
+    a2 = np.concatenate([inv, inv]) * 5.0
+    two = O.rope(O.rope(x, np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)),
+                 np.cos(a2).astype(np.float32), np.sin(a2).astype(np.float32))
+    one = O.rope(x, np.cos(ang + a2).astype(np.float32), np.sin(ang + a2).astype(np.float32))
+    assert np.allclose(two, one, rtol=1e-4, atol=1e-5)
+    # a plausible slip (sign on the wrong half) is caught by the textbook form
+    bad = x.astype(np.float64) * c - rh * s
+    assert np.max(np.abs(out - bad)) > 1e-2

@@ -4,8 +4,11 @@
 // Reference semantics: wisp/quant.py:17-22 (size), 25-57 (_pack/_unpack),
 // 60-73 (quantize), 76-87 (dequant). Bit-exactness rules:
 //  * dequant: w = float(q)*float(s) then + float(m), two separately rounded
-//    binary32 ops (no FMA contraction: `#pragma clang fp contract(off)` in the
-//    kernels below), then round-to-nearest-even to bf16 (v_cvt_pk_bf16_f32).
+//    binary32 ops, then round-to-nearest-even to bf16 (v_cvt_pk_bf16_f32).
+//    q*s is exact in binary32 (q < 256, s an fp16 value: at most 8 + 11
+//    significant bits), so rounding it changes nothing; the kernels are
+//    written with plain operators under `#pragma clang fp contract(off)`,
+//    which keeps mul and add separate in the ISA.
 //  * quantize: binary32 sub/div with __fsub_rn/__fdiv_rn (IEEE, correctly
 //    rounded), round-half-even (rintf), fp16 RTNE conversion with subnormals.
 // Dequant is HBM-bound: it reads nbytes and writes 6n bytes per expert.
@@ -80,8 +83,8 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ row
     uint32_t w[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const float a = __fadd_rn(__fmul_rn((float)q[2 * i], s), m);
-        const float bb = __fadd_rn(__fmul_rn((float)q[2 * i + 1], s), m);
+        const float a = (float)q[2 * i] * s + m;
+        const float bb = (float)q[2 * i + 1] * s + m;
         w[i] = pack_bf16x2(a, bb);
     }
 #pragma unroll
@@ -120,7 +123,7 @@ __global__ __launch_bounds__(256) void k_dequant_any(const uint8_t* __restrict__
         q = (((hi << 8) | lo) >> (p & 7)) & 7u;
     }
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(buf + ncode);
-    const float v = __fadd_rn(__fmul_rn((float)q, h2f(sc[g])), h2f(sc[ng + g]));
+    const float v = (float)q * h2f(sc[g]) + h2f(sc[ng + g]);
     out[b * N + e] = f32_to_bf16(v);
 }
 

@@ -35,6 +35,7 @@ SIGNATURES = {
     "wisp_moe_down_sum": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp]),
     "wisp_moe_down": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp]),
     "wisp_moe_decode": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp, _vp]),
+    "wisp_rope_decode": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "wisp_set_tuning": (_i32, [_i32, _i32, _i32]),
     "wisp_act_read": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp]),
 }

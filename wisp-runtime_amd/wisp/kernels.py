@@ -118,3 +118,34 @@ def gate_up_act(pool, meta, x, k, n, H, I, bits, group=128) -> torch.Tensor:
 def set_tuning(gu_rows: int = 0, gu_waves: int = 0, dn_iters: int = 0) -> None:
     """Launch-shape knobs of the two decode kernels (0 keeps the current value)."""
     _lib.check(_lib.lib().wisp_set_tuning(gu_rows, gu_waves, dn_iters), "set_tuning")
+
+
+_ROPE_DTYPES = {torch.float32: 0, torch.bfloat16: 1}
+
+
+def rope_decode(q, k, cos, sin):
+    """kernels.py:352-371. q: [1,Hq,1,D], k: [1,Hk,1,D] (HF layout, possibly strided views),
+    cos/sin: [1,1,D] -> rotated (qo, ko), same shapes, contiguous, in q's dtype. One launch."""
+    Hq, D = q.shape[1], q.shape[3]
+    Hk = k.shape[1]
+    dev = _lib.require_gpu(q, k, cos, sin, what="rope_decode")
+    dt = _ROPE_DTYPES.get(q.dtype)
+    if dt is None or k.dtype != q.dtype:
+        raise TypeError(f"rope_decode supports float32 and bfloat16 q/k of one dtype (got {q.dtype}, {k.dtype})")
+    if q.stride(3) != 1:
+        q = q.contiguous()
+    if k.stride(3) != 1:
+        k = k.contiguous()
+    cos = cos.reshape(-1).to(q.dtype).contiguous()
+    sin = sin.reshape(-1).to(q.dtype).contiguous()
+    assert cos.numel() == D and sin.numel() == D
+    qo = torch.empty((1, Hq, 1, D), dtype=q.dtype, device=dev)
+    ko = torch.empty((1, Hk, 1, D), dtype=k.dtype, device=dev)
+    _lib.check(
+        _lib.lib().wisp_rope_decode(
+            _lib.ptr(q), q.stride(1), _lib.ptr(k), k.stride(1), _lib.ptr(cos), _lib.ptr(sin), Hq, Hk, D, dt,
+            _lib.ptr(qo), _lib.ptr(ko), _lib.stream(dev),
+        ),
+        "rope_decode",
+    )
+    return qo, ko
