@@ -4,9 +4,12 @@
  *
  * Plain pointers, sizes and a stream handle; no torch types. Every device
  * pointer is a HIP device address; `stream` is a hipStream_t passed as void*
- * (NULL = the default stream). Entry points are asynchronous: they enqueue
- * kernels on `stream` and return; none allocates, frees or synchronises, so
- * all of them may be captured into a hipGraph.
+ * (NULL = the default stream). The kernel entry points are asynchronous: they
+ * enqueue kernels on `stream` and return; none allocates, frees or
+ * synchronises, so all of them may be captured into a hipGraph. The expert
+ * cache entry points (wisp_core_*, wisp_cache_*) are host-side: they allocate,
+ * copy and synchronise where stated and run between graph replays, as the
+ * reference's paging step does.
  *
  * Return value: WISP_OK (0) on success; WISP_EINVAL (-1) when an argument
  * precondition fails (the reference raises AssertionError for the same
@@ -112,6 +115,81 @@ int wisp_moe_decode(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, con
  * 1 = bfloat16 (all tensors). Replaces wisp/kernels.py:325-371 (rope_decode). */
 int wisp_rope_decode(const void* q, int64_t q_head_stride, const void* k, int64_t k_head_stride, const void* cos,
                      const void* sin, int hq, int hk, int d, int dtype, void* qo, void* ko, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Expert cache bookkeeping (host only, no device calls). Keys are
+ * layer*n_experts + expert; slots [0, n_static) are the static region.
+ * policy 0 = lru, 1 = wsa (decayed frequency), 2 = static. Arithmetic is
+ * binary64 in the reference's order, so slot choices are identical.
+ * Replaces wisp/cache_core.py:15-149 (CacheCore).
+ * ------------------------------------------------------------------------- */
+int wisp_core_create(int64_t nslots, int policy, double decay, int64_t n_static, double admit_after, void** out);
+void wisp_core_destroy(void* core);
+/* cache_core.py:30-37 (step), 39-45 (note), 47-48 (norm_freq), 54-55 (lookup: -1 if absent) */
+void wisp_core_step(void* core);
+void wisp_core_note(void* core, const int64_t* keys, int64_t n);
+double wisp_core_norm_freq(void* core, int64_t key);
+int64_t wisp_core_lookup(void* core, int64_t key);
+/* cache_core.py:87-106 (ensure): slots[n] aligned with keys; the (key, slot)
+ * pairs to load in load_keys/load_slots[*nloads] (capacity n). WISP_EINVAL if
+ * no slot is evictable (the reference's RuntimeError). */
+int wisp_core_ensure(void* core, const int64_t* keys, int64_t n, int64_t* slots, int64_t* load_keys,
+                     int64_t* load_slots, int64_t* nloads);
+/* cache_core.py:108-123 (split): hits and misses, nothing loaded */
+int wisp_core_split(void* core, const int64_t* keys, int64_t n, int64_t* hit_keys, int64_t* hit_slots, int64_t* nhit,
+                    int64_t* miss_keys, int64_t* nmiss);
+/* cache_core.py:64-84 (acquire) and 125-132 (admit: slot, or -1) */
+int wisp_core_acquire(void* core, int64_t key, const int64_t* prot, int64_t nprot, int64_t* slot);
+int64_t wisp_core_admit(void* core, int64_t key, const int64_t* prot, int64_t nprot);
+/* cache_core.py:57-62 (preload into the static region) */
+int wisp_core_preload(void* core, const int64_t* keys, int64_t n);
+/* cache_core.py:135-149 (resized): a new core in *out keeping the hottest
+ * keys; the (key, new slot) pairs to copy in keys/slots[*n] (capacity nslots). */
+int wisp_core_resized(void* core, int64_t nslots, void** out, int64_t* keys, int64_t* slots, int64_t* n);
+/* Inspection: s[11] = nslots, policy, n_static, tick, hits, misses,
+ * evictions, calls, nfree, nresident, nfreq; d[3] = decay, admit_after, inc.
+ * Arrays (any may be NULL): slot_key/last/score [nslots], free [nfree] (next
+ * slot handed out last), freq keys/values [nfreq] in first-use order. */
+void wisp_core_state(void* core, int64_t* s, double* d);
+void wisp_core_arrays(void* core, int64_t* slot_key, double* last, double* score, int64_t* free_list,
+                      int64_t* freq_keys, double* freq_vals);
+
+/* ---------------------------------------------------------------------------
+ * Expert cache: a hipMalloc slot pool [nslots, slot_bytes] filled from a host
+ * store (pinned rows of row_bytes, caller-owned, outliving the cache) by
+ * hipMemcpyAsync on a side stream of default priority. Replaces
+ * wisp/cache.py:9-162 (ExpertCache). The cache takes ownership of `core`.
+ * decode_on_load: quantized rows are staged and dequantized once into bf16
+ * slots (slot_bytes = 3n*2), cache.py:25-37, 62-71.
+ * ------------------------------------------------------------------------- */
+int wisp_cache_create(void* core, int64_t slot_bytes, const uint8_t* host, int64_t host_rows, int64_t row_bytes,
+                      int bits, int64_t n, int64_t group, int decode_on_load, int64_t staging_rows, int device,
+                      void** out);
+void wisp_cache_destroy(void* cache);
+void* wisp_cache_core(void* cache);
+void* wisp_cache_pool(void* cache);
+void* wisp_cache_copy_stream(void* cache);
+void wisp_cache_counters(void* cache, int64_t* bytes_h2d, int64_t* n_loads);
+/* A DLManagedTensor* (DLPack) viewing the pool as uint8 [nslots, slot_bytes]
+ * on the ROCm device; the view keeps the pool memory alive. A view never
+ * handed to a consumer is released with wisp_cache_pool_dlpack_free. */
+void* wisp_cache_pool_dlpack(void* cache);
+void wisp_cache_pool_dlpack_free(void* managed);
+/* cache.py:50-76 (_issue): copies of host row keys[i] into slots[i] on the
+ * side stream, ordered after the work queued on `compute`. */
+int wisp_cache_issue(void* cache, const int64_t* keys, const int64_t* slots, int64_t n, void* compute);
+/* cache.py:78-81 (sync_compute): `compute` waits for the issued copies. */
+int wisp_cache_sync_compute(void* cache, void* compute);
+/* cache.py:87-91 (ensure): residency, copies, ordering, in one call. */
+int wisp_cache_ensure(void* cache, const int64_t* keys, int64_t n, int64_t* slots, void* compute);
+/* One layer's host step of the graph decoder (graphdec.py:216-231): ensure the
+ * k routed keys, write [slots | weights] into meta_host (pinned float32 [2k])
+ * and copy it to meta_dev on `compute`. slots (may be NULL) receives the slots. */
+int wisp_cache_prepare_layer(void* cache, const int64_t* keys, const float* weights, int k, float* meta_host,
+                             float* meta_dev, int64_t* slots, void* compute);
+/* cache.py:144-158 (resize): synchronises the device, keeps the hottest
+ * experts, releases the old pool, allocates the new one, re-copies. */
+int wisp_cache_resize(void* cache, int64_t nslots);
 
 /* Launch-shape tuning, process-wide: gu_rows = rows of one expert per wave in
  * kernel 1, gu_waves = waves per workgroup in kernel 1, dn_iters = row

@@ -132,6 +132,18 @@ def test_rope_argument_validation():
     assert L.wisp_rope_decode(*null_q) == _lib.WISP_EINVAL
 
 
+def test_expert_cache_needs_a_gpu():
+    """The slot pool is device memory: without a GPU the cache refuses to build (no host pool)."""
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    from wisp.cache import ExpertCache
+    from wisp.store import ExpertStore
+
+    st = ExpertStore(1, 2, 256 * 128, 4, 128, pin=False)
+    with pytest.raises(RuntimeError):
+        ExpertCache(st, 2, device="cuda:0")
+
+
 def test_no_cpu_fallback():
     """The product path raises on CPU tensors instead of computing on the host."""
     w3 = torch.randn(3, 2048)

@@ -1,0 +1,653 @@
+// Expert cache for batch-1 MoE decode: slot bookkeeping (CacheCore) and the
+// hipMalloc slot pool filled from a pinned host store by hipMemcpyAsync on a
+// side stream (ExpertCache). Host code only; no kernels of its own (the
+// decode-on-load mode reuses the dequant kernel).
+//
+// Reference semantics:
+//   CacheCore  wisp/cache_core.py:15-149 (LRU / WSA / static policies, ensure,
+//              split, admit, preload, resized)
+//   ExpertCache wisp/cache.py:9-162 (pool, _issue ordering, sync_compute,
+//              ensure, decode_on_load, resize)
+//   one layer's host step of the graph decoder, wisp/graphdec.py:216-231
+//              (ensure the routed experts, write [slots | weights] into the
+//              pinned meta buffer, copy it to the device on the compute stream)
+//
+// Arithmetic of the bookkeeping (ticks, decayed frequencies, renormalisation at
+// 1e100, first-index argmin over the dynamic region, stable hottest-first sort
+// in resized) is binary64, in the reference's order, so slot choices match it
+// exactly. A persistent native core removes the per-layer Python bookkeeping
+// between graph replays (48 host decisions per token).
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <new>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "wisp_internal.hpp"
+
+namespace wisp {
+
+enum Policy { kLRU = 0, kWSA = 1, kStatic = 2 };
+
+struct Core {
+    int64_t nslots = 0, n_static = 0;
+    int policy = kLRU;
+    double decay = 0.9995, admit_after = 2.0;
+    std::vector<int64_t> slot_key;
+    std::vector<double> last, score;
+    std::unordered_map<int64_t, int64_t> key2slot;
+    std::vector<int64_t> free;  // a stack: back() is handed out next
+    int64_t tick = 0;
+    double inc = 1.0;
+    std::unordered_map<int64_t, double> freq;
+    std::vector<int64_t> freq_order;  // insertion order of freq's keys
+    int64_t hits = 0, misses = 0, evictions = 0, calls = 0;
+
+    Core(int64_t n, int pol, double dec, int64_t nst, double adm)
+        : nslots(n), n_static(nst), policy(pol), decay(dec), admit_after(adm), slot_key(n, -1), last(n, 0.0),
+          score(n, 0.0) {
+        for (int64_t s = n - 1; s >= nst; --s) free.push_back(s);
+    }
+
+    double& freq_at(int64_t k) {  // defaultdict(float) access
+        auto it = freq.find(k);
+        if (it != freq.end()) return it->second;
+        freq_order.push_back(k);
+        return freq.emplace(k, 0.0).first->second;
+    }
+
+    void step() {
+        tick += 1;
+        inc /= decay;
+        if (inc > 1e100) {
+            for (auto& kv : freq) kv.second /= 1e100;
+            for (double& v : score) v /= 1e100;
+            inc /= 1e100;
+        }
+    }
+
+    void note(const int64_t* keys, int64_t n) {
+        for (int64_t i = 0; i < n; ++i) {
+            double& f = freq_at(keys[i]);
+            f += inc;
+            auto it = key2slot.find(keys[i]);
+            if (it != key2slot.end()) {
+                last[it->second] = (double)tick;
+                score[it->second] = f;
+            }
+        }
+    }
+
+    double norm_freq(int64_t k) const {
+        auto it = freq.find(k);
+        return (it == freq.end() ? 0.0 : it->second) / inc;
+    }
+
+    int64_t lookup(int64_t k) const {
+        auto it = key2slot.find(k);
+        return it == key2slot.end() ? -1 : it->second;
+    }
+
+    // cache_core.py:64-84; returns -1 when nothing is evictable
+    int64_t acquire(int64_t key, const std::unordered_set<int64_t>& prot) {
+        int64_t s;
+        if (!free.empty()) {
+            s = free.back();
+            free.pop_back();
+        } else {
+            const std::vector<double>& src = policy == kLRU ? last : score;
+            int64_t j = -1;
+            double best = INFINITY;
+            for (int64_t i = n_static; i < nslots; ++i) {
+                const double v = prot.count(i) ? INFINITY : src[i];
+                if (j < 0 || v < best) {
+                    best = v;
+                    j = i;
+                }
+            }
+            if (j < 0 || !std::isfinite(best)) return -1;
+            s = j;
+            key2slot.erase(slot_key[s]);
+            evictions += 1;
+        }
+        slot_key[s] = key;
+        key2slot[key] = s;
+        last[s] = (double)tick;
+        score[s] = freq_at(key);
+        return s;
+    }
+};
+
+static int no_slot() {
+    set_error("no evictable slot: dynamic region smaller than the working request");
+    return WISP_EINVAL;
+}
+
+// ---------------------------------------------------------------------------
+// slot pool memory shared between the cache and DLPack views of it
+struct PoolBlock {
+    void* ptr = nullptr;
+    int device = 0;
+    std::atomic<int> refs{1};
+};
+
+static void pool_release(PoolBlock* b) {
+    if (b && b->refs.fetch_sub(1) == 1) {
+        int cur = 0;
+        (void)hipGetDevice(&cur);
+        (void)hipSetDevice(b->device);
+        (void)hipFree(b->ptr);
+        (void)hipSetDevice(cur);
+        delete b;
+    }
+}
+
+// DLPack (unversioned ABI) structures, as consumed by torch.utils.dlpack
+struct DLDevice {
+    int32_t device_type;
+    int32_t device_id;
+};
+struct DLDataType {
+    uint8_t code;
+    uint8_t bits;
+    uint16_t lanes;
+};
+struct DLTensor {
+    void* data;
+    DLDevice device;
+    int32_t ndim;
+    DLDataType dtype;
+    int64_t* shape;
+    int64_t* strides;
+    uint64_t byte_offset;
+};
+struct DLManagedTensor {
+    DLTensor dl_tensor;
+    void* manager_ctx;
+    void (*deleter)(DLManagedTensor*);
+};
+struct PoolView {
+    DLManagedTensor m;
+    int64_t shape[2];
+    int64_t strides[2];
+    PoolBlock* block;
+};
+static void view_deleter(DLManagedTensor* m) {
+    PoolView* v = reinterpret_cast<PoolView*>(m);
+    pool_release(v->block);
+    delete v;
+}
+
+struct Cache {
+    Core* core = nullptr;
+    PoolBlock* pool = nullptr;
+    int device = 0;
+    int64_t nslots = 0, slot_bytes = 0;
+    const uint8_t* host = nullptr;  // pinned store rows (caller-owned)
+    int64_t host_rows = 0, row_bytes = 0;
+    int bits = 4;
+    int64_t n = 0, group = 128;
+    bool decode_on_load = false;
+    uint8_t* staging = nullptr;  // decode_on_load: staging rows of quantized bytes
+    int64_t staging_rows = 0;
+    hipStream_t copy = nullptr;
+    hipEvent_t order = nullptr, done = nullptr;
+    bool pending = false;
+    int64_t bytes_h2d = 0, n_loads = 0;
+};
+
+static int hip_fail(hipError_t e, const char* what) {
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return (int)e;
+}
+
+static int alloc_pool(Cache& c) {
+    PoolBlock* b = new (std::nothrow) PoolBlock();
+    if (!b) return fail_inval("out of host memory");
+    b->device = c.device;
+    const hipError_t e = hipMalloc(&b->ptr, (size_t)(c.nslots * c.slot_bytes));
+    if (e != hipSuccess) {
+        delete b;
+        return hip_fail(e, "hipMalloc(slot pool)");
+    }
+    c.pool = b;
+    return WISP_OK;
+}
+
+// cache.py:50-76: copies of [(key, slot)] on the side stream, ordered after
+// the work already queued on the compute stream (those slots may still be read)
+static int issue(Cache& c, const int64_t* keys, const int64_t* slots, int64_t n, hipStream_t compute) {
+    if (n <= 0) return WISP_OK;
+    for (int64_t i = 0; i < n; ++i)
+        if (keys[i] < 0 || keys[i] >= c.host_rows || slots[i] < 0 || slots[i] >= c.nslots)
+            return fail_inval("key outside the host store or slot outside the pool");
+    hipError_t e = hipEventRecord(c.order, compute);
+    if (e == hipSuccess) e = hipStreamWaitEvent(c.copy, c.order, 0);
+    if (e != hipSuccess) return hip_fail(e, "ordering the copy stream");
+    uint8_t* pool = static_cast<uint8_t*>(c.pool->ptr);
+    if (!c.decode_on_load) {
+        for (int64_t i = 0; i < n; ++i) {
+            e = hipMemcpyAsync(pool + slots[i] * c.slot_bytes, c.host + keys[i] * c.row_bytes, (size_t)c.row_bytes,
+                               hipMemcpyHostToDevice, c.copy);
+            if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(expert row)");
+        }
+    } else {
+        // cache.py:62-71: quantized rows cross PCIe into staging, then are
+        // dequantized once into the bf16 slots
+        for (int64_t i0 = 0; i0 < n; i0 += c.staging_rows) {
+            const int64_t m = std::min<int64_t>(c.staging_rows, n - i0);
+            for (int64_t j = 0; j < m; ++j) {
+                e = hipMemcpyAsync(c.staging + j * c.row_bytes, c.host + keys[i0 + j] * c.row_bytes,
+                                   (size_t)c.row_bytes, hipMemcpyHostToDevice, c.copy);
+                if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(staging row)");
+            }
+            for (int64_t j = 0; j < m; ++j) {
+                const int rc = wisp_dequant(c.staging + j * c.row_bytes, c.row_bytes, nullptr, 1, 1, c.n, c.bits,
+                                            c.group, reinterpret_cast<uint16_t*>(pool + slots[i0 + j] * c.slot_bytes),
+                                            c.copy);
+                if (rc) return rc;
+            }
+        }
+    }
+    e = hipEventRecord(c.done, c.copy);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord(copies done)");
+    c.pending = true;
+    c.bytes_h2d += n * c.row_bytes;
+    c.n_loads += n;
+    return WISP_OK;
+}
+
+static int sync_compute(Cache& c, hipStream_t compute) {
+    if (!c.pending) return WISP_OK;
+    const hipError_t e = hipStreamWaitEvent(compute, c.done, 0);
+    return e == hipSuccess ? WISP_OK : hip_fail(e, "hipStreamWaitEvent(copies done)");
+}
+
+// cache_core.py:87-106; loads (key, slot) pairs are returned in order
+static int core_ensure(Core& c, const int64_t* keys, int64_t n, int64_t* slots, std::vector<int64_t>& lk,
+                       std::vector<int64_t>& ls) {
+    c.step();
+    c.note(keys, n);
+    c.calls += 1;
+    std::unordered_set<int64_t> prot;
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t s = c.lookup(keys[i]);
+        slots[i] = s;
+        if (s >= 0) {
+            prot.insert(s);
+            c.hits += 1;
+        }
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        if (slots[i] >= 0) continue;
+        const int64_t s = c.acquire(keys[i], prot);
+        if (s < 0) return no_slot();
+        slots[i] = s;
+        prot.insert(s);
+        lk.push_back(keys[i]);
+        ls.push_back(s);
+        c.misses += 1;
+    }
+    return WISP_OK;
+}
+
+static Core* as_core(void* h) { return static_cast<Core*>(h); }
+static Cache* as_cache(void* h) { return static_cast<Cache*>(h); }
+
+}  // namespace wisp
+
+using namespace wisp;
+
+// ------------------------------------------------------------------ CacheCore
+extern "C" int wisp_core_create(int64_t nslots, int policy, double decay, int64_t n_static, double admit_after,
+                                void** out) {
+    clear_error();
+    if (!out) return fail_inval("null out");
+    if (nslots < 1 || n_static < 0 || n_static > nslots) return fail_inval("need 0 <= n_static <= nslots, nslots >= 1");
+    if (policy < kLRU || policy > kStatic) return fail_inval("policy must be 0 (lru), 1 (wsa) or 2 (static)");
+    if (!(decay > 0.0)) return fail_inval("decay must be > 0");
+    Core* c = new (std::nothrow) Core(nslots, policy, decay, n_static, admit_after);
+    if (!c) return fail_inval("out of host memory");
+    *out = c;
+    return WISP_OK;
+}
+
+extern "C" void wisp_core_destroy(void* h) { delete as_core(h); }
+
+extern "C" void wisp_core_step(void* h) { as_core(h)->step(); }
+
+extern "C" void wisp_core_note(void* h, const int64_t* keys, int64_t n) { as_core(h)->note(keys, n); }
+
+extern "C" double wisp_core_norm_freq(void* h, int64_t key) { return as_core(h)->norm_freq(key); }
+
+extern "C" int64_t wisp_core_lookup(void* h, int64_t key) { return as_core(h)->lookup(key); }
+
+extern "C" int wisp_core_ensure(void* h, const int64_t* keys, int64_t n, int64_t* slots, int64_t* load_keys,
+                                int64_t* load_slots, int64_t* nloads) {
+    clear_error();
+    std::vector<int64_t> lk, ls;
+    const int rc = core_ensure(*as_core(h), keys, n, slots, lk, ls);
+    for (size_t i = 0; i < lk.size(); ++i) {
+        load_keys[i] = lk[i];
+        load_slots[i] = ls[i];
+    }
+    *nloads = (int64_t)lk.size();
+    return rc;
+}
+
+extern "C" int wisp_core_split(void* h, const int64_t* keys, int64_t n, int64_t* hit_keys, int64_t* hit_slots,
+                               int64_t* nhit, int64_t* miss_keys, int64_t* nmiss) {
+    clear_error();
+    Core& c = *as_core(h);
+    c.step();
+    c.note(keys, n);
+    c.calls += 1;
+    int64_t a = 0, b = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t s = c.lookup(keys[i]);
+        if (s < 0) {
+            miss_keys[b++] = keys[i];
+        } else {
+            hit_keys[a] = keys[i];
+            hit_slots[a++] = s;
+        }
+    }
+    c.hits += a;
+    c.misses += b;
+    *nhit = a;
+    *nmiss = b;
+    return WISP_OK;
+}
+
+extern "C" int wisp_core_acquire(void* h, int64_t key, const int64_t* prot, int64_t nprot, int64_t* slot) {
+    clear_error();
+    std::unordered_set<int64_t> p(prot, prot + nprot);
+    const int64_t s = as_core(h)->acquire(key, p);
+    if (s < 0) return no_slot();
+    *slot = s;
+    return WISP_OK;
+}
+
+// cache_core.py:125-132: slot, or -1 when resident already, not worth it, or nothing evictable
+extern "C" int64_t wisp_core_admit(void* h, int64_t key, const int64_t* prot, int64_t nprot) {
+    Core& c = *as_core(h);
+    if (c.lookup(key) >= 0 || !(c.norm_freq(key) >= c.admit_after)) return -1;
+    std::unordered_set<int64_t> p(prot, prot + nprot);
+    return c.acquire(key, p);
+}
+
+extern "C" int wisp_core_preload(void* h, const int64_t* keys, int64_t n) {
+    clear_error();
+    Core& c = *as_core(h);
+    if (n > c.n_static) return fail_inval("more preload keys than static slots");
+    for (int64_t s = 0; s < n; ++s) {
+        c.slot_key[s] = keys[s];
+        c.key2slot[keys[s]] = s;
+    }
+    return WISP_OK;
+}
+
+// cache_core.py:135-149: new core keeping the hottest resident keys
+extern "C" int wisp_core_resized(void* h, int64_t nslots, void** out, int64_t* keys, int64_t* slots, int64_t* n) {
+    clear_error();
+    Core& c = *as_core(h);
+    if (c.n_static != 0) return fail_inval("resize is not supported with a static region");
+    if (nslots < 1) return fail_inval("nslots must be >= 1");
+    Core* nc = new (std::nothrow) Core(nslots, c.policy, c.decay, 0, c.admit_after);
+    if (!nc) return fail_inval("out of host memory");
+    nc->tick = c.tick;
+    nc->inc = c.inc;
+    nc->freq = c.freq;
+    nc->freq_order = c.freq_order;
+    nc->hits = c.hits;
+    nc->misses = c.misses;
+    nc->evictions = c.evictions;
+    nc->calls = c.calls;
+    const std::vector<double>& rank = c.policy == kLRU ? c.last : c.score;
+    std::vector<int64_t> live;
+    for (int64_t s = 0; s < c.nslots; ++s)
+        if (c.slot_key[s] >= 0) live.push_back(s);
+    std::stable_sort(live.begin(), live.end(), [&](int64_t a, int64_t b) { return -rank[a] < -rank[b]; });
+    const int64_t keep = std::min<int64_t>(nslots, (int64_t)live.size());
+    for (int64_t ns = 0; ns < keep; ++ns) {
+        const int64_t s = live[ns];
+        nc->slot_key[ns] = c.slot_key[s];
+        nc->key2slot[c.slot_key[s]] = ns;
+        nc->last[ns] = c.last[s];
+        nc->score[ns] = c.score[s];
+        keys[ns] = c.slot_key[s];
+        slots[ns] = ns;
+    }
+    nc->free.clear();
+    for (int64_t s = nslots - 1; s >= keep; --s) nc->free.push_back(s);
+    *n = keep;
+    *out = nc;
+    return WISP_OK;
+}
+
+// scalars: [nslots, policy, n_static, tick, hits, misses, evictions, calls, nfree, nresident, nfreq]
+// doubles: [decay, admit_after, inc]
+extern "C" void wisp_core_state(void* h, int64_t* s, double* d) {
+    const Core& c = *as_core(h);
+    const int64_t v[11] = {c.nslots, c.policy,  c.n_static, c.tick, c.hits,
+                           c.misses, c.evictions, c.calls, (int64_t)c.free.size(), (int64_t)c.key2slot.size(),
+                           (int64_t)c.freq.size()};
+    for (int i = 0; i < 11; ++i) s[i] = v[i];
+    d[0] = c.decay;
+    d[1] = c.admit_after;
+    d[2] = c.inc;
+}
+
+// snapshots: slot_key/last/score [nslots], free [nfree] (bottom of the stack first),
+// freq keys/values [nfreq] in insertion order
+extern "C" void wisp_core_arrays(void* h, int64_t* slot_key, double* last, double* score, int64_t* free_list,
+                                 int64_t* freq_keys, double* freq_vals) {
+    const Core& c = *as_core(h);
+    for (int64_t s = 0; s < c.nslots; ++s) {
+        if (slot_key) slot_key[s] = c.slot_key[s];
+        if (last) last[s] = c.last[s];
+        if (score) score[s] = c.score[s];
+    }
+    if (free_list)
+        for (size_t i = 0; i < c.free.size(); ++i) free_list[i] = c.free[i];
+    if (freq_keys || freq_vals)
+        for (size_t i = 0; i < c.freq_order.size(); ++i) {
+            if (freq_keys) freq_keys[i] = c.freq_order[i];
+            if (freq_vals) freq_vals[i] = c.freq.at(c.freq_order[i]);
+        }
+}
+
+// ------------------------------------------------------------------ ExpertCache
+extern "C" int wisp_cache_create(void* core, int64_t slot_bytes, const uint8_t* host, int64_t host_rows,
+                                 int64_t row_bytes, int bits, int64_t n, int64_t group, int decode_on_load,
+                                 int64_t staging_rows, int device, void** out) {
+    clear_error();
+    if (!core || !host || !out) return fail_inval("null core, host or out");
+    if (host_rows < 1 || row_bytes < 1) return fail_inval("empty host store");
+    if (decode_on_load && bits < 16) {
+        if (wisp_expert_nbytes(n, bits, group) != row_bytes) return fail_inval("row_bytes != expert_nbytes(n, bits)");
+        if (slot_bytes != 3 * n * 2) return fail_inval("decode_on_load slots hold 3n bf16 values");
+        if (staging_rows < 1) return fail_inval("staging_rows must be >= 1");
+    } else if (slot_bytes < row_bytes) {
+        return fail_inval("slot_bytes < row_bytes");
+    }
+    if (slot_bytes % 16) return fail_inval("slot_bytes must be a multiple of 16");
+    Cache* c = new (std::nothrow) Cache();
+    if (!c) return fail_inval("out of host memory");
+    c->core = as_core(core);
+    c->device = device;
+    c->nslots = c->core->nslots;
+    c->slot_bytes = slot_bytes;
+    c->host = host;
+    c->host_rows = host_rows;
+    c->row_bytes = row_bytes;
+    c->bits = bits;
+    c->n = n;
+    c->group = group;
+    c->decode_on_load = decode_on_load && bits < 16;
+    c->staging_rows = c->decode_on_load ? staging_rows : 0;
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    hipError_t e = hipSetDevice(device);
+    int rc = e == hipSuccess ? alloc_pool(*c) : hip_fail(e, "hipSetDevice");
+    if (!rc && c->decode_on_load) {
+        e = hipMalloc(reinterpret_cast<void**>(&c->staging), (size_t)(c->staging_rows * row_bytes));
+        if (e != hipSuccess) rc = hip_fail(e, "hipMalloc(staging)");
+    }
+    if (!rc) {
+        e = hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking);  // default priority
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&c->order, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&c->done, hipEventDisableTiming);
+        if (e != hipSuccess) rc = hip_fail(e, "creating the copy stream / events");
+    }
+    (void)hipSetDevice(cur);
+    if (rc) {
+        if (c->done) (void)hipEventDestroy(c->done);
+        if (c->order) (void)hipEventDestroy(c->order);
+        if (c->copy) (void)hipStreamDestroy(c->copy);
+        if (c->staging) (void)hipFree(c->staging);
+        pool_release(c->pool);
+        delete c;
+        return rc;
+    }
+    *out = c;
+    return WISP_OK;
+}
+
+// Frees the cache's share of the pool (views keep it alive) and its core.
+extern "C" void wisp_cache_destroy(void* h) {
+    Cache* c = as_cache(h);
+    if (!c) return;
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->copy);
+    (void)hipEventDestroy(c->done);
+    (void)hipEventDestroy(c->order);
+    (void)hipStreamDestroy(c->copy);
+    if (c->staging) (void)hipFree(c->staging);
+    (void)hipSetDevice(cur);
+    pool_release(c->pool);
+    delete c->core;
+    delete c;
+}
+
+extern "C" void* wisp_cache_core(void* h) { return as_cache(h)->core; }
+extern "C" void* wisp_cache_pool(void* h) { return as_cache(h)->pool->ptr; }
+extern "C" void* wisp_cache_copy_stream(void* h) { return as_cache(h)->copy; }
+
+extern "C" void wisp_cache_counters(void* h, int64_t* bytes_h2d, int64_t* n_loads) {
+    *bytes_h2d = as_cache(h)->bytes_h2d;
+    *n_loads = as_cache(h)->n_loads;
+}
+
+// A DLPack view [nslots, slot_bytes] uint8 of the pool on the ROCm device; the
+// view holds a reference, so the memory outlives the cache while it is used.
+extern "C" void* wisp_cache_pool_dlpack(void* h) {
+    Cache* c = as_cache(h);
+    PoolView* v = new (std::nothrow) PoolView();
+    if (!v) return nullptr;
+    c->pool->refs.fetch_add(1);
+    v->block = c->pool;
+    v->shape[0] = c->nslots;
+    v->shape[1] = c->slot_bytes;
+    v->strides[0] = c->slot_bytes;
+    v->strides[1] = 1;
+    v->m.dl_tensor.data = c->pool->ptr;
+    v->m.dl_tensor.device = DLDevice{10 /* kDLROCM */, c->device};
+    v->m.dl_tensor.ndim = 2;
+    v->m.dl_tensor.dtype = DLDataType{1 /* kDLUInt */, 8, 1};
+    v->m.dl_tensor.shape = v->shape;
+    v->m.dl_tensor.strides = v->strides;
+    v->m.dl_tensor.byte_offset = 0;
+    v->m.manager_ctx = v;
+    v->m.deleter = view_deleter;
+    return &v->m;
+}
+
+// Delete a view that was never handed to a consumer.
+extern "C" void wisp_cache_pool_dlpack_free(void* m) {
+    if (m) view_deleter(static_cast<DLManagedTensor*>(m));
+}
+
+extern "C" int wisp_cache_issue(void* h, const int64_t* keys, const int64_t* slots, int64_t n, void* compute) {
+    clear_error();
+    return issue(*as_cache(h), keys, slots, n, (hipStream_t)compute);
+}
+
+extern "C" int wisp_cache_sync_compute(void* h, void* compute) {
+    clear_error();
+    return sync_compute(*as_cache(h), (hipStream_t)compute);
+}
+
+// cache.py:87-91: ensure residency, issue the misses' copies, order compute after them
+extern "C" int wisp_cache_ensure(void* h, const int64_t* keys, int64_t n, int64_t* slots, void* compute) {
+    clear_error();
+    Cache& c = *as_cache(h);
+    std::vector<int64_t> lk, ls;
+    int rc = core_ensure(*c.core, keys, n, slots, lk, ls);
+    if (rc) return rc;
+    rc = issue(c, lk.data(), ls.data(), (int64_t)lk.size(), (hipStream_t)compute);
+    if (rc) return rc;
+    return sync_compute(c, (hipStream_t)compute);
+}
+
+// graphdec.py:216-231 for one layer: slots = ensure(keys); meta_host = [slots |
+// weights] (pinned, float32 [2k]); meta_dev <- meta_host on the compute stream,
+// ordered after the expert copies. Returns the slots in `slots` (may be NULL).
+extern "C" int wisp_cache_prepare_layer(void* h, const int64_t* keys, const float* weights, int k, float* meta_host,
+                                        float* meta_dev, int64_t* slots, void* compute) {
+    clear_error();
+    if (k < 1 || k > 64 || !keys || !weights || !meta_host || !meta_dev) return fail_inval("bad prepare_layer args");
+    int64_t sl[64];
+    int rc = wisp_cache_ensure(h, keys, k, sl, compute);
+    if (rc) return rc;
+    for (int j = 0; j < k; ++j) {
+        meta_host[j] = (float)sl[j];
+        meta_host[k + j] = weights[j];
+        if (slots) slots[j] = sl[j];
+    }
+    const hipError_t e = hipMemcpyAsync(meta_dev, meta_host, sizeof(float) * 2 * k, hipMemcpyHostToDevice,
+                                        (hipStream_t)compute);
+    return e == hipSuccess ? WISP_OK : hip_fail(e, "hipMemcpyAsync(meta)");
+}
+
+// cache.py:144-158: keep the hottest experts in a pool of `nslots` rows. The
+// device is synchronised, the old pool released before the new one is
+// allocated, and the kept experts re-copied from the host store.
+extern "C" int wisp_cache_resize(void* h, int64_t nslots) {
+    clear_error();
+    Cache& c = *as_cache(h);
+    if (c.decode_on_load) return fail_inval("resize is not supported with decode_on_load");
+    if (nslots == c.nslots) return WISP_OK;
+    std::vector<int64_t> keys(std::max<int64_t>(nslots, 1)), slots(keys.size());
+    int64_t nk = 0;
+    void* nc = nullptr;
+    int rc = wisp_core_resized(c.core, nslots, &nc, keys.data(), slots.data(), &nk);
+    if (rc) return rc;
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    (void)hipSetDevice(c.device);
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        wisp_core_destroy(nc);
+        (void)hipSetDevice(cur);
+        return hip_fail(e, "hipDeviceSynchronize");
+    }
+    delete c.core;
+    c.core = as_core(nc);
+    pool_release(c.pool);
+    c.pool = nullptr;
+    c.pending = false;
+    c.nslots = nslots;
+    rc = alloc_pool(c);
+    if (!rc) rc = issue(c, keys.data(), slots.data(), nk, c.copy);
+    if (!rc) {
+        e = hipStreamSynchronize(c.copy);
+        if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize(copy)");
+    }
+    (void)hipSetDevice(cur);
+    return rc;
+}

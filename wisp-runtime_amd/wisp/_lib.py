@@ -19,7 +19,7 @@ ABI_VERSION = 1
 
 WISP_OK, WISP_EINVAL, WISP_EALIGN = 0, -1, -2
 
-_i64, _i32, _vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+_i64, _i32, _vp, _f64 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_double
 
 # name -> (restype, argtypes); mirrors include/wisp_hip.h
 SIGNATURES = {
@@ -36,6 +36,33 @@ SIGNATURES = {
     "wisp_moe_down": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp]),
     "wisp_moe_decode": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp, _vp]),
     "wisp_rope_decode": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "wisp_core_create": (_i32, [_i64, _i32, _f64, _i64, _f64, _vp]),
+    "wisp_core_destroy": (None, [_vp]),
+    "wisp_core_step": (None, [_vp]),
+    "wisp_core_note": (None, [_vp, _vp, _i64]),
+    "wisp_core_norm_freq": (_f64, [_vp, _i64]),
+    "wisp_core_lookup": (_i64, [_vp, _i64]),
+    "wisp_core_ensure": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _vp]),
+    "wisp_core_split": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "wisp_core_acquire": (_i32, [_vp, _i64, _vp, _i64, _vp]),
+    "wisp_core_admit": (_i64, [_vp, _i64, _vp, _i64]),
+    "wisp_core_preload": (_i32, [_vp, _vp, _i64]),
+    "wisp_core_resized": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp]),
+    "wisp_core_state": (None, [_vp, _vp, _vp]),
+    "wisp_core_arrays": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "wisp_cache_create": (_i32, [_vp, _i64, _vp, _i64, _i64, _i32, _i64, _i64, _i32, _i64, _i32, _vp]),
+    "wisp_cache_destroy": (None, [_vp]),
+    "wisp_cache_core": (_vp, [_vp]),
+    "wisp_cache_pool": (_vp, [_vp]),
+    "wisp_cache_copy_stream": (_vp, [_vp]),
+    "wisp_cache_counters": (None, [_vp, _vp, _vp]),
+    "wisp_cache_pool_dlpack": (_vp, [_vp]),
+    "wisp_cache_pool_dlpack_free": (None, [_vp]),
+    "wisp_cache_issue": (_i32, [_vp, _vp, _vp, _i64, _vp]),
+    "wisp_cache_sync_compute": (_i32, [_vp, _vp]),
+    "wisp_cache_ensure": (_i32, [_vp, _vp, _i64, _vp, _vp]),
+    "wisp_cache_prepare_layer": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
+    "wisp_cache_resize": (_i32, [_vp, _i64]),
     "wisp_set_tuning": (_i32, [_i32, _i32, _i32]),
     "wisp_act_read": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp]),
 }

@@ -1,0 +1,231 @@
+"""GPU expert cache: one hipMalloc slot pool, filled from the pinned host store by
+hipMemcpyAsync on a side stream. Same interface as the reference's wisp/cache.py
+(ExpertCache, cache.py:9-162).
+
+The pool, the side stream, the copy ordering (an event recorded on the compute stream
+before the copies, the compute stream waiting on the copies' event afterwards) and the
+bookkeeping core are native (libwisp_hip.so); `gpu` is a torch view of the pool
+(DLPack), so the decode kernels and graph captures take it like the reference's tensor.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+import torch.utils.dlpack
+
+from . import _lib
+from .cache_core import _POLICIES, CacheCore
+from .quant import dequant, dequant_rows
+
+
+def _i64(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(list(a), dtype=np.int64).reshape(-1))
+
+
+def _p(a: np.ndarray) -> ctypes.c_void_p:
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+_PyCapsule_New = ctypes.pythonapi.PyCapsule_New
+_PyCapsule_New.restype = ctypes.py_object
+_PyCapsule_New.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p]
+
+
+class ExpertCache:
+    def __init__(
+        self,
+        store,
+        nslots,
+        device="cuda",
+        policy="lru",
+        decay=0.9995,
+        n_static=0,
+        admit_after=2.0,
+        preload_keys=None,
+        cpu_store=None,
+        decode_on_load=False,
+        staging_rows=8,
+    ):
+        assert policy in _POLICIES, policy
+        self.store, self.device = store, torch.device(device)
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        # decode_on_load: experts cross PCIe quantized, are dequantized once on arrival and
+        # kept as bf16 (cache.py:25-27)
+        self.decode_on_load = bool(decode_on_load) and store.bits < 16
+        self.cpu_store = cpu_store
+        self.nslots = nslots
+        self.slot_bytes = 3 * store.n * 2 if self.decode_on_load else store.nbytes
+        host = store.host
+        assert host.dtype == torch.uint8 and host.dim() == 2 and host.is_contiguous() and not host.is_cuda
+        core = CacheCore(nslots, policy, decay, n_static, admit_after)
+        h = ctypes.c_void_p()
+        _lib.check(
+            _lib.lib().wisp_cache_create(
+                core._h, self.slot_bytes, ctypes.c_void_p(host.data_ptr()), host.shape[0], host.shape[1],
+                store.bits, store.n, store.group, int(self.decode_on_load), staging_rows, self.device.index,
+                ctypes.byref(h),
+            ),
+            "ExpertCache",
+        )
+        core._release()  # the native cache owns the core now
+        self._h = h
+        self._host = host  # keep the store rows alive as long as the cache
+        self._view()
+        self.copy_stream = torch.cuda.ExternalStream(_lib.lib().wisp_cache_copy_stream(self._h), device=self.device)
+        if n_static:
+            assert preload_keys is not None and len(preload_keys) <= n_static
+            self._issue(self.core.preload(list(preload_keys)))
+            self.sync_all()
+
+    def _view(self):
+        m = _lib.lib().wisp_cache_pool_dlpack(self._h)
+        if not m:
+            raise RuntimeError("ExpertCache: could not create the pool view")
+        try:
+            cap = _PyCapsule_New(m, b"dltensor", None)
+            self.gpu = torch.utils.dlpack.from_dlpack(cap)
+        except Exception:
+            _lib.lib().wisp_cache_pool_dlpack_free(m)
+            raise
+
+    @property
+    def core(self) -> CacheCore:
+        """The bookkeeping core (owned by the native cache)."""
+        return CacheCore._wrap(_lib.lib().wisp_cache_core(self._h), owned=False)
+
+    @property
+    def bytes_h2d(self) -> int:
+        b, n = ctypes.c_int64(), ctypes.c_int64()
+        _lib.lib().wisp_cache_counters(self._h, ctypes.byref(b), ctypes.byref(n))
+        return b.value
+
+    @property
+    def n_loads(self) -> int:
+        b, n = ctypes.c_int64(), ctypes.c_int64()
+        _lib.lib().wisp_cache_counters(self._h, ctypes.byref(b), ctypes.byref(n))
+        return n.value
+
+    def _stream(self):
+        return ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+
+    # ---- copies ---------------------------------------------------------
+    def _issue(self, pairs):
+        """Async host->GPU copies of [(key, slot)] on the side stream, ordered after queued compute."""
+        if not pairs:
+            return
+        k = _i64(p[0] for p in pairs)
+        s = _i64(p[1] for p in pairs)
+        _lib.check(_lib.lib().wisp_cache_issue(self._h, _p(k), _p(s), k.size, self._stream()), "ExpertCache._issue")
+
+    def sync_compute(self):
+        """Make the current compute stream wait for all issued copies."""
+        _lib.check(_lib.lib().wisp_cache_sync_compute(self._h, self._stream()), "sync_compute")
+
+    def sync_all(self):
+        torch.cuda.synchronize(self.device)
+
+    # ---- policies -------------------------------------------------------
+    def ensure(self, keys):
+        k = _i64(keys)
+        slots = np.empty(max(k.size, 1), np.int64)
+        rc = _lib.lib().wisp_cache_ensure(self._h, _p(k), k.size, _p(slots), self._stream())
+        if rc != 0:
+            raise RuntimeError(_lib.lib().wisp_last_error().decode())
+        return [int(v) for v in slots[: k.size]]
+
+    def prepare_layer(self, keys, weights, meta_host: torch.Tensor, meta_dev: torch.Tensor):
+        """One layer's host step of the graph decoder (graphdec.py:216-231) in one native call:
+        ensure `keys`, write [slots | weights] into meta_host (pinned float32 [2k]) and copy it
+        to meta_dev on the current stream. Returns the slots."""
+        k = _i64(keys)
+        w = np.ascontiguousarray(np.asarray(weights, dtype=np.float32).reshape(-1))
+        assert w.size == k.size and meta_host.numel() >= 2 * k.size and meta_dev.numel() >= 2 * k.size
+        slots = np.empty(max(k.size, 1), np.int64)
+        rc = _lib.lib().wisp_cache_prepare_layer(
+            self._h, _p(k), _p(w), k.size, ctypes.c_void_p(meta_host.data_ptr()),
+            ctypes.c_void_p(meta_dev.data_ptr()), _p(slots), self._stream(),
+        )
+        if rc != 0:
+            raise RuntimeError(_lib.lib().wisp_last_error().decode())
+        return [int(v) for v in slots[: k.size]]
+
+    def split(self, keys):
+        return self.core.split(keys)
+
+    def admit_async(self, miss_keys, protected_slots):
+        core, prot, pairs = self.core, list(protected_slots), []
+        for k in miss_keys:
+            s = core.admit(k, prot)
+            if s is not None:
+                prot.append(s)
+                pairs.append((k, s))
+        self._issue(pairs)  # not waited on here; the next ensure()/sync_compute() will
+        return len(pairs)
+
+    def prefetch(self, keys, protected_slots):
+        core, prot, pairs = self.core, list(protected_slots), []
+        for k in keys:
+            if core.lookup(k) is not None:
+                continue
+            try:
+                s = core.acquire(k, prot)
+            except RuntimeError:
+                break
+            prot.append(s)
+            pairs.append((k, s))
+        self._issue(pairs)
+        return len(pairs)
+
+    # ---- weights --------------------------------------------------------
+    def weights_batched(self, idx):
+        """idx: LongTensor of slots on the GPU -> [k, 3, n] bf16 (gather + dequant in one kernel)."""
+        st = self.store
+        if st.bits == 16 or self.decode_on_load:
+            return self.gpu.index_select(0, idx).view(torch.bfloat16).view(len(idx), 3, st.n)
+        return dequant_rows(self.gpu, idx, st.n, st.bits, st.group)
+
+    def weights(self, slots):
+        """List of [3, n] bf16 tensors on the GPU for the given slots."""
+        st = self.store
+        if st.bits == 16 or self.decode_on_load:
+            return [self.gpu[s].view(torch.bfloat16).view(3, st.n) for s in slots]
+        idx = torch.as_tensor(slots, device=self.device)
+        return list(dequant_rows(self.gpu, idx, st.n, st.bits, st.group).unbind(0))
+
+    def cpu_weights(self, key):
+        """[3, n] bf16 on the host for store row `key` (dequantized by the GPU kernel)."""
+        st = self.cpu_store if self.cpu_store is not None else self.store
+        b = st.host[key]
+        if st.bits == 16:
+            return b.view(torch.bfloat16).view(3, st.n)
+        return dequant(b[None].to(self.device), st.n, st.bits, st.group)[0].cpu()
+
+    def resize(self, nslots):
+        """Grow/shrink the slot pool in place, keeping the hottest experts. The old pool is
+        released before the new one is allocated (views of it still held elsewhere keep it
+        alive until they are dropped); the kept experts are re-copied from the host store."""
+        assert not self.decode_on_load
+        if nslots == self.nslots:
+            return
+        torch.cuda.synchronize(self.device)
+        self.gpu = None
+        _lib.check(_lib.lib().wisp_cache_resize(self._h, nslots), "ExpertCache.resize")
+        self.nslots = nslots
+        self._view()
+
+    def free(self):
+        """Release the pool (views still held elsewhere keep their memory until dropped)."""
+        if getattr(self, "_h", None):
+            self.gpu = None
+            _lib.lib().wisp_cache_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
