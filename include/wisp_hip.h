@@ -116,6 +116,22 @@ int wisp_moe_decode(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, con
 int wisp_rope_decode(const void* q, int64_t q_head_stride, const void* k, int64_t k_head_stride, const void* cos,
                      const void* sin, int hq, int hk, int d, int dtype, void* qo, void* ko, void* stream);
 
+/* Workspace bytes of wisp_attn_decode: hq * ceil(tmax/64) * (2 + d) * 4. */
+int64_t wisp_attn_ws_bytes(int hq, int d, int tmax);
+
+/* Grouped-query attention of one decode token over a static KV cache:
+ * o[h] = sum_{t <= *pos} softmax_t(scale * q[h].k[h/G][t]) v[h/G][t], G = hq/hk.
+ * q: bf16 [hq, d] contiguous; kc, vc: bf16, KV head j's [tmax, d] rows start
+ * at j*kv_head_stride elements; pos: device int64 (read when the kernels run,
+ * so a captured graph follows it); ws: wisp_attn_ws_bytes; out: bf16 [hq, d].
+ * fp32 scores (exact bf16 products), fp32 softmax and sum, bf16 store.
+ * d in {64, 128, 256}, G in {1, 2, 4, 8} (and 16 at d = 128). Two launches.
+ * Replaces the masked grouped scaled_dot_product_attention of
+ * wisp/graphdec.py:171-174. */
+int wisp_attn_decode(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t kv_head_stride,
+                     const int64_t* pos, int hq, int hk, int d, int tmax, float scale, void* ws, uint16_t* out,
+                     void* stream);
+
 /* ---------------------------------------------------------------------------
  * Expert cache bookkeeping (host only, no device calls). Keys are
  * layer*n_experts + expert; slots [0, n_static) are the static region.

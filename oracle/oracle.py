@@ -203,3 +203,20 @@ def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
     if lib().wo_rope(_p(x), nh, d, _p(c), _p(s), _p(out)) != 0:
         raise ValueError("bad arguments to rope")
     return out
+
+
+# ---------------------------------------------------------------- decode attention
+def attn_decode(q: np.ndarray, k: np.ndarray, v: np.ndarray, pos: int, scale: float) -> np.ndarray:
+    """graphdec.py:171-174 in binary64: q [Hq, D], k/v [Hk, T, D] (float values), positions
+    0..pos attend; query head h uses KV head h // (Hq/Hk). Returns float64 [Hq, D]."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    Hq, Hk = q.shape[0], k.shape[0]
+    G = Hq // Hk
+    out = np.empty_like(q)
+    for h in range(Hq):
+        s = (k[h // G, : pos + 1] @ q[h]) * scale
+        w = np.exp(s - s.max())
+        out[h] = (w / w.sum()) @ v[h // G, : pos + 1]
+    return out

@@ -352,3 +352,56 @@ def test_rope_decode_reference_criterion():
     for got, ref in ((qo.cpu(), qr), (ko.cpu(), kr)):
         assert got.shape == ref.shape
         assert (got.float() - ref.float()).abs().max() < 3e-2 * ref.float().abs().max()
+
+
+# ---------------------------------------------------------------- decode attention (graphdec.py:171-174)
+def _bf16_np(a):
+    return O.bf16_bits_to_f32(O.f32_to_bf16_bits(np.asarray(a, np.float32))).reshape(np.shape(a))
+
+
+def _attn_case(Hq, Hk, D, T, seed):
+    rng = np.random.default_rng(seed)
+    q = _bf16_np(rng.standard_normal((Hq, D)))
+    k = _bf16_np(rng.standard_normal((Hk, T, D)))
+    v = _bf16_np(rng.standard_normal((Hk, T, D)))
+    tb = lambda a: torch.from_numpy(a).to(torch.bfloat16).to(DEV)  # noqa: E731 (exact: values are bf16)
+    return q, k, v, tb(q).view(1, Hq, 1, D), tb(k)[None].contiguous(), tb(v)[None].contiguous()
+
+
+@pytest.mark.parametrize("Hq,Hk,D,T", [(32, 4, 128, 256), (8, 8, 64, 130), (4, 1, 256, 70), (32, 2, 128, 64),
+                                       (16, 4, 128, 4096)])
+def test_attn_decode_matches_oracle(Hq, Hk, D, T):
+    q, k, v, tq, tk, tv = _attn_case(Hq, Hk, D, T, seed=Hq + D + T)
+    scale = D ** -0.5
+    for pos in sorted({0, 1, 63, 64, min(100, T - 1), T - 1}):
+        if pos >= T:
+            continue
+        p = torch.tensor([pos], dtype=torch.int64, device=DEV)
+        out = kernels.attn_decode(tq, tk, tv, p, scale)
+        torch.cuda.synchronize()
+        ref = O.attn_decode(q, k, v, pos, scale)
+        r = _bf16_np(ref)
+        got = out.float().cpu().numpy().reshape(Hq, D)
+        err = np.linalg.norm(got - r) / np.linalg.norm(r)
+        assert err <= 1e-3, (pos, err)
+        assert np.max(np.abs(got - ref)) <= 1e-2 * np.max(np.abs(ref)), pos
+
+
+def test_attn_decode_graph_follows_device_position():
+    Hq, Hk, D, T = 32, 4, 128, 512
+    q, k, v, tq, tk, tv = _attn_case(Hq, Hk, D, T, seed=3)
+    p = torch.zeros(1, dtype=torch.int64, device=DEV)
+    kernels.attn_decode(tq, tk, tv, p, 0.125)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = kernels.attn_decode(tq, tk, tv, p, 0.125)
+    for pos in (5, 300, 64, 511):
+        p.fill_(pos)
+        g.replay()
+        eager = kernels.attn_decode(tq, tk, tv, p, 0.125)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), pos
+        r = _bf16_np(O.attn_decode(q, k, v, pos, 0.125))
+        got = out.float().cpu().numpy().reshape(Hq, D)
+        assert np.linalg.norm(got - r) / np.linalg.norm(r) <= 1e-3, pos

@@ -287,3 +287,40 @@ def test_rope_rotation_properties():
     # a plausible slip (sign on the wrong half) is caught by the textbook form
     bad = x.astype(np.float64) * c - rh * s
     assert np.max(np.abs(out - bad)) > 1e-2
+
+
+# ---------------------------------------------------------------- decode attention (graphdec.py:171-174)
+def test_attn_oracle_special_cases():
+    rng = np.random.default_rng(8)
+    Hq, Hk, T, D = 8, 2, 40, 16
+    q = rng.standard_normal((Hq, D))
+    k = rng.standard_normal((Hk, T, D))
+    v = rng.standard_normal((Hk, T, D))
+    # pos 0: the only position gets all the weight
+    out = O.attn_decode(q, k, v, 0, 0.25)
+    assert np.array_equal(out, v[np.arange(Hq) // 4, 0])
+    # equal keys: uniform weights, the mean of the attended values
+    ke = np.repeat(k[:, :1], T, axis=1)
+    out = O.attn_decode(q, ke, v, 17, 0.25)
+    assert np.allclose(out, v[np.arange(Hq) // 4, :18].mean(axis=1), rtol=1e-12, atol=1e-12)
+
+
+def test_attn_oracle_matches_torch_sdpa_repeat_kv():
+    """The library routine (scaled_dot_product_attention with the KV heads repeated, as
+    tests/test_fastattn.py:26-35 of the reference states the grouping), masked to t <= pos."""
+    rng = np.random.default_rng(9)
+    Hq, Hk, T, D, pos, scale = 32, 4, 77, 128, 50, 128 ** -0.5
+    q = rng.standard_normal((Hq, D)).astype(np.float32)
+    k = rng.standard_normal((Hk, T, D)).astype(np.float32)
+    v = rng.standard_normal((Hk, T, D)).astype(np.float32)
+    out = O.attn_decode(q, k, v, pos, scale)
+    tq = torch.from_numpy(q).view(1, Hq, 1, D).double()
+    tk = torch.from_numpy(k).repeat_interleave(Hq // Hk, dim=0)[None].double()
+    tv = torch.from_numpy(v).repeat_interleave(Hq // Hk, dim=0)[None].double()
+    mask = (torch.arange(T) <= pos).view(1, 1, 1, T)
+    ref = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, attn_mask=mask, scale=scale)
+    assert np.allclose(out, ref.view(Hq, D).numpy(), rtol=1e-10, atol=1e-10)
+    # a head-mapping slip (h % Hk instead of h // G) would not match
+    bad = np.stack([O.attn_decode(q[h : h + 1], k[h % Hk : h % Hk + 1], v[h % Hk : h % Hk + 1], pos, scale)[0]
+                    for h in range(Hq)])
+    assert not np.allclose(bad, out, atol=1e-3)

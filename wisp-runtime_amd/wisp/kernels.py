@@ -149,3 +149,30 @@ def rope_decode(q, k, cos, sin):
         "rope_decode",
     )
     return qo, ko
+
+
+def attn_decode(q, kc, vc, pos, scale):
+    """Masked grouped attention of one decode token over a static KV cache (the
+    scaled_dot_product_attention of graphdec.py:171-174), as two HIP launches.
+    q: [1, Hq, 1, D] or [Hq, D] bf16; kc, vc: [1, Hk, Tmax, D] bf16 (contiguous rows);
+    pos: int64 device tensor (one element, read at run time; positions <= pos attend).
+    Returns [1, Hq, 1, D] bf16."""
+    Hq, D = q.shape[-3] if q.dim() == 4 else q.shape[0], q.shape[-1]
+    Hk, tmax = kc.shape[1], kc.shape[2]
+    dev = _lib.require_gpu(q, kc, vc, pos, what="attn_decode")
+    if q.dtype != torch.bfloat16 or kc.dtype != torch.bfloat16 or vc.dtype != torch.bfloat16:
+        raise TypeError("attn_decode takes bfloat16 q, k and v")
+    assert kc.shape == vc.shape and kc.stride(-1) == 1 and kc.stride(-2) == D and vc.stride() == kc.stride()
+    assert pos.dtype == torch.int64 and pos.numel() >= 1
+    q = q.reshape(Hq, D).contiguous()
+    L = _lib.lib()
+    ws = torch.empty(L.wisp_attn_ws_bytes(Hq, D, tmax), dtype=torch.uint8, device=dev)
+    out = torch.empty((1, Hq, 1, D), dtype=torch.bfloat16, device=dev)
+    _lib.check(
+        L.wisp_attn_decode(
+            _lib.ptr(q), _lib.ptr(kc), _lib.ptr(vc), kc.stride(1), _lib.ptr(pos), Hq, Hk, D, tmax, float(scale),
+            _lib.ptr(ws), _lib.ptr(out), _lib.stream(dev),
+        ),
+        "attn_decode",
+    )
+    return out
