@@ -301,6 +301,104 @@ def measure(W: Layers, steps: int, warmup: int):
     return dict(steps=n, warmup=warm_reps * W.layers, layer=t_two, gu=t_gu, dn=t_dn)
 
 
+# ----------------------------------------------------------------------------- C4: full decode step
+def zipf_layer_experts(rng, E: int, k: int, s: float, perm):
+    """k distinct experts of one layer: Zipf(s) over ranks 1..E (Gumbel-top-k on -s*log r),
+    mapped to expert ids through the layer's permutation."""
+    import numpy as np
+
+    g = rng.gumbel(size=E) - s * np.log(np.arange(1, E + 1))
+    return [int(perm[r]) for r in np.argsort(-g)[:k]]
+
+
+def run_c4(a) -> dict:
+    """Config 4: a 48-layer Qwen3-30B-A3B-shaped decode step (random-init weights), 4-bit experts in
+    a pinned host store, a 512-slot LRU expert cache paged over PCIe, graph replay between the
+    per-layer paging points, static bf16 KV of length 4096. Routing is Zipf(1.1) per layer."""
+    import time
+
+    import numpy as np
+    from transformers import Qwen3MoeConfig
+
+    from wisp.cache import ExpertCache
+    from wisp.graphdec import GraphDecoder
+    from wisp.model import random_skeleton
+    from wisp.moe import Runtime
+    from wisp.store import ExpertStore
+
+    dev = torch.device("cuda:0")
+    Lr, E_, k, tmax = a.c4_layers, 128, 8, 4096
+    cfg = Qwen3MoeConfig(vocab_size=151936, hidden_size=H, intermediate_size=6144, moe_intermediate_size=I,
+                         num_hidden_layers=Lr, num_attention_heads=32, num_key_value_heads=4, head_dim=128,
+                         num_experts=E_, num_experts_per_tok=k, norm_topk_prob=True, rms_norm_eps=1e-6,
+                         rope_theta=1e6, max_position_embeddings=40960, decoder_sparse_step=1, mlp_only_layers=[])
+    t0 = time.time()
+    store = ExpertStore(Lr, E_, H * I, a.bits, G)
+    gen = torch.Generator(device=dev).manual_seed(2)
+    for key in range(Lr * E_):
+        w3 = torch.randn((3, H * I), generator=gen, device=dev) * 0.02
+        store.host[key].copy_(quantize(w3, a.bits, G), non_blocking=False)
+        if key % 1024 == 1023:
+            print(f"[bench] c4 store: {key + 1} experts", file=sys.stderr, flush=True)
+    print(f"[bench] c4 store {store.total_gib:.1f} GiB pinned={store.pinned} in {time.time() - t0:.0f}s",
+          file=sys.stderr, flush=True)
+    rt = Runtime(store, fused=2)
+    rt.cache = ExpertCache(store, a.c4_slots)
+    model = random_skeleton(cfg, rt, device=dev)
+    rng = np.random.default_rng(4)
+    perms = [rng.permutation(E_) for _ in range(Lr)]
+
+    class ZipfDecoder(GraphDecoder):
+        """The routing weights come from the model's router; the expert ids are drawn Zipf(1.1)."""
+
+        def _prepare(self, i, row):
+            row = list(row)
+            row[:k] = zipf_layer_experts(rng, E_, k, 1.1, perms[i])
+            super()._prepare(i, row)
+
+    dec = ZipfDecoder(model, rt, tmax=tmax)
+    pos0 = tmax - a.c4_tokens - a.c4_warmup - 8
+    with torch.no_grad():  # a filled context: random K/V up to pos0
+        for i in range(Lr):
+            dec.kc[i][:, :, :pos0].normal_()
+            dec.vc[i][:, :, :pos0].normal_()
+        dec.pos = pos0
+        tok = torch.zeros(1, dtype=torch.long, device=dev)
+        for w in range(a.c4_warmup):
+            tok = dec.next(tok).argmax(-1)
+            print(f"[bench] c4 warm-up token {w}", file=sys.stderr, flush=True)
+        torch.cuda.synchronize()
+        st0 = dict(rt.cache.core.stats)
+        b0 = rt.cache.bytes_h2d
+        t1 = time.perf_counter()
+        for _ in range(a.c4_tokens):
+            tok = dec.next(tok).argmax(-1)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t1
+    st1 = rt.cache.core.stats
+    hits, misses = st1["hits"] - st0["hits"], st1["misses"] - st0["misses"]
+    tps = a.c4_tokens / dt
+    return {
+        "metric": "decode tok/s, C4 (48-layer Qwen3-30B-A3B shape, 512-slot LRU, Zipf(1.1) routing, KV 4096)",
+        "value": round(tps, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.c4_tokens,
+        "warmup": a.c4_warmup,
+        "ms_per_step": round(1e3 * dt / a.c4_tokens, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"C4: {Lr} layers, {E_} experts {a.bits}-bit, top-{k}, {a.c4_slots} slots, "
+                               f"context {pos0}..{pos0 + a.c4_warmup + a.c4_tokens} of {tmax}, random-init weights",
+                   "hit_rate": round(hits / max(1, hits + misses), 4),
+                   "h2d_MB_per_token": round((rt.cache.bytes_h2d - b0) / a.c4_tokens / 1e6, 2),
+                   "store_GiB": round(store.total_gib, 2)},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -315,6 +413,12 @@ def main():
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write the PMC traffic summary under profiles/ from two counter_collection.csv files")
     ap.add_argument("--pmc-command", default="", help="command text recorded in the PMC summary")
+    ap.add_argument("--workload", default="c2", choices=["c2", "c4"], help="c2: one MoE layer (default); "
+                    "c4: full decode steps through the graph decoder and the expert cache")
+    ap.add_argument("--c4-layers", type=int, default=48)
+    ap.add_argument("--c4-slots", type=int, default=512)
+    ap.add_argument("--c4-tokens", type=int, default=32)
+    ap.add_argument("--c4-warmup", type=int, default=8)
     ap.add_argument("--summarize-trace", nargs=3, metavar=("TRACE_CSV", "STATS_CSV", "BENCH_JSON"),
                     help="write the kernel-trace summary under profiles/ from a rocprofv3 run of bench.py")
     a = ap.parse_args()
@@ -349,6 +453,9 @@ def main():
         _lib.check(_lib.lib().wisp_set_tuning(gr, gw, dn), "set_tuning")
     if a.pmc_pass:
         pmc_pass(a.bits)
+        return
+    if a.workload == "c4":
+        print(json.dumps(run_c4(a)))
         return
 
     bits = a.bits
