@@ -399,6 +399,90 @@ def run_c4(a) -> dict:
     }
 
 
+# ----------------------------------------------------------------------------- C5: grouped prefill
+def run_c5(a) -> dict:
+    """Config 5: chunked-prefill grouped dequant-GEMM. T tokens, each routed top-8 over 128
+    experts by Zipf(1.1); per-expert token groups run the 4-bit dequant-into-LDS + bf16 MFMA
+    kernels (gate_up+SiLU, down, combine). Experts are resident in slot pools rotated past
+    the Infinity Cache; the three launches per chunk are captured in a graph and timed with
+    HIP events."""
+    import numpy as np
+
+    from wisp import kernels as K
+
+    dev = torch.device("cuda:0")
+    W = Layers(dev, a.bits, a.c5_pools)  # 128 experts per pool, quantized on the GPU
+    nb, P_ = W.nb, a.c5_pools
+    peak_tflops = 2500.0
+    out_rows = []
+    rng = np.random.default_rng(7)
+    perm = rng.permutation(E)
+    L = _lib.lib()
+    for T in [int(t) for t in a.c5_tokens.split(",")]:
+        sel = np.array([zipf_layer_experts(rng, E, K_TOP, 1.1, perm) for _ in range(T)], np.int64)
+        w = torch.rand((T, K_TOP), generator=torch.Generator().manual_seed(T)).to(torch.bfloat16).float()
+        x = torch.randn((T, H), generator=torch.Generator(device=dev).manual_seed(T), device=dev).to(torch.bfloat16)
+        order, tok, back, uniq, first, count = K._prefill_plan(sel, list(range(E)), K_TOP)
+        Pn = int(order.size)
+        plans = []
+        for l in range(P_):
+            groups = np.stack([uniq + l * E, first, count], 1).astype(np.int32)
+            ints = torch.from_numpy(np.concatenate([groups.reshape(-1), tok, back.reshape(-1)])).to(dev)
+            plans.append(ints)
+        wp = w.reshape(-1)[torch.from_numpy(order)].to(dev).contiguous()
+        ws = torch.empty(L.wisp_prefill_ws_bytes(Pn, H, I), dtype=torch.uint8, device=dev)
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+        ng = len(uniq)
+
+        def launch(l, st):
+            ints = plans[l]
+            _lib.check(L.wisp_moe_prefill(
+                _lib.ptr(W.pool), nb, W.pool.shape[0], _lib.ptr(ints), ng, int(count.max()), _lib.ptr(ints[ng * 3:]),
+                _lib.ptr(wp),
+                _lib.ptr(ints[ng * 3 + Pn:]), Pn, _lib.ptr(x), T, K_TOP, H, I, a.bits, G, _lib.ptr(ws),
+                _lib.ptr(out), None, st), "moe_prefill")
+
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(W.stream):
+            st = _lib.stream(dev)
+            for l in range(P_):
+                launch(l, st)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=W.stream):
+                st = _lib.stream(dev)
+                for l in range(P_):
+                    launch(l, st)
+        torch.cuda.synchronize()
+        for _ in range(2):
+            g.replay()
+        reps = max(1, a.c5_reps)
+        t = W.timed(g, reps, False) / (reps * P_)
+        flops = T * K_TOP * 6 * H * I
+        byts = ng * nb + 2 * T * H + 2 * 2 * Pn * I + 2 * 4 * Pn * H + 2 * T * H
+        out_rows.append({"T": T, "experts_touched": ng, "us": round(t * 1e6, 2),
+                         "TFLOP/s": round(flops / t / 1e12, 2), "mfma_util": round(flops / t / 1e12 / peak_tflops, 4),
+                         "GB/s": round(byts / t / 1e9, 1), "hbm_frac": round(byts / t / 1e9 / PEAK_HBM_GBS, 4),
+                         "bytes": byts, "flops": flops})
+        print(f"[bench] c5 T={T}: {out_rows[-1]}", file=sys.stderr, flush=True)
+    last = out_rows[-1]
+    return {
+        "metric": "grouped prefill TFLOP/s, C5 (4-bit experts, top-8 of 128, Zipf(1.1) routing)",
+        "value": last["TFLOP/s"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": a.c5_reps,
+        "warmup": 2,
+        "ms_per_step": round(last["us"] / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"C5: T in {a.c5_tokens}, H={H} I={I}, {a.c5_pools} expert pools rotated",
+                   "per_T": out_rows},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -413,8 +497,11 @@ def main():
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write the PMC traffic summary under profiles/ from two counter_collection.csv files")
     ap.add_argument("--pmc-command", default="", help="command text recorded in the PMC summary")
-    ap.add_argument("--workload", default="c2", choices=["c2", "c4"], help="c2: one MoE layer (default); "
-                    "c4: full decode steps through the graph decoder and the expert cache")
+    ap.add_argument("--workload", default="c2", choices=["c2", "c4", "c5"], help="c2: one MoE layer (default); "
+                    "c4: full decode steps through the graph decoder and the expert cache; c5: grouped prefill")
+    ap.add_argument("--c5-tokens", default="64,256,512")
+    ap.add_argument("--c5-pools", type=int, default=8)
+    ap.add_argument("--c5-reps", type=int, default=10)
     ap.add_argument("--c4-layers", type=int, default=48)
     ap.add_argument("--c4-slots", type=int, default=512)
     ap.add_argument("--c4-tokens", type=int, default=32)
@@ -456,6 +543,9 @@ def main():
         return
     if a.workload == "c4":
         print(json.dumps(run_c4(a)))
+        return
+    if a.workload == "c5":
+        print(json.dumps(run_c5(a)))
         return
 
     bits = a.bits

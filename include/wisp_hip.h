@@ -132,6 +132,31 @@ int wisp_attn_decode(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, 
                      const int64_t* pos, int hq, int hk, int d, int tmax, float scale, void* ws, uint16_t* out,
                      void* stream);
 
+/* Workspace bytes of wisp_moe_prefill: act bf16 [pairs, I] (rounded up to 256)
+ * followed by y fp32 [pairs, H]. */
+int64_t wisp_prefill_ws_bytes(int64_t pairs, int64_t H, int64_t I);
+
+/* Grouped MoE prefill: for the (token, expert) pairs of a chunk of T tokens,
+ * sorted by expert, every routed expert's token group runs gate/up + SiLU*up
+ * and down as bf16 MFMA GEMMs on weight tiles dequantized (bit-exactly) into
+ * LDS from slot-pool rows; y = w * down(...) per pair in fp32; per token
+ * s[t] = sum of its pairs' y in ascending expert id (fp32).
+ * groups: device int32 [ngroups][3] = (slot, first pair, pair count);
+ * max_group: the largest pair count (sets the launch shape; results do not
+ * depend on it);
+ * tok/w: device int32 / float [pairs] token and routing weight of each pair;
+ * back: device int32 [T][k], the pair of token t's j-th expert (ascending id),
+ * -1 if that expert is not in this call; x: bf16 [T, H]; ws:
+ * wisp_prefill_ws_bytes(pairs, H, I), 256-byte aligned. out: bf16 [T, H] =
+ * bf16(s), or, when acc (fp32 [T, H]) is not NULL, acc += s and out unused.
+ * group must be 128; H, I multiples of 128; bits 4/3/2. An invalid slot id
+ * makes its pairs' outputs NaN. Replaces the per-expert dequant + F.linear of
+ * wisp/moe.py:131-137 (three launches for all routed experts). */
+int wisp_moe_prefill(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const int32_t* groups, int ngroups,
+                     int max_group, const int32_t* tok, const float* w, const int32_t* back, int64_t pairs, const uint16_t* x, int T,
+                     int k, int64_t H, int64_t I, int bits, int64_t group, void* ws, uint16_t* out, float* acc,
+                     void* stream);
+
 /* ---------------------------------------------------------------------------
  * Expert cache bookkeeping (host only, no device calls). Keys are
  * layer*n_experts + expert; slots [0, n_static) are the static region.

@@ -220,3 +220,30 @@ def attn_decode(q: np.ndarray, k: np.ndarray, v: np.ndarray, pos: int, scale: fl
         w = np.exp(s - s.max())
         out[h] = (w / w.sum()) @ v[h // G, : pos + 1]
     return out
+
+
+# ---------------------------------------------------------------- grouped prefill (moe.py:131-151)
+def moe_prefill_f64(pool: np.ndarray, expert_slots: dict, x_bf16: np.ndarray, sel: np.ndarray, rw: np.ndarray,
+                    H: int, I: int, bits: int, group: int = 128) -> np.ndarray:
+    """The per-expert dequant -> MLP -> weighted sum of moe.py:131-151 in binary64, with the
+    weights dequantized bit-exactly to bf16 (quant.py:76-87, as the reference's F.linear
+    sees them) and the activation between the two GEMMs rounded to bf16 (the operand type
+    of both the reference's second F.linear and the MFMA). x_bf16: uint16 [T, H];
+    sel/rw: [T, k]. Experts missing from expert_slots are skipped. Returns float64 [T, H]."""
+    x = bf16_bits_to_f32(np.asarray(x_bf16, np.uint16)).reshape(-1, H).astype(np.float64)
+    sel = np.asarray(sel)
+    rw = np.asarray(rw, np.float64)
+    T = x.shape[0]
+    n = H * I
+    out = np.zeros((T, H), np.float64)
+    for e in sorted(int(v) for v in np.unique(sel)):
+        if e not in expert_slots:
+            continue
+        W = bf16_bits_to_f32(dequant(pool[expert_slots[e]][None], n, bits, group)[0]).astype(np.float64)
+        Wg, Wu, Wd = W[0].reshape(I, H), W[1].reshape(I, H), W[2].reshape(H, I)
+        tt, jj = np.nonzero(sel == e)
+        g, u = x[tt] @ Wg.T, x[tt] @ Wu.T
+        a = g / (1.0 + np.exp(-g)) * u
+        a = bf16_bits_to_f32(f32_to_bf16_bits(a.astype(np.float32))).reshape(a.shape).astype(np.float64)
+        out[tt] += rw[tt, jj][:, None] * (a @ Wd.T)
+    return out

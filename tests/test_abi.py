@@ -132,6 +132,26 @@ def test_rope_argument_validation():
     assert L.wisp_rope_decode(*null_q) == _lib.WISP_EINVAL
 
 
+def test_prefill_argument_validation():
+    L = _lib.lib()
+    nb = 2506752
+
+    def call(**kw):
+        a = dict(pool=FAKE, slot_bytes=nb, nslots=128, groups=FAKE, ngroups=4, max_group=8, tok=FAKE, w=FAKE,
+                 back=FAKE, pairs=64, x=FAKE, T=8, k=8, H=2048, I=768, bits=4, group=128, ws=FAKE, out=FAKE, acc=None)
+        a.update(kw)
+        return L.wisp_moe_prefill(*a.values(), None)
+
+    assert call(group=64) == _lib.WISP_EINVAL  # one quant group per K step
+    assert call(H=2176, I=768, slot_bytes=nb * 2) == _lib.WISP_EINVAL  # H % 256
+    assert call(pairs=65) == _lib.WISP_EINVAL  # more pairs than T*k
+    assert call(bits=8) == _lib.WISP_EINVAL
+    assert call(out=None) == _lib.WISP_EINVAL  # neither out nor acc
+    assert call(slot_bytes=nb - 16) == _lib.WISP_EINVAL
+    assert call(x=ctypes.c_void_p(0x100002)) == _lib.WISP_EALIGN
+    assert L.wisp_prefill_ws_bytes(64, 2048, 768) == 64 * 768 * 2 + 64 * 2048 * 4
+
+
 def test_expert_cache_needs_a_gpu():
     """The slot pool is device memory: without a GPU the cache refuses to build (no host pool)."""
     if torch.cuda.is_available():

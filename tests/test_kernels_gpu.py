@@ -405,3 +405,61 @@ def test_attn_decode_graph_follows_device_position():
         r = _bf16_np(O.attn_decode(q, k, v, pos, 0.125))
         got = out.float().cpu().numpy().reshape(Hq, D)
         assert np.linalg.norm(got - r) / np.linalg.norm(r) <= 1e-3, pos
+
+
+# ---------------------------------------------------------------- grouped prefill (moe.py:131-151)
+def _prefill_case(E, H, I, T, k, bits, seed, hot=False):
+    rng = np.random.default_rng(seed)
+    pool = _pool(E, H, I, bits, 128, seed=seed)
+    x = O.f32_to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32)).reshape(T, H)
+    sel, rw = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+    if hot:  # every token routes to expert 0 (a group larger than one workgroup pass)
+        for t in range(T):
+            if 0 not in sel[t]:
+                sel[t, -1] = 0
+    return pool, x, sel, rw
+
+
+def _run_prefill(pool_np, x, sel, rw, H, I, bits, slots=None, acc=None):
+    pool = torch.from_numpy(pool_np).to(DEV)
+    E = pool_np.shape[0]
+    slots = {e: e for e in range(E)} if slots is None else slots
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV)
+    out = kernels.moe_prefill(pool, slots, xt, torch.from_numpy(sel), torch.from_numpy(rw).to(DEV), H * I, H, I,
+                              bits, acc=acc)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("E,H,I,T,k,hot", [(6, 256, 128, 1, 2, False), (6, 256, 128, 17, 2, False),
+                                          (4, 256, 128, 300, 2, True), (16, 2048, 768, 64, 8, False),
+                                          (12, 512, 384, 40, 4, False)])
+def test_moe_prefill_matches_oracle(bits, E, H, I, T, k, hot):
+    pool, x, sel, rw = _prefill_case(E, H, I, T, k, bits, seed=E + T + bits, hot=hot)
+    out = _run_prefill(pool, x, sel, rw, H, I, bits)
+    ref = O.moe_prefill_f64(pool, {e: e for e in range(E)}, x, sel, rw, H, I, bits)
+    r = O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.astype(np.float32))).reshape(ref.shape)
+    got = out.float().cpu().numpy()
+    err = np.linalg.norm(got - r) / np.linalg.norm(r)
+    print(f"prefill bits={bits} T={T} H={H}: rel-L2 {err:.3e}")
+    assert err <= 1e-3, err
+    assert np.max(np.abs(got - ref)) <= 2e-2 * np.max(np.abs(ref))
+
+
+def test_moe_prefill_expert_chunks_accumulate_and_invalid_slot():
+    E, H, I, T, k, bits = 6, 256, 128, 24, 2, 4
+    pool, x, sel, rw = _prefill_case(E, H, I, T, k, bits, seed=31)
+    acc = torch.zeros((T, H), dtype=torch.float32, device=DEV)
+    for chunk in ([0, 1, 2], [3, 4, 5]):
+        _run_prefill(pool, x, sel, rw, H, I, bits, slots={e: e for e in chunk}, acc=acc)
+    one = _run_prefill(pool, x, sel, rw, H, I, bits).float()
+    assert torch.allclose(acc.to(torch.bfloat16).float(), one, rtol=1e-2, atol=1e-3)
+    ref = O.moe_prefill_f64(pool, {e: e for e in range(E)}, x, sel, rw, H, I, bits)
+    r = O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.astype(np.float32))).reshape(ref.shape)
+    got = acc.to(torch.bfloat16).float().cpu().numpy()
+    assert np.linalg.norm(got - r) / np.linalg.norm(r) <= 1e-3
+    # an invalid slot id poisons exactly the tokens routed to that expert
+    bad = _run_prefill(pool, x, sel, rw, H, I, bits, slots={**{e: e for e in range(E)}, 2: 99}).float().cpu()
+    hit = torch.from_numpy((sel == 2).any(axis=1))
+    assert torch.isnan(bad[hit]).all() and torch.isfinite(bad[~hit]).all()

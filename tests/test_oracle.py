@@ -324,3 +324,39 @@ def test_attn_oracle_matches_torch_sdpa_repeat_kv():
     bad = np.stack([O.attn_decode(q[h : h + 1], k[h % Hk : h % Hk + 1], v[h % Hk : h % Hk + 1], pos, scale)[0]
                     for h in range(Hq)])
     assert not np.allclose(bad, out, atol=1e-3)
+
+
+# ---------------------------------------------------------------- grouped prefill oracle (moe.py:131-151)
+def _pf_case(E=5, H=256, I=128, T=7, k=2, bits=4, seed=0):
+    rng = np.random.default_rng(seed)
+    pool = np.stack([O.quantize((rng.standard_normal(3 * H * I) * 0.02).astype(np.float32), bits, 128)
+                     for _ in range(E)])
+    x = O.f32_to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32)).reshape(T, H)
+    sel, rw = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+    return pool, x, sel, rw
+
+
+def test_prefill_oracle_one_token_matches_decode_oracle():
+    pool, x, sel, rw = _pf_case(T=1)
+    slots = {e: e for e in range(5)}
+    pf = O.moe_prefill_f64(pool, slots, x, sel, rw, 256, 128, 4)[0]
+    _, _, dec = O.moe_layer_f64(pool, sel[0], rw[0], x[0], 256, 128, 4)
+    err = np.linalg.norm(pf - dec) / np.linalg.norm(dec)
+    assert 0 < err < 1e-2  # only the bf16 rounding of W and of the activation differ
+    # a gate/up swap (SiLU on the up projection) is far off
+    W = [O.bf16_bits_to_f32(O.dequant(pool[e][None], 256 * 128, 4)[0]).astype(np.float64) for e in sel[0]]
+    xf = O.bf16_bits_to_f32(x[0]).astype(np.float64)
+    bad = sum(w * (W[j][2].reshape(256, 128) @ ((lambda g, u: u / (1 + np.exp(-u)) * g)(
+        W[j][0].reshape(128, 256) @ xf, W[j][1].reshape(128, 256) @ xf))) for j, w in enumerate(rw[0]))
+    assert np.linalg.norm(bad - dec) / np.linalg.norm(dec) > 0.1
+
+
+def test_prefill_oracle_additive_over_experts_and_token_equivariant():
+    pool, x, sel, rw = _pf_case(T=9, seed=1)
+    slots = {e: e for e in range(5)}
+    full = O.moe_prefill_f64(pool, slots, x, sel, rw, 256, 128, 4)
+    parts = sum(O.moe_prefill_f64(pool, {e: e}, x, sel, rw, 256, 128, 4) for e in range(5))
+    assert np.allclose(full, parts, rtol=1e-12, atol=1e-12)
+    perm = np.random.default_rng(2).permutation(9)
+    permuted = O.moe_prefill_f64(pool, slots, x[perm], sel[perm], rw[perm], 256, 128, 4)
+    assert np.allclose(permuted, full[perm], rtol=1e-12, atol=1e-12)

@@ -1,0 +1,403 @@
+// Grouped MoE prefill on gfx950: T tokens, each routed to k experts; per expert
+// the token group runs gate/up (+ SiLU * up) and down as bf16 MFMA GEMMs whose
+// weight tiles are dequantized into LDS from the packed slot-pool rows.
+//
+// Reference semantics: wisp/moe.py:131-137 (with 147-151): for every routed
+// expert, dequantize its buffer to bf16 (quant.py:76-87, bit-exact here), run
+// the expert MLP down(SiLU(gate x) * up x) on its tokens, weight by the token's
+// routing weight and accumulate into the token's output, experts in ascending
+// id order. Here the GEMMs accumulate in fp32 (MFMA), the activation between
+// them is rounded to bf16 once (the MFMA operand type), the per-token sum is
+// fp32 and the output is rounded to bf16 once.
+//
+// Data (all device, built by the caller from the routing):
+//   pairs: the T*k (token, expert) pairs sorted by expert; tok[p] the token of
+//          pair p, w[p] its routing weight; groups[u] = (slot, first pair,
+//          pair count) of the u-th routed expert; back[t*k + j] = the pair of
+//          token t's j-th expert in ascending expert id.
+//   ws:    act bf16 [P, I] (gate_up output) | y fp32 [P, H] (weighted down output)
+// Kernels:
+//   k_pf_gate_up  grid (I/128, U, Z): per wave 32 act columns of one expert
+//                 (their 32 gate and 32 up rows); K = H in 128-wide steps (one
+//                 quant group per row).
+//   k_pf_down     grid (H/256, U, Z): per wave 64 down rows; K = I.
+//   (workgroup z takes the group's token passes z, z+Z, ...)
+//   k_pf_combine  out[t] = bf16(sum_j y[back[t, j]]).
+// Waves work independently (no LDS, no barriers): a wave owns 64 weight rows
+// (four 16-row tiles; gate_up: 32 gate rows and the same 32 up rows), streams
+// their codes one 128-wide K step (one quant group) ahead, dequantizes them in
+// registers straight into MFMA B fragments, and multiplies them against up to
+// MT 16-token tiles of the group (v_mfma_f32_16x16x32_bf16, tokens as M, rows
+// as N); each token fragment is reused by the four row tiles.
+// K order inside a step: lane group g = lane/16 holds the step's 32-code chunk
+// g, and MFMA k-substep s takes its codes 8s..8s+7; the A operand (token rows,
+// read from L2) uses the same order, which leaves the dot products unchanged.
+// Groups larger than one pass (MT*16 tokens) spread over Z workgroups.
+// MFMA 16x16x32 bf16 lane layout (lane l): A[row l%16][k 8*(l/16) + 0..7],
+// B[k 8*(l/16) + 0..7][col l%16], D[row 4*(l/16) + 0..3][col l%16].
+// With the weights read once per expert the path is HBM-bound for T <= 512.
+#include <math.h>
+
+#include <algorithm>
+
+#include "wisp_device.hpp"
+#include "wisp_internal.hpp"
+
+namespace wisp {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kPfWaves = 4;  // waves per workgroup, 16 weight rows each
+
+struct Prefill {
+    const uint8_t* pool;
+    int64_t slot_bytes, nmb;  // nmb: code bytes of one matrix
+    int nslots, H, I, NGM, P, T;
+    const int32_t* groups;  // [U][3]
+    const int32_t* tok;     // [P]
+    const float* w;         // [P]
+    const uint16_t* x;      // [T, H]
+    uint16_t* act;          // [P, I]
+    float* y;               // [P, H]
+};
+
+__device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                    c, 0, 0, 0);
+}
+
+// byte N of v as a float (v_cvt_f32_ubyteN: one instruction, no extract)
+__device__ __forceinline__ float ubyte0(uint32_t v) { float r; asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v)); return r; }
+__device__ __forceinline__ float ubyte1(uint32_t v) { float r; asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v)); return r; }
+__device__ __forceinline__ float ubyte2(uint32_t v) { float r; asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v)); return r; }
+__device__ __forceinline__ float ubyte3(uint32_t v) { float r; asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v)); return r; }
+template <int B>
+__device__ __forceinline__ float ubyte(uint32_t v) {
+    return B == 0 ? ubyte0(v) : B == 1 ? ubyte1(v) : B == 2 ? ubyte2(v) : ubyte3(v);
+}
+
+// Dequantize 32 consecutive weights (one chunk) to 16 bf16 pairs, bit-exact with
+// the dequant kernel: w = RTNE_bf16(fp32(q*s) + m). q*s is exact in binary32
+// (q < 16, s an fp16 value), so a fused multiply-add rounds exactly where the
+// separate multiply and add would. 4- and 2-bit codes are first spread one per
+// byte, so that each becomes a float with one v_cvt_f32_ubyteN.
+template <int BITS>
+__device__ __forceinline__ void dequant_chunk(const uint32_t* d, float s, float m, uint32_t* out) {
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t e = d[w] & 0x0F0F0F0Fu;         // codes 8w, 8w+2, 8w+4, 8w+6
+            const uint32_t o = (d[w] >> 4) & 0x0F0F0F0Fu;  // codes 8w+1, 8w+3, 8w+5, 8w+7
+            out[4 * w + 0] = pack_bf16x2(__builtin_fmaf(ubyte<0>(e), s, m), __builtin_fmaf(ubyte<0>(o), s, m));
+            out[4 * w + 1] = pack_bf16x2(__builtin_fmaf(ubyte<1>(e), s, m), __builtin_fmaf(ubyte<1>(o), s, m));
+            out[4 * w + 2] = pack_bf16x2(__builtin_fmaf(ubyte<2>(e), s, m), __builtin_fmaf(ubyte<2>(o), s, m));
+            out[4 * w + 3] = pack_bf16x2(__builtin_fmaf(ubyte<3>(e), s, m), __builtin_fmaf(ubyte<3>(o), s, m));
+        }
+    } else if constexpr (BITS == 2) {
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            uint32_t f[4];  // f[j] byte b = code 16w + 4b + j
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f[j] = (d[w] >> (2 * j)) & 0x03030303u;
+#define WISP_Q2(B)                                                                                      \
+    out[8 * w + 2 * B] = pack_bf16x2(__builtin_fmaf(ubyte<B>(f[0]), s, m), __builtin_fmaf(ubyte<B>(f[1]), s, m));  \
+    out[8 * w + 2 * B + 1] = pack_bf16x2(__builtin_fmaf(ubyte<B>(f[2]), s, m), __builtin_fmaf(ubyte<B>(f[3]), s, m));
+            WISP_Q2(0)
+            WISP_Q2(1)
+            WISP_Q2(2)
+            WISP_Q2(3)
+#undef WISP_Q2
+        }
+    } else {
+        uint32_t q[32];
+        chunk_codes<BITS>(d, q);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            out[i] = pack_bf16x2(__builtin_fmaf((float)q[2 * i], s, m), __builtin_fmaf((float)q[2 * i + 1], s, m));
+    }
+}
+
+// Group u's (slot, first pair, count). Returns 0 for a group whose pair range is
+// invalid (nothing is written), 1 for an invalid slot id (its rows are written
+// as NaN, nothing is read from the pool), 2 for a valid group.
+__device__ __forceinline__ int group_state(const Prefill& F, int u, int& slot, int& p0, int& cnt) {
+    slot = F.groups[3 * u];
+    p0 = F.groups[3 * u + 1];
+    cnt = F.groups[3 * u + 2];
+    if (!(p0 >= 0 && cnt > 0 && p0 + cnt <= F.P)) return 0;
+    return (slot >= 0 && slot < F.nslots) ? 2 : 1;
+}
+
+// One K step's codes and fp16 scale/min (packed s | m << 16) of a lane's row.
+template <int BITS>
+__device__ __forceinline__ void pf_load(const uint8_t* rc, const uint16_t* scp, const uint16_t* mnp, int kc,
+                                        uint32_t* cd, uint32_t& sm) {
+    load_chunk<BITS>(rc + (int64_t)kc * 16 * BITS, cd);  // 128 codes per K step
+    sm = (uint32_t)scp[kc] | ((uint32_t)mnp[kc] << 16);
+}
+
+// The step's 4 MFMA B fragments (k-substeps 0..3) from the lane's chunk.
+template <int BITS>
+__device__ __forceinline__ void pf_bfrag(const uint32_t* cd, uint32_t sm, uint4* b) {
+    uint32_t v[16];
+    dequant_chunk<BITS>(cd, h2f((uint16_t)(sm & 0xFFFFu)), h2f((uint16_t)(sm >> 16)), v);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) b[s] = make_uint4(v[4 * s], v[4 * s + 1], v[4 * s + 2], v[4 * s + 3]);
+}
+
+// One wave's GEMM over K steps 0..nk-1 for 4 weight row tiles (16 rows each;
+// row pointers rc[j] at the lane's row and chunk, scale/min bases sp/mp[j]) and
+// up to MT 16-token tiles (A row pointers arow[mt], uint4 units at the lane's k
+// offset; tiles at or past `ntile` are skipped). Codes are loaded one step
+// ahead; a step's A fragments are loaded at its start and the dequantization
+// of its four B tiles overlaps their latency. Each A fragment feeds all four
+// row tiles, so the A operand is read once per 64 weight rows.
+template <int BITS, int MT>
+__device__ __forceinline__ void pf_wave_gemm(const uint8_t* const* rc, const uint16_t* const* sp,
+                                             const uint16_t* const* mp, const uint4* const* arow, int nk, int ntile,
+                                             f32x4_t (*acc)[4]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    uint32_t cd[4][BITS], sm[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pf_load<BITS>(rc[j], sp[j], mp[j], 0, cd[j], sm[j]);
+    for (int kc = 0; kc < nk; ++kc) {
+        uint4 xa[MT][4];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+            if (mt < ntile)
+#pragma unroll
+                for (int s = 0; s < 4; ++s) xa[mt][s] = arow[mt][kc * 16 + s];
+        const int kn = kc + 1 < nk ? kc + 1 : kc;  // the last step loads itself again (in bounds)
+        uint32_t cdn[4][BITS], smn[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pf_load<BITS>(rc[j], sp[j], mp[j], kn, cdn[j], smn[j]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint4 b[4];
+            pf_bfrag<BITS>(cd[j], sm[j], b);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    if (mt < ntile) acc[mt][j] = mfma16(xa[mt][s], b[s], acc[mt][j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int i = 0; i < BITS; ++i) cd[j][i] = cdn[j][i];
+            sm[j] = smn[j];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// gate_up: act[p][r] = bf16(silu(g) * u), g/u = x[tok[p]] . W{gate,up}[r]
+// grid (I/128, U, Z); wave w of workgroup x owns act columns c0 = (4x + w)*32
+// .. +31: row tiles {gate c0, gate c0+16, up c0, up c0+16}.
+template <int BITS, int MT>
+__global__ __launch_bounds__(256) void k_pf_gate_up(const Prefill F) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int c0 = (blockIdx.x * kPfWaves + wv) * 32, u = blockIdx.y;
+    int slot, p0, cnt;
+    const int gs = group_state(F, u, slot, p0, cnt);
+    if (gs == 0) return;
+    if (gs == 1) {
+        for (int i = lane; i < cnt * 32; i += 64)
+            F.act[(int64_t)(p0 + i / 32) * F.I + c0 + (i & 31)] = 0x7FC0;  // bf16 NaN
+        return;
+    }
+    const uint8_t* base = F.pool + (int64_t)slot * F.slot_bytes;
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * F.nmb);
+    const uint16_t* mn = sc + 3 * F.NGM;
+    const int nk = F.H / 128;
+    const int64_t rowb = (int64_t)F.H * BITS / 8;
+    const uint8_t* rc[4];
+    const uint16_t *sp[4], *mp[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int mat = j >> 1, r = c0 + (j & 1) * 16 + n;
+        rc[j] = base + mat * F.nmb + (int64_t)r * rowb + g * 4 * BITS;
+        sp[j] = sc + (int64_t)mat * F.NGM + (int64_t)r * nk;
+        mp[j] = mn + (int64_t)mat * F.NGM + (int64_t)r * nk;
+    }
+    constexpr int MB = MT * 16;
+    for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
+        const uint4* arow[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            int t = F.tok[p0 + min(mb + mt * 16 + n, cnt - 1)];  // rows past cnt repeat the last pair
+            t = min(max(t, 0), F.T - 1);
+            arow[mt] = reinterpret_cast<const uint4*>(F.x + (int64_t)t * F.H) + g * 4;
+        }
+        f32x4_t acc[MT][4];
+        pf_wave_gemm<BITS, MT>(rc, sp, mp, arow, nk, (cnt - mb + 15) / 16, acc);
+        // D layout: acc[mt][j][i] = token mb + mt*16 + 4g + i, row tile j column n
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = mb + mt * 16 + 4 * g + i;
+                if (m < cnt) {
+                    uint16_t* dst = F.act + (int64_t)(p0 + m) * F.I + c0 + n;
+                    dst[0] = f32_to_bf16(silu_mul(acc[mt][0][i], acc[mt][2][i]));
+                    dst[16] = f32_to_bf16(silu_mul(acc[mt][1][i], acc[mt][3][i]));
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// down: y[p][h] = w[p] * (act[p] . Wdown[h]), fp32
+// grid (H/256, U, Z); wave w of workgroup x owns rows (4x + w)*64 .. +63.
+template <int BITS, int MT>
+__global__ __launch_bounds__(256) void k_pf_down(const Prefill F) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int h0 = (blockIdx.x * kPfWaves + wv) * 64, u = blockIdx.y;
+    int slot, p0, cnt;
+    const int gs = group_state(F, u, slot, p0, cnt);
+    if (gs == 0) return;
+    if (gs == 1) {
+        for (int i = lane; i < cnt * 64; i += 64)
+            F.y[(int64_t)(p0 + i / 64) * F.H + h0 + (i & 63)] = __builtin_nanf("");
+        return;
+    }
+    const uint8_t* base = F.pool + (int64_t)slot * F.slot_bytes;
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * F.nmb);
+    const uint16_t* mn = sc + 3 * F.NGM;
+    const int nk = F.I / 128;
+    const uint8_t* rc[4];
+    const uint16_t *sp[4], *mp[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int h = h0 + j * 16 + n;
+        rc[j] = base + 2 * F.nmb + (int64_t)h * ((int64_t)F.I * BITS / 8) + g * 4 * BITS;
+        sp[j] = sc + 2 * (int64_t)F.NGM + (int64_t)h * nk;
+        mp[j] = mn + 2 * (int64_t)F.NGM + (int64_t)h * nk;
+    }
+    constexpr int MB = MT * 16;
+    for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
+        const uint4* arow[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int m = min(mb + mt * 16 + n, cnt - 1);
+            arow[mt] = reinterpret_cast<const uint4*>(F.act + (int64_t)(p0 + m) * F.I) + g * 4;
+        }
+        f32x4_t acc[MT][4];
+        pf_wave_gemm<BITS, MT>(rc, sp, mp, arow, nk, (cnt - mb + 15) / 16, acc);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = mb + mt * 16 + 4 * g + i;
+                if (m < cnt) {
+                    const float wp = F.w[p0 + m];
+                    float* dst = F.y + (int64_t)(p0 + m) * F.H + h0 + n;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) dst[j * 16] = wp * acc[mt][j][i];
+                }
+            }
+    }
+}
+
+// s = sum_j y[back[t*k + j]][h], j in ascending expert id (back = -1: no pair in
+// this call); out[t][h] = bf16(s), or acc[t][h] += s when acc is given
+__global__ __launch_bounds__(256) void k_pf_combine(const float* __restrict__ y, const int32_t* __restrict__ back,
+                                                    int T, int k, int H, int P, uint16_t* __restrict__ out,
+                                                    float* __restrict__ acc) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)T * H) return;
+    const int t = (int)(i / H), h = (int)(i - (int64_t)t * H);
+    float s = 0.f;
+    for (int j = 0; j < k; ++j) {
+        const int p = back[t * k + j];
+        if (p == -1) continue;
+        s += (p >= 0 && p < P) ? y[(int64_t)p * H + h] : __builtin_nanf("");
+    }
+    if (acc)
+        acc[i] += s;
+    else
+        out[i] = f32_to_bf16(s);
+}
+
+// MT (16-token tiles per wave and pass) from the largest group; Z workgroups
+// share a larger group's passes
+template <int BITS, int MT>
+static void launch_pf_mt(const Prefill& F, int ngroups, int max_group, hipStream_t st) {
+    const unsigned z = (unsigned)std::min(64, std::max(1, (max_group + MT * 16 - 1) / (MT * 16)));
+    hipLaunchKernelGGL((k_pf_gate_up<BITS, MT>), dim3((unsigned)(F.I / 128), (unsigned)ngroups, z), dim3(256), 0, st,
+                       F);
+    hipLaunchKernelGGL((k_pf_down<BITS, MT>), dim3((unsigned)(F.H / 256), (unsigned)ngroups, z), dim3(256), 0, st, F);
+}
+template <int BITS>
+static void launch_pf(const Prefill& F, int ngroups, int max_group, hipStream_t st) {
+    if (max_group <= 16)
+        launch_pf_mt<BITS, 1>(F, ngroups, max_group, st);
+    else if (max_group <= 32)
+        launch_pf_mt<BITS, 2>(F, ngroups, max_group, st);
+    else
+        launch_pf_mt<BITS, 4>(F, ngroups, max_group, st);
+}
+
+}  // namespace wisp
+
+using namespace wisp;
+
+extern "C" int64_t wisp_prefill_ws_bytes(int64_t pairs, int64_t H, int64_t I) {
+    if (pairs < 1 || H < 1 || I < 1) return -1;
+    return (pairs * I * 2 + 255) / 256 * 256 + pairs * H * 4;
+}
+
+// moe.py:131-151 (grouped: one launch per GEMM for all routed experts)
+extern "C" int wisp_moe_prefill(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const int32_t* groups,
+                                int ngroups, int max_group, const int32_t* tok, const float* w, const int32_t* back, int64_t pairs,
+                                const uint16_t* x, int T, int k, int64_t H, int64_t I, int bits, int64_t group,
+                                void* ws, uint16_t* out, float* acc, void* stream) {
+    clear_error();
+    if (!pool || !groups || !tok || !w || !back || !x || !ws || (!out && !acc)) return fail_inval("null pointer");
+    if (!(bits == 4 || bits == 3 || bits == 2)) return fail_inval("bits must be 4, 3 or 2");
+    if (group != 128) return fail_inval("the grouped prefill needs group 128 (one quant group per K step)");
+    if (H % 256 || I % 128 || H > (1 << 16) || I > (1 << 16))
+        return fail_inval("H a multiple of 256 and I of 128, both <= 65536");
+    if (T < 1 || k < 1 || ngroups < 1 || pairs < 1 || pairs > (int64_t)T * k)
+        return fail_inval("need 1 <= pairs <= T*k and at least one group");
+    if (nslots < 1 || nslots > (1 << 24)) return fail_inval("nslots out of range");
+    const int64_t n = H * I;
+    if (slot_bytes < wisp_expert_nbytes(n, bits, group)) return fail_inval("slot_bytes < expert size");
+    if (!aligned(pool, 16) || slot_bytes % 16 || !aligned(x, 16) || !aligned(ws, 256)) {
+        set_error("pool, x and ws must be 16/16/256-byte aligned, slot_bytes a multiple of 16");
+        return WISP_EALIGN;
+    }
+    Prefill F;
+    F.pool = pool;
+    F.slot_bytes = slot_bytes;
+    F.nmb = n * bits / 8;
+    F.nslots = (int)nslots;
+    F.H = (int)H;
+    F.I = (int)I;
+    F.NGM = (int)(n / group);
+    F.P = (int)pairs;
+    F.T = T;
+    F.groups = groups;
+    F.tok = tok;
+    F.w = w;
+    F.x = x;
+    F.act = static_cast<uint16_t*>(ws);
+    F.y = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + (pairs * I * 2 + 255) / 256 * 256);
+    hipStream_t st = (hipStream_t)stream;
+    max_group = std::max(1, std::min(max_group, T));  // a launch-shape hint; any value is correct
+    switch (bits) {
+    case 4: launch_pf<4>(F, ngroups, max_group, st); break;
+    case 3: launch_pf<3>(F, ngroups, max_group, st); break;
+    default: launch_pf<2>(F, ngroups, max_group, st); break;
+    }
+    const int64_t total = (int64_t)T * H;
+    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                       (const float*)F.y, back, T, k, (int)H, (int)pairs, out, acc);
+    return check_launch("k_pf");
+}

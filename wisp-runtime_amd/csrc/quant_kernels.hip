@@ -27,30 +27,10 @@ __device__ __forceinline__ void unpack32(const uint8_t* codes, int64_t c, uint32
         const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
         for (int i = 0; i < 32; ++i) q[i] = (w[i >> 2] >> (8 * (i & 3))) & 255u;
-    } else if constexpr (BITS == 4) {
-        uint32_t d[4];
-        load_chunk<4>(codes + c * 16, d);
-#pragma unroll
-        for (int i = 0; i < 32; ++i) q[i] = (d[i >> 3] >> (4 * (i & 7))) & 15u;
-    } else if constexpr (BITS == 2) {
-        uint32_t d[2];
-        load_chunk<2>(codes + c * 8, d);
-#pragma unroll
-        for (int i = 0; i < 32; ++i) q[i] = (d[i >> 4] >> (2 * (i & 15))) & 3u;
     } else {
-        uint32_t d[3];
-        load_chunk<3>(codes + c * 12, d);
-        const uint64_t lo = (uint64_t)d[0] | ((uint64_t)d[1] << 32);
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            const int b = 3 * i;
-            if (b + 3 <= 64)
-                q[i] = (uint32_t)(lo >> b) & 7u;
-            else if (b >= 64)
-                q[i] = (d[2] >> (b - 64)) & 7u;
-            else
-                q[i] = (uint32_t)((lo >> b) | ((uint64_t)d[2] << (64 - b))) & 7u;
-        }
+        uint32_t d[BITS];
+        load_chunk<BITS>(codes + c * 4 * BITS, d);
+        chunk_codes<BITS>(d, q);
     }
 }
 

@@ -221,6 +221,33 @@ __device__ __forceinline__ void load_chunk<2>(const uint8_t* p, uint32_t* d) {
     d[0] = v.x; d[1] = v.y;
 }
 
+// The 32 codes of one loaded chunk (BITS dwords, little-endian): element i
+// sits at bit BITS*i (the packing of quant.py:25-40; 3-bit codes may straddle
+// dwords).
+template <int BITS>
+__device__ __forceinline__ void chunk_codes(const uint32_t* d, uint32_t* q) {
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) q[i] = (d[i >> 3] >> (4 * (i & 7))) & 15u;
+    } else if constexpr (BITS == 2) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) q[i] = (d[i >> 4] >> (2 * (i & 15))) & 3u;
+    } else {
+        static_assert(BITS == 3, "chunk_codes: 4, 3 or 2 bits");
+        const uint64_t lo = (uint64_t)d[0] | ((uint64_t)d[1] << 32);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const int b = 3 * i;
+            if (b + 3 <= 64)
+                q[i] = (uint32_t)(lo >> b) & 7u;
+            else if (b >= 64)
+                q[i] = (d[2] >> (b - 64)) & 7u;
+            else
+                q[i] = (uint32_t)((lo >> b) | ((uint64_t)d[2] << (64 - b))) & 7u;
+        }
+    }
+}
+
 // bf16 pair (2^elo(P), 2^ehi(P)): dot2 of a stored operand pair with it gives
 // the sum of the two true (unscaled) operand values.
 template <int BITS>

@@ -38,6 +38,9 @@ SIGNATURES = {
     "wisp_rope_decode": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "wisp_attn_ws_bytes": (_i64, [_i32, _i32, _i32]),
     "wisp_attn_decode": (_i32, [_vp, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, ctypes.c_float, _vp, _vp, _vp]),
+    "wisp_prefill_ws_bytes": (_i64, [_i64, _i64, _i64]),
+    "wisp_moe_prefill": (_i32, [_vp, _i64, _i64, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _i64, _i64,
+                                _i32, _i64, _vp, _vp, _vp, _vp]),
     "wisp_core_create": (_i32, [_i64, _i32, _f64, _i64, _f64, _vp]),
     "wisp_core_destroy": (None, [_vp]),
     "wisp_core_step": (None, [_vp]),

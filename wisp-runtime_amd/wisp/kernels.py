@@ -176,3 +176,74 @@ def attn_decode(q, kc, vc, pos, scale):
         "attn_decode",
     )
     return out
+
+
+def _prefill_plan(sel_cpu, experts, k):
+    """Host-side grouping of the (token, expert) pairs whose expert is in `experts`:
+    pairs sorted by expert (tokens ascending within an expert), the per-expert
+    (first pair, count), and back[t, j] = pair of token t's j-th expert in ascending
+    expert id (-1 when that expert is not in `experts`)."""
+    import numpy as np
+
+    T = sel_cpu.shape[0]
+    flat = sel_cpu.reshape(-1)
+    keep = np.isin(flat, np.asarray(experts, dtype=flat.dtype))
+    idx = np.flatnonzero(keep)
+    order = idx[np.argsort(flat[idx], kind="stable")]  # original pair ids, sorted by expert
+    pair_of = np.full(T * k, -1, np.int64)
+    pair_of[order] = np.arange(order.size)
+    rank = np.argsort(sel_cpu, axis=1, kind="stable")  # token t's experts in ascending id
+    back = np.take_along_axis(pair_of.reshape(T, k), rank, axis=1)
+    ex_sorted = flat[order]
+    uniq, first, count = np.unique(ex_sorted, return_index=True, return_counts=True)
+    return order, (order // k).astype(np.int32), back.astype(np.int32), uniq, first, count
+
+
+def moe_prefill(pool, expert_slots, x, sel, rw, n, H, I, bits, group=128, acc=None):
+    """Grouped MoE over T tokens (the dequant + F.linear loop of moe.py:131-151 as three
+    launches). x: [T, H] bf16; sel: [T, k] expert ids; rw: [T, k] routing weights;
+    expert_slots: {expert id: slot} for the experts to run (others are skipped).
+    Returns bf16 [T, H] = per token sum over its experts (ascending id) of
+    w * down(SiLU(gate x) * up x); with `acc` (fp32 [T, H]) the sum is added to it instead
+    (chunks of experts) and acc is returned."""
+    import numpy as np
+
+    assert n == H * I and H % group == 0 and I % group == 0
+    _check_pool(pool)
+    dev = _lib.require_gpu(pool, x, what="moe_prefill")
+    x = x.reshape(-1, H)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"x must be bfloat16 (got {x.dtype})")
+    x = x.contiguous()
+    T, k = sel.shape
+    sel_cpu = sel.detach().cpu().numpy()
+    experts = sorted(int(e) for e in expert_slots)
+    order, tok, back, uniq, first, count = _prefill_plan(sel_cpu, experts, k)
+    P = int(order.size)
+    if acc is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    else:
+        assert acc.dtype == torch.float32 and acc.shape == (T, H) and acc.is_contiguous()
+        out = None
+    if P == 0:
+        if out is not None:
+            out.zero_()
+        return acc if out is None else out
+    groups = np.stack([np.array([expert_slots[int(e)] for e in uniq], np.int64), first, count], 1).astype(np.int32)
+    ints = torch.from_numpy(np.concatenate([groups.reshape(-1), tok, back.reshape(-1)])).to(dev, non_blocking=True)
+    g_dev = ints[: groups.size]
+    tok_dev = ints[groups.size : groups.size + P]
+    back_dev = ints[groups.size + P :]
+    w_pairs = rw.reshape(-1).to(device=dev, dtype=torch.float32)
+    w_pairs = w_pairs.index_select(0, torch.from_numpy(order).to(dev, non_blocking=True)).contiguous()
+    L = _lib.lib()
+    ws = torch.empty(L.wisp_prefill_ws_bytes(P, H, I), dtype=torch.uint8, device=dev)
+    _lib.check(
+        L.wisp_moe_prefill(
+            _lib.ptr(pool), pool.stride(0), pool.shape[0], _lib.ptr(g_dev), len(uniq), int(count.max()), _lib.ptr(tok_dev),
+            _lib.ptr(w_pairs), _lib.ptr(back_dev), P, _lib.ptr(x), T, k, H, I, bits, group, _lib.ptr(ws),
+            _lib.ptr(out), _lib.ptr(acc), _lib.stream(dev),
+        ),
+        "moe_prefill",
+    )
+    return acc if out is None else out

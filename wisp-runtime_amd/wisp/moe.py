@@ -180,13 +180,31 @@ class PagedMoEBlock(nn.Module):
         return y.view(B, T, H)
 
     def _forward_dequant(self, x, rw, sel, pred, B, T, H):
-        """Several tokens: per routed expert, dequantize its slot and run three bf16 GEMMs on its
-        tokens, weighted and accumulated in expert order (moe.py:82-151, 'transfer' policy)."""
+        """Several tokens (moe.py:82-151, 'transfer' policy), experts paged in chunks of rt.chunk.
+        4/3/2-bit experts with group 128: the grouped prefill kernels (dequant into LDS + bf16
+        MFMA, three launches per chunk, fp32 accumulation across chunks). Otherwise: per routed
+        expert, dequantize its slot and run three bf16 GEMMs on its tokens."""
         rt, cache = self.rt, self.rt.cache
         sel_cpu = sel.cpu()
         self._record(sel_cpu)
         base = self.layer_idx * self.E
         keys = [base + int(e) for e in torch.unique(sel_cpu).tolist()]
+        st = cache.store
+        if st.bits in (2, 3, 4) and st.group == 128 and not cache.decode_on_load and x.dtype == torch.bfloat16:
+            from .kernels import moe_prefill
+
+            acc = torch.zeros((x.shape[0], H), dtype=torch.float32, device=x.device)
+            used = []
+            for i in range(0, len(keys), rt.chunk):
+                ck = keys[i : i + rt.chunk]
+                cs = cache.ensure(ck)
+                moe_prefill(cache.gpu, {kk - base: s for kk, s in zip(ck, cs)}, x, sel_cpu, rw, st.n, H, self.I,
+                            st.bits, st.group, acc=acc)
+                rt.stats["gpu_experts"] += len(ck)
+                used = list(cs)
+            if pred is not None:
+                self._prefetch_next(pred.cpu(), used)
+            return acc.to(x.dtype).view(B, T, H)
         out = torch.zeros_like(x)
         used = []
         for i in range(0, len(keys), rt.chunk):
