@@ -6,7 +6,14 @@ import it; the product package never does.
 
 The arithmetic lives in ``wisp_oracle.c`` (built to ``liboracle_wisp.so`` by
 ``oracle/Makefile``); this module wraps it with numpy arrays and adds the
-routing step of the caller. Each function names the reference lines it restates.
+routing step of the caller, the decode attention and the grouped prefill (binary64
+numpy). Each function names the reference lines it restates.
+
+Pins of the numpy-side functions (tests/test_oracle.py): route -> torch's softmax/topk;
+attn_decode -> torch's scaled_dot_product_attention with repeated KV heads, the
+one-position and equal-key closed forms, a head-mapping slip; moe_prefill_f64 -> the
+decode-layer oracle at one token, additivity over experts, token equivariance, a
+gate/up swap.
 """
 
 from __future__ import annotations
