@@ -38,9 +38,14 @@ FLAGS = [
 ]
 
 
+# kernarg preloading: the decode kernels' leading scalar arguments arrive in
+# SGPRs at dispatch instead of through a memory read at the kernel's start
+EXTRA = {"moe_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+
+
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     msg = "\n".join(
         line for line in (r.stdout + r.stderr).splitlines() if "is not a recognized feature for this target" not in line

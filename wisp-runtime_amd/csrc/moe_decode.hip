@@ -49,11 +49,11 @@ struct Layer {
 };
 
 // slot id from the meta buffer: -1 unless an exact integer in [0, nslots)
-__device__ __forceinline__ int slot_of(const float* meta, int j, int nslots) {
-    const float f = meta[j];
+__device__ __forceinline__ int slot_from(float f, int nslots) {
     const int s = (int)f;
     return (f >= 0.f && f < (float)nslots && (float)s == f) ? s : -1;
 }
+__device__ __forceinline__ int slot_of(const float* meta, int j, int nslots) { return slot_from(meta[j], nslots); }
 
 __device__ __forceinline__ void wave_sync_lds() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -175,8 +175,11 @@ __device__ __forceinline__ int lanes_per_sum(int NQ) {
 // part: this wave's LDS scratch, T*2*64 floats.
 // ===========================================================================
 template <int BITS, int SPR_T, int T, bool QSC>
-__device__ __forceinline__ void gate_up_rows(const Layer& L, const uint16_t* __restrict__ x,
-                                             uint32_t* __restrict__ act, int j, int slot, int r0, float* part) {
+// The lanes' x words (xw, chunk `seg` of x) are loaded by the caller before the
+// slot id is known; `ok` false (invalid slot id) reads slot 0 and writes NaN rows.
+__device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __restrict__ base, bool ok,
+                                             const uint32_t (&xw)[16], uint32_t* __restrict__ act, int j, int r0,
+                                             float* part) {
     const int SPR = SPR_T ? SPR_T : L.spr_gu;
     const int RPI = 64 / SPR;
     const int lane = threadIdx.x & 63;
@@ -184,19 +187,11 @@ __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint16_t* __r
     const int seg = lane - rr * SPR;
     const bool lane_on = rr < RPI;
     rr = lane_on ? rr : RPI - 1;  // idle lanes repeat an active lane's addresses
-    const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb);
     const uint16_t* mn = sc + 3 * L.NGM;
     const int gi = seg >> L.gsh;
 
-    // this lane's 32 x values first, then the weight codes and fp16 scale/min
-    // loads, all issued before any use
-    uint32_t xw[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint4 q = reinterpret_cast<const uint4*>(x + 32 * seg)[i];
-        xw[4 * i] = q.x; xw[4 * i + 1] = q.y; xw[4 * i + 2] = q.z; xw[4 * i + 3] = q.w;
-    }
+    // the weight codes and fp16 scale/min loads, all issued before any use
     uint32_t cg[T][BITS], cu[T][BITS];
     uint32_t sv[T][QSC ? 1 : 4];
 #pragma unroll
@@ -267,37 +262,45 @@ __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint16_t* __r
         }
         if (q < NQ && sub == 0 && m == 0) {
             const int r = r0 + t * RPI + rq;
-            if (r < L.I) write_act<BITS>(act, j, L.I, r, silu_mul(v, u));
+            if (r < L.I) write_act<BITS>(act, j, L.I, r, ok ? silu_mul(v, u) : __builtin_nanf(""));
         }
-    }
-}
-
-// NaN activation rows for an expert whose slot id is invalid (nothing is read)
-template <int BITS>
-__device__ __forceinline__ void gate_up_invalid(const Layer& L, uint32_t* act, int j, int r0, int nrows) {
-    const int lane = threadIdx.x & 63;
-    for (int i = lane; i < nrows; i += 64) {
-        const int r = r0 + i;
-        if (r < L.I) write_act<BITS>(act, j, L.I, r, __builtin_nanf(""));
     }
 }
 
 // Kernel 1 (fast path), two-kernel form.
 // grid = (ceil(I / (NW*T*RPI)), k), block = 64*NW.
+// The leading scalar arguments are preloaded into SGPRs at dispatch (kernarg
+// preloading, built with -amdgpu-kernarg-preload-count): the slot-id read and
+// the x loads need no kernel-argument fetch first, so the only memory round
+// trip before the weight loads is the slot id itself.
 template <int BITS, int SPR_T, int T, int NW, bool QSC>
-__global__ __launch_bounds__(64 * NW) void k_gate_up(const Layer L, const uint16_t* __restrict__ x,
-                                                      uint32_t* __restrict__ act) {
+__global__ __launch_bounds__(64 * NW) void k_gate_up(const float* __restrict__ meta,
+                                                      const uint8_t* __restrict__ pool, int64_t slot_bytes,
+                                                      int nslots, const uint16_t* __restrict__ x,
+                                                      uint32_t* __restrict__ act, const Layer L) {
     __shared__ float part[NW][T * 2 * 64];
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = blockIdx.y;
-    const int RPI = 64 / (SPR_T ? SPR_T : L.spr_gu);
-    const int r0 = (blockIdx.x * NW + wv) * (T * RPI);
-    const int slot = __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots));
-    if (slot < 0) {
-        gate_up_invalid<BITS>(L, act, j, r0, T * RPI);
-        return;
+    // issue the slot-id read, the remaining kernel-argument reads and the x loads
+    // together; the scheduling barrier keeps every use (and so every wait) after them
+    const float f = meta[j];
+    const Layer Lc = L;
+    uint32_t xw[16];
+    {
+        const int seg = (threadIdx.x & 63) % (SPR_T ? SPR_T : Lc.spr_gu);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 q = reinterpret_cast<const uint4*>(x + 32 * seg)[i];
+            xw[4 * i] = q.x; xw[4 * i + 1] = q.y; xw[4 * i + 2] = q.z; xw[4 * i + 3] = q.w;
+        }
     }
-    gate_up_rows<BITS, SPR_T, T, QSC>(L, x, act, j, slot, r0, part[wv]);
+    __builtin_amdgcn_sched_barrier(0);
+    const int slot = __builtin_amdgcn_readfirstlane(slot_from(f, nslots));
+    const bool ok = slot >= 0;
+    const uint8_t* base = pool + (int64_t)(ok ? slot : 0) * slot_bytes;
+    const int RPI = 64 / (SPR_T ? SPR_T : Lc.spr_gu);
+    const int r0 = (blockIdx.x * NW + wv) * (T * RPI);
+    gate_up_rows<BITS, SPR_T, T, QSC>(Lc, base, ok, xw, act, j, r0, part[wv]);
 }
 
 // Kernel 1 (generic): any H, G; one wave per (row, expert).
@@ -348,39 +351,50 @@ __global__ __launch_bounds__(64) void k_gate_up_generic(const Layer L, const uin
 // loaded at the start); else y[j*H + h] = y_j[h].
 // ===========================================================================
 template <int BITS, int SPR_T, int T, bool WSUM, bool QSC>
-__device__ __forceinline__ void down_rows(const Layer& L, const uint32_t* __restrict__ act,
-                                          uint16_t* __restrict__ out, float* __restrict__ y, int h0, float* lds) {
+// `meta`, `pool`, `slot_bytes`, `nslots`, `k` and `I` repeat fields of L as
+// the kernel's preloaded scalar arguments (no kernel-argument fetch before the
+// activation loads and the slot-id read). An invalid slot id reads slot 0 and
+// yields NaN partials.
+__device__ __forceinline__ void down_rows(const Layer& L, const float* meta,
+                                          const uint8_t* __restrict__ pool, int64_t slot_bytes, int nslots, int k,
+                                          int I, const uint32_t* __restrict__ act, uint16_t* __restrict__ out,
+                                          float* __restrict__ y, int h0, float* lds) {
     static_assert(!QSC || T % 2 == 0, "quad-shared scales cover two rows per load");
     const int SPR = SPR_T ? SPR_T : L.spr_dn;
     const int RPI = 64 / SPR;
     const int RW = T * RPI;
     const int lane = threadIdx.x & 63;
-    const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const bool active = j < L.k;
+    const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // expert; the block has k waves
     int rr = lane / SPR;
     const int seg = lane - rr * SPR;
     const bool lane_on = rr < RPI;
     rr = lane_on ? rr : RPI - 1;
-    float* part = lds + j * (T * 64);     // [T][64], this wave's partials (j < k)
-    float* rows = lds + L.k * (T * 64);   // [k][RW]
-    uint32_t* stage = reinterpret_cast<uint32_t*>(rows + L.k * RW) + (int64_t)j * (L.I / 32 * 36);
-    const int slot = active ? __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots)) : -1;
-    const float wj = (WSUM && active) ? L.meta[L.k + j] : 0.f;  // issued now, used at the end
+    float* part = lds + j * (T * 64);   // [T][64], this wave's partials (j < k)
+    float* rows = lds + k * (T * 64);   // [k][RW]
+    uint32_t* stage = reinterpret_cast<uint32_t*>(rows + k * RW) + (int64_t)j * (I / 32 * 36);
 
-    if (active) {
+    {
+        // issue the activation loads (their address needs no memory read), the
+        // slot-id and weight reads from meta together; the scheduling barrier keeps
+        // every use (and so every wait) after them
+        const float f = meta[j];
+        const float wj = WSUM ? meta[k + j] : 0.f;  // used at the end
+        const uint4* asrc = reinterpret_cast<const uint4*>(act + (int64_t)j * I);
+        const int na16 = I >> 2;
+        constexpr int APL = SPR_T ? (SPR_T * 8 + 63) / 64 : 8;
+        uint4 apiece[APL];
+#pragma unroll
+        for (int k2 = 0; k2 < APL; ++k2) apiece[k2] = asrc[min(lane + 64 * k2, na16 - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+        const int slot = __builtin_amdgcn_readfirstlane(slot_from(f, nslots));
+        const bool ok = slot >= 0;
         float p[T];
-        if (slot >= 0) {
-            const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
+        {
+            const uint8_t* base = pool + (int64_t)(ok ? slot : 0) * slot_bytes;
             const uint8_t* dcodes = base + 2 * L.nmb;
             const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb) + 2 * L.NGM;
             const uint16_t* mn = sc + 3 * L.NGM;
             const int gi = seg >> L.gsh;
-            const uint4* asrc = reinterpret_cast<const uint4*>(act + (int64_t)j * L.I);
-            const int na16 = L.I >> 2;
-            constexpr int APL = SPR_T ? (SPR_T * 8 + 63) / 64 : 8;
-            uint4 apiece[APL];  // activation first, so staging it waits for nothing else
-#pragma unroll
-            for (int k2 = 0; k2 < APL; ++k2) apiece[k2] = asrc[min(lane + 64 * k2, na16 - 1)];
             uint32_t cd[T][BITS], sv[T];
 #pragma unroll
             for (int t = 0; t < T; ++t) {
@@ -400,16 +414,19 @@ __device__ __forceinline__ void down_rows(const Layer& L, const uint32_t* __rest
 #pragma unroll
             for (int k2 = 0; k2 < APL; ++k2) {
                 const int i = min(lane + 64 * k2, na16 - 1);
-                reinterpret_cast<uint4*>(stage)[i + (i >> 3)] = apiece[k2];
+                // halves swapped, so the compiler cannot fold the load and this store
+                // into one copy placed here (the loads must stay at the kernel's start)
+                const uint4 a = apiece[k2];
+                reinterpret_cast<uint4*>(stage)[i + (i >> 3)] = make_uint4(a.z, a.w, a.x, a.y);
             }
             wave_sync_lds();
             uint32_t AH[16], AL[16];
             const uint4* ap = reinterpret_cast<const uint4*>(stage + seg * 36);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint4 hq = ap[i], lq = ap[4 + i];
-                AH[4 * i] = hq.x; AH[4 * i + 1] = hq.y; AH[4 * i + 2] = hq.z; AH[4 * i + 3] = hq.w;
-                AL[4 * i] = lq.x; AL[4 * i + 1] = lq.y; AL[4 * i + 2] = lq.z; AL[4 * i + 3] = lq.w;
+                const uint4 hq = ap[i], lq = ap[4 + i];  // halves swapped in the stage
+                AH[4 * i] = hq.z; AH[4 * i + 1] = hq.w; AH[4 * i + 2] = hq.x; AH[4 * i + 3] = hq.y;
+                AL[4 * i] = lq.z; AL[4 * i + 1] = lq.w; AL[4 * i + 2] = lq.x; AL[4 * i + 3] = lq.y;
             }
             float vh, th, vl, tl;
             operand_sums<BITS>(AH, vh, th);
@@ -419,7 +436,7 @@ __device__ __forceinline__ void down_rows(const Layer& L, const uint32_t* __rest
             const uint32_t B = bias_vgpr();
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-                const bool ok = lane_on && (h0 + t * RPI + rr < L.H);
+                const bool row_ok = lane_on && (h0 + t * RPI + rr < L.H);
                 const float d = chunk_dot_hl<BITS>(cd[t], AH, AL, bias, B);
                 uint32_t s_, m_;
                 if (QSC) {
@@ -431,11 +448,8 @@ __device__ __forceinline__ void down_rows(const Layer& L, const uint32_t* __rest
                     m_ = sv[t] >> 16;
                 }
                 const float v = h2f((uint16_t)s_) * d + h2f((uint16_t)m_) * as;
-                p[t] = ok ? v : 0.f;
+                p[t] = !ok ? __builtin_nanf("") : (row_ok ? v : 0.f);
             }
-        } else {
-#pragma unroll
-            for (int t = 0; t < T; ++t) p[t] = __builtin_nanf("");
         }
 #pragma unroll
         for (int t = 0; t < T; ++t) part[t * 64 + lane] = p[t];
@@ -466,7 +480,7 @@ __device__ __forceinline__ void down_rows(const Layer& L, const uint32_t* __rest
             const int h = h0 + q;
             if (h < L.H) {
                 float acc = 0.f;
-                for (int jj = 0; jj < L.k; ++jj) acc += rows[jj * RW + q];
+                for (int jj = 0; jj < k; ++jj) acc += rows[jj * RW + q];
                 out[h] = f32_to_bf16(acc);
             }
         }
@@ -476,11 +490,15 @@ __device__ __forceinline__ void down_rows(const Layer& L, const uint32_t* __rest
 // Kernel 2 (fast path), two-kernel form.
 // grid = ceil(H / (T*RPI)), block = 64*k, dynamic LDS as for down_rows.
 template <int BITS, int SPR_T, int T, bool WSUM, bool QSC>
-__global__ __launch_bounds__(1024) void k_down(const Layer L, const uint32_t* __restrict__ act,
-                                               uint16_t* __restrict__ out, float* __restrict__ y) {
+// The leading scalar arguments are preloaded into SGPRs at dispatch, as for
+// k_gate_up.
+__global__ __launch_bounds__(1024) void k_down(const float* meta, const uint8_t* __restrict__ pool,
+                                               int64_t slot_bytes, int nslots, int k, int I,
+                                               const uint32_t* __restrict__ act, uint16_t* __restrict__ out,
+                                               float* __restrict__ y, const Layer L) {
     extern __shared__ float lds[];
     const int RW = T * (64 / (SPR_T ? SPR_T : L.spr_dn));
-    down_rows<BITS, SPR_T, T, WSUM, QSC>(L, act, out, y, blockIdx.x * RW, lds);
+    down_rows<BITS, SPR_T, T, WSUM, QSC>(L, meta, pool, slot_bytes, nslots, k, I, act, out, y, blockIdx.x * RW, lds);
 }
 
 // Kernel 2 (generic): any I, G; one workgroup (k waves) per output row.
@@ -583,7 +601,8 @@ static void launch_gu(const Layer& L, const uint16_t* x, uint32_t* act, hipStrea
     const int RPI = 64 / L.spr_gu;
     const int rows_wg = NW * T * RPI;
     const dim3 grid((L.I + rows_wg - 1) / rows_wg, L.k);
-    hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW, QSC>), grid, dim3(64 * NW), 0, st, L, x, act);
+    hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW, QSC>), grid, dim3(64 * NW), 0, st, L.meta, L.pool, L.slot_bytes,
+                       L.nslots, x, act, L);
 }
 
 template <int BITS>
@@ -624,8 +643,8 @@ template <int BITS, int SPR, int T, bool WSUM, bool QSC>
 static void launch_dn(const Layer& L, const uint32_t* act, uint16_t* out, float* y, hipStream_t st) {
     const int RW = T * (64 / L.spr_dn);
     const size_t lds = dn_lds_bytes(L, T);
-    hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM, QSC>), dim3((L.H + RW - 1) / RW), dim3(64 * L.k), lds, st, L,
-                       act, out, y);
+    hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM, QSC>), dim3((L.H + RW - 1) / RW), dim3(64 * L.k), lds, st, L.meta,
+                       L.pool, L.slot_bytes, L.nslots, L.k, L.I, act, out, y, L);
 }
 
 template <int BITS, bool WSUM>
