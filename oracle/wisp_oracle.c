@@ -21,8 +21,9 @@
  * so every float expression rounds exactly where the reference's torch ops
  * round).
  *
- * Pinning (each function is checked by something other than itself; all in
- * tests/test_oracle.py):
+ * Pinning (each function is checked by something other than itself; in
+ * tests/test_oracle.py, and against the reference's own outputs in
+ * tests/test_golden.py):
  *   wo_f32_to_f16 / wo_f32_to_bf16 / wo_*_to_f32 .. torch's own conversions on
  *       random, tie, subnormal, overflow and NaN inputs
  *   wo_expert_nbytes ... reference KATs (test_quant.py:39-40, architecture.md:82)
@@ -31,14 +32,19 @@
  *                        evaluated independently for every element
  *   wo_quantize ........ hand-derived KATs (half-even ties, constant group,
  *                        1e-5 clamp), nearest-level property, reference error
- *                        bounds and monotonicity (test_quant.py:15-34)
+ *                        bounds and monotonicity (test_quant.py:15-34); the
+ *                        reference quantize's bytes (sha256, 12 experts)
  *   wo_dequant ......... hand KATs incl. the fp32-then-bf16 double rounding,
- *                        numpy float32 elementwise semantics
+ *                        numpy float32 elementwise semantics; the reference
+ *                        dequant's bf16 output (sha256, 12 experts)
  *   wo_moe_layer_f64 ... dense numpy dequant->matvec (the unfolded form) at
- *                        several shapes and bit widths
+ *                        several shapes and bit widths; the reference kernels'
+ *                        outputs (q4, q4_fast, q3_fast), every element equal
+ *                        under the fixture's bf16 rounding
  *   wo_rope ............ hand KAT (d = 2: complex multiplication), rotation
  *                        preserves the norm and composes (angle addition),
- *                        float64 textbook rotate-half formula
+ *                        float64 textbook rotate-half formula; the reference
+ *                        rope_decode's fp32 and bf16 outputs, bit for bit
  * No function is parity-unpinned.
  */
 #include <math.h>
