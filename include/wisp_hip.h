@@ -138,8 +138,8 @@ int64_t wisp_prefill_ws_bytes(int64_t pairs, int64_t H, int64_t I);
 
 /* Grouped MoE prefill: for the (token, expert) pairs of a chunk of T tokens,
  * sorted by expert, every routed expert's token group runs gate/up + SiLU*up
- * and down as bf16 MFMA GEMMs on weight tiles dequantized (bit-exactly) into
- * LDS from slot-pool rows; y = w * down(...) per pair in fp32; per token
+ * and down as bf16 MFMA GEMMs on weight tiles dequantized (bit-exactly) in
+ * registers from slot-pool rows; y = w * down(...) per pair in fp32; per token
  * s[t] = sum of its pairs' y in ascending expert id (fp32).
  * groups: device int32 [ngroups][3] = (slot, first pair, pair count);
  * max_group: the largest pair count (sets the launch shape; results do not
@@ -148,8 +148,9 @@ int64_t wisp_prefill_ws_bytes(int64_t pairs, int64_t H, int64_t I);
  * back: device int32 [T][k], the pair of token t's j-th expert (ascending id),
  * -1 if that expert is not in this call; x: bf16 [T, H]; ws:
  * wisp_prefill_ws_bytes(pairs, H, I), 256-byte aligned. out: bf16 [T, H] =
- * bf16(s), or, when acc (fp32 [T, H]) is not NULL, acc += s and out unused.
- * group must be 128; H, I multiples of 128; bits 4/3/2. An invalid slot id
+ * bf16(s) (8-byte aligned), or, when acc (fp32 [T, H], 16-byte aligned) is
+ * not NULL, acc += s and out unused. group must be 128; H a multiple of 256,
+ * I of 128; 1 <= k <= 32; bits 4/3/2. An invalid slot id
  * makes its pairs' outputs NaN. Replaces the per-expert dequant + F.linear of
  * wisp/moe.py:131-137 (three launches for all routed experts). */
 int wisp_moe_prefill(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const int32_t* groups, int ngroups,

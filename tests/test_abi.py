@@ -149,6 +149,9 @@ def test_prefill_argument_validation():
     assert call(out=None) == _lib.WISP_EINVAL  # neither out nor acc
     assert call(slot_bytes=nb - 16) == _lib.WISP_EINVAL
     assert call(x=ctypes.c_void_p(0x100002)) == _lib.WISP_EALIGN
+    assert call(k=33, T=2, pairs=64) == _lib.WISP_EINVAL  # k <= 32
+    assert call(out=ctypes.c_void_p(0x100004)) == _lib.WISP_EALIGN  # out: 8-byte stores
+    assert call(out=None, acc=ctypes.c_void_p(0x100008)) == _lib.WISP_EALIGN  # acc: 16-byte
     assert L.wisp_prefill_ws_bytes(64, 2048, 768) == 64 * 768 * 2 + 64 * 2048 * 4
 
 

@@ -129,12 +129,21 @@ __device__ __forceinline__ int group_state(const Prefill& F, int u, int& slot, i
     return (slot >= 0 && slot < F.nslots) ? 2 : 1;
 }
 
-// One K step's codes and fp16 scale/min (packed s | m << 16) of a lane's row.
+// A wave's 4 weight row tiles: the lane's code and scale pointers for tile 0
+// (its row and chunk) and the tiles' offsets from them (wave-uniform).
+struct PfRows {
+    const uint8_t* rc;   // codes of tile 0 at the lane's row and chunk
+    const uint16_t* sp;  // fp16 scales of tile 0's row (one per 128-code group)
+    int64_t mn_off;      // mins - scales, in fp16 elements
+    int64_t code_off[4], scale_off[4];
+};
+
+// One K step's codes and fp16 scale/min (packed s | m << 16) of a lane's row in tile j.
 template <int BITS>
-__device__ __forceinline__ void pf_load(const uint8_t* rc, const uint16_t* scp, const uint16_t* mnp, int kc,
-                                        uint32_t* cd, uint32_t& sm) {
-    load_chunk<BITS>(rc + (int64_t)kc * 16 * BITS, cd);  // 128 codes per K step
-    sm = (uint32_t)scp[kc] | ((uint32_t)mnp[kc] << 16);
+__device__ __forceinline__ void pf_load(const PfRows& R, int j, int kc, uint32_t* cd, uint32_t& sm) {
+    load_chunk<BITS>(R.rc + R.code_off[j] + (int64_t)kc * 16 * BITS, cd);  // 128 codes per K step
+    const uint16_t* s = R.sp + R.scale_off[j] + kc;
+    sm = (uint32_t)s[0] | ((uint32_t)s[R.mn_off] << 16);
 }
 
 // The step's 4 MFMA B fragments (k-substeps 0..3) from the lane's chunk.
@@ -146,35 +155,54 @@ __device__ __forceinline__ void pf_bfrag(const uint32_t* cd, uint32_t sm, uint4*
     for (int s = 0; s < 4; ++s) b[s] = make_uint4(v[4 * s], v[4 * s + 1], v[4 * s + 2], v[4 * s + 3]);
 }
 
-// One wave's GEMM over K steps 0..nk-1 for 4 weight row tiles (16 rows each;
-// row pointers rc[j] at the lane's row and chunk, scale/min bases sp/mp[j]) and
-// up to MT 16-token tiles (A row pointers arow[mt], uint4 units at the lane's k
-// offset; tiles at or past `ntile` are skipped). Codes are loaded one step
-// ahead; a step's A fragments are loaded at its start and the dequantization
-// of its four B tiles overlaps their latency. Each A fragment feeds all four
-// row tiles, so the A operand is read once per 64 weight rows.
-template <int BITS, int MT>
-__device__ __forceinline__ void pf_wave_gemm(const uint8_t* const* rc, const uint16_t* const* sp,
-                                             const uint16_t* const* mp, const uint4* const* arow, int nk, int ntile,
-                                             f32x4_t (*acc)[4]) {
+// LDS row stride of a staged A tile in uint4: 16 (one K step, 128 bf16) + 1 pad,
+// so the 16 rows one fragment read touches start 16 bytes apart (no bank
+// conflicts for the 128-bit reads).
+constexpr int kArs = 17;
+
+// One pass of the workgroup GEMM. The 4 waves share the pass's NT*16 A rows
+// (the token or activation rows of the group's pairs), staged one K step at a
+// time in LDS (double-buffered, one barrier per step: each thread copies NT
+// uint4 of the next step, crow[r] = its copy rows r*16 + threadIdx.x/16 at
+// column threadIdx.x%16). Each wave multiplies them with its own 4 weight row
+// tiles (16 rows each; row pointers rc[j] at the lane's row and chunk,
+// scale/min bases sp/mp[j]), whose codes are loaded one step ahead and
+// dequantized in registers. Every thread of the workgroup calls it with the
+// same nk; NT is the pass's exact tile count, so the loop has no branches.
+template <int BITS, int NT>
+__device__ __forceinline__ void pf_gemm(const PfRows& R, const uint4* const* crow, uint4* lds, int nk,
+                                        f32x4_t (*acc)[4]) {
+    constexpr int BUF = NT * 16 * kArs;
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int cm = threadIdx.x >> 4, cc = threadIdx.x & 15;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    u32x4_t av[NT];  // next step's A pieces (ext-vector type: kept in registers)
+#pragma unroll
+    for (int r = 0; r < NT; ++r) av[r] = *reinterpret_cast<const u32x4_t*>(crow[r]);
     uint32_t cd[4][BITS], sm[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pf_load<BITS>(rc[j], sp[j], mp[j], 0, cd[j], sm[j]);
+    for (int j = 0; j < 4; ++j) pf_load<BITS>(R, j, 0, cd[j], sm[j]);
+    u32x4_t* ldv = reinterpret_cast<u32x4_t*>(lds);
+#pragma unroll
+    for (int r = 0; r < NT; ++r) ldv[(r * 16 + cm) * kArs + cc] = av[r];
     for (int kc = 0; kc < nk; ++kc) {
-        uint4 xa[MT][4];
+        const bool more = kc + 1 < nk;
+        const int kn = more ? kc + 1 : kc;  // the last step loads itself again (in bounds)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-            if (mt < ntile)
-#pragma unroll
-                for (int s = 0; s < 4; ++s) xa[mt][s] = arow[mt][kc * 16 + s];
-        const int kn = kc + 1 < nk ? kc + 1 : kc;  // the last step loads itself again (in bounds)
+        for (int r = 0; r < NT; ++r) av[r] = *reinterpret_cast<const u32x4_t*>(crow[r] + kn * 16);
         uint32_t cdn[4][BITS], smn[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pf_load<BITS>(rc[j], sp[j], mp[j], kn, cdn[j], smn[j]);
+        for (int j = 0; j < 4; ++j) pf_load<BITS>(R, j, kn, cdn[j], smn[j]);
+        __syncthreads();  // step kc's A tile is in buffer kc&1; step kc-1's reads are done
+        const uint4* A = lds + (kc & 1) * BUF;
+        uint4 xa[NT][4];
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) xa[mt][s] = A[(mt * 16 + n) * kArs + 4 * g + s];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint4 b[4];
@@ -182,8 +210,11 @@ __device__ __forceinline__ void pf_wave_gemm(const uint8_t* const* rc, const uin
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-                    if (mt < ntile) acc[mt][j] = mfma16(xa[mt][s], b[s], acc[mt][j]);
+                for (int mt = 0; mt < NT; ++mt) acc[mt][j] = mfma16(xa[mt][s], b[s], acc[mt][j]);
+        }
+        if (more) {  // buffer (kc+1)&1 was last read in step kc-1, before this step's barrier
+#pragma unroll
+            for (int r = 0; r < NT; ++r) ldv[((kc + 1) & 1) * BUF + (r * 16 + cm) * kArs + cc] = av[r];
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -194,12 +225,69 @@ __device__ __forceinline__ void pf_wave_gemm(const uint8_t* const* rc, const uin
     }
 }
 
+// One pass of kernel gate_up over NT 16-token tiles starting at pair mb of the
+// group: A rows are the pairs' tokens (rows past cnt repeat the last pair).
+template <int BITS, int NT>
+__device__ __forceinline__ void pf_gate_up_pass(const Prefill& F, const PfRows& R, int nk, int c0, int p0, int cnt,
+                                                int mb, uint4* lds) {
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const uint4* crow[NT];
+#pragma unroll
+    for (int r = 0; r < NT; ++r) {
+        int t = F.tok[p0 + min(mb + r * 16 + (int)(threadIdx.x >> 4), cnt - 1)];
+        t = min(max(t, 0), F.T - 1);
+        crow[r] = reinterpret_cast<const uint4*>(F.x + (int64_t)t * F.H) + (threadIdx.x & 15);
+    }
+    f32x4_t acc[NT][4];
+    pf_gemm<BITS, NT>(R, crow, lds, nk, acc);
+    // D layout: acc[mt][j][i] = token mb + mt*16 + 4g + i, row tile j column n
+#pragma unroll
+    for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = mb + mt * 16 + 4 * g + i;
+            if (m < cnt) {
+                uint16_t* dst = F.act + (int64_t)(p0 + m) * F.I + c0 + n;
+                dst[0] = f32_to_bf16(silu_mul(acc[mt][0][i], acc[mt][2][i]));
+                dst[16] = f32_to_bf16(silu_mul(acc[mt][1][i], acc[mt][3][i]));
+            }
+        }
+}
+
+// One pass of kernel down (A rows: the pairs' activations), stores w * y.
+template <int BITS, int NT>
+__device__ __forceinline__ void pf_down_pass(const Prefill& F, const PfRows& R, int nk, int h0, int p0, int cnt,
+                                             int mb, uint4* lds) {
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const uint4* crow[NT];
+#pragma unroll
+    for (int r = 0; r < NT; ++r) {
+        const int m = min(mb + r * 16 + (int)(threadIdx.x >> 4), cnt - 1);
+        crow[r] = reinterpret_cast<const uint4*>(F.act + (int64_t)(p0 + m) * F.I) + (threadIdx.x & 15);
+    }
+    f32x4_t acc[NT][4];
+    pf_gemm<BITS, NT>(R, crow, lds, nk, acc);
+#pragma unroll
+    for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = mb + mt * 16 + 4 * g + i;
+            if (m < cnt) {
+                const float wp = F.w[p0 + m];
+                float* dst = F.y + (int64_t)(p0 + m) * F.H + h0 + n;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) dst[j * 16] = wp * acc[mt][j][i];
+            }
+        }
+}
+
 // ---------------------------------------------------------------------------
 // gate_up: act[p][r] = bf16(silu(g) * u), g/u = x[tok[p]] . W{gate,up}[r]
 // grid (I/128, U, Z); wave w of workgroup x owns act columns c0 = (4x + w)*32
 // .. +31: row tiles {gate c0, gate c0+16, up c0, up c0+16}.
 template <int BITS, int MT>
-__global__ __launch_bounds__(256) void k_pf_gate_up(const Prefill F) {
+__global__ __launch_bounds__(256, 1) void k_pf_gate_up(const Prefill F) {
+    __shared__ uint4 lds[2 * MT * 16 * kArs];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int c0 = (blockIdx.x * kPfWaves + wv) * 32, u = blockIdx.y;
@@ -216,38 +304,24 @@ __global__ __launch_bounds__(256) void k_pf_gate_up(const Prefill F) {
     const uint16_t* mn = sc + 3 * F.NGM;
     const int nk = F.H / 128;
     const int64_t rowb = (int64_t)F.H * BITS / 8;
-    const uint8_t* rc[4];
-    const uint16_t *sp[4], *mp[4];
+    PfRows R;
+    R.rc = base + (int64_t)(c0 + n) * rowb + g * 4 * BITS;
+    R.sp = sc + (int64_t)(c0 + n) * nk;
+    R.mn_off = mn - sc;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int mat = j >> 1, r = c0 + (j & 1) * 16 + n;
-        rc[j] = base + mat * F.nmb + (int64_t)r * rowb + g * 4 * BITS;
-        sp[j] = sc + (int64_t)mat * F.NGM + (int64_t)r * nk;
-        mp[j] = mn + (int64_t)mat * F.NGM + (int64_t)r * nk;
+    for (int j = 0; j < 4; ++j) {  // tiles gate c0, gate c0+16, up c0, up c0+16
+        const int mat = j >> 1, dr = (j & 1) * 16;
+        R.code_off[j] = mat * F.nmb + dr * rowb;
+        R.scale_off[j] = (int64_t)mat * F.NGM + (int64_t)dr * nk;
     }
     constexpr int MB = MT * 16;
     for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
-        const uint4* arow[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            int t = F.tok[p0 + min(mb + mt * 16 + n, cnt - 1)];  // rows past cnt repeat the last pair
-            t = min(max(t, 0), F.T - 1);
-            arow[mt] = reinterpret_cast<const uint4*>(F.x + (int64_t)t * F.H) + g * 4;
-        }
-        f32x4_t acc[MT][4];
-        pf_wave_gemm<BITS, MT>(rc, sp, mp, arow, nk, (cnt - mb + 15) / 16, acc);
-        // D layout: acc[mt][j][i] = token mb + mt*16 + 4g + i, row tile j column n
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = mb + mt * 16 + 4 * g + i;
-                if (m < cnt) {
-                    uint16_t* dst = F.act + (int64_t)(p0 + m) * F.I + c0 + n;
-                    dst[0] = f32_to_bf16(silu_mul(acc[mt][0][i], acc[mt][2][i]));
-                    dst[16] = f32_to_bf16(silu_mul(acc[mt][1][i], acc[mt][3][i]));
-                }
-            }
+        const int nt = min(MT, (cnt - mb + 15) / 16);  // 16-token tiles in this pass (workgroup-uniform)
+        if (MT >= 4 && nt >= 4) pf_gate_up_pass<BITS, (MT >= 4 ? 4 : 1)>(F, R, nk, c0, p0, cnt, mb, lds);
+        else if (MT >= 3 && nt == 3) pf_gate_up_pass<BITS, (MT >= 3 ? 3 : 1)>(F, R, nk, c0, p0, cnt, mb, lds);
+        else if (MT >= 2 && nt == 2) pf_gate_up_pass<BITS, (MT >= 2 ? 2 : 1)>(F, R, nk, c0, p0, cnt, mb, lds);
+        else pf_gate_up_pass<BITS, 1>(F, R, nk, c0, p0, cnt, mb, lds);
+        __syncthreads();  // the next pass restages LDS buffer 0
     }
 }
 
@@ -255,7 +329,8 @@ __global__ __launch_bounds__(256) void k_pf_gate_up(const Prefill F) {
 // down: y[p][h] = w[p] * (act[p] . Wdown[h]), fp32
 // grid (H/256, U, Z); wave w of workgroup x owns rows (4x + w)*64 .. +63.
 template <int BITS, int MT>
-__global__ __launch_bounds__(256) void k_pf_down(const Prefill F) {
+__global__ __launch_bounds__(256, 1) void k_pf_down(const Prefill F) {
+    __shared__ uint4 lds[2 * MT * 16 * kArs];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int h0 = (blockIdx.x * kPfWaves + wv) * 64, u = blockIdx.y;
@@ -271,58 +346,64 @@ __global__ __launch_bounds__(256) void k_pf_down(const Prefill F) {
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * F.nmb);
     const uint16_t* mn = sc + 3 * F.NGM;
     const int nk = F.I / 128;
-    const uint8_t* rc[4];
-    const uint16_t *sp[4], *mp[4];
+    const int64_t rowb = (int64_t)F.I * BITS / 8;
+    PfRows R;
+    R.rc = base + 2 * F.nmb + (int64_t)(h0 + n) * rowb + g * 4 * BITS;
+    R.sp = sc + 2 * (int64_t)F.NGM + (int64_t)(h0 + n) * nk;
+    R.mn_off = mn - sc;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int h = h0 + j * 16 + n;
-        rc[j] = base + 2 * F.nmb + (int64_t)h * ((int64_t)F.I * BITS / 8) + g * 4 * BITS;
-        sp[j] = sc + 2 * (int64_t)F.NGM + (int64_t)h * nk;
-        mp[j] = mn + 2 * (int64_t)F.NGM + (int64_t)h * nk;
+    for (int j = 0; j < 4; ++j) {  // tiles h0, h0+16, h0+32, h0+48
+        R.code_off[j] = (int64_t)j * 16 * rowb;
+        R.scale_off[j] = (int64_t)j * 16 * nk;
     }
     constexpr int MB = MT * 16;
     for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
-        const uint4* arow[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const int m = min(mb + mt * 16 + n, cnt - 1);
-            arow[mt] = reinterpret_cast<const uint4*>(F.act + (int64_t)(p0 + m) * F.I) + g * 4;
-        }
-        f32x4_t acc[MT][4];
-        pf_wave_gemm<BITS, MT>(rc, sp, mp, arow, nk, (cnt - mb + 15) / 16, acc);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = mb + mt * 16 + 4 * g + i;
-                if (m < cnt) {
-                    const float wp = F.w[p0 + m];
-                    float* dst = F.y + (int64_t)(p0 + m) * F.H + h0 + n;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) dst[j * 16] = wp * acc[mt][j][i];
-                }
-            }
+        const int nt = min(MT, (cnt - mb + 15) / 16);
+        if (MT >= 4 && nt >= 4) pf_down_pass<BITS, (MT >= 4 ? 4 : 1)>(F, R, nk, h0, p0, cnt, mb, lds);
+        else if (MT >= 3 && nt == 3) pf_down_pass<BITS, (MT >= 3 ? 3 : 1)>(F, R, nk, h0, p0, cnt, mb, lds);
+        else if (MT >= 2 && nt == 2) pf_down_pass<BITS, (MT >= 2 ? 2 : 1)>(F, R, nk, h0, p0, cnt, mb, lds);
+        else pf_down_pass<BITS, 1>(F, R, nk, h0, p0, cnt, mb, lds);
+        __syncthreads();
     }
 }
 
 // s = sum_j y[back[t*k + j]][h], j in ascending expert id (back = -1: no pair in
-// this call); out[t][h] = bf16(s), or acc[t][h] += s when acc is given
+// this call); out[t][h] = bf16(s), or acc[t][h] += s when acc is given.
+// A thread takes 4 consecutive h of one token; its up to KMAX y rows are all
+// requested before the ordered sum (k <= KMAX; H % 4 == 0).
+template <int KMAX>
 __global__ __launch_bounds__(256) void k_pf_combine(const float* __restrict__ y, const int32_t* __restrict__ back,
                                                     int T, int k, int H, int P, uint16_t* __restrict__ out,
                                                     float* __restrict__ acc) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= (int64_t)T * H) return;
     const int t = (int)(i / H), h = (int)(i - (int64_t)t * H);
-    float s = 0.f;
-    for (int j = 0; j < k; ++j) {
-        const int p = back[t * k + j];
-        if (p == -1) continue;
-        s += (p >= 0 && p < P) ? y[(int64_t)p * H + h] : __builtin_nanf("");
+    int pj[KMAX];
+    float4 v[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+        pj[j] = j < k ? back[t * k + j] : -1;
+        const bool in = pj[j] >= 0 && pj[j] < P;
+        v[j] = in ? *reinterpret_cast<const float4*>(y + (int64_t)pj[j] * H + h) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    if (acc)
-        acc[i] += s;
-    else
-        out[i] = f32_to_bf16(s);
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+        if (pj[j] == -1) continue;
+        if (pj[j] < 0 || pj[j] >= P) {
+            const float nan = __builtin_nanf("");
+            v[j] = make_float4(nan, nan, nan, nan);
+        }
+        s.x += v[j].x; s.y += v[j].y; s.z += v[j].z; s.w += v[j].w;
+    }
+    if (acc) {
+        float4* a = reinterpret_cast<float4*>(acc + i);
+        float4 o = *a;
+        o.x += s.x; o.y += s.y; o.z += s.z; o.w += s.w;
+        *a = o;
+    } else {
+        *reinterpret_cast<uint2*>(out + i) = make_uint2(pack_bf16x2(s.x, s.y), pack_bf16x2(s.z, s.w));
+    }
 }
 
 // MT (16-token tiles per wave and pass) from the largest group; Z workgroups
@@ -364,13 +445,14 @@ extern "C" int wisp_moe_prefill(const uint8_t* pool, int64_t slot_bytes, int64_t
     if (group != 128) return fail_inval("the grouped prefill needs group 128 (one quant group per K step)");
     if (H % 256 || I % 128 || H > (1 << 16) || I > (1 << 16))
         return fail_inval("H a multiple of 256 and I of 128, both <= 65536");
-    if (T < 1 || k < 1 || ngroups < 1 || pairs < 1 || pairs > (int64_t)T * k)
-        return fail_inval("need 1 <= pairs <= T*k and at least one group");
+    if (T < 1 || k < 1 || k > 32 || ngroups < 1 || pairs < 1 || pairs > (int64_t)T * k)
+        return fail_inval("need 1 <= k <= 32, 1 <= pairs <= T*k and at least one group");
     if (nslots < 1 || nslots > (1 << 24)) return fail_inval("nslots out of range");
     const int64_t n = H * I;
     if (slot_bytes < wisp_expert_nbytes(n, bits, group)) return fail_inval("slot_bytes < expert size");
-    if (!aligned(pool, 16) || slot_bytes % 16 || !aligned(x, 16) || !aligned(ws, 256)) {
-        set_error("pool, x and ws must be 16/16/256-byte aligned, slot_bytes a multiple of 16");
+    if (!aligned(pool, 16) || slot_bytes % 16 || !aligned(x, 16) || !aligned(ws, 256) || (out && !aligned(out, 8)) ||
+        (acc && !aligned(acc, 16))) {
+        set_error("pool, x, ws, out and acc must be 16/16/256/8/16-byte aligned, slot_bytes a multiple of 16");
         return WISP_EALIGN;
     }
     Prefill F;
@@ -396,8 +478,12 @@ extern "C" int wisp_moe_prefill(const uint8_t* pool, int64_t slot_bytes, int64_t
     case 3: launch_pf<3>(F, ngroups, max_group, st); break;
     default: launch_pf<2>(F, ngroups, max_group, st); break;
     }
-    const int64_t total = (int64_t)T * H;
-    hipLaunchKernelGGL(k_pf_combine, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
-                       (const float*)F.y, back, T, k, (int)H, (int)pairs, out, acc);
+    const unsigned nblk = (unsigned)(((int64_t)T * H / 4 + 255) / 256);
+    if (k <= 8)
+        hipLaunchKernelGGL(k_pf_combine<8>, dim3(nblk), dim3(256), 0, st, (const float*)F.y, back, T, k, (int)H,
+                           (int)pairs, out, acc);
+    else
+        hipLaunchKernelGGL(k_pf_combine<32>, dim3(nblk), dim3(256), 0, st, (const float*)F.y, back, T, k, (int)H,
+                           (int)pairs, out, acc);
     return check_launch("k_pf");
 }
