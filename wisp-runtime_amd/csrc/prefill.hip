@@ -131,19 +131,53 @@ __device__ __forceinline__ int group_state(const Prefill& F, int u, int& slot, i
 
 // A wave's 4 weight row tiles: the lane's code and scale pointers for tile 0
 // (its row and chunk) and the tiles' offsets from them (wave-uniform).
+// Scale/min table of a workgroup's 256 weight rows, staged in LDS when a row has
+// at most kPfSmSteps quant groups (K <= 2048): entry [local row][K step] =
+// s | m << 16 (fp16 bits).
+constexpr int kPfSmSteps = 16;
+
 struct PfRows {
     const uint8_t* rc;   // codes of tile 0 at the lane's row and chunk
-    const uint16_t* sp;  // fp16 scales of tile 0's row (one per 128-code group)
+    const uint16_t* sp;  // fp16 scales of tile 0's row (one per 128-code group), global
     int64_t mn_off;      // mins - scales, in fp16 elements
     int64_t code_off[4], scale_off[4];
+    const uint32_t* sml;  // LDS table at tile 0's row (nullptr: read sp/mn from global memory)
+    int sml_off[4];       // per-tile offsets in the LDS table, entries
 };
 
 // One K step's codes and fp16 scale/min (packed s | m << 16) of a lane's row in tile j.
 template <int BITS>
 __device__ __forceinline__ void pf_load(const PfRows& R, int j, int kc, uint32_t* cd, uint32_t& sm) {
     load_chunk<BITS>(R.rc + R.code_off[j] + (int64_t)kc * 16 * BITS, cd);  // 128 codes per K step
-    const uint16_t* s = R.sp + R.scale_off[j] + kc;
-    sm = (uint32_t)s[0] | ((uint32_t)s[R.mn_off] << 16);
+    if (R.sml) {
+        sm = R.sml[R.sml_off[j] + kc];
+    } else {
+        const uint16_t* s = R.sp + R.scale_off[j] + kc;
+        sm = (uint32_t)s[0] | ((uint32_t)s[R.mn_off] << 16);
+    }
+}
+
+// Stage nrows * nk scale/min pairs (two contiguous fp16 runs, scales at `sc`,
+// mins at sc + mn_off) into sml[local0 * nk ...] packed s | m << 16, with
+// 16-byte loads (nrows * nk a multiple of 8; both runs 16-byte aligned). All
+// threads of the workgroup take part.
+__device__ __forceinline__ void pf_stage_scales(const uint16_t* sc, int64_t mn_off, int nrows, int nk, int local0,
+                                                uint32_t* sml) {
+    const int total = nrows * nk;  // entries, 8 per 16-byte load
+    for (int e = (int)threadIdx.x * 8; e < total; e += 256 * 8) {
+        const uint4 vs = *reinterpret_cast<const uint4*>(sc + e);
+        const uint4 vm = *reinterpret_cast<const uint4*>(sc + mn_off + e);
+        const uint32_t s4[4] = {vs.x, vs.y, vs.z, vs.w}, m4[4] = {vm.x, vm.y, vm.z, vm.w};
+        uint32_t o[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            o[2 * i] = (s4[i] & 0xFFFFu) | (m4[i] << 16);
+            o[2 * i + 1] = (s4[i] >> 16) | (m4[i] & 0xFFFF0000u);
+        }
+        uint4* dst = reinterpret_cast<uint4*>(sml + local0 * nk + e);
+        dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+        dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
 }
 
 // The step's 4 MFMA B fragments (k-substeps 0..3) from the lane's chunk.
@@ -163,39 +197,51 @@ constexpr int kArs = 17;
 // One pass of the workgroup GEMM. The 4 waves share the pass's NT*16 A rows
 // (the token or activation rows of the group's pairs), staged one K step at a
 // time in LDS (double-buffered, one barrier per step: each thread copies NT
-// uint4 of the next step, crow[r] = its copy rows r*16 + threadIdx.x/16 at
-// column threadIdx.x%16). Each wave multiplies them with its own 4 weight row
-// tiles (16 rows each; row pointers rc[j] at the lane's row and chunk,
-// scale/min bases sp/mp[j]), whose codes are loaded one step ahead and
-// dequantized in registers. Every thread of the workgroup calls it with the
-// same nk; NT is the pass's exact tile count, so the loop has no branches.
+// uint4 of a step, crow[r] = its copy rows r*16 + threadIdx.x/16 at column
+// threadIdx.x%16). Each wave multiplies them with its own 4 weight row tiles
+// (PfRows), whose codes are dequantized in registers.
+// Prefetch: step kc's codes are requested at the start of step kc-1 and the
+// A tile of step kc+1 at the start of step kc-1 (written to LDS after step kc's
+// MFMAs). Loads go into two register sets that swap roles every step (the
+// loop is unrolled by two), never through a register copy: on this hardware a
+// copy of a load's destination waits for the load, which would serialise the
+// prefetch. Every thread of the workgroup calls it with the same nk; NT is the
+// pass's exact tile count, so the loop has no branches.
+template <int BITS, int NT>
+struct PfStage {
+    uint32_t cd[4][BITS], sm[4];  // one step's codes and packed scale/min, per row tile
+    u32x4_t av[NT];               // this thread's pieces of one step's A tile
+};
+
 template <int BITS, int NT>
 __device__ __forceinline__ void pf_gemm(const PfRows& R, const uint4* const* crow, uint4* lds, int nk,
                                         f32x4_t (*acc)[4]) {
     constexpr int BUF = NT * 16 * kArs;
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const int cm = threadIdx.x >> 4, cc = threadIdx.x & 15;
+    u32x4_t* ldv = reinterpret_cast<u32x4_t*>(lds);
 #pragma unroll
     for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    u32x4_t av[NT];  // next step's A pieces (ext-vector type: kept in registers)
+    auto load_codes = [&](PfStage<BITS, NT>& S, int kc) {
 #pragma unroll
-    for (int r = 0; r < NT; ++r) av[r] = *reinterpret_cast<const u32x4_t*>(crow[r]);
-    uint32_t cd[4][BITS], sm[4];
+        for (int j = 0; j < 4; ++j) pf_load<BITS>(R, j, kc, S.cd[j], S.sm[j]);
+    };
+    auto load_a = [&](PfStage<BITS, NT>& S, int kc) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pf_load<BITS>(R, j, 0, cd[j], sm[j]);
-    u32x4_t* ldv = reinterpret_cast<u32x4_t*>(lds);
+        for (int r = 0; r < NT; ++r) S.av[r] = *reinterpret_cast<const u32x4_t*>(crow[r] + kc * 16);
+    };
+    auto put_a = [&](const PfStage<BITS, NT>& S, int buf) {
 #pragma unroll
-    for (int r = 0; r < NT; ++r) ldv[(r * 16 + cm) * kArs + cc] = av[r];
-    for (int kc = 0; kc < nk; ++kc) {
-        const bool more = kc + 1 < nk;
-        const int kn = more ? kc + 1 : kc;  // the last step loads itself again (in bounds)
-#pragma unroll
-        for (int r = 0; r < NT; ++r) av[r] = *reinterpret_cast<const u32x4_t*>(crow[r] + kn * 16);
-        uint32_t cdn[4][BITS], smn[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pf_load<BITS>(R, j, kn, cdn[j], smn[j]);
+        for (int r = 0; r < NT; ++r) ldv[buf * BUF + (r * 16 + cm) * kArs + cc] = S.av[r];
+    };
+    // step kc: C holds its codes and the A tile of step kc+1; N receives the
+    // codes of step kc+1 and the A tile of step kc+2
+    auto step = [&](PfStage<BITS, NT>& C, PfStage<BITS, NT>& N, int kc) {
+        const int k1 = min(kc + 1, nk - 1), k2 = min(kc + 2, nk - 1);  // past the end: reload (in bounds)
+        load_codes(N, k1);
+        load_a(N, k2);
         __syncthreads();  // step kc's A tile is in buffer kc&1; step kc-1's reads are done
         const uint4* A = lds + (kc & 1) * BUF;
         uint4 xa[NT][4];
@@ -206,23 +252,25 @@ __device__ __forceinline__ void pf_gemm(const PfRows& R, const uint4* const* cro
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint4 b[4];
-            pf_bfrag<BITS>(cd[j], sm[j], b);
+            pf_bfrag<BITS>(C.cd[j], C.sm[j], b);
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
                 for (int mt = 0; mt < NT; ++mt) acc[mt][j] = mfma16(xa[mt][s], b[s], acc[mt][j]);
         }
-        if (more) {  // buffer (kc+1)&1 was last read in step kc-1, before this step's barrier
-#pragma unroll
-            for (int r = 0; r < NT; ++r) ldv[((kc + 1) & 1) * BUF + (r * 16 + cm) * kArs + cc] = av[r];
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-            for (int i = 0; i < BITS; ++i) cd[j][i] = cdn[j][i];
-            sm[j] = smn[j];
-        }
+        if (kc + 1 < nk) put_a(C, (kc + 1) & 1);  // buffer last read in step kc-1
+    };
+    PfStage<BITS, NT> S0, S1;
+    load_a(S0, 0);
+    load_codes(S0, 0);
+    put_a(S0, 0);
+    load_a(S0, min(1, nk - 1));
+    int kc = 0;
+    for (; kc + 1 < nk; kc += 2) {
+        step(S0, S1, kc);
+        step(S1, S0, kc + 1);
     }
+    if (kc < nk) step(S0, S1, kc);
 }
 
 // One pass of kernel gate_up over NT 16-token tiles starting at pair mb of the
@@ -288,6 +336,7 @@ __device__ __forceinline__ void pf_down_pass(const Prefill& F, const PfRows& R, 
 template <int BITS, int MT>
 __global__ __launch_bounds__(256, 1) void k_pf_gate_up(const Prefill F) {
     __shared__ uint4 lds[2 * MT * 16 * kArs];
+    __shared__ uint32_t sml[256 * kPfSmSteps];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int c0 = (blockIdx.x * kPfWaves + wv) * 32, u = blockIdx.y;
@@ -308,11 +357,20 @@ __global__ __launch_bounds__(256, 1) void k_pf_gate_up(const Prefill F) {
     R.rc = base + (int64_t)(c0 + n) * rowb + g * 4 * BITS;
     R.sp = sc + (int64_t)(c0 + n) * nk;
     R.mn_off = mn - sc;
+    R.sml = nullptr;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {  // tiles gate c0, gate c0+16, up c0, up c0+16
         const int mat = j >> 1, dr = (j & 1) * 16;
         R.code_off[j] = mat * F.nmb + dr * rowb;
         R.scale_off[j] = (int64_t)mat * F.NGM + (int64_t)dr * nk;
+        R.sml_off[j] = (mat * 128 + dr) * nk;  // local rows: gate 0..127, up 128..255
+    }
+    if (nk <= kPfSmSteps) {  // the workgroup's 128 gate and 128 up rows' scale/min, once
+        const int r0 = blockIdx.x * kPfWaves * 32;
+        pf_stage_scales(sc + (int64_t)r0 * nk, mn - sc, 128, nk, 0, sml);
+        pf_stage_scales(sc + F.NGM + (int64_t)r0 * nk, mn - sc, 128, nk, 128, sml);
+        __syncthreads();
+        R.sml = sml + (wv * 32 + n) * nk;
     }
     constexpr int MB = MT * 16;
     for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
@@ -331,6 +389,7 @@ __global__ __launch_bounds__(256, 1) void k_pf_gate_up(const Prefill F) {
 template <int BITS, int MT>
 __global__ __launch_bounds__(256, 1) void k_pf_down(const Prefill F) {
     __shared__ uint4 lds[2 * MT * 16 * kArs];
+    __shared__ uint32_t sml[256 * kPfSmSteps];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int h0 = (blockIdx.x * kPfWaves + wv) * 64, u = blockIdx.y;
@@ -351,10 +410,18 @@ __global__ __launch_bounds__(256, 1) void k_pf_down(const Prefill F) {
     R.rc = base + 2 * F.nmb + (int64_t)(h0 + n) * rowb + g * 4 * BITS;
     R.sp = sc + 2 * (int64_t)F.NGM + (int64_t)(h0 + n) * nk;
     R.mn_off = mn - sc;
+    R.sml = nullptr;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {  // tiles h0, h0+16, h0+32, h0+48
         R.code_off[j] = (int64_t)j * 16 * rowb;
         R.scale_off[j] = (int64_t)j * 16 * nk;
+        R.sml_off[j] = j * 16 * nk;
+    }
+    if (nk <= kPfSmSteps) {  // the workgroup's 256 rows' scale/min, once
+        const int hb = blockIdx.x * kPfWaves * 64;
+        pf_stage_scales(sc + 2 * (int64_t)F.NGM + (int64_t)hb * nk, mn - sc, 256, nk, 0, sml);
+        __syncthreads();
+        R.sml = sml + (wv * 64 + n) * nk;
     }
     constexpr int MB = MT * 16;
     for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
