@@ -423,6 +423,8 @@ def run_c5(a) -> dict:
         w = torch.rand((T, K_TOP), generator=torch.Generator().manual_seed(T)).to(torch.bfloat16).float()
         x = torch.randn((T, H), generator=torch.Generator(device=dev).manual_seed(T), device=dev).to(torch.bfloat16)
         order, tok, back, uniq, first, count = K._prefill_plan(sel, list(range(E)), K_TOP)
+        ng_experts = len(uniq)
+        uniq, first, count = K._prefill_chunks(uniq, first, count)
         Pn = int(order.size)
         plans = []
         for l in range(P_):
@@ -458,8 +460,8 @@ def run_c5(a) -> dict:
         reps = max(1, a.c5_reps)
         t = W.timed(g, reps, False) / (reps * P_)
         flops = T * K_TOP * 6 * H * I
-        byts = ng * nb + 2 * T * H + 2 * 2 * Pn * I + 2 * 4 * Pn * H + 2 * T * H
-        out_rows.append({"T": T, "experts_touched": ng, "us": round(t * 1e6, 2),
+        byts = ng_experts * nb + 2 * T * H + 2 * 2 * Pn * I + 2 * 4 * Pn * H + 2 * T * H
+        out_rows.append({"T": T, "experts_touched": ng_experts, "work_items": ng, "us": round(t * 1e6, 2),
                          "TFLOP/s": round(flops / t / 1e12, 2), "mfma_util": round(flops / t / 1e12 / peak_tflops, 4),
                          "GB/s": round(byts / t / 1e9, 1), "hbm_frac": round(byts / t / 1e9 / PEAK_HBM_GBS, 4),
                          "bytes": byts, "flops": flops})

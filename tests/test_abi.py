@@ -186,3 +186,22 @@ def test_no_cpu_fallback():
 def test_meta_layout_helpers():
     m = O.meta(np.array([5, 0, 3]), np.array([0.5, 0.25, 0.25], np.float32))
     assert m.tolist() == [5.0, 0.0, 3.0, 0.5, 0.25, 0.25]
+
+
+@pytest.mark.parametrize("chunk", [64, 32, 1])
+def test_prefill_work_items_partition_each_group(chunk):
+    # work items of the grouped prefill: consecutive pieces of each expert's pair
+    # range, none larger than `chunk`, largest first, covering every pair once
+    rng = np.random.default_rng(chunk)
+    sel = np.stack([rng.choice(16, 4, replace=False) for _ in range(97)])
+    order, tok, back, uniq, first, count = kernels._prefill_plan(sel, list(range(0, 16, 2)), 4)
+    ex, start, cnt = kernels._prefill_chunks(uniq, first, count, chunk)
+    assert (cnt >= 1).all() and (cnt <= chunk).all()
+    assert (np.diff(cnt) <= 0).all()
+    covered = np.zeros(order.size, np.int64)
+    for e, s, c in zip(ex, start, cnt):
+        covered[s:s + c] += 1
+        g = int(np.flatnonzero(uniq == e)[0])
+        assert first[g] <= s and s + c <= first[g] + count[g]
+    assert (covered == 1).all()
+    assert kernels._prefill_chunks(uniq, first, count, 1 << 20)[2].tolist() == sorted(count.tolist(), reverse=True)

@@ -199,6 +199,25 @@ def _prefill_plan(sel_cpu, experts, k):
     return order, (order // k).astype(np.int32), back.astype(np.int32), uniq, first, count
 
 
+PREFILL_CHUNK = 64  # pairs per work item of the grouped prefill: one workgroup pass (4 tiles of 16)
+
+
+def _prefill_chunks(uniq, first, count, chunk=PREFILL_CHUNK):
+    """Split each expert's pair range into work items of at most `chunk` pairs, the
+    largest first. Each item becomes one group of the launch, so every workgroup
+    of the grid has work (a launch sized for the largest group would hold idle
+    workgroups that wait for a free slot before they can exit) and the longest
+    items start first."""
+    import numpy as np
+
+    n = (count + chunk - 1) // chunk
+    ex = np.repeat(uniq, n)
+    start = np.repeat(first, n) + (np.arange(n.sum()) - np.repeat(np.cumsum(n) - n, n)) * chunk
+    cnt = np.minimum(np.repeat(first + count, n) - start, chunk)
+    o = np.argsort(-cnt, kind="stable")
+    return ex[o], start[o], cnt[o]
+
+
 def moe_prefill(pool, expert_slots, x, sel, rw, n, H, I, bits, group=128, acc=None):
     """Grouped MoE over T tokens (the dequant + F.linear loop of moe.py:131-151 as three
     launches). x: [T, H] bf16; sel: [T, k] expert ids; rw: [T, k] routing weights;
@@ -229,6 +248,7 @@ def moe_prefill(pool, expert_slots, x, sel, rw, n, H, I, bits, group=128, acc=No
         if out is not None:
             out.zero_()
         return acc if out is None else out
+    uniq, first, count = _prefill_chunks(uniq, first, count)
     groups = np.stack([np.array([expert_slots[int(e)] for e in uniq], np.int64), first, count], 1).astype(np.int32)
     ints = torch.from_numpy(np.concatenate([groups.reshape(-1), tok, back.reshape(-1)])).to(dev, non_blocking=True)
     g_dev = ints[: groups.size]
