@@ -463,3 +463,19 @@ def test_moe_prefill_expert_chunks_accumulate_and_invalid_slot():
     bad = _run_prefill(pool, x, sel, rw, H, I, bits, slots={**{e: e for e in range(E)}, 2: 99}).float().cpu()
     hit = torch.from_numpy((sel == 2).any(axis=1))
     assert torch.isnan(bad[hit]).all() and torch.isfinite(bad[~hit]).all()
+
+
+@pytest.mark.parametrize("bits", [4, 3])
+@pytest.mark.parametrize("chunk", [1 << 20, 16])
+def test_moe_prefill_any_group_partition(bits, chunk, monkeypatch):
+    # the launch accepts any partition of the pairs into groups: whole experts
+    # (a 300-pair group takes several passes of the grid's z workgroups) or
+    # 16-pair items give the same result as the default work items
+    E, H, I, T, k = 4, 256, 128, 300, 2
+    pool, x, sel, rw = _prefill_case(E, H, I, T, k, bits, seed=77 + bits, hot=True)
+    base = _run_prefill(pool, x, sel, rw, H, I, bits).float()
+    orig = kernels._prefill_chunks
+    monkeypatch.setattr(kernels, "_prefill_chunks", lambda u, f, c, chunk_=None: orig(u, f, c, chunk))
+    got = _run_prefill(pool, x, sel, rw, H, I, bits).float()
+    print(f"prefill partition chunk={chunk} bits={bits}: max |diff| {float((got - base).abs().max()):.3e}")
+    assert torch.equal(got, base)
