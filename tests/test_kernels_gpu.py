@@ -434,7 +434,9 @@ def _run_prefill(pool_np, x, sel, rw, H, I, bits, slots=None, acc=None):
 @pytest.mark.parametrize("bits", [4, 3, 2])
 @pytest.mark.parametrize("E,H,I,T,k,hot", [(6, 256, 128, 1, 2, False), (6, 256, 128, 17, 2, False),
                                           (4, 256, 128, 300, 2, True), (16, 2048, 768, 64, 8, False),
-                                          (12, 512, 384, 40, 4, False)])
+                                          (12, 512, 384, 40, 4, False),
+                                          # K > 2048: scale/min read from global memory, not the LDS table
+                                          (4, 4096, 256, 20, 2, False), (4, 256, 4096, 20, 2, False)])
 def test_moe_prefill_matches_oracle(bits, E, H, I, T, k, hot):
     pool, x, sel, rw = _prefill_case(E, H, I, T, k, bits, seed=E + T + bits, hot=hot)
     out = _run_prefill(pool, x, sel, rw, H, I, bits)
