@@ -233,6 +233,38 @@ int wisp_cache_prepare_layer(void* cache, const int64_t* keys, const float* weig
  * experts, releases the old pool, allocates the new one, re-copies. */
 int wisp_cache_resize(void* cache, int64_t nslots);
 
+/* ---------------------------------------------------------------------------
+ * gpt-oss experts (wisp/gptoss.py). An expert is gate_up [H, 2I] (gate/up
+ * interleaved on the output axis) and down [I, H], input-major, stored in the
+ * flat [3, n] slot layout [gate_up.flat[:n] | gate_up.flat[n:] | down.flat]
+ * (gptoss.py:32-37), plus bf16 biases gate_up_bias [E, 2I], down_bias [E, H]
+ * indexed by expert id.
+ * ------------------------------------------------------------------------- */
+/* gptoss.py:22-29 (mxfp4_to_bf16): blocks [ngroups, 16] uint8 (two e2m1 codes
+ * per byte, low nibble first), scales [ngroups] uint8 (exponent, bias 127) ->
+ * out bf16 [ngroups * 32], bit-exact with the reference's float32 product and
+ * .to(bfloat16) (NaN -> 0x7FC0). blocks and out 16-byte aligned. */
+int wisp_mxfp4_to_bf16(const uint8_t* blocks, const uint8_t* scales, int64_t ngroups, uint16_t* out, void* stream);
+
+/* Bytes of the wisp_gptoss_decode workspace (fp32 partial sums). */
+int64_t wisp_gptoss_ws_bytes(int k, int64_t H, int64_t I);
+
+/* gptoss.py:126-131 (PagedGptOssBlock.forward, decode N == 1): for the k routed
+ * experts, gu = x @ W_gu + gate_up_bias[e], the clamped SwiGLU
+ * act = (clamp(up, -limit, limit) + 1) * gate * sigmoid(alpha * gate) with
+ * gate = min(gu[2i], limit), up = gu[2i+1], o = act @ W_d + down_bias[e], and
+ * out = sum_j w_j * o_j, with bf16 weights (bit-exact dequant) and the
+ * reference's bf16 rounding of every intermediate tensor (fp32 products and
+ * sums). meta = float32 [slot ids (k) | weights (k) | expert ids (k)] on the
+ * device (read at run time, so graphs follow it); an invalid slot or expert id
+ * makes the output NaN. bits 4/3/2; H % 32 == 0, I % 16 == 0, group % 32 == 0;
+ * pool and slot_bytes aligned as for wisp_moe_decode; x 4-byte, ws 16-byte
+ * aligned, ws of wisp_gptoss_ws_bytes(k, H, I). Three launches. */
+int wisp_gptoss_decode(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k, int64_t H,
+                       int64_t I, int bits, int64_t group, const uint16_t* x, const uint16_t* gate_up_bias,
+                       const uint16_t* down_bias, int64_t n_experts, float alpha, float limit, void* ws,
+                       uint16_t* out, void* stream);
+
 /* Launch-shape tuning, process-wide: gu_rows = rows of one expert per wave in
  * kernel 1, gu_waves = waves per workgroup in kernel 1, dn_iters = row
  * iterations per workgroup in kernel 2 (each in {1,2,4,8}; 0 keeps the

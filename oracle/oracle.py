@@ -254,3 +254,82 @@ def moe_prefill_f64(pool: np.ndarray, expert_slots: dict, x_bf16: np.ndarray, se
         a = bf16_bits_to_f32(f32_to_bf16_bits(a.astype(np.float32))).reshape(a.shape).astype(np.float64)
         out[tt] += rw[tt, jj][:, None] * (a @ Wd.T)
     return out
+
+
+# ---------------------------------------------------------------- gpt-oss experts
+# e2m1 code -> value (gptoss.py:19)
+FP4 = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0)
+
+
+def _bf16r(a) -> np.ndarray:
+    """Round binary32 values through bf16 (RTNE) and back, as a bf16 tensor op does."""
+    a = np.asarray(a, np.float32)
+    return bf16_bits_to_f32(f32_to_bf16_bits(a)).reshape(a.shape)
+
+
+def mxfp4_to_bf16_bits(blocks, scales) -> np.ndarray:
+    """gptoss.py:22-29. blocks [..., G, 16] uint8 (low nibble first), scales [..., G] uint8
+    -> bf16 bits [..., G*32]: binary32 FP4[code] * 2^(scale - 127) (exact, or inf/NaN for
+    scale 255), then torch's .to(bfloat16): RTNE, every NaN -> 0x7FC0."""
+    b = np.asarray(blocks, np.uint8)
+    s = np.asarray(scales, np.uint8)
+    lut = np.array(FP4, np.float32)
+    v = np.stack([lut[b & 15], lut[b >> 4]], -1).reshape(*b.shape[:-1], 32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        p = np.ldexp(np.float32(1.0), s.astype(np.int32) - 127).astype(np.float32)  # exact powers of two
+        v = (v * p[..., None]).astype(np.float32)
+    out = f32_to_bf16_bits(v).reshape(v.shape)
+    out[np.isnan(v)] = 0x7FC0
+    return out.reshape(*b.shape[:-2], b.shape[-2] * 32)
+
+
+def gptoss_act(gu: np.ndarray, alpha: float = 1.702, limit: float = 7.0) -> np.ndarray:
+    """The clamped SwiGLU of gptoss.py:120-122 on bf16 values (float32 array), every
+    tensor op rounded to bf16: gate = min(gu[::2], limit), up = clamp(gu[1::2]),
+    act = bf16(bf16(up + 1) * bf16(gate * bf16(sigmoid(bf16(gate * alpha)))))."""
+    gu = np.asarray(gu, np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        gate = np.minimum(gu[..., 0::2], np.float32(limit))
+        up = np.clip(gu[..., 1::2], np.float32(-limit), np.float32(limit))
+        ga = _bf16r(gate * np.float32(alpha))
+        sg = _bf16r(np.float32(1) / (np.float32(1) + np.exp(-ga)))
+        glu = _bf16r(gate * sg)
+        return _bf16r(_bf16r(up + np.float32(1)) * glu)
+
+
+def gptoss_block_ref(pool: np.ndarray, expert_slot: dict, x_bf16: np.ndarray, ti: np.ndarray, sc: np.ndarray,
+                     gub_bf16: np.ndarray, db_bf16: np.ndarray, H: int, I: int, bits: int, group: int = 128,
+                     alpha: float = 1.702, limit: float = 7.0) -> np.ndarray:
+    """PagedGptOssBlock.forward (gptoss.py:108-143) after routing: x_bf16 uint16 [N, H],
+    ti [N, k] expert ids, sc [N, k] routing weights (bf16 values), biases as bf16 bits.
+    Weights dequantized bit-exactly to bf16 (quant.py:76-87); GEMVs in binary64, each
+    bf16 tensor of the reference rounded at the same point. N == 1 follows the decode
+    path (weighted outputs summed over the k experts in float32, one rounding); N > 1
+    follows the prefill path (index_add_ into bf16 in ascending expert order, a rounding
+    per add). Returns bf16 bits [N, H]."""
+    x = bf16_bits_to_f32(np.asarray(x_bf16, np.uint16)).reshape(-1, H).astype(np.float64)
+    ti = np.asarray(ti).reshape(x.shape[0], -1)
+    sc = np.asarray(sc, np.float32).reshape(ti.shape)
+    gub = bf16_bits_to_f32(np.asarray(gub_bf16, np.uint16)).reshape(-1, 2 * I)
+    db = bf16_bits_to_f32(np.asarray(db_bf16, np.uint16)).reshape(-1, H)
+    N, n = x.shape[0], H * I
+
+    def expert_out(e, rows):
+        W = bf16_bits_to_f32(dequant(pool[expert_slot[e]][None], n, bits, group)[0]).astype(np.float64)
+        gu = _bf16r(_bf16r((rows @ W[:2].reshape(H, 2 * I)).astype(np.float32)) + gub[e])
+        act = gptoss_act(gu, alpha, limit).astype(np.float64)
+        return _bf16r(_bf16r((act @ W[2].reshape(I, H)).astype(np.float32)) + db[e])
+
+    if N == 1:
+        y = np.zeros(H, np.float32)
+        for j in range(ti.shape[1]):
+            o = expert_out(int(ti[0, j]), x)[0]
+            y = (y + _bf16r(o * sc[0, j])).astype(np.float32)
+        return f32_to_bf16_bits(y).reshape(1, H)
+    y = np.zeros((N, H), np.float32)
+    for e in sorted(int(v) for v in np.unique(ti)):
+        tok, pos = np.nonzero(ti == e)
+        w = _bf16r(expert_out(e, x[tok]) * sc[tok, pos][:, None])
+        for r, t in enumerate(tok):  # index_add_ in token order within the expert
+            y[t] = _bf16r(y[t] + w[r])
+    return f32_to_bf16_bits(y).reshape(N, H)

@@ -360,3 +360,102 @@ def test_prefill_oracle_additive_over_experts_and_token_equivariant():
     perm = np.random.default_rng(2).permutation(9)
     permuted = O.moe_prefill_f64(pool, slots, x[perm], sel[perm], rw[perm], 256, 128, 4)
     assert np.allclose(permuted, full[perm], rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------- gpt-oss
+def test_mxfp4_oracle_matches_transformers():
+    # the reference pins its decoder against transformers' own (tests/test_gptoss.py:11-16);
+    # here that library routine pins the oracle, over every code and a wide scale range
+    from transformers.integrations.mxfp4 import convert_moe_packed_tensors
+
+    rng = np.random.default_rng(5)
+    blocks = rng.integers(0, 256, (3, 8, 5, 16), dtype=np.uint8)
+    blocks[0, 0, 0] = np.arange(16, dtype=np.uint8) * 17  # every code in both nibbles
+    scales = rng.integers(100, 150, (3, 8, 5), dtype=np.uint8)
+    ref = convert_moe_packed_tensors(torch.from_numpy(blocks), torch.from_numpy(scales))  # [E, K, out]
+    got = O.mxfp4_to_bf16_bits(blocks, scales)  # [E, out, K]
+    assert np.array_equal(got.transpose(0, 2, 1), ref.contiguous().view(torch.int16).numpy().view(np.uint16))
+
+
+def test_mxfp4_oracle_closed_forms():
+    # value = FP4[code] * 2^(scale - 127): code 1 is 0.5, code 7 is 6, code 9 is -0.5
+    b = np.zeros((1, 16), np.uint8)
+    b[0, :3] = [0x71, 0x09, 0x00]
+    for s, want in [(127, [0x3F00, 0x40C0, 0xBF00, 0x0000]),   # 0.5, 6, -0.5, 0
+                    (0, [0x0020, 0x0140, 0x8020, 0x0000]),     # scale 2^-127: bf16 subnormals 2^-128 ...
+                    (255, [0x7F80, 0x7F80, 0xFF80, 0x7FC0]),   # 2^128 = inf: 0 * inf = NaN
+                    (130, [0x4080, 0x4240, 0xC080, 0x0000])]:  # 4, 48, -4
+        got = O.mxfp4_to_bf16_bits(b, np.array([s], np.uint8))
+        assert [int(v) for v in (got[0], got[1], got[2], got[4])] == want, s
+
+
+def _gptoss_reference(N, seed=1):
+    """transformers' GptOssMLP (float weights ~N(0, 0.3), bf16, CPU), the reference's test model
+    (tests/test_gptoss.py:39-62), with its routing."""
+    from transformers import GptOssConfig
+    from transformers.models.gpt_oss.modeling_gpt_oss import GptOssMLP
+
+    torch.manual_seed(seed)
+    cfg = GptOssConfig(hidden_size=64, intermediate_size=64, num_hidden_layers=1, num_local_experts=8,
+                       num_experts_per_tok=2, num_attention_heads=2, num_key_value_heads=1, head_dim=32, vocab_size=50)
+    ref = GptOssMLP(cfg).to(torch.bfloat16)
+    with torch.no_grad():
+        for p in ref.parameters():
+            p.normal_(0, 0.3)
+        x = torch.randn(1, N, 64).to(torch.bfloat16)
+        want, _ = ref(x)
+        logits = torch.nn.functional.linear(x.reshape(-1, 64), ref.router.weight, ref.router.bias)
+        tv, ti = torch.topk(logits, 2, dim=-1)
+        sc = torch.nn.functional.softmax(tv, dim=1, dtype=tv.dtype)
+    return ref, x, want, ti, sc
+
+
+def _w3_bits(ref, e):
+    H, I = 64, 64
+    gu, dn = ref.experts.gate_up_proj[e].data, ref.experts.down_proj[e].data
+    f = gu.reshape(-1)
+    w3 = torch.stack([f[: H * I], f[H * I :], dn.reshape(-1)])
+    return w3.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("N", [1, 5])
+def test_gptoss_oracle_matches_transformers(N):
+    # bits = 16 (raw bf16 rows): the oracle restates gptoss.py:108-143 and must reproduce
+    # transformers' GptOssMLP up to accumulation order; a planted mistake (gate/up bias
+    # halves swapped, or a different clamp) must not
+    ref, x, want, ti, sc = _gptoss_reference(N)
+    H = I = 64
+    pool = np.stack([_w3_bits(ref, e).reshape(-1).view(np.uint8) for e in range(8)])
+    gub = ref.experts.gate_up_proj_bias.data.contiguous().view(torch.int16).numpy().view(np.uint16)
+    db = ref.experts.down_proj_bias.data.contiguous().view(torch.int16).numpy().view(np.uint16)
+    xb = x.reshape(N, H).contiguous().view(torch.int16).numpy().view(np.uint16)
+    args = (pool, {e: e for e in range(8)}, xb, ti.numpy(), sc.float().numpy())
+
+    def rel(bits_out):
+        got = O.bf16_bits_to_f32(bits_out).reshape(N, H)
+        w = want.reshape(N, H).float().numpy()
+        return np.linalg.norm(got - w) / np.linalg.norm(w)
+
+    err = rel(O.gptoss_block_ref(*args, gub, db, H, I, 16, 64))
+    print(f"gpt-oss oracle vs transformers, N={N}: rel-L2 {err:.2e}")
+    assert err <= 1e-2, err
+    swapped = gub.reshape(8, I, 2)[:, :, ::-1].reshape(8, 2 * I).copy()
+    assert rel(O.gptoss_block_ref(*args, swapped, db, H, I, 16, 64)) > 10 * max(err, 1e-3)
+    assert rel(O.gptoss_block_ref(*args, gub, db, H, I, 16, 64, limit=0.5)) > 10 * max(err, 1e-3)
+
+
+def test_gptoss_oracle_decode_sum_is_one_rounding():
+    # N == 1 sums the k weighted outputs in float32 and rounds once (gptoss.py:131), so with
+    # one expert of weight 1 it equals the per-expert output, and it is additive over a
+    # split of the expert list up to that final rounding
+    ref, x, want, ti, sc = _gptoss_reference(1, seed=3)
+    H = I = 64
+    pool = np.stack([_w3_bits(ref, e).reshape(-1).view(np.uint8) for e in range(8)])
+    gub = ref.experts.gate_up_proj_bias.data.contiguous().view(torch.int16).numpy().view(np.uint16)
+    db = ref.experts.down_proj_bias.data.contiguous().view(torch.int16).numpy().view(np.uint16)
+    xb = x.reshape(1, H).contiguous().view(torch.int16).numpy().view(np.uint16)
+    slots = {e: e for e in range(8)}
+    both = O.bf16_bits_to_f32(O.gptoss_block_ref(pool, slots, xb, ti.numpy(), sc.float().numpy(), gub, db, H, I, 16, 64))
+    parts = [O.bf16_bits_to_f32(O.gptoss_block_ref(pool, slots, xb, ti.numpy()[:, j:j + 1], sc.float().numpy()[:, j:j + 1],
+                                                   gub, db, H, I, 16, 64)) for j in range(2)]
+    assert np.allclose(both, parts[0] + parts[1], rtol=2 ** -7, atol=1e-6)

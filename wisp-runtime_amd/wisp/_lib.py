@@ -41,6 +41,10 @@ SIGNATURES = {
     "wisp_prefill_ws_bytes": (_i64, [_i64, _i64, _i64]),
     "wisp_moe_prefill": (_i32, [_vp, _i64, _i64, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _i64, _i64,
                                 _i32, _i64, _vp, _vp, _vp, _vp]),
+    "wisp_mxfp4_to_bf16": (_i32, [_vp, _vp, _i64, _vp, _vp]),
+    "wisp_gptoss_ws_bytes": (_i64, [_i32, _i64, _i64]),
+    "wisp_gptoss_decode": (_i32, [_vp, _i64, _i64, _vp, _i32, _i64, _i64, _i32, _i64, _vp, _vp, _vp, _i64,
+                                  ctypes.c_float, ctypes.c_float, _vp, _vp, _vp]),
     "wisp_core_create": (_i32, [_i64, _i32, _f64, _i64, _f64, _vp]),
     "wisp_core_destroy": (None, [_vp]),
     "wisp_core_step": (None, [_vp]),

@@ -268,3 +268,51 @@ def moe_prefill(pool, expert_slots, x, sel, rw, n, H, I, bits, group=128, acc=No
         "moe_prefill",
     )
     return acc if out is None else out
+
+
+# ---------------------------------------------------------------------------- gpt-oss
+def mxfp4_to_bf16(blocks: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """gptoss.py:22-29: blocks [..., G, 16] uint8 (two e2m1 codes per byte, low nibble
+    first), scales [..., G] uint8 (power-of-two exponents, bias 127) -> [..., G*32]
+    bfloat16, bit-exact with the reference (float32 product, then .to(bfloat16))."""
+    assert blocks.dtype == torch.uint8 and scales.dtype == torch.uint8 and blocks.shape[-1] == 16
+    assert tuple(blocks.shape[:-1]) == tuple(scales.shape), "scales must be blocks.shape[:-1]"
+    dev = _lib.require_gpu(blocks, scales, what="mxfp4_to_bf16")
+    b = blocks.contiguous()
+    if b.data_ptr() % 16:
+        b = b.clone()
+    s = scales.contiguous()
+    ng = s.numel()
+    out = torch.empty(ng * 32, dtype=torch.bfloat16, device=dev)
+    _lib.check(_lib.lib().wisp_mxfp4_to_bf16(_lib.ptr(b), _lib.ptr(s), ng, _lib.ptr(out), _lib.stream(dev)),
+               "mxfp4_to_bf16")
+    return out.view(*blocks.shape[:-2], blocks.shape[-2] * 32)
+
+
+def gptoss_decode(pool, meta, x, gate_up_bias, down_bias, k, n, H, I, bits, group=128, alpha=1.702, limit=7.0):
+    """One token through k gpt-oss experts (PagedGptOssBlock's decode step,
+    gptoss.py:126-131) as three kernel launches. meta: float32 [3k] on the GPU =
+    [slot ids | routing weights | expert ids]; gate_up_bias bf16 [E, 2I], down_bias
+    bf16 [E, H] indexed by expert id. Returns bf16 [H]."""
+    assert n == H * I
+    _check_pool(pool)
+    dev = _lib.require_gpu(pool, meta, x, gate_up_bias, down_bias, what=f"gptoss_decode (bits={bits})")
+    assert meta.dtype == torch.float32 and meta.numel() >= 3 * k, "meta must be float32 [3k]"
+    assert gate_up_bias.dtype == torch.bfloat16 and down_bias.dtype == torch.bfloat16
+    E = gate_up_bias.shape[0]
+    assert gate_up_bias.shape == (E, 2 * I) and down_bias.shape == (E, H), "biases must be [E, 2I] and [E, H]"
+    meta = meta.contiguous()
+    x = _prep_x(x)
+    assert x.numel() == H
+    gub, db = gate_up_bias.contiguous(), down_bias.contiguous()
+    L = _lib.lib()
+    ws = torch.empty(L.wisp_gptoss_ws_bytes(k, H, I), dtype=torch.uint8, device=dev)
+    out = torch.empty((H,), dtype=torch.bfloat16, device=dev)
+    _lib.check(
+        L.wisp_gptoss_decode(
+            _lib.ptr(pool), pool.stride(0), pool.shape[0], _lib.ptr(meta), k, H, I, bits, group, _lib.ptr(x),
+            _lib.ptr(gub), _lib.ptr(db), E, float(alpha), float(limit), _lib.ptr(ws), _lib.ptr(out), _lib.stream(dev),
+        ),
+        "gptoss_decode",
+    )
+    return out

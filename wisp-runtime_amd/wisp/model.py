@@ -48,6 +48,10 @@ def load_skeleton(model_dir, rt, device="cuda", dtype=torch.bfloat16):
     from transformers import AutoConfig
 
     cfg = AutoConfig.from_pretrained(model_dir)
+    if cfg.model_type == "gpt_oss":  # model.py:25-28
+        from .gptoss import load_skeleton_gptoss
+
+        return load_skeleton_gptoss(model_dir, rt, device)
     model = _meta_model(cfg, dtype)
     _gates_with_storage(model, cfg, device, dtype)
     attach(model, rt)
