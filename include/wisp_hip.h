@@ -265,6 +265,42 @@ int wisp_gptoss_decode(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, 
                        const uint16_t* down_bias, int64_t n_experts, float alpha, float limit, void* ws,
                        uint16_t* out, void* stream);
 
+/* ---- dense part of a graph-decoder step (csrc/decode_layer.hip) ----
+ * These replace the transformers modules that wisp/graphdec.py:160-203 runs at
+ * batch 1 (Qwen3MoeRMSNorm, the bf16 nn.Linear q/k/v/o and router layers, the
+ * residual adds, q_norm/k_norm + rope_decode + the KV store, route()), with the
+ * modules' bf16 rounding points. All vectors bf16 unless stated; everything is
+ * caller-owned and only enqueued on `stream` (graph-capture safe). */
+
+/* y[o] = bf16(W[o] . x), W bf16 [O, K] row-major as up to three row blocks
+ * (w0: rows [0, r1), w1: [r1, r2), w2: [r2, O); one launch for q/k/v).
+ * norm_w == NULL: x = a. norm_w != NULL: h = a (+ b if b), bf16 add;
+ * x = bf16(norm_w * bf16(h * rsqrt(sum(h^2)/K + eps))) (Qwen3MoeRMSNorm);
+ * h_out / x_out (optional) receive h and x. a_row (optional, device int64):
+ * a is a [*, K] table and its row *a_row is used (embedding lookup).
+ * res (optional): y = bf16(res + bf16(W x)). K a multiple of 8 up to 8192;
+ * a, b, norm_w, h_out, x_out and the weights 16-byte aligned.
+ * Replaces graphdec.py:160-181 (input_layernorm, q/k/v_proj, o_proj + residual,
+ * post_attention_layernorm, gate) and :195-203 (embed_tokens, norm, lm_head). */
+int wisp_dl_gemv(const void* a, const int64_t* a_row, const void* b, const void* norm_w, float eps, void* h_out,
+                 void* x_out, const void* w0, const void* w1, const void* w2, int64_t r1, int64_t r2, int64_t O,
+                 int64_t K, const void* res, void* y, void* stream);
+
+/* qkv = [q (hq*d) | k (hk*d) | v (hk*d)]: each q/k head RMSNorm'd over d with
+ * q_norm_w / k_norm_w (as above), rotated by rope_decode's rule with the bf16
+ * tables cos/sin [tmax, d] at row *pos (device int64); q -> qo [hq*d], k and v
+ * -> kc/vc [hk, tmax, d] (head stride head_stride elements) at position *pos.
+ * d in {64, 128, 256}. Replaces graphdec.py:163-172. */
+int wisp_dl_qk_rope(const void* qkv, const void* q_norm_w, const void* k_norm_w, float eps, const void* cos,
+                    const void* sin, const int64_t* pos, int hq, int hk, int d, void* kc, void* vc,
+                    int64_t head_stride, void* qo, void* stream);
+
+/* route() at batch 1 (wisp/moe.py:41-47) plus pack_meta's order: softmax in
+ * float32 of the bf16 logits [E], top-k (descending, equal values by lower
+ * index), divided by their sum if norm_topk, rounded to bf16; row (float32)
+ * = [ids (k) | weights (k)]. E <= 1024, k <= 16. One launch. */
+int wisp_dl_route(const void* logits, int E, int k, int norm_topk, float* row, void* stream);
+
 /* Launch-shape tuning, process-wide: gu_rows = rows of one expert per wave in
  * kernel 1, gu_waves = waves per workgroup in kernel 1, dn_iters = row
  * iterations per workgroup in kernel 2 (each in {1,2,4,8}; 0 keeps the

@@ -42,6 +42,11 @@ SIGNATURES = {
     "wisp_moe_prefill": (_i32, [_vp, _i64, _i64, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _i64, _i64,
                                 _i32, _i64, _vp, _vp, _vp, _vp]),
     "wisp_mxfp4_to_bf16": (_i32, [_vp, _vp, _i64, _vp, _vp]),
+    "wisp_dl_gemv": (_i32, [_vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp,
+                            _vp, _vp]),
+    "wisp_dl_qk_rope": (_i32, [_vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _i64, _vp,
+                               _vp]),
+    "wisp_dl_route": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp]),
     "wisp_gptoss_ws_bytes": (_i64, [_i32, _i64, _i64]),
     "wisp_gptoss_decode": (_i32, [_vp, _i64, _i64, _vp, _i32, _i64, _i64, _i32, _i64, _vp, _vp, _vp, _i64,
                                   ctypes.c_float, ctypes.c_float, _vp, _vp, _vp]),

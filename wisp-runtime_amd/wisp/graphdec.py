@@ -13,9 +13,11 @@ hipGraph and replayed:
 Every buffer a segment touches is static: the KV cache [1, Hk, Tmax, D] per layer, the
 token and position in `ctl` (device), the routing in `meta_dev`. Attention always spans
 the Tmax slots with the position read on the device, so the graphs do not depend on the
-length. The decode segments run this package's gfx950 kernels: rope_decode,
-attn_decode (grouped attention over the static cache), and the two MoE decode kernels
-on the expert cache's slot pool. Prefill runs the model's own modules in chunks, with
+length. The decode segments run only this package's gfx950 kernels, nine launches per
+layer: RMSNorm + q/k/v projection, q/k head norm + rope + KV store, grouped attention
+over the static cache (two), o_proj + residual, RMSNorm + router gate, route, and the
+two MoE decode kernels on the expert cache's slot pool (the model's modules would be
+about sixty small kernels per layer at batch 1). Prefill runs the model's own modules in chunks, with
 attention computed in float32, writing K/V straight into the static buffers.
 """
 
@@ -70,6 +72,42 @@ class GraphDecoder:
         self.meta_dev = torch.zeros(2 * self.k, dtype=torch.float32, device=self.dev)
         self.meta_host = torch.zeros(2 * self.k, dtype=torch.float32, pin_memory=True)
         self.graphs, self._key = None, None
+        self._dense_setup(cfg)
+
+    def _dense_setup(self, cfg):
+        """Weights and static buffers of the fused decode segments (csrc/decode_layer.hip):
+        per layer the input/post-attention RMSNorm weights, q/k/v/o, q_norm/k_norm and the
+        router gate, all bf16 and contiguous as the modules hold them."""
+        Hq, Hk, D, H = self.Hq, self.Hk, self.D, self.H
+        W = []
+        for lay in self.layers:
+            at, blk = lay.self_attn, lay.mlp
+            for lin in (at.q_proj, at.k_proj, at.v_proj, at.o_proj, blk.gate):
+                if getattr(lin, "bias", None) is not None:
+                    raise AssertionError("GraphDecoder's decode kernels take bias-free projections (Qwen3-MoE)")
+            if not (hasattr(at, "q_norm") and hasattr(at, "k_norm")):
+                raise AssertionError("GraphDecoder's decode kernels take Qwen3-style attention (q_norm, k_norm)")
+            W.append(dict(
+                ln1=lay.input_layernorm.weight, eps1=lay.input_layernorm.variance_epsilon,
+                q=at.q_proj.weight, k=at.k_proj.weight, v=at.v_proj.weight, o=at.o_proj.weight,
+                qn=at.q_norm.weight, kn=at.k_norm.weight, epsq=at.q_norm.variance_epsilon,
+                ln2=lay.post_attention_layernorm.weight, eps2=lay.post_attention_layernorm.variance_epsilon,
+                gate=blk.gate.weight, scale=getattr(at, "scaling", D**-0.5), norm_topk=blk.norm_topk,
+            ))
+        for w in W:
+            for key in ("ln1", "q", "k", "v", "o", "qn", "kn", "ln2", "gate"):
+                t = w[key]
+                if t.dtype != self.dt or not t.is_contiguous() or t.device != self.dev:
+                    raise AssertionError(f"decode kernels need contiguous {self.dt} weights on {self.dev} ({key})")
+        self.W = W
+        nrm = self.model.model.norm
+        self.w_final, self.eps_final = nrm.weight, nrm.variance_epsilon
+        self.w_embed, self.w_head = self.model.model.embed_tokens.weight, self.model.lm_head.weight
+        d = dict(device=self.dev, dtype=self.dt)
+        self.hbuf = torch.zeros(H, **d)  # residual stream before attention (h)
+        self.qkv = torch.zeros((Hq + 2 * Hk) * D, **d)
+        self.qo = torch.zeros(Hq * D, **d)
+        self.rlogits = torch.zeros(self.E, **d)
 
     # ---------------------------------------------------------------- static buffers
     def _alloc(self, tmax):
@@ -157,50 +195,45 @@ class GraphDecoder:
         return logits
 
     # ---------------------------------------------------------------- segment bodies
-    def _attn_router(self, i, h):
-        lay = self.layers[i]
-        at, blk = lay.self_attn, lay.mlp
-        Hq, Hk, D, H = self.Hq, self.Hk, self.D, self.H
-        xn = lay.input_layernorm(h)
-        q = at.q_norm(at.q_proj(xn).view(1, 1, Hq, D)).transpose(1, 2)
-        k = at.k_norm(at.k_proj(xn).view(1, 1, Hk, D)).transpose(1, 2)
-        v = at.v_proj(xn).view(1, 1, Hk, D).transpose(1, 2)
+    def _attn_router(self, i, a, a_row=None, b=None):
+        """Attention and router of layer i on h = a (+ b), graphdec.py:160-192, as six
+        launches: RMSNorm + q/k/v (one GEMV), q/k head norm + rope + KV store, attention
+        (two), o_proj + residual, RMSNorm + router gate, route. Leaves h + attention in hm,
+        the MoE input in xn and [expert ids | weights] in row."""
+        w, Hq, Hk, D, H = self.W[i], self.Hq, self.Hk, self.D, self.H
         pos = self.ctl[1:2]
-        cos = self.cos.index_select(0, pos).view(1, 1, D)
-        sin = self.sin.index_select(0, pos).view(1, 1, D)
-        q, k = kernels.rope_decode(q, k, cos, sin)
-        self.kc[i].index_copy_(2, pos, k)
-        self.vc[i].index_copy_(2, pos, v)
-        o = kernels.attn_decode(q, self.kc[i], self.vc[i], pos, getattr(at, "scaling", D**-0.5))
-        hm = h + at.o_proj(o.reshape(1, 1, Hq * D))
-        xn2 = lay.post_attention_layernorm(hm)
-        sel, rw = route(blk.gate(xn2.view(1, H)), self.k, blk.norm_topk, xn2.dtype)
-        parts = [sel.float(), rw.float()]
+        kernels.dl_gemv(self.qkv, w["q"], a, w1=w["k"], w2=w["v"], a_row=a_row, b=b, norm_w=w["ln1"],
+                        eps=w["eps1"], h_out=self.hbuf)
+        kernels.dl_qk_rope(self.qkv, w["qn"], w["kn"], w["epsq"], self.cos, self.sin, pos, Hq, Hk, D,
+                           self.kc[i], self.vc[i], self.qo)
+        o = kernels.attn_decode(self.qo.view(Hq, D), self.kc[i], self.vc[i], pos, w["scale"])
+        kernels.dl_gemv(self.hm.view(H), w["o"], o.view(Hq * D), res=self.hbuf)
+        kernels.dl_gemv(self.rlogits, w["gate"], self.hm.view(H), norm_w=w["ln2"], eps=w["eps2"],
+                        x_out=self.xn.view(H))
+        kernels.dl_route(self.rlogits, self.k, w["norm_topk"], self.row.view(-1))
         if self.prefetch:
-            ng = getattr(blk, "next_gate", None)
-            parts.append(torch.topk(ng(xn2.view(1, H)), self.k, dim=-1).indices.float() if ng is not None
-                         else torch.zeros(1, self.k, device=self.dev))
-        self.hm.copy_(hm)
-        self.xn.copy_(xn2)
-        self.row.copy_(torch.cat(parts, 1))
+            ng = getattr(self.layers[i].mlp, "next_gate", None)
+            pred = (torch.topk(ng(self.xn.view(1, H)), self.k, dim=-1).indices.float() if ng is not None
+                    else torch.zeros(1, self.k, device=self.dev))
+            self.row[:, 2 * self.k :].copy_(pred)
 
     def _moe(self, i):
-        """MoE of layer i from the static buffers -> [1, 1, H]."""
+        """MoE of layer i from the static buffers -> [H]."""
         c = self.rt.cache
         st = c.store
-        y = kernels.moe_decode_fast(c.gpu, self.meta_dev, self.xn.view(self.H), self.k, st.n, self.H,
-                                    self.layers[i].mlp.I, st.bits, st.group)
-        return y.view(1, 1, self.H)
+        return kernels.moe_decode_fast(c.gpu, self.meta_dev, self.xn.view(self.H), self.k, st.n, self.H,
+                                       self.layers[i].mlp.I, st.bits, st.group)
 
     def _seg(self, j):
-        if j == 0:
-            h = self.model.model.embed_tokens(self.ctl[0:1].view(1, 1))
-        else:
-            h = self.hm + self._moe(j - 1)
+        if j == 0:  # h = embed_tokens(token)
+            a, a_row, b = self.w_embed, self.ctl[0:1], None
+        else:  # h = hm + MoE(j - 1)
+            a, a_row, b = self.hm.view(self.H), None, self._moe(j - 1)
         if j < self.L:
-            self._attn_router(j, h)
+            self._attn_router(j, a, a_row, b)
         else:
-            self.logits.copy_(self.model.lm_head(self.model.model.norm(h)).view(1, -1))
+            kernels.dl_gemv(self.logits.view(-1), self.w_head, a, a_row=a_row, b=b, norm_w=self.w_final,
+                            eps=self.eps_final)
 
     # ---------------------------------------------------------------- host step of one layer
     def _prepare(self, i, row):

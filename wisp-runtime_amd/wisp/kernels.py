@@ -316,3 +316,83 @@ def gptoss_decode(pool, meta, x, gate_up_bias, down_bias, k, n, H, I, bits, grou
         "gptoss_decode",
     )
     return out
+
+
+# ----------------------------------------------------------------------------- decode-step dense kernels
+def _bf16_vec(t, what):
+    if t.dtype != torch.bfloat16 or not t.is_contiguous():
+        raise TypeError(f"{what} must be a contiguous bfloat16 tensor")
+    return t
+
+
+def dl_gemv(y, w0, a, *, w1=None, w2=None, r1=None, r2=None, a_row=None, b=None, norm_w=None, eps=0.0, h_out=None,
+            x_out=None, res=None):
+    """y[o] = bf16(W[o] . x) for a bf16 weight W [O, K] given as up to three row blocks
+    (w0: rows [0, r1), w1: [r1, r2), w2: [r2, O)), one launch. With norm_w, x is the
+    RMSNorm of h = a (+ b) (Qwen3MoeRMSNorm at bf16; h and x optionally stored to h_out and
+    x_out); otherwise x = a. a_row (int64 device tensor): use row a_row of a [*, K]. res:
+    y = bf16(res + bf16(W x)). Replaces the nn.Linear / RMSNorm / residual modules of
+    graphdec.py:160-203 at batch 1. All tensors are caller-owned (graph-capture safe)."""
+    blocks = [w for w in (w0, w1, w2) if w is not None]
+    K = w0.shape[1]
+    O = sum(w.shape[0] for w in blocks)
+    r1 = w0.shape[0] if r1 is None else r1
+    r2 = r1 + (w1.shape[0] if w1 is not None else 0) if r2 is None else r2
+    for w in blocks:
+        _bf16_vec(w, "weight")
+        assert w.dim() == 2 and w.shape[1] == K
+    _bf16_vec(y, "y")
+    assert y.numel() == O and a.dtype == torch.bfloat16
+    dev = _lib.require_gpu(y, w0, a, what="dl_gemv")
+    if a_row is not None:
+        assert a_row.dtype == torch.int64 and a.dim() == 2 and a.shape[1] == K and a.is_contiguous()
+    else:
+        assert a.numel() == K and a.is_contiguous()
+    for t, n in ((b, "b"), (norm_w, "norm_w"), (h_out, "h_out"), (x_out, "x_out")):
+        if t is not None:
+            _bf16_vec(t, n)
+            assert t.numel() == K, n
+    if res is not None:
+        _bf16_vec(res, "res")
+        assert res.numel() == O
+    p = lambda t: None if t is None else _lib.ptr(t)  # noqa: E731
+    _lib.check(
+        _lib.lib().wisp_dl_gemv(p(a), p(a_row), p(b), p(norm_w), float(eps), p(h_out), p(x_out), p(w0), p(w1), p(w2),
+                                r1, r2, O, K, p(res), p(y), _lib.stream(dev)),
+        "dl_gemv",
+    )
+    return y
+
+
+def dl_qk_rope(qkv, q_norm_w, k_norm_w, eps, cos, sin, pos, hq, hk, d, kc, vc, qo):
+    """Per-head RMSNorm of the q and k heads of qkv = [q (hq*d) | k (hk*d) | v (hk*d)],
+    rope_decode at position `pos` (int64 device tensor) with the bf16 tables cos/sin
+    [tmax, d], q -> qo [hq*d], k and v -> the static caches kc/vc [1, hk, tmax, d] at pos.
+    Replaces graphdec.py:163-172 (q_norm, k_norm, rope_decode, index_copy_)."""
+    for t, n in ((qkv, "qkv"), (q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w"), (cos, "cos"), (sin, "sin"),
+                 (qo, "qo")):
+        _bf16_vec(t, n)
+    assert qkv.numel() == (hq + 2 * hk) * d and qo.numel() == hq * d
+    assert kc.shape == vc.shape and kc.shape[1] == hk and kc.shape[3] == d and kc.stride() == vc.stride()
+    assert kc.stride(-1) == 1 and kc.stride(-2) == d and cos.shape[-1] == d and sin.shape == cos.shape
+    assert pos.dtype == torch.int64
+    dev = _lib.require_gpu(qkv, kc, vc, pos, what="dl_qk_rope")
+    _lib.check(
+        _lib.lib().wisp_dl_qk_rope(_lib.ptr(qkv), _lib.ptr(q_norm_w), _lib.ptr(k_norm_w), float(eps), _lib.ptr(cos),
+                                   _lib.ptr(sin), _lib.ptr(pos), hq, hk, d, _lib.ptr(kc), _lib.ptr(vc), kc.stride(1),
+                                   _lib.ptr(qo), _lib.stream(dev)),
+        "dl_qk_rope",
+    )
+    return qo
+
+
+def dl_route(logits, k, norm_topk, row):
+    """route() of wisp/moe.py:41-47 at batch 1 on the device: softmax (float32) of the bf16
+    router logits [E], top-k, renormalised if norm_topk, weights rounded to bf16;
+    row[:k] = expert ids (float32), row[k:2k] = weights. One launch."""
+    _bf16_vec(logits, "logits")
+    assert row.dtype == torch.float32 and row.is_contiguous() and row.numel() >= 2 * k
+    dev = _lib.require_gpu(logits, row, what="dl_route")
+    _lib.check(_lib.lib().wisp_dl_route(_lib.ptr(logits), logits.numel(), k, int(bool(norm_topk)), _lib.ptr(row),
+                                        _lib.stream(dev)), "dl_route")
+    return row
