@@ -343,21 +343,23 @@ def run_c4(a) -> dict:
     print(f"[bench] c4 store {store.total_gib:.1f} GiB pinned={store.pinned} in {time.time() - t0:.0f}s",
           file=sys.stderr, flush=True)
     rt = Runtime(store, fused=2)
-    rt.cache = ExpertCache(store, a.c4_slots)
+    rt.cache = ExpertCache(store, a.c4_slots, copy=a.c4_copy)
     model = random_skeleton(cfg, rt, device=dev)
     rng = np.random.default_rng(4)
     perms = [rng.permutation(E_) for _ in range(Lr)]
 
+    pos0 = tmax - a.c4_tokens - a.c4_warmup - 8
+    # the synthetic routing is workload input, drawn before the run like x: ids[token][layer]
+    draws = [[np.asarray(zipf_layer_experts(rng, E_, k, 1.1, perms[i]), dtype=np.int64) for i in range(Lr)]
+             for _ in range(a.c4_warmup + a.c4_tokens + 1)]
+
     class ZipfDecoder(GraphDecoder):
         """The routing weights come from the model's router; the expert ids are drawn Zipf(1.1)."""
 
-        def _prepare(self, i, row):
-            row = list(row)
-            row[:k] = zipf_layer_experts(rng, E_, k, 1.1, perms[i])
-            super()._prepare(i, row)
+        def _expert_ids(self, i):
+            return draws[self.pos - pos0][i]
 
     dec = ZipfDecoder(model, rt, tmax=tmax)
-    pos0 = tmax - a.c4_tokens - a.c4_warmup - 8
     with torch.no_grad():  # a filled context: random K/V up to pos0
         for i in range(Lr):
             dec.kc[i][:, :, :pos0].normal_()
@@ -395,7 +397,7 @@ def run_c4(a) -> dict:
                                f"context {pos0}..{pos0 + a.c4_warmup + a.c4_tokens} of {tmax}, random-init weights",
                    "hit_rate": round(hits / max(1, hits + misses), 4),
                    "h2d_MB_per_token": round((rt.cache.bytes_h2d - b0) / a.c4_tokens / 1e6, 2),
-                   "store_GiB": round(store.total_gib, 2)},
+                   "store_GiB": round(store.total_gib, 2), "copy": rt.cache.copy},
     }
 
 
@@ -508,6 +510,8 @@ def main():
     ap.add_argument("--c4-slots", type=int, default=512)
     ap.add_argument("--c4-tokens", type=int, default=32)
     ap.add_argument("--c4-warmup", type=int, default=8)
+    ap.add_argument("--c4-copy", default="auto", choices=["dma", "kernel", "auto"],
+                    help="how expert misses cross PCIe (ExpertCache copy=)")
     ap.add_argument("--summarize-trace", nargs=3, metavar=("TRACE_CSV", "STATS_CSV", "BENCH_JSON"),
                     help="write the kernel-trace summary under profiles/ from a rocprofv3 run of bench.py")
     a = ap.parse_args()

@@ -229,6 +229,25 @@ int wisp_cache_ensure(void* cache, const int64_t* keys, int64_t n, int64_t* slot
  * and copy it to meta_dev on `compute`. slots (may be NULL) receives the slots. */
 int wisp_cache_prepare_layer(void* cache, const int64_t* keys, const float* weights, int k, float* meta_host,
                              float* meta_dev, int64_t* slots, void* compute);
+
+/* graphdec.py:216-231 and :305-306 for one layer including the router row: copy
+ * row_dev = float32 [ids (k) | weights (k)] (device) into the pinned row_host on
+ * `compute` and wait for it (the decoder's one sync per layer), then
+ * wisp_cache_prepare_layer with keys key_base + id, every id in [0, n_ids)
+ * (else WISP_EINVAL). ids (may be NULL) replaces the row's expert ids; the
+ * weights always come from the row. */
+int wisp_cache_prepare_row(void* cache, const float* row_dev, float* row_host, int k, int64_t key_base,
+                           int64_t n_ids, const int64_t* ids, float* meta_host, float* meta_dev, int64_t* slots,
+                           void* compute);
+
+/* How misses cross PCIe: mode 0 (default) = one hipMemcpyAsync per expert row
+ * on the side stream (cache.py:56-60, the DMA engines); mode 1 = a page kernel
+ * on the side stream that reads the pinned store rows over PCIe (one launch per
+ * 16 rows; MI355X: 53-56 GB/s for 4+ rows against 46-47 GB/s). Mode 1 needs a
+ * store mapped for the device (hipHostGetDevicePointer succeeds), 16-byte rows
+ * and no decode_on_load; otherwise WISP_EINVAL and the mode is unchanged. No
+ * reference counterpart (the reference always uses tensor copies). */
+int wisp_cache_set_copy_mode(void* cache, int mode);
 /* cache.py:144-158 (resize): synchronises the device, keeps the hottest
  * experts, releases the old pool, allocates the new one, re-copies. */
 int wisp_cache_resize(void* cache, int64_t nslots);

@@ -39,9 +39,11 @@ def test_pool_is_a_native_allocation_viewed_by_torch():
     c.free()
 
 
-def test_ensure_pages_rows_and_matches_reference_bookkeeping():
+@pytest.mark.parametrize("copy", ["dma", "kernel"])
+def test_ensure_pages_rows_and_matches_reference_bookkeeping(copy):
     st = _store(2, 6, 4, seed=1)
-    c = ExpertCache(st, 5)
+    c = ExpertCache(st, 5, copy=copy)
+    assert c.copy == copy
     ref = RefCore(5, "lru")
     rng = np.random.default_rng(2)
     for it in range(30):
@@ -57,10 +59,11 @@ def test_ensure_pages_rows_and_matches_reference_bookkeeping():
     c.free()
 
 
-def test_copy_waits_for_queued_reads_of_the_evicted_slot():
+@pytest.mark.parametrize("copy", ["dma", "kernel"])
+def test_copy_waits_for_queued_reads_of_the_evicted_slot(copy):
     """cache.py:54-56: a copy into a slot starts only after the compute work queued before it."""
     st = _store(1, 4, 4, seed=3)
-    c = ExpertCache(st, 1)
+    c = ExpertCache(st, 1, copy=copy)
     (s,) = c.ensure([0])
     torch.cuda.synchronize()
     a = torch.randn(4096, 4096, device="cuda")
@@ -190,4 +193,49 @@ def test_graph_replays_follow_prepare_layer():
         r = O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.astype(np.float32)))
         got = out.float().cpu().numpy()
         assert np.linalg.norm(got - r) / np.linalg.norm(r) <= 1e-3, it
+    c.free()
+
+
+@pytest.mark.parametrize("bits", [4, 3, 2])
+def test_page_kernel_copies_rows_exactly(bits):
+    """copy="kernel": the GPU reads the pinned store rows itself; the pages must equal the host
+    rows byte for byte, for batches below, at and above one launch's 16 rows."""
+    st = _store(3, 12, bits, seed=3 + bits)  # 36 distinct rows
+    c = ExpertCache(st, 40, copy="kernel")
+    assert c.copy == "kernel"
+    rng = np.random.default_rng(bits)
+    done = set()
+    for n in (1, 5, 16, 17, 36):
+        keys = [int(v) for v in rng.choice(36, size=n, replace=False)]
+        slots = c.ensure(keys)
+        got = _rows(c, slots)
+        for j, k in enumerate(keys):
+            assert torch.equal(got[j], st.host[k]), (n, k)
+        done.update(keys)
+    assert c.n_loads == len(done)
+    c.free()
+
+
+def test_page_kernel_follows_reference_bookkeeping_under_eviction():
+    st = _store(2, 6, 4, seed=11)
+    c = ExpertCache(st, 5, copy="kernel")
+    ref = RefCore(5, "lru")
+    rng = np.random.default_rng(12)
+    for it in range(30):
+        keys = [int(v) for v in rng.choice(12, size=3, replace=False)]
+        slots = c.ensure(keys)
+        assert slots == ref.ensure(keys)[0], it
+        got = _rows(c, slots)
+        for j, k in enumerate(keys):
+            assert torch.equal(got[j], st.host[k]), (it, k)
+    c.free()
+
+
+def test_page_kernel_needs_a_pinned_store():
+    st = ExpertStore(1, 4, N, 4, G, pin=False)
+    assert not st.pinned
+    with pytest.raises(RuntimeError):
+        ExpertCache(st, 2, copy="kernel")
+    c = ExpertCache(st, 2, copy="auto")  # falls back to the DMA copies
+    assert c.copy == "dma"
     c.free()

@@ -194,6 +194,8 @@ struct Cache {
     int64_t staging_rows = 0;
     hipStream_t copy = nullptr;
     hipEvent_t order = nullptr, done = nullptr;
+    int copy_mode = 0;                   // 0: hipMemcpyAsync per row, 1: k_page_rows
+    const uint8_t* host_dev = nullptr;   // the host store's device address (copy_mode 1)
     bool pending = false;
     int64_t bytes_h2d = 0, n_loads = 0;
 };
@@ -216,6 +218,39 @@ static int alloc_pool(Cache& c) {
     return WISP_OK;
 }
 
+// Copy mode 1: the GPU reads the pinned host rows itself over PCIe. Grid
+// (kPageSplit, pairs): each workgroup copies one contiguous part of one row
+// with 16-byte loads, 4 in flight per thread. On MI355X this streams
+// 53-56 GB/s for 4+ rows against 46-47 GB/s for one hipMemcpyAsync per row.
+constexpr int kPageMax = 16;    // pairs per launch
+constexpr int kPageSplit = 32;  // workgroups per row
+struct PagePairs {
+    int64_t key[kPageMax];
+    int64_t slot[kPageMax];
+};
+typedef uint32_t pg_u32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void k_page_rows(const pg_u32x4* __restrict__ host, pg_u32x4* __restrict__ pool,
+                                                   const PagePairs p, int64_t row16, int64_t slot16, int64_t per) {
+    const int r = blockIdx.y;
+    const pg_u32x4* src = host + p.key[r] * row16;
+    pg_u32x4* dst = pool + p.slot[r] * slot16;
+    const int64_t b0 = (int64_t)blockIdx.x * per, b1 = min(row16, b0 + per);
+    constexpr int U = 4;
+    for (int64_t i = b0 + threadIdx.x; i < b1; i += 256 * U) {
+        pg_u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t ii = i + (int64_t)u * 256;
+            if (ii < b1) v[u] = __builtin_nontemporal_load(src + ii);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t ii = i + (int64_t)u * 256;
+            if (ii < b1) dst[ii] = v[u];
+        }
+    }
+}
+
 // cache.py:50-76: copies of [(key, slot)] on the side stream, ordered after
 // the work already queued on the compute stream (those slots may still be read)
 static int issue(Cache& c, const int64_t* keys, const int64_t* slots, int64_t n, hipStream_t compute) {
@@ -227,7 +262,23 @@ static int issue(Cache& c, const int64_t* keys, const int64_t* slots, int64_t n,
     if (e == hipSuccess) e = hipStreamWaitEvent(c.copy, c.order, 0);
     if (e != hipSuccess) return hip_fail(e, "ordering the copy stream");
     uint8_t* pool = static_cast<uint8_t*>(c.pool->ptr);
-    if (!c.decode_on_load) {
+    if (!c.decode_on_load && c.copy_mode == 1) {
+        const int64_t row16 = c.row_bytes / 16, slot16 = c.slot_bytes / 16;
+        const int64_t per = ((row16 + kPageSplit - 1) / kPageSplit + 1023) / 1024 * 1024;
+        for (int64_t i0 = 0; i0 < n; i0 += kPageMax) {
+            const int m = (int)std::min<int64_t>(kPageMax, n - i0);
+            PagePairs pp;
+            for (int j = 0; j < kPageMax; ++j) {
+                pp.key[j] = keys[i0 + std::min(j, m - 1)];
+                pp.slot[j] = slots[i0 + std::min(j, m - 1)];
+            }
+            hipLaunchKernelGGL(k_page_rows, dim3(kPageSplit, m), dim3(256), 0, c.copy,
+                               reinterpret_cast<const pg_u32x4*>(c.host_dev), reinterpret_cast<pg_u32x4*>(pool), pp,
+                               row16, slot16, per);
+            e = hipGetLastError();
+            if (e != hipSuccess) return hip_fail(e, "k_page_rows launch");
+        }
+    } else if (!c.decode_on_load) {
         for (int64_t i = 0; i < n; ++i) {
             e = hipMemcpyAsync(pool + slots[i] * c.slot_bytes, c.host + keys[i] * c.row_bytes, (size_t)c.row_bytes,
                                hipMemcpyHostToDevice, c.copy);
@@ -612,6 +663,64 @@ extern "C" int wisp_cache_prepare_layer(void* h, const int64_t* keys, const floa
     const hipError_t e = hipMemcpyAsync(meta_dev, meta_host, sizeof(float) * 2 * k, hipMemcpyHostToDevice,
                                         (hipStream_t)compute);
     return e == hipSuccess ? WISP_OK : hip_fail(e, "hipMemcpyAsync(meta)");
+}
+
+// graphdec.py:216-231 + :305-306 for one layer, the router row included: copy
+// row_dev = [expert ids (k) | weights (k)] (float32, on the device) into the
+// pinned row_host on the compute stream and wait for it (the one sync per
+// layer), then prepare_layer with keys key_base + id, id in [0, n_ids). ids (may be NULL)
+// replaces the row's expert ids (a caller's own routing); the weights always
+// come from the row.
+extern "C" int wisp_cache_prepare_row(void* h, const float* row_dev, float* row_host, int k, int64_t key_base,
+                                      int64_t n_ids, const int64_t* ids, float* meta_host, float* meta_dev,
+                                      int64_t* slots, void* compute) {
+    clear_error();
+    if (k < 1 || k > 64 || !row_dev || !row_host || !meta_host || !meta_dev) return fail_inval("bad prepare_row args");
+    hipStream_t st = (hipStream_t)compute;
+    hipError_t e = hipMemcpyAsync(row_host, row_dev, sizeof(float) * 2 * k, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "reading the router row");
+    int64_t keys[64];
+    for (int j = 0; j < k; ++j) {
+        int64_t id;
+        if (ids) {
+            id = ids[j];
+        } else {
+            const float f = row_host[j];
+            if (!(f >= 0.f && f < 16777216.f) || (float)(int64_t)f != f) return fail_inval("router row holds a bad id");
+            id = (int64_t)f;
+        }
+        if (id < 0 || id >= n_ids) return fail_inval("expert id outside [0, n_ids)");
+        keys[j] = key_base + id;
+    }
+    return wisp_cache_prepare_layer(h, keys, row_host + k, k, meta_host, meta_dev, slots, compute);
+}
+
+// Copy mode: 0 = one hipMemcpyAsync per row (the DMA engines), 1 = k_page_rows
+// (the GPU reads the pinned host rows over PCIe). Mode 1 needs a host store
+// mapped into the device's address space (pinned by hipHostMalloc or
+// registered) and 16-byte rows; otherwise it is refused.
+extern "C" int wisp_cache_set_copy_mode(void* h, int mode) {
+    clear_error();
+    Cache& c = *as_cache(h);
+    if (mode == 0) {
+        c.copy_mode = 0;
+        return WISP_OK;
+    }
+    if (mode != 1) return fail_inval("copy mode must be 0 (hipMemcpyAsync) or 1 (page kernel)");
+    if (c.decode_on_load) return fail_inval("the page kernel does not stage decode-on-load rows");
+    if (c.row_bytes % 16 || c.slot_bytes % 16 || !aligned(c.host, 16))
+        return fail_inval("the page kernel needs 16-byte rows and a 16-byte aligned host store");
+    void* dptr = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&dptr, const_cast<uint8_t*>(c.host), 0);
+    if (e != hipSuccess || !dptr) {
+        (void)hipGetLastError();
+        set_error("the host store is not mapped for the device (not pinned): %s", hipGetErrorString(e));
+        return WISP_EINVAL;
+    }
+    c.host_dev = static_cast<const uint8_t*>(dptr);
+    c.copy_mode = 1;
+    return WISP_OK;
 }
 
 // cache.py:144-158: keep the hottest experts in a pool of `nslots` rows. The

@@ -76,6 +76,8 @@ SIGNATURES = {
     "wisp_cache_sync_compute": (_i32, [_vp, _vp]),
     "wisp_cache_ensure": (_i32, [_vp, _vp, _i64, _vp, _vp]),
     "wisp_cache_prepare_layer": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
+    "wisp_cache_prepare_row": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "wisp_cache_set_copy_mode": (_i32, [_vp, _i32]),
     "wisp_cache_resize": (_i32, [_vp, _i64]),
     "wisp_set_tuning": (_i32, [_i32, _i32, _i32]),
     "wisp_act_read": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp]),

@@ -48,8 +48,14 @@ class ExpertCache:
         cpu_store=None,
         decode_on_load=False,
         staging_rows=8,
+        copy="auto",
     ):
+        """copy: how misses cross PCIe. "dma" = one hipMemcpyAsync per expert row on the side
+        stream (the DMA engines); "kernel" = one page kernel per batch of rows on the side
+        stream, the GPU reading the pinned store directly (needs a pinned store; faster for
+        several rows at once); "auto" = "kernel" when the store allows it, else "dma"."""
         assert policy in _POLICIES, policy
+        assert copy in ("dma", "kernel", "auto"), copy
         self.store, self.device = store, torch.device(device)
         if self.device.index is None:
             self.device = torch.device("cuda", torch.cuda.current_device())
@@ -74,6 +80,15 @@ class ExpertCache:
         core._release()  # the native cache owns the core now
         self._h = h
         self._host = host  # keep the store rows alive as long as the cache
+        self.copy = "dma"
+        if copy != "dma" and not self.decode_on_load:
+            rc = _lib.lib().wisp_cache_set_copy_mode(self._h, 1)
+            if rc == 0:
+                self.copy = "kernel"
+            elif copy == "kernel":
+                raise RuntimeError(_lib.lib().wisp_last_error().decode())
+        elif copy == "kernel":
+            raise RuntimeError("copy='kernel' does not stage decode-on-load rows")
         self._view()
         self.copy_stream = torch.cuda.ExternalStream(_lib.lib().wisp_cache_copy_stream(self._h), device=self.device)
         if n_static:
@@ -152,6 +167,26 @@ class ExpertCache:
         if rc != 0:
             raise RuntimeError(_lib.lib().wisp_last_error().decode())
         return [int(v) for v in slots[: k.size]]
+
+    def prepare_row(self, row_dev: torch.Tensor, row_host: torch.Tensor, key_base: int, k: int, n_ids: int, ids,
+                    meta_host: torch.Tensor, meta_dev: torch.Tensor):
+        """prepare_layer with the router row read back natively: row_dev float32 [>= 2k]
+        (device) = [expert ids | weights] is copied into the pinned row_host and waited for;
+        keys = key_base + id (every id in [0, n_ids)), with `ids` (int64 numpy [k]) replacing
+        the row's ids if given."""
+        assert row_dev.dtype == torch.float32 and row_host.dtype == torch.float32 and row_host.numel() >= 2 * k
+        assert meta_host.numel() >= 2 * k and meta_dev.numel() >= 2 * k
+        idp = None
+        if ids is not None:
+            ids = np.ascontiguousarray(ids, dtype=np.int64)
+            assert ids.size == k
+            idp = _p(ids)
+        rc = _lib.lib().wisp_cache_prepare_row(
+            self._h, ctypes.c_void_p(row_dev.data_ptr()), ctypes.c_void_p(row_host.data_ptr()), k, key_base, n_ids, idp,
+            ctypes.c_void_p(meta_host.data_ptr()), ctypes.c_void_p(meta_dev.data_ptr()), None, self._stream(),
+        )
+        if rc != 0:
+            raise RuntimeError(_lib.lib().wisp_last_error().decode())
 
     def split(self, keys):
         return self.core.split(keys)

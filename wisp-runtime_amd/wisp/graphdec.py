@@ -71,6 +71,7 @@ class GraphDecoder:
         self.logits = torch.zeros(1, cfg.vocab_size, **d)
         self.meta_dev = torch.zeros(2 * self.k, dtype=torch.float32, device=self.dev)
         self.meta_host = torch.zeros(2 * self.k, dtype=torch.float32, pin_memory=True)
+        self.row_host = torch.zeros(3 * self.k, dtype=torch.float32, pin_memory=True)
         self.graphs, self._key = None, None
         self._dense_setup(cfg)
 
@@ -236,6 +237,11 @@ class GraphDecoder:
                             eps=self.eps_final)
 
     # ---------------------------------------------------------------- host step of one layer
+    def _expert_ids(self, i):
+        """Expert ids of layer i replacing the router's choice (int64 [k]), or None for the
+        router's own. A hook for synthetic routing; the weights stay the router's."""
+        return None
+
     def _prepare(self, i, row):
         rt, cache, k = self.rt, self.rt.cache, self.k
         ex = [int(v) for v in row[:k]]
@@ -310,8 +316,16 @@ class GraphDecoder:
         self.ctl[0:1].copy_(token.reshape(1))
         self.ctl[1].fill_(self.pos)
         self._run(0)
+        rt = self.rt
+        fast = not self.prefetch and rt.recorder is None
         for i in range(self.L):
-            self._prepare(i, self.row.cpu()[0].tolist())  # the one sync per layer
+            if fast:  # read the row, ensure, copy, write meta: one native call (the one sync per layer)
+                rt.cache.prepare_row(self.row, self.row_host, i * self.E, self.k, self.E, self._expert_ids(i),
+                                     self.meta_host, self.meta_dev)
+                rt.stats["layer_calls"] += 1
+                rt.stats["gpu_experts"] += self.k
+            else:
+                self._prepare(i, self.row.cpu()[0].tolist())  # the one sync per layer
             self._run(i + 1)
         self.pos += 1
         return self.logits
