@@ -240,6 +240,17 @@ int wisp_cache_prepare_row(void* cache, const float* row_dev, float* row_host, i
                            int64_t n_ids, const int64_t* ids, float* meta_host, float* meta_dev, int64_t* slots,
                            void* compute);
 
+/* wisp_cache_prepare_row for a row that the GPU writes into row_host itself
+ * (wisp_dl_route with host_row/host_flag): wait until *flag != flag_before
+ * (spinning, at most timeout_ms, then WISP_EINVAL), then as prepare_row.
+ * In copy mode 1 the misses' page kernel runs on `compute` and also writes
+ * meta_dev, so no copy-stream events or meta copy are needed; in mode 0 the
+ * copies and the meta copy are those of prepare_layer. *flag_after receives
+ * the flag value seen. */
+int wisp_cache_prepare_signaled(void* cache, float* row_host, const volatile uint32_t* flag, uint32_t flag_before,
+                                uint32_t* flag_after, int timeout_ms, int k, int64_t key_base, int64_t n_ids,
+                                const int64_t* ids, float* meta_host, float* meta_dev, void* compute);
+
 /* How misses cross PCIe: mode 0 (default) = one hipMemcpyAsync per expert row
  * on the side stream (cache.py:56-60, the DMA engines); mode 1 = a page kernel
  * on the side stream that reads the pinned store rows over PCIe (one launch per
@@ -317,8 +328,13 @@ int wisp_dl_qk_rope(const void* qkv, const void* q_norm_w, const void* k_norm_w,
 /* route() at batch 1 (wisp/moe.py:41-47) plus pack_meta's order: softmax in
  * float32 of the bf16 logits [E], top-k (descending, equal values by lower
  * index), divided by their sum if norm_topk, rounded to bf16; row (float32)
- * = [ids (k) | weights (k)]. E <= 1024, k <= 16. One launch. */
-int wisp_dl_route(const void* logits, int E, int k, int norm_topk, float* row, void* stream);
+ * = [ids (k) | weights (k)]. E <= 1024, k <= 16. One launch.
+ * host_row / host_flag (optional, together; pinned host memory) also receive
+ * the row and then host_flag = ++*seq (seq: a device uint32), written with
+ * system-scope stores in that order, so the host can wait for the row by
+ * watching host_flag (graphdec.py:305's sync without a stream sync). */
+int wisp_dl_route(const void* logits, int E, int k, int norm_topk, float* row, float* host_row, uint32_t* host_flag,
+                  uint32_t* seq, void* stream);
 
 /* Launch-shape tuning, process-wide: gu_rows = rows of one expert per wave in
  * kernel 1, gu_waves = waves per workgroup in kernel 1, dn_iters = row

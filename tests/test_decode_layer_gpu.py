@@ -162,3 +162,20 @@ def test_route_matches_moe_route(E, k, norm):
         assert all(row[k + i].item() >= row[k + i + 1].item() for i in range(k - 1))
         checked += 1
     assert checked >= 15
+
+
+def test_route_signals_the_host_after_the_row():
+    """With host buffers the route kernel also writes the row to pinned host memory and then
+    bumps the host flag (graphdec.py:305's per-layer sync without a stream sync)."""
+    g = torch.Generator(device=DEV).manual_seed(5)
+    E, k = 128, 8
+    row = torch.empty(2 * k, dtype=torch.float32, device=DEV)
+    host_row = torch.zeros(3 * k, dtype=torch.float32, pin_memory=True)
+    flag = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    seq = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for it in range(4):
+        logits = torch.randn(E, generator=g, device=DEV).to(torch.bfloat16)
+        kernels.dl_route(logits, k, True, row, host_row, flag, seq)
+        torch.cuda.synchronize()
+        assert int(flag[0]) == it + 1 and int(seq.item()) == it + 1
+        assert torch.equal(host_row[: 2 * k], row.cpu())

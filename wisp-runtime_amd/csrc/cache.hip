@@ -19,6 +19,7 @@
 // between graph replays (48 host decisions per token).
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <new>
 #include <unordered_map>
@@ -228,10 +229,18 @@ struct PagePairs {
     int64_t key[kPageMax];
     int64_t slot[kPageMax];
 };
+// optional payload: workgroup (0, 0) also stores n floats to dst (the layer's meta)
+struct PageMeta {
+    float v[32];
+    float* dst;
+    int n;
+};
 typedef uint32_t pg_u32x4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void k_page_rows(const pg_u32x4* __restrict__ host, pg_u32x4* __restrict__ pool,
-                                                   const PagePairs p, int64_t row16, int64_t slot16, int64_t per) {
+                                                   const PagePairs p, int64_t row16, int64_t slot16, int64_t per,
+                                                   const PageMeta pm) {
     const int r = blockIdx.y;
+    if (blockIdx.x == 0 && r == 0 && (int)threadIdx.x < pm.n) pm.dst[threadIdx.x] = pm.v[threadIdx.x];
     const pg_u32x4* src = host + p.key[r] * row16;
     pg_u32x4* dst = pool + p.slot[r] * slot16;
     const int64_t b0 = (int64_t)blockIdx.x * per, b1 = min(row16, b0 + per);
@@ -249,6 +258,50 @@ __global__ __launch_bounds__(256) void k_page_rows(const pg_u32x4* __restrict__ 
             if (ii < b1) dst[ii] = v[u];
         }
     }
+}
+
+__global__ __launch_bounds__(64) void k_write_meta(const PageMeta pm) {
+    if ((int)threadIdx.x < pm.n) pm.dst[threadIdx.x] = pm.v[threadIdx.x];
+}
+
+// Copy mode 1, misses of one layer on the compute stream itself (ordered after
+// the queued reads of the evicted slots by stream order), the layer's meta
+// written by the first launch (or by k_write_meta when nothing is missing).
+static int page_on_stream(Cache& c, const int64_t* keys, const int64_t* slots, int64_t n, const float* meta, int nmeta,
+                          float* meta_dev, hipStream_t st) {
+    PageMeta pm;
+    for (int i = 0; i < nmeta; ++i) pm.v[i] = meta[i];
+    pm.dst = meta_dev;
+    pm.n = nmeta;
+    hipError_t e;
+    if (n == 0) {
+        hipLaunchKernelGGL(k_write_meta, dim3(1), dim3(64), 0, st, pm);
+        e = hipGetLastError();
+        return e == hipSuccess ? WISP_OK : hip_fail(e, "k_write_meta launch");
+    }
+    for (int64_t i = 0; i < n; ++i)
+        if (keys[i] < 0 || keys[i] >= c.host_rows || slots[i] < 0 || slots[i] >= c.nslots)
+            return fail_inval("key outside the host store or slot outside the pool");
+    uint8_t* pool = static_cast<uint8_t*>(c.pool->ptr);
+    const int64_t row16 = c.row_bytes / 16, slot16 = c.slot_bytes / 16;
+    const int64_t per = ((row16 + kPageSplit - 1) / kPageSplit + 1023) / 1024 * 1024;
+    for (int64_t i0 = 0; i0 < n; i0 += kPageMax) {
+        const int m = (int)std::min<int64_t>(kPageMax, n - i0);
+        PagePairs pp;
+        for (int j = 0; j < kPageMax; ++j) {
+            pp.key[j] = keys[i0 + std::min(j, m - 1)];
+            pp.slot[j] = slots[i0 + std::min(j, m - 1)];
+        }
+        hipLaunchKernelGGL(k_page_rows, dim3(kPageSplit, m), dim3(256), 0, st,
+                           reinterpret_cast<const pg_u32x4*>(c.host_dev), reinterpret_cast<pg_u32x4*>(pool), pp, row16,
+                           slot16, per, pm);
+        e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(e, "k_page_rows launch");
+        pm.n = 0;  // meta once
+    }
+    c.bytes_h2d += n * c.row_bytes;
+    c.n_loads += n;
+    return WISP_OK;
 }
 
 // cache.py:50-76: copies of [(key, slot)] on the side stream, ordered after
@@ -272,9 +325,12 @@ static int issue(Cache& c, const int64_t* keys, const int64_t* slots, int64_t n,
                 pp.key[j] = keys[i0 + std::min(j, m - 1)];
                 pp.slot[j] = slots[i0 + std::min(j, m - 1)];
             }
+            PageMeta none;
+            none.dst = nullptr;
+            none.n = 0;
             hipLaunchKernelGGL(k_page_rows, dim3(kPageSplit, m), dim3(256), 0, c.copy,
                                reinterpret_cast<const pg_u32x4*>(c.host_dev), reinterpret_cast<pg_u32x4*>(pool), pp,
-                               row16, slot16, per);
+                               row16, slot16, per, none);
             e = hipGetLastError();
             if (e != hipSuccess) return hip_fail(e, "k_page_rows launch");
         }
@@ -694,6 +750,62 @@ extern "C" int wisp_cache_prepare_row(void* h, const float* row_dev, float* row_
         keys[j] = key_base + id;
     }
     return wisp_cache_prepare_layer(h, keys, row_host + k, k, meta_host, meta_dev, slots, compute);
+}
+
+// prepare_row for a row the GPU writes into pinned host memory itself (the
+// route kernel's host_row / host_flag): spin until the flag moves, then the
+// layer's step. Copy mode 1 pages on the compute stream with the meta written
+// by the page kernel; mode 0 goes through prepare_layer.
+extern "C" int wisp_cache_prepare_signaled(void* h, float* row_host, const volatile uint32_t* flag,
+                                           uint32_t flag_before, uint32_t* flag_after, int timeout_ms, int k,
+                                           int64_t key_base, int64_t n_ids, const int64_t* ids, float* meta_host,
+                                           float* meta_dev, void* compute) {
+    clear_error();
+    if (k < 1 || k > 16 || !row_host || !flag || !meta_host || !meta_dev) return fail_inval("bad prepare_signaled args");
+    const auto t0 = std::chrono::steady_clock::now();
+    uint32_t f;
+    unsigned spins = 0;
+    while ((f = *flag) == flag_before) {
+        if ((++spins & 4095u) == 0 &&
+            std::chrono::duration_cast<std::chrono::milliseconds>(std::chrono::steady_clock::now() - t0).count() >
+                timeout_ms) {
+            set_error("timed out after %d ms waiting for the router row", timeout_ms);
+            return WISP_EINVAL;
+        }
+        __builtin_ia32_pause();
+    }
+    std::atomic_thread_fence(std::memory_order_acquire);
+    if (flag_after) *flag_after = f;
+    const volatile float* row = row_host;
+    int64_t keys[16];
+    float w[16];
+    for (int j = 0; j < k; ++j) {
+        int64_t id;
+        if (ids) {
+            id = ids[j];
+        } else {
+            const float v = row[j];
+            if (!(v >= 0.f && v < 16777216.f) || (float)(int64_t)v != v) return fail_inval("router row holds a bad id");
+            id = (int64_t)v;
+        }
+        if (id < 0 || id >= n_ids) return fail_inval("expert id outside [0, n_ids)");
+        keys[j] = key_base + id;
+        w[j] = row[k + j];
+    }
+    Cache& c = *as_cache(h);
+    hipStream_t st = (hipStream_t)compute;
+    if (c.copy_mode != 1) return wisp_cache_prepare_layer(h, keys, w, k, meta_host, meta_dev, nullptr, compute);
+    int64_t sl[16];
+    std::vector<int64_t> lk, ls;
+    int rc = core_ensure(*c.core, keys, k, sl, lk, ls);
+    if (rc) return rc;
+    for (int j = 0; j < k; ++j) {
+        meta_host[j] = (float)sl[j];
+        meta_host[k + j] = w[j];
+    }
+    rc = sync_compute(c, st);  // copies still pending on the side stream (prefetch, admit)
+    if (rc) return rc;
+    return page_on_stream(c, lk.data(), ls.data(), (int64_t)lk.size(), meta_host, 2 * k, meta_dev, st);
 }
 
 // Copy mode: 0 = one hipMemcpyAsync per row (the DMA engines), 1 = k_page_rows

@@ -310,8 +310,13 @@ __global__ __launch_bounds__(64) void k_dl_qkrope(const uint16_t* __restrict__ q
 // index first), optional renormalisation over the k, weights rounded to bf16.
 // row = [ids (k, as float) | weights (k, bf16 values as float)]. One wave.
 constexpr int kRouteMaxPerLane = 16;  // E <= 1024
+// host_row / host_flag (optional, pinned host memory mapped for the device):
+// the row is also written there with system-scope stores and, once those have
+// completed, host_flag = ++*seq (seq: a device counter), so the host can wait
+// for the row by watching host_flag instead of synchronising the stream.
 __global__ __launch_bounds__(64) void k_dl_route(const uint16_t* __restrict__ logits, int E, int k, int norm,
-                                                 float* __restrict__ row) {
+                                                 float* __restrict__ row, float* host_row, uint32_t* host_flag,
+                                                 uint32_t* seq) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x;
     float v[kRouteMaxPerLane];
@@ -364,8 +369,19 @@ __global__ __launch_bounds__(64) void k_dl_route(const uint16_t* __restrict__ lo
         float s = 0.f;
         for (int r = 0; r < k; ++r) s += sel_v[r];
         for (int r = 0; r < k; ++r) {
-            row[r] = (float)sel_i[r];
-            row[k + r] = rbf(norm ? sel_v[r] / s : sel_v[r]);
+            const float id = (float)sel_i[r], w = rbf(norm ? sel_v[r] / s : sel_v[r]);
+            row[r] = id;
+            row[k + r] = w;
+            if (host_row) {
+                __hip_atomic_store(host_row + r, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(host_row + k + r, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
+        if (host_row) {
+            const uint32_t n = *seq + 1;
+            *seq = n;
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the row stores have completed
+            __hip_atomic_store(host_flag, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
 }
@@ -479,12 +495,31 @@ extern "C" int wisp_dl_qk_rope(const void* qkv, const void* q_norm_w, const void
 }
 
 // wisp/moe.py:41-47 (route) at batch 1 + pack_meta's [ids | weights] order
-extern "C" int wisp_dl_route(const void* logits, int E, int k, int norm_topk, float* row, void* stream) {
+extern "C" int wisp_dl_route(const void* logits, int E, int k, int norm_topk, float* row, float* host_row,
+                             uint32_t* host_flag, uint32_t* seq, void* stream) {
     clear_error();
     if (!logits || !row) return fail_inval("null pointer");
     if (E < 1 || E > 64 * kRouteMaxPerLane) return fail_inval("E must be in [1, 1024]");
     if (k < 1 || k > 16 || k > E) return fail_inval("k must be in [1, min(16, E)]");
+    if ((host_row != nullptr) != (host_flag != nullptr) || (host_row && !seq))
+        return fail_inval("host_row, host_flag and seq go together");
+    float* hr = nullptr;
+    uint32_t* hf = nullptr;
+    if (host_row) {  // device addresses of the pinned host buffers
+        void* d1 = nullptr;
+        void* d2 = nullptr;
+        hipError_t e = hipHostGetDevicePointer(&d1, host_row, 0);
+        if (e == hipSuccess) e = hipHostGetDevicePointer(&d2, host_flag, 0);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            set_error("host_row / host_flag are not pinned host memory mapped for the device: %s",
+                      hipGetErrorString(e));
+            return WISP_EINVAL;
+        }
+        hr = static_cast<float*>(d1);
+        hf = static_cast<uint32_t*>(d2);
+    }
     hipLaunchKernelGGL(k_dl_route, dim3(1), dim3(64), 0, (hipStream_t)stream, (const uint16_t*)logits, E, k,
-                       norm_topk ? 1 : 0, row);
+                       norm_topk ? 1 : 0, row, hr, hf, seq);
     return check_launch("k_dl_route");
 }

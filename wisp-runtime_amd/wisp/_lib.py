@@ -46,7 +46,7 @@ SIGNATURES = {
                             _vp, _vp]),
     "wisp_dl_qk_rope": (_i32, [_vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _i64, _vp,
                                _vp]),
-    "wisp_dl_route": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp]),
+    "wisp_dl_route": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "wisp_gptoss_ws_bytes": (_i64, [_i32, _i64, _i64]),
     "wisp_gptoss_decode": (_i32, [_vp, _i64, _i64, _vp, _i32, _i64, _i64, _i32, _i64, _vp, _vp, _vp, _i64,
                                   ctypes.c_float, ctypes.c_float, _vp, _vp, _vp]),
@@ -77,6 +77,8 @@ SIGNATURES = {
     "wisp_cache_ensure": (_i32, [_vp, _vp, _i64, _vp, _vp]),
     "wisp_cache_prepare_layer": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
     "wisp_cache_prepare_row": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "wisp_cache_prepare_signaled": (_i32, [_vp, _vp, _vp, ctypes.c_uint32, _vp, _i32, _i32, _i64, _i64, _vp, _vp, _vp,
+                                           _vp]),
     "wisp_cache_set_copy_mode": (_i32, [_vp, _i32]),
     "wisp_cache_resize": (_i32, [_vp, _i64]),
     "wisp_set_tuning": (_i32, [_i32, _i32, _i32]),

@@ -188,6 +188,27 @@ class ExpertCache:
         if rc != 0:
             raise RuntimeError(_lib.lib().wisp_last_error().decode())
 
+    def prepare_signaled(self, row_host: torch.Tensor, flag_host: torch.Tensor, flag_before: int, key_base: int,
+                         k: int, n_ids: int, ids, meta_host: torch.Tensor, meta_dev: torch.Tensor,
+                         timeout_ms: int = 10000) -> int:
+        """prepare_row for a row the route kernel writes into the pinned row_host itself: wait
+        until flag_host moves from flag_before, then ensure / copy / meta. Returns the flag."""
+        assert row_host.is_pinned() and flag_host.is_pinned() and row_host.numel() >= 2 * k
+        idp = None
+        if ids is not None:
+            ids = np.ascontiguousarray(ids, dtype=np.int64)
+            assert ids.size == k
+            idp = _p(ids)
+        after = ctypes.c_uint32()
+        rc = _lib.lib().wisp_cache_prepare_signaled(
+            self._h, ctypes.c_void_p(row_host.data_ptr()), ctypes.c_void_p(flag_host.data_ptr()),
+            flag_before & 0xFFFFFFFF, ctypes.byref(after), timeout_ms, k, key_base, n_ids, idp,
+            ctypes.c_void_p(meta_host.data_ptr()), ctypes.c_void_p(meta_dev.data_ptr()), self._stream(),
+        )
+        if rc != 0:
+            raise RuntimeError(_lib.lib().wisp_last_error().decode())
+        return after.value
+
     def split(self, keys):
         return self.core.split(keys)
 

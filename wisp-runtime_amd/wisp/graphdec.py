@@ -72,6 +72,9 @@ class GraphDecoder:
         self.meta_dev = torch.zeros(2 * self.k, dtype=torch.float32, device=self.dev)
         self.meta_host = torch.zeros(2 * self.k, dtype=torch.float32, pin_memory=True)
         self.row_host = torch.zeros(3 * self.k, dtype=torch.float32, pin_memory=True)
+        # the route kernel also writes the row here and bumps the flag (no stream sync per layer)
+        self.flag_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self.seq_dev = torch.zeros(1, dtype=torch.int32, device=self.dev)
         self.graphs, self._key = None, None
         self._dense_setup(cfg)
 
@@ -211,7 +214,8 @@ class GraphDecoder:
         kernels.dl_gemv(self.hm.view(H), w["o"], o.view(Hq * D), res=self.hbuf)
         kernels.dl_gemv(self.rlogits, w["gate"], self.hm.view(H), norm_w=w["ln2"], eps=w["eps2"],
                         x_out=self.xn.view(H))
-        kernels.dl_route(self.rlogits, self.k, w["norm_topk"], self.row.view(-1))
+        kernels.dl_route(self.rlogits, self.k, w["norm_topk"], self.row.view(-1), self.row_host, self.flag_host,
+                         self.seq_dev)
         if self.prefetch:
             ng = getattr(self.layers[i].mlp, "next_gate", None)
             pred = (torch.topk(ng(self.xn.view(1, H)), self.k, dim=-1).indices.float() if ng is not None
@@ -315,13 +319,14 @@ class GraphDecoder:
             self.capture()
         self.ctl[0:1].copy_(token.reshape(1))
         self.ctl[1].fill_(self.pos)
-        self._run(0)
         rt = self.rt
         fast = not self.prefetch and rt.recorder is None
+        flag = int(self.flag_host[0])  # no route kernel is in flight here
+        self._run(0)
         for i in range(self.L):
-            if fast:  # read the row, ensure, copy, write meta: one native call (the one sync per layer)
-                rt.cache.prepare_row(self.row, self.row_host, i * self.E, self.k, self.E, self._expert_ids(i),
-                                     self.meta_host, self.meta_dev)
+            if fast:  # wait for the row the route kernel writes to host memory, then ensure / copy / meta
+                flag = rt.cache.prepare_signaled(self.row_host, self.flag_host, flag, i * self.E, self.k, self.E,
+                                                 self._expert_ids(i), self.meta_host, self.meta_dev)
                 rt.stats["layer_calls"] += 1
                 rt.stats["gpu_experts"] += self.k
             else:

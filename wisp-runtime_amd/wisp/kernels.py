@@ -386,13 +386,20 @@ def dl_qk_rope(qkv, q_norm_w, k_norm_w, eps, cos, sin, pos, hq, hk, d, kc, vc, q
     return qo
 
 
-def dl_route(logits, k, norm_topk, row):
+def dl_route(logits, k, norm_topk, row, host_row=None, host_flag=None, seq=None):
     """route() of wisp/moe.py:41-47 at batch 1 on the device: softmax (float32) of the bf16
     router logits [E], top-k, renormalised if norm_topk, weights rounded to bf16;
-    row[:k] = expert ids (float32), row[k:2k] = weights. One launch."""
+    row[:k] = expert ids (float32), row[k:2k] = weights. One launch. With host_row (pinned
+    float32 [>= 2k]), host_flag (pinned int32 [1]) and seq (device int32 [1]) the row is also
+    written to host_row and then host_flag = ++seq, for a host that waits on the flag."""
     _bf16_vec(logits, "logits")
     assert row.dtype == torch.float32 and row.is_contiguous() and row.numel() >= 2 * k
     dev = _lib.require_gpu(logits, row, what="dl_route")
+    hr = hf = sq = None
+    if host_row is not None:
+        assert host_row.is_pinned() and host_flag.is_pinned() and host_row.dtype == torch.float32
+        assert host_row.numel() >= 2 * k and host_flag.dtype == torch.int32 and seq.is_cuda
+        hr, hf, sq = _lib.ptr(host_row), _lib.ptr(host_flag), _lib.ptr(seq)
     _lib.check(_lib.lib().wisp_dl_route(_lib.ptr(logits), logits.numel(), k, int(bool(norm_topk)), _lib.ptr(row),
-                                        _lib.stream(dev)), "dl_route")
+                                        hr, hf, sq, _lib.stream(dev)), "dl_route")
     return row
