@@ -284,6 +284,25 @@ def summarize_trace(trace_csv: str, stats_csv: str, bits: int, cmd: str, bench_l
     return "\n".join(lines) + "\n"
 
 
+def summarize_stats(stats_csv: str, title: str, cmd: str, bench_line: str, top: int = 16) -> str:
+    """Markdown table of the `top` kernels by total time from a rocprofv3 --stats CSV (any
+    workload), with the command that made it and the profiled process's bench line."""
+    import csv
+
+    with open(stats_csv) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: -float(r["TotalDurationNs"]))
+    lines = [f"# {title} (rocprofv3)", "", "Command (from the repository root on the GPU box):", "", "```", cmd, "```",
+             "", "| kernel | calls | total ms | avg ns | min ns | max ns | % of kernel time |",
+             "|---|---|---|---|---|---|---|"]
+    for r in rows[:top]:
+        name = r["Name"] if len(r["Name"]) <= 110 else r["Name"][:107] + "..."
+        lines.append(f"| `{name}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.2f} | "
+                     f"{float(r['AverageNs']):.0f} | {r['MinNs']} | {r['MaxNs']} | {float(r['Percentage']):.2f} |")
+    lines += ["", "bench.py's own line from the profiled process (the profiler adds per-dispatch overhead, so its "
+              "times are not the figures of record):", "", "```", bench_line.strip(), "```"]
+    return "\n".join(lines) + "\n"
+
+
 def measure(W: Layers, steps: int, warmup: int):
     """Seconds per layer (both kernels, routing meta refreshed before every replay) and per
     kernel alone: graph replays over all layers, HIP events on the replay stream."""
@@ -512,9 +531,20 @@ def main():
     ap.add_argument("--c4-warmup", type=int, default=8)
     ap.add_argument("--c4-copy", default="auto", choices=["dma", "kernel", "auto"],
                     help="how expert misses cross PCIe (ExpertCache copy=)")
+    ap.add_argument("--summarize-stats", nargs=4, metavar=("STATS_CSV", "BENCH_LOG", "TITLE", "NAME"),
+                    help="write profiles/NAME.md from a rocprofv3 --stats CSV (command text from --pmc-command)")
     ap.add_argument("--summarize-trace", nargs=3, metavar=("TRACE_CSV", "STATS_CSV", "BENCH_JSON"),
                     help="write the kernel-trace summary under profiles/ from a rocprofv3 run of bench.py")
     a = ap.parse_args()
+
+    if a.summarize_stats:
+        with open(a.summarize_stats[1]) as f:
+            bench_line = [ln for ln in f if ln.startswith("{")][-1]
+        text = summarize_stats(a.summarize_stats[0], a.summarize_stats[2], a.pmc_command, bench_line)
+        with open(os.path.join(PROFILES, a.summarize_stats[3] + ".md"), "w") as f:
+            f.write(text)
+        print(text)
+        return
 
     if a.summarize_trace:
         with open(a.summarize_trace[2]) as f:
