@@ -369,7 +369,7 @@ def _attn_case(Hq, Hk, D, T, seed):
 
 
 @pytest.mark.parametrize("Hq,Hk,D,T", [(32, 4, 128, 256), (8, 8, 64, 130), (4, 1, 256, 70), (32, 2, 128, 64),
-                                       (16, 4, 128, 4096)])
+                                       (16, 4, 128, 4096), (8, 2, 128, 6000)])
 def test_attn_decode_matches_oracle(Hq, Hk, D, T):
     q, k, v, tq, tk, tv = _attn_case(Hq, Hk, D, T, seed=Hq + D + T)
     scale = D ** -0.5
