@@ -45,11 +45,25 @@ struct Core {
     std::unordered_map<int64_t, double> freq;
     std::vector<int64_t> freq_order;  // insertion order of freq's keys
     int64_t hits = 0, misses = 0, evictions = 0, calls = 0;
+    // protected slots of the current request: pmark[s] == pgen (one array pass per victim search)
+    std::vector<uint32_t> pmark;
+    uint32_t pgen = 0;
 
     Core(int64_t n, int pol, double dec, int64_t nst, double adm)
         : nslots(n), n_static(nst), policy(pol), decay(dec), admit_after(adm), slot_key(n, -1), last(n, 0.0),
-          score(n, 0.0) {
+          score(n, 0.0), pmark(n, 0) {
         for (int64_t s = n - 1; s >= nst; --s) free.push_back(s);
+    }
+
+    // start a new protected set (empty)
+    void prot_begin() {
+        if (++pgen == 0) {  // wrapped: clear the marks once
+            std::fill(pmark.begin(), pmark.end(), 0u);
+            pgen = 1;
+        }
+    }
+    void prot_add(int64_t s) {
+        if (s >= 0 && s < nslots) pmark[s] = pgen;
     }
 
     double& freq_at(int64_t k) {  // defaultdict(float) access
@@ -92,7 +106,8 @@ struct Core {
     }
 
     // cache_core.py:64-84; returns -1 when nothing is evictable
-    int64_t acquire(int64_t key, const std::unordered_set<int64_t>& prot) {
+    // (the protected slots are those marked since the last prot_begin)
+    int64_t acquire(int64_t key) {
         int64_t s;
         if (!free.empty()) {
             s = free.back();
@@ -102,7 +117,7 @@ struct Core {
             int64_t j = -1;
             double best = INFINITY;
             for (int64_t i = n_static; i < nslots; ++i) {
-                const double v = prot.count(i) ? INFINITY : src[i];
+                const double v = pmark[i] == pgen ? INFINITY : src[i];
                 if (j < 0 || v < best) {
                     best = v;
                     j = i;
@@ -378,21 +393,21 @@ static int core_ensure(Core& c, const int64_t* keys, int64_t n, int64_t* slots, 
     c.step();
     c.note(keys, n);
     c.calls += 1;
-    std::unordered_set<int64_t> prot;
+    c.prot_begin();
     for (int64_t i = 0; i < n; ++i) {
         const int64_t s = c.lookup(keys[i]);
         slots[i] = s;
         if (s >= 0) {
-            prot.insert(s);
+            c.prot_add(s);
             c.hits += 1;
         }
     }
     for (int64_t i = 0; i < n; ++i) {
         if (slots[i] >= 0) continue;
-        const int64_t s = c.acquire(keys[i], prot);
+        const int64_t s = c.acquire(keys[i]);
         if (s < 0) return no_slot();
         slots[i] = s;
-        prot.insert(s);
+        c.prot_add(s);
         lk.push_back(keys[i]);
         ls.push_back(s);
         c.misses += 1;
@@ -470,8 +485,10 @@ extern "C" int wisp_core_split(void* h, const int64_t* keys, int64_t n, int64_t*
 
 extern "C" int wisp_core_acquire(void* h, int64_t key, const int64_t* prot, int64_t nprot, int64_t* slot) {
     clear_error();
-    std::unordered_set<int64_t> p(prot, prot + nprot);
-    const int64_t s = as_core(h)->acquire(key, p);
+    Core& c = *as_core(h);
+    c.prot_begin();
+    for (int64_t i = 0; i < nprot; ++i) c.prot_add(prot[i]);
+    const int64_t s = c.acquire(key);
     if (s < 0) return no_slot();
     *slot = s;
     return WISP_OK;
@@ -481,8 +498,9 @@ extern "C" int wisp_core_acquire(void* h, int64_t key, const int64_t* prot, int6
 extern "C" int64_t wisp_core_admit(void* h, int64_t key, const int64_t* prot, int64_t nprot) {
     Core& c = *as_core(h);
     if (c.lookup(key) >= 0 || !(c.norm_freq(key) >= c.admit_after)) return -1;
-    std::unordered_set<int64_t> p(prot, prot + nprot);
-    return c.acquire(key, p);
+    c.prot_begin();
+    for (int64_t i = 0; i < nprot; ++i) c.prot_add(prot[i]);
+    return c.acquire(key);
 }
 
 extern "C" int wisp_core_preload(void* h, const int64_t* keys, int64_t n) {

@@ -309,22 +309,29 @@ __global__ __launch_bounds__(64) void k_dl_qkrope(const uint16_t* __restrict__ q
 // softmax (binary32) over E bf16 logits, top-k (descending; equal values: lower
 // index first), optional renormalisation over the k, weights rounded to bf16.
 // row = [ids (k, as float) | weights (k, bf16 values as float)]. One wave.
-constexpr int kRouteMaxPerLane = 16;  // E <= 1024
 // host_row / host_flag (optional, pinned host memory mapped for the device):
 // the row is also written there with system-scope stores and, once those have
 // completed, host_flag = ++*seq (seq: a device counter), so the host can wait
 // for the row by watching host_flag instead of synchronising the stream.
+// EPL = logits per lane (a power of two >= E/64): every load is issued before
+// any use (addresses clamped into range, the extra values masked afterwards).
+template <int EPL>
 __global__ __launch_bounds__(64) void k_dl_route(const uint16_t* __restrict__ logits, int E, int k, int norm,
                                                  float* __restrict__ row, float* host_row, uint32_t* host_flag,
                                                  uint32_t* seq) {
 #pragma clang fp contract(off)
+    constexpr int kRouteMaxPerLane = EPL;
     const int lane = threadIdx.x;
+    const uint32_t seq0 = host_row ? *seq : 0u;  // requested with the logits
+    uint32_t raw[kRouteMaxPerLane];
+#pragma unroll
+    for (int t = 0; t < kRouteMaxPerLane; ++t) raw[t] = logits[min(lane + 64 * t, E - 1)];
     float v[kRouteMaxPerLane];
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < kRouteMaxPerLane; ++t) {
         const int i = lane + 64 * t;
-        v[t] = i < E ? bf(logits[i]) : -INFINITY;
+        v[t] = i < E ? bf(raw[t]) : -INFINITY;
         mx = fmaxf(mx, v[t]);
     }
     mx = wave_max(mx);
@@ -365,23 +372,24 @@ __global__ __launch_bounds__(64) void k_dl_route(const uint16_t* __restrict__ lo
         for (int t = 0; t < kRouteMaxPerLane; ++t)
             if (lane + 64 * t == bi) v[t] = -1.f;
     }
-    if (lane == 0) {
-        float s = 0.f;
-        for (int r = 0; r < k; ++r) s += sel_v[r];
-        for (int r = 0; r < k; ++r) {
-            const float id = (float)sel_i[r], w = rbf(norm ? sel_v[r] / s : sel_v[r]);
-            row[r] = id;
-            row[k + r] = w;
-            if (host_row) {
-                __hip_atomic_store(host_row + r, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                __hip_atomic_store(host_row + k + r, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            }
-        }
-        if (host_row) {
-            const uint32_t n = *seq + 1;
-            *seq = n;
-            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the row stores have completed
-            __hip_atomic_store(host_flag, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    // every lane holds the same selection: lanes r < k store id r, lanes k + r weight r
+    float tot = 0.f;
+    for (int r = 0; r < k; ++r) tot += sel_v[r];
+    float val = 0.f;
+    for (int r = 0; r < k; ++r) {
+        if (lane == r) val = (float)sel_i[r];
+        if (lane == k + r) val = rbf(norm ? sel_v[r] / tot : sel_v[r]);
+    }
+    if (lane < 2 * k) {
+        row[lane] = val;
+        if (host_row) __hip_atomic_store(host_row + lane, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    if (host_row) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this lane's row store has completed
+        __builtin_amdgcn_wave_barrier();     // ... and every other lane's (one wave)
+        if (lane == 0) {
+            *seq = seq0 + 1;
+            __hip_atomic_store(host_flag, seq0 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
 }
@@ -499,7 +507,7 @@ extern "C" int wisp_dl_route(const void* logits, int E, int k, int norm_topk, fl
                              uint32_t* host_flag, uint32_t* seq, void* stream) {
     clear_error();
     if (!logits || !row) return fail_inval("null pointer");
-    if (E < 1 || E > 64 * kRouteMaxPerLane) return fail_inval("E must be in [1, 1024]");
+    if (E < 1 || E > 1024) return fail_inval("E must be in [1, 1024]");
     if (k < 1 || k > 16 || k > E) return fail_inval("k must be in [1, min(16, E)]");
     if ((host_row != nullptr) != (host_flag != nullptr) || (host_row && !seq))
         return fail_inval("host_row, host_flag and seq go together");
@@ -519,7 +527,13 @@ extern "C" int wisp_dl_route(const void* logits, int E, int k, int norm_topk, fl
         hr = static_cast<float*>(d1);
         hf = static_cast<uint32_t*>(d2);
     }
-    hipLaunchKernelGGL(k_dl_route, dim3(1), dim3(64), 0, (hipStream_t)stream, (const uint16_t*)logits, E, k,
-                       norm_topk ? 1 : 0, row, hr, hf, seq);
+    hipStream_t st = (hipStream_t)stream;
+    const uint16_t* lg = (const uint16_t*)logits;
+    const int nt = norm_topk ? 1 : 0;
+    if (E <= 64) hipLaunchKernelGGL(k_dl_route<1>, dim3(1), dim3(64), 0, st, lg, E, k, nt, row, hr, hf, seq);
+    else if (E <= 128) hipLaunchKernelGGL(k_dl_route<2>, dim3(1), dim3(64), 0, st, lg, E, k, nt, row, hr, hf, seq);
+    else if (E <= 256) hipLaunchKernelGGL(k_dl_route<4>, dim3(1), dim3(64), 0, st, lg, E, k, nt, row, hr, hf, seq);
+    else if (E <= 512) hipLaunchKernelGGL(k_dl_route<8>, dim3(1), dim3(64), 0, st, lg, E, k, nt, row, hr, hf, seq);
+    else hipLaunchKernelGGL(k_dl_route<16>, dim3(1), dim3(64), 0, st, lg, E, k, nt, row, hr, hf, seq);
     return check_launch("k_dl_route");
 }
