@@ -17,21 +17,20 @@
 //          token t's j-th expert in ascending expert id.
 //   ws:    act bf16 [P, I] (gate_up output) | y fp32 [P, H] (weighted down output)
 // Kernels:
-//   k_pf_gate_up  grid (I/128, U, Z): per wave 32 act columns of one expert
-//                 (their 32 gate and 32 up rows); K = H in 128-wide steps (one
-//                 quant group per row).
-//   k_pf_down     grid (H/256, U, Z): per wave 64 down rows; K = I.
+//   k_pf_gate_up  grid (I/128, U, Z), 8 waves: per wave 16 act columns of one
+//                 expert (their gate and up rows); K = H.
+//   k_pf_down     grid (H/256, U, Z), 8 waves: per wave 32 down rows; K = I.
 //   (workgroup z takes the group's token passes z, z+Z, ...)
 //   k_pf_combine  out[t] = bf16(sum_j y[back[t, j]]).
-// Waves work independently (no LDS, no barriers): a wave owns 64 weight rows
-// (four 16-row tiles; gate_up: 32 gate rows and the same 32 up rows), streams
-// their codes one 128-wide K step (one quant group) ahead, dequantizes them in
-// registers straight into MFMA B fragments, and multiplies them against up to
-// MT 16-token tiles of the group (v_mfma_f32_16x16x32_bf16, tokens as M, rows
-// as N); each token fragment is reused by the four row tiles.
-// K order inside a step: lane group g = lane/16 holds the step's 32-code chunk
-// g, and MFMA k-substep s takes its codes 8s..8s+7; the A operand (token rows,
-// read from L2) uses the same order, which leaves the dot products unchanged.
+// A wave owns 32 weight rows (two 16-row tiles), streams their codes one step
+// (a pair of 128-wide quant groups, so whole 128-byte lines of a row) ahead,
+// dequantizes them in registers straight into MFMA B fragments, and multiplies
+// them against up to MT 16-token tiles of the group staged in LDS
+// (v_mfma_f32_16x16x32_bf16, tokens as M, rows as N); each token fragment is
+// reused by the two row tiles.
+// K order inside a group: lane group g = lane/16 holds the group's 32-code
+// chunk g, and MFMA k-substep s takes its codes 8s..8s+7; the A operand uses the
+// same order, which leaves the dot products unchanged.
 // Groups larger than one pass (MT*16 tokens) spread over Z workgroups.
 // MFMA 16x16x32 bf16 lane layout (lane l): A[row l%16][k 8*(l/16) + 0..7],
 // B[k 8*(l/16) + 0..7][col l%16], D[row 4*(l/16) + 0..3][col l%16].
@@ -48,7 +47,11 @@ namespace wisp {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kPfWaves = 4;  // waves per workgroup, 16 weight rows each
+// A workgroup owns 256 weight rows as NW waves x TPW 16-row tiles (NW * TPW = 16):
+// 4 waves x 4 tiles for passes of up to two token tiles, 8 waves x 2 tiles for
+// four (measured on C5: fewer, larger waves are faster while the passes are
+// short, more waves once the 4-tile passes need registers).
+constexpr int kPfMaxTiles = 4;
 
 struct Prefill {
     const uint8_t* pool;
@@ -129,7 +132,7 @@ __device__ __forceinline__ int group_state(const Prefill& F, int u, int& slot, i
     return (slot >= 0 && slot < F.nslots) ? 2 : 1;
 }
 
-// A wave's 4 weight row tiles: the lane's code and scale pointers for tile 0
+// A wave's weight row tiles: the lane's code and scale pointers for tile 0
 // (its row and chunk) and the tiles' offsets from them (wave-uniform).
 // Scale/min table of a workgroup's 256 weight rows, staged in LDS when a row has
 // at most kPfSmSteps quant groups (K <= 2048): entry [local row][K step] =
@@ -140,9 +143,9 @@ struct PfRows {
     const uint8_t* rc;   // codes of tile 0 at the lane's row and chunk
     const uint16_t* sp;  // fp16 scales of tile 0's row (one per 128-code group), global
     int64_t mn_off;      // mins - scales, in fp16 elements
-    int64_t code_off[4], scale_off[4];
+    int64_t code_off[kPfMaxTiles], scale_off[kPfMaxTiles];
     const uint32_t* sml;  // LDS table at tile 0's row (nullptr: read sp/mn from global memory)
-    int sml_off[4];       // per-tile offsets in the LDS table, entries
+    int sml_off[kPfMaxTiles];  // per-tile offsets in the LDS table, entries
 };
 
 // One K step's codes and fp16 scale/min (packed s | m << 16) of a lane's row in tile j.
@@ -164,7 +167,7 @@ __device__ __forceinline__ void pf_load(const PfRows& R, int j, int kc, uint32_t
 __device__ __forceinline__ void pf_stage_scales(const uint16_t* sc, int64_t mn_off, int nrows, int nk, int local0,
                                                 uint32_t* sml) {
     const int total = nrows * nk;  // entries, 8 per 16-byte load
-    for (int e = (int)threadIdx.x * 8; e < total; e += 256 * 8) {
+    for (int e = (int)threadIdx.x * 8; e < total; e += (int)blockDim.x * 8) {
         const uint4 vs = *reinterpret_cast<const uint4*>(sc + e);
         const uint4 vm = *reinterpret_cast<const uint4*>(sc + mn_off + e);
         const uint32_t s4[4] = {vs.x, vs.y, vs.z, vs.w}, m4[4] = {vm.x, vm.y, vm.z, vm.w};
@@ -194,44 +197,46 @@ __device__ __forceinline__ void pf_bfrag(const uint32_t* cd, uint32_t sm, uint4*
 // conflicts for the 128-bit reads).
 constexpr int kArs = 33;
 
-// One pass of the workgroup GEMM. The 4 waves share the pass's NT*16 A rows
+// One pass of the workgroup GEMM. The NW waves share the pass's NT*16 A rows
 // (the token or activation rows of the group's pairs), staged a PAIR of K groups
-// (256 values) at a time in LDS, double-buffered with one barrier per pair: each
-// thread copies NT x 2 uint4 of a pair, crow[r] = its copy rows r*16 +
-// threadIdx.x/16 at column threadIdx.x%16. Each wave multiplies them with its
-// own 4 weight row tiles (PfRows), whose codes are dequantized in registers.
-// Weight reads: step 2q takes row tiles 0 and 1 over groups 2q and 2q+1, step
-// 2q+1 tiles 2 and 3 over the same groups. A lane's pieces of groups 2q and
-// 2q+1 of one row are the two halves of one 128-byte line, requested back to
-// back. (Requested one K step apart, ~1.5 us, the two half-lines of a row reach
-// HBM separately; a loads-only measurement with compute between the steps:
-// 3.7 TB/s against 5.4 TB/s for whole lines.) Each step's codes are requested
-// one step ahead, the next pair's A pieces at the start of the pair.
-// Loads go into register sets that swap roles (the loop is unrolled by the two
-// steps of a pair), never through a register copy: on this hardware a copy of
-// a load's destination waits for the load, which would serialise the prefetch.
-// Every thread of the workgroup calls it with the same nk; NT is the pass's
-// exact tile count, so the loop has no per-tile branches.
+// (256 values) at a time in LDS, double-buffered with one barrier per pair:
+// thread t copies the pieces t + k*64*NW (k < RPT) of a pair, piece i being A
+// row i/32, group half (i/16)&1, 16-byte column i%16; crow[k] = the start of
+// its k-th row plus its column.
+// Weight reads: a step covers two of the wave's row tiles over one group pair
+// (TPW/2 steps per pair), so a lane requests its pieces of groups 2q and 2q+1
+// of a row back to back -- the two halves of one 128-byte line. (Half lines
+// requested one K step apart, ~1.5 us, reach HBM separately; a loads-only
+// measurement with compute between the steps: 3.7 TB/s against 5.4 TB/s for
+// whole lines.) Each step's codes are requested one step ahead, the next
+// pair's A pieces at the start of a pair and written to LDS at its end.
+// Loads go into register sets that swap roles (the loop is unrolled by two
+// steps), never through a register copy: on this hardware a copy of a load's
+// destination waits for the load, which would serialise the prefetch. Every
+// thread of the workgroup calls it with the same nk; NT is the pass's exact
+// tile count, so the loop has no per-tile branches.
 template <int BITS>
 struct PfStep {
-    uint32_t cd[2][2][BITS], sm[2][2];  // [row tile of the step][group of the pair]: codes, packed s | m << 16
+    uint32_t cd[2][2][BITS], sm[2][2];  // [row tile of the step][group of the pair]: codes, s | m << 16
 };
 
-template <int BITS, int NT>
+template <int BITS, int NT, int NW>
 __device__ __forceinline__ void pf_gemm(const PfRows& R, const uint4* const* crow, uint4* lds, int nk,
-                                        f32x4_t (*acc)[4]) {
+                                        f32x4_t (*acc)[16 / NW]) {
+    constexpr int TPW = 16 / NW, TP = TPW / 2;  // row tiles per wave, steps per group pair
+    constexpr int RPT = 8 * NT / NW;           // A pieces per thread and pair
     constexpr int BUF = NT * 16 * kArs;
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
-    const int cm = threadIdx.x >> 4, cc = threadIdx.x & 15;
-    const int npairs = (nk + 1) >> 1;
+    const int cm = threadIdx.x >> 5, hh = (threadIdx.x >> 4) & 1, cc = threadIdx.x & 15;
+    const int npairs = (nk + 1) >> 1, nsteps = npairs * TP;
     u32x4_t* ldv = reinterpret_cast<u32x4_t*>(lds);
 #pragma unroll
     for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    // step st: row tiles 2*(st&1) + {0, 1}, groups 2*(st>>1) + {0, 1} (past the end: reload, in bounds)
+        for (int j = 0; j < TPW; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // step st: row tiles 2*(st%TP) + {0, 1}, groups 2*(st/TP) + {0, 1} (past the end: reload, in bounds)
     auto load_step = [&](PfStep<BITS>& S, int st) {
-        const int q = st >> 1, t0 = 2 * (st & 1);
+        const int q = st / TP, t0 = 2 * (st - q * TP);
         const int k0 = min(2 * q, nk - 1), k1 = min(2 * q + 1, nk - 1);
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
@@ -239,23 +244,18 @@ __device__ __forceinline__ void pf_gemm(const PfRows& R, const uint4* const* cro
             pf_load<BITS>(R, t0 + jj, k1, S.cd[jj][1], S.sm[jj][1]);
         }
     };
-    auto load_a = [&](u32x4_t (*av)[2], int q) {
-        const int k0 = min(2 * q, nk - 1), k1 = min(2 * q + 1, nk - 1);
+    auto load_a = [&](u32x4_t* av, int q) {
+        const int kg = min(2 * q + hh, nk - 1);
 #pragma unroll
-        for (int r = 0; r < NT; ++r) {
-            av[r][0] = *reinterpret_cast<const u32x4_t*>(crow[r] + k0 * 16);
-            av[r][1] = *reinterpret_cast<const u32x4_t*>(crow[r] + k1 * 16);
-        }
+        for (int k = 0; k < RPT; ++k) av[k] = *reinterpret_cast<const u32x4_t*>(crow[k] + kg * 16);
     };
-    auto put_a = [&](const u32x4_t (*av)[2], int buf) {
+    auto put_a = [&](const u32x4_t* av, int buf) {
 #pragma unroll
-        for (int r = 0; r < NT; ++r) {
-            ldv[buf * BUF + (r * 16 + cm) * kArs + cc] = av[r][0];
-            ldv[buf * BUF + (r * 16 + cm) * kArs + 16 + cc] = av[r][1];
-        }
+        for (int k = 0; k < RPT; ++k) ldv[buf * BUF + (cm + 2 * NW * k) * kArs + 16 * hh + cc] = av[k];
     };
-    // the MFMAs of one step: its two row tiles against the pair's A tile (buffer q&1)
-    auto compute = [&](const PfStep<BITS>& S, int t0, int q) {
+    // the MFMAs of step st: its two row tiles against the pair's A tile (buffer q&1)
+    auto compute = [&](const PfStep<BITS>& S, int st) {
+        const int q = st / TP, t0 = 2 * (st - q * TP);
         const uint4* A = lds + (q & 1) * BUF;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -272,41 +272,55 @@ __device__ __forceinline__ void pf_gemm(const PfRows& R, const uint4* const* cro
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
 #pragma unroll
-                    for (int mt = 0; mt < NT; ++mt) acc[mt][t0 + jj] = mfma16(xa[mt][s], b[s], acc[mt][t0 + jj]);
+                    for (int mt = 0; mt < NT; ++mt)
+                        acc[mt][t0 + jj] = mfma16(xa[mt][s], b[s], acc[mt][t0 + jj]);
             }
         }
     };
+    // the A tile around step st: the next pair's pieces requested (and the barrier)
+    // at a pair's first step, written to LDS after its last
+    auto step = [&](const PfStep<BITS>& C, PfStep<BITS>& N, u32x4_t* an, int st) {
+        const int q = st / TP;
+        if (st == q * TP) {
+            load_a(an, min(q + 1, npairs - 1));
+            load_step(N, st + 1);
+            __syncthreads();  // pair q's A tile is in buffer q&1; pair q-1's reads are done
+        } else {
+            load_step(N, st + 1);
+        }
+        compute(C, st);
+        if (st == q * TP + TP - 1 && q + 1 < npairs) put_a(an, (q + 1) & 1);  // buffer last read in pair q-1
+    };
     PfStep<BITS> S0, S1;
-    u32x4_t an[NT][2];
+    u32x4_t an[RPT];
     load_a(an, 0);
     load_step(S0, 0);
     put_a(an, 0);
-    for (int q = 0; q < npairs; ++q) {
-        load_a(an, min(q + 1, npairs - 1));  // the next pair's A pieces
-        load_step(S1, 2 * q + 1);
-        __syncthreads();  // pair q's A tile is in buffer q&1; pair q-1's reads are done
-        compute(S0, 0, q);
-        load_step(S0, 2 * q + 2);
-        compute(S1, 2, q);
-        if (q + 1 < npairs) put_a(an, (q + 1) & 1);  // buffer last read in pair q-1
+    for (int st = 0;; st += 2) {
+        step(S0, S1, an, st);
+        if (st + 1 >= nsteps) break;
+        step(S1, S0, an, st + 1);
+        if (st + 2 >= nsteps) break;
     }
 }
 
 // One pass of kernel gate_up over NT 16-token tiles starting at pair mb of the
 // group: A rows are the pairs' tokens (rows past cnt repeat the last pair).
-template <int BITS, int NT>
+// The wave's tiles j < TPW/2 are gate rows c0 + 16j, the others the same up rows.
+template <int BITS, int NT, int NW>
 __device__ __forceinline__ void pf_gate_up_pass(const Prefill& F, const PfRows& R, int nk, int c0, int p0, int cnt,
                                                 int mb, uint4* lds) {
+    constexpr int TPW = 16 / NW, HT = TPW / 2, RPT = 8 * NT / NW;
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
-    const uint4* crow[NT];
+    const uint4* crow[RPT];
 #pragma unroll
-    for (int r = 0; r < NT; ++r) {
-        int t = F.tok[p0 + min(mb + r * 16 + (int)(threadIdx.x >> 4), cnt - 1)];
+    for (int k = 0; k < RPT; ++k) {
+        int t = F.tok[p0 + min(mb + (int)(threadIdx.x >> 5) + 2 * NW * k, cnt - 1)];
         t = min(max(t, 0), F.T - 1);
-        crow[r] = reinterpret_cast<const uint4*>(F.x + (int64_t)t * F.H) + (threadIdx.x & 15);
+        crow[k] = reinterpret_cast<const uint4*>(F.x + (int64_t)t * F.H) + (threadIdx.x & 15);
     }
-    f32x4_t acc[NT][4];
-    pf_gemm<BITS, NT>(R, crow, lds, nk, acc);
+    f32x4_t acc[NT][TPW];
+    pf_gemm<BITS, NT, NW>(R, crow, lds, nk, acc);
     // D layout: acc[mt][j][i] = token mb + mt*16 + 4g + i, row tile j column n
 #pragma unroll
     for (int mt = 0; mt < NT; ++mt)
@@ -315,25 +329,26 @@ __device__ __forceinline__ void pf_gate_up_pass(const Prefill& F, const PfRows& 
             const int m = mb + mt * 16 + 4 * g + i;
             if (m < cnt) {
                 uint16_t* dst = F.act + (int64_t)(p0 + m) * F.I + c0 + n;
-                dst[0] = f32_to_bf16(silu_mul(acc[mt][0][i], acc[mt][2][i]));
-                dst[16] = f32_to_bf16(silu_mul(acc[mt][1][i], acc[mt][3][i]));
+#pragma unroll
+                for (int j = 0; j < HT; ++j) dst[16 * j] = f32_to_bf16(silu_mul(acc[mt][j][i], acc[mt][j + HT][i]));
             }
         }
 }
 
 // One pass of kernel down (A rows: the pairs' activations), stores w * y.
-template <int BITS, int NT>
+template <int BITS, int NT, int NW>
 __device__ __forceinline__ void pf_down_pass(const Prefill& F, const PfRows& R, int nk, int h0, int p0, int cnt,
                                              int mb, uint4* lds) {
+    constexpr int TPW = 16 / NW, RPT = 8 * NT / NW;
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
-    const uint4* crow[NT];
+    const uint4* crow[RPT];
 #pragma unroll
-    for (int r = 0; r < NT; ++r) {
-        const int m = min(mb + r * 16 + (int)(threadIdx.x >> 4), cnt - 1);
-        crow[r] = reinterpret_cast<const uint4*>(F.act + (int64_t)(p0 + m) * F.I) + (threadIdx.x & 15);
+    for (int k = 0; k < RPT; ++k) {
+        const int m = min(mb + (int)(threadIdx.x >> 5) + 2 * NW * k, cnt - 1);
+        crow[k] = reinterpret_cast<const uint4*>(F.act + (int64_t)(p0 + m) * F.I) + (threadIdx.x & 15);
     }
-    f32x4_t acc[NT][4];
-    pf_gemm<BITS, NT>(R, crow, lds, nk, acc);
+    f32x4_t acc[NT][TPW];
+    pf_gemm<BITS, NT, NW>(R, crow, lds, nk, acc);
 #pragma unroll
     for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
@@ -343,28 +358,29 @@ __device__ __forceinline__ void pf_down_pass(const Prefill& F, const PfRows& R, 
                 const float wp = F.w[p0 + m];
                 float* dst = F.y + (int64_t)(p0 + m) * F.H + h0 + n;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) dst[j * 16] = wp * acc[mt][j][i];
+                for (int j = 0; j < TPW; ++j) dst[j * 16] = wp * acc[mt][j][i];
             }
         }
 }
 
 // ---------------------------------------------------------------------------
 // gate_up: act[p][r] = bf16(silu(g) * u), g/u = x[tok[p]] . W{gate,up}[r]
-// grid (I/128, U, Z); wave w of workgroup x owns act columns c0 = (4x + w)*32
-// .. +31: row tiles {gate c0, gate c0+16, up c0, up c0+16}.
-template <int BITS, int MT>
-__global__ __launch_bounds__(256, 1) void k_pf_gate_up(const Prefill F) {
+// grid (I/128, U, Z), NW waves; wave w of workgroup x owns act columns
+// c0 = x*128 + w*8*TPW .. +8*TPW-1: row tiles {gate c0 + 16j, up c0 + 16j}.
+template <int BITS, int MT, int NW>
+__global__ __launch_bounds__(64 * NW) void k_pf_gate_up(const Prefill F) {
+    constexpr int TPW = 16 / NW, HT = TPW / 2, CW = 8 * TPW;
     __shared__ uint4 lds[2 * MT * 16 * kArs];
     __shared__ uint32_t sml[256 * kPfSmSteps];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int c0 = (blockIdx.x * kPfWaves + wv) * 32, u = blockIdx.y;
+    const int c0 = blockIdx.x * 128 + wv * CW, u = blockIdx.y;
     int slot, p0, cnt;
     const int gs = group_state(F, u, slot, p0, cnt);
     if (gs == 0) return;
     if (gs == 1) {
-        for (int i = lane; i < cnt * 32; i += 64)
-            F.act[(int64_t)(p0 + i / 32) * F.I + c0 + (i & 31)] = 0x7FC0;  // bf16 NaN
+        for (int i = lane; i < cnt * CW; i += 64)
+            F.act[(int64_t)(p0 + i / CW) * F.I + c0 + (i % CW)] = 0x7FC0;  // bf16 NaN
         return;
     }
     const uint8_t* base = F.pool + (int64_t)slot * F.slot_bytes;
@@ -378,46 +394,48 @@ __global__ __launch_bounds__(256, 1) void k_pf_gate_up(const Prefill F) {
     R.mn_off = mn - sc;
     R.sml = nullptr;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {  // tiles gate c0, gate c0+16, up c0, up c0+16
-        const int mat = j >> 1, dr = (j & 1) * 16;
+    for (int j = 0; j < TPW; ++j) {  // tiles gate c0 + 16j (j < HT), up c0 + 16(j - HT)
+        const int mat = j / HT, dr = (j % HT) * 16;
         R.code_off[j] = mat * F.nmb + dr * rowb;
         R.scale_off[j] = (int64_t)mat * F.NGM + (int64_t)dr * nk;
         R.sml_off[j] = (mat * 128 + dr) * nk;  // local rows: gate 0..127, up 128..255
     }
     if (nk <= kPfSmSteps) {  // the workgroup's 128 gate and 128 up rows' scale/min, once
-        const int r0 = blockIdx.x * kPfWaves * 32;
+        const int r0 = blockIdx.x * 128;
         pf_stage_scales(sc + (int64_t)r0 * nk, mn - sc, 128, nk, 0, sml);
         pf_stage_scales(sc + F.NGM + (int64_t)r0 * nk, mn - sc, 128, nk, 128, sml);
         __syncthreads();
-        R.sml = sml + (wv * 32 + n) * nk;
+        R.sml = sml + (wv * CW + n) * nk;
     }
     constexpr int MB = MT * 16;
     for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
         const int nt = min(MT, (cnt - mb + 15) / 16);  // 16-token tiles in this pass (workgroup-uniform)
-        if (MT >= 4 && nt >= 4) pf_gate_up_pass<BITS, (MT >= 4 ? 4 : 1)>(F, R, nk, c0, p0, cnt, mb, lds);
-        else if (MT >= 3 && nt == 3) pf_gate_up_pass<BITS, (MT >= 3 ? 3 : 1)>(F, R, nk, c0, p0, cnt, mb, lds);
-        else if (MT >= 2 && nt == 2) pf_gate_up_pass<BITS, (MT >= 2 ? 2 : 1)>(F, R, nk, c0, p0, cnt, mb, lds);
-        else pf_gate_up_pass<BITS, 1>(F, R, nk, c0, p0, cnt, mb, lds);
+        if (MT >= 4 && nt >= 4) pf_gate_up_pass<BITS, (MT >= 4 ? 4 : 1), NW>(F, R, nk, c0, p0, cnt, mb, lds);
+        else if (MT >= 3 && nt == 3) pf_gate_up_pass<BITS, (MT >= 3 ? 3 : 1), NW>(F, R, nk, c0, p0, cnt, mb, lds);
+        else if (MT >= 2 && nt == 2) pf_gate_up_pass<BITS, (MT >= 2 ? 2 : 1), NW>(F, R, nk, c0, p0, cnt, mb, lds);
+        else pf_gate_up_pass<BITS, 1, NW>(F, R, nk, c0, p0, cnt, mb, lds);
         __syncthreads();  // the next pass restages LDS buffer 0
     }
 }
 
 // ---------------------------------------------------------------------------
 // down: y[p][h] = w[p] * (act[p] . Wdown[h]), fp32
-// grid (H/256, U, Z); wave w of workgroup x owns rows (4x + w)*64 .. +63.
-template <int BITS, int MT>
-__global__ __launch_bounds__(256, 1) void k_pf_down(const Prefill F) {
+// grid (H/256, U, Z), NW waves; wave w of workgroup x owns rows
+// x*256 + w*16*TPW .. +16*TPW-1.
+template <int BITS, int MT, int NW>
+__global__ __launch_bounds__(64 * NW) void k_pf_down(const Prefill F) {
+    constexpr int TPW = 16 / NW, RW = 16 * TPW;
     __shared__ uint4 lds[2 * MT * 16 * kArs];
     __shared__ uint32_t sml[256 * kPfSmSteps];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int h0 = (blockIdx.x * kPfWaves + wv) * 64, u = blockIdx.y;
+    const int h0 = blockIdx.x * 256 + wv * RW, u = blockIdx.y;
     int slot, p0, cnt;
     const int gs = group_state(F, u, slot, p0, cnt);
     if (gs == 0) return;
     if (gs == 1) {
-        for (int i = lane; i < cnt * 64; i += 64)
-            F.y[(int64_t)(p0 + i / 64) * F.H + h0 + (i & 63)] = __builtin_nanf("");
+        for (int i = lane; i < cnt * RW; i += 64)
+            F.y[(int64_t)(p0 + i / RW) * F.H + h0 + (i % RW)] = __builtin_nanf("");
         return;
     }
     const uint8_t* base = F.pool + (int64_t)slot * F.slot_bytes;
@@ -431,24 +449,24 @@ __global__ __launch_bounds__(256, 1) void k_pf_down(const Prefill F) {
     R.mn_off = mn - sc;
     R.sml = nullptr;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {  // tiles h0, h0+16, h0+32, h0+48
+    for (int j = 0; j < TPW; ++j) {  // tiles h0 + 16j
         R.code_off[j] = (int64_t)j * 16 * rowb;
         R.scale_off[j] = (int64_t)j * 16 * nk;
         R.sml_off[j] = j * 16 * nk;
     }
     if (nk <= kPfSmSteps) {  // the workgroup's 256 rows' scale/min, once
-        const int hb = blockIdx.x * kPfWaves * 64;
+        const int hb = blockIdx.x * 256;
         pf_stage_scales(sc + 2 * (int64_t)F.NGM + (int64_t)hb * nk, mn - sc, 256, nk, 0, sml);
         __syncthreads();
-        R.sml = sml + (wv * 64 + n) * nk;
+        R.sml = sml + (wv * RW + n) * nk;
     }
     constexpr int MB = MT * 16;
     for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
         const int nt = min(MT, (cnt - mb + 15) / 16);
-        if (MT >= 4 && nt >= 4) pf_down_pass<BITS, (MT >= 4 ? 4 : 1)>(F, R, nk, h0, p0, cnt, mb, lds);
-        else if (MT >= 3 && nt == 3) pf_down_pass<BITS, (MT >= 3 ? 3 : 1)>(F, R, nk, h0, p0, cnt, mb, lds);
-        else if (MT >= 2 && nt == 2) pf_down_pass<BITS, (MT >= 2 ? 2 : 1)>(F, R, nk, h0, p0, cnt, mb, lds);
-        else pf_down_pass<BITS, 1>(F, R, nk, h0, p0, cnt, mb, lds);
+        if (MT >= 4 && nt >= 4) pf_down_pass<BITS, (MT >= 4 ? 4 : 1), NW>(F, R, nk, h0, p0, cnt, mb, lds);
+        else if (MT >= 3 && nt == 3) pf_down_pass<BITS, (MT >= 3 ? 3 : 1), NW>(F, R, nk, h0, p0, cnt, mb, lds);
+        else if (MT >= 2 && nt == 2) pf_down_pass<BITS, (MT >= 2 ? 2 : 1), NW>(F, R, nk, h0, p0, cnt, mb, lds);
+        else pf_down_pass<BITS, 1, NW>(F, R, nk, h0, p0, cnt, mb, lds);
         __syncthreads();
     }
 }
@@ -496,10 +514,12 @@ __global__ __launch_bounds__(256) void k_pf_combine(const float* __restrict__ y,
 // share a larger group's passes
 template <int BITS, int MT>
 static void launch_pf_mt(const Prefill& F, int ngroups, int max_group, hipStream_t st) {
+    constexpr int NW = MT >= 4 ? 8 : 4;
     const unsigned z = (unsigned)std::min(64, std::max(1, (max_group + MT * 16 - 1) / (MT * 16)));
-    hipLaunchKernelGGL((k_pf_gate_up<BITS, MT>), dim3((unsigned)(F.I / 128), (unsigned)ngroups, z), dim3(256), 0, st,
-                       F);
-    hipLaunchKernelGGL((k_pf_down<BITS, MT>), dim3((unsigned)(F.H / 256), (unsigned)ngroups, z), dim3(256), 0, st, F);
+    hipLaunchKernelGGL((k_pf_gate_up<BITS, MT, NW>), dim3((unsigned)(F.I / 128), (unsigned)ngroups, z),
+                       dim3(64 * NW), 0, st, F);
+    hipLaunchKernelGGL((k_pf_down<BITS, MT, NW>), dim3((unsigned)(F.H / 256), (unsigned)ngroups, z), dim3(64 * NW),
+                       0, st, F);
 }
 template <int BITS>
 static void launch_pf(const Prefill& F, int ngroups, int max_group, hipStream_t st) {
