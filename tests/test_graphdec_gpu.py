@@ -106,6 +106,37 @@ def test_graph_and_eager_decode_agree():
     rt.cache.free()
 
 
+def test_prefetch_and_recorder_paths_give_the_same_tokens():
+    """The per-layer host step with prefetch of the next layer's predicted experts (and with a
+    routing recorder) reads the row through the generic path; only slot placement may change,
+    so the logits are bit-identical to the signalled fast path's."""
+    cfg, ref, gpu, rt = _models(seed=7, nslots=12)
+    ids = torch.randint(0, 128, (1, 6), generator=torch.Generator().manual_seed(8))
+    outs = []
+    for mode in ("fast", "prefetch", "recorder"):
+        rt.cache.free()
+        rt.cache = ExpertCache(rt.store, 12)
+        rt.prefetch = mode == "prefetch"
+        rt.recorder = [] if mode == "recorder" else None
+        rt.reset_stats()
+        dec = GraphDecoder(gpu, rt, tmax=64)
+        with torch.no_grad():
+            lg = dec.prefill(ids[0].cuda())
+            seq, t = [], lg.argmax(-1)
+            for _ in range(5):
+                lg = dec.next(t).clone()
+                seq.append(lg)
+                t = lg.argmax(-1)
+        outs.append(torch.stack(seq))
+        if mode == "prefetch":
+            assert rt.stats["prefetched"] > 0
+        if mode == "recorder":
+            assert len(rt.recorder) >= 5 * L
+    rt.prefetch, rt.recorder = False, None
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    rt.cache.free()
+
+
 def test_resize_and_reprefill_keep_context():
     cfg, ref, gpu, rt = _models(seed=5)
     ids = torch.randint(0, 128, (1, 20), generator=torch.Generator().manual_seed(6))
