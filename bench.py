@@ -303,6 +303,38 @@ def summarize_stats(stats_csv: str, title: str, cmd: str, bench_line: str, top: 
     return "\n".join(lines) + "\n"
 
 
+def summarize_c5(runs, cmds) -> str:
+    """Markdown table of the grouped-prefill kernels from rocprofv3 --stats CSVs of
+    `bench.py --workload c5 --c5-tokens T` runs: runs = [(T, stats_csv, bench_log)].
+    Weight bytes = the touched experts' code + scale + min bytes of each kernel's matrices."""
+    import csv
+
+    gu_w = 2 * (H * I * 4 // 8 + 2 * 2 * (H * I // G))  # gate+up codes, fp16 scales and mins
+    dn_w = H * I * 4 // 8 + 2 * 2 * (H * I // G)
+    lines = ["# Kernel trace, grouped prefill, C5 4-bit (rocprofv3)", "",
+             "Commands (from the repository root on the GPU box), one per token count T:", "", "```"]
+    lines += cmds + ["```", "",
+                     f"Weight bytes are the touched experts' code + scale + min bytes of the kernel's matrices "
+                     f"(gate+up: {gu_w:,} B per expert, down: {dn_w:,} B); token, activation and output bytes are not "
+                     f"counted.", "",
+                     "| T | kernel | calls | avg ns | min ns | max ns | experts | weight B | weight GB/s at avg |",
+                     "|---|---|---|---|---|---|---|---|---|"]
+    for T, stats_csv, log in runs:
+        with open(log) as f:
+            res = json.loads([ln for ln in f if ln.startswith("{")][-1])
+        ex = [p["experts_touched"] for p in res["config"]["per_T"] if p["T"] == T][0]
+        with open(stats_csv) as f:
+            rows = [r for r in csv.DictReader(f) if "k_pf" in r["Name"]]
+        for r in sorted(rows, key=lambda r: ("gate_up" not in r["Name"], "combine" in r["Name"])):
+            name = r["Name"].split("(")[0].replace("void ", "")
+            wb = ex * (gu_w if "gate_up" in name else dn_w if "down" in name else 0)
+            avg = float(r["AverageNs"])
+            gbs = f"{wb / avg:.0f}" if wb else "—"
+            lines.append(f"| {T} | `{name}` | {r['Calls']} | {avg:.0f} | {r['MinNs']} | {r['MaxNs']} | {ex} | "
+                         f"{wb if wb else '—'} | {gbs} |")
+    return "\n".join(lines) + "\n"
+
+
 def measure(W: Layers, steps: int, warmup: int):
     """Seconds per layer (both kernels, routing meta refreshed before every replay) and per
     kernel alone: graph replays over all layers, HIP events on the replay stream."""
@@ -531,11 +563,29 @@ def main():
     ap.add_argument("--c4-warmup", type=int, default=8)
     ap.add_argument("--c4-copy", default="auto", choices=["dma", "kernel", "auto"],
                     help="how expert misses cross PCIe (ExpertCache copy=)")
+    ap.add_argument("--summarize-c5", nargs="+", metavar="T:STATS_CSV:BENCH_LOG",
+                    help="write profiles/moe_prefill_c5_q4_kernel_trace.md from per-T rocprofv3 --stats runs")
     ap.add_argument("--summarize-stats", nargs=4, metavar=("STATS_CSV", "BENCH_LOG", "TITLE", "NAME"),
                     help="write profiles/NAME.md from a rocprofv3 --stats CSV (command text from --pmc-command)")
     ap.add_argument("--summarize-trace", nargs=3, metavar=("TRACE_CSV", "STATS_CSV", "BENCH_JSON"),
                     help="write the kernel-trace summary under profiles/ from a rocprofv3 run of bench.py")
     a = ap.parse_args()
+
+    if a.summarize_c5:
+        runs = []
+        for spec in a.summarize_c5:
+            t, st_csv, log = spec.split(":")
+            runs.append((int(t), st_csv, log))
+        cmds = [f"cd /tmp && TMPDIR=/tmp rocprofv3 --kernel-trace --stats --output-format csv -d "
+                f"$REPO/gpurun_out/prof_c5_t{t} -o c5 -- python3 $REPO/bench.py --workload c5 --c5-tokens {t} "
+                f"--no-cpu-baseline > $REPO/gpurun_out/prof_c5_t{t}.log" for t, _, _ in runs]
+        cmds.append("python3 bench.py --summarize-c5 " + " ".join(
+            f"{t}:gpurun_out/prof_c5_t{t}/c5_kernel_stats.csv:gpurun_out/prof_c5_t{t}.log" for t, _, _ in runs))
+        text = summarize_c5(runs, cmds)
+        with open(os.path.join(PROFILES, "moe_prefill_c5_q4_kernel_trace.md"), "w") as f:
+            f.write(text)
+        print(text)
+        return
 
     if a.summarize_stats:
         with open(a.summarize_stats[1]) as f:
