@@ -155,6 +155,52 @@ def test_prefill_argument_validation():
     assert L.wisp_prefill_ws_bytes(64, 2048, 768) == 64 * 768 * 2 + 64 * 2048 * 4
 
 
+def test_decode_layer_argument_validation():
+    """The graph decoder's dense kernels reject bad shapes and pointers before any launch."""
+    L = _lib.lib()
+
+    def gemv(**kw):
+        a = dict(a=FAKE, a_row=None, b=None, norm_w=None, eps=1e-6, h_out=None, x_out=None, w0=FAKE, w1=None,
+                 w2=None, r1=128, r2=128, O=128, K=2048, res=None, y=FAKE)
+        a.update(kw)
+        return L.wisp_dl_gemv(*a.values(), None)
+
+    assert gemv(K=2052) == _lib.WISP_EINVAL  # K a multiple of 8
+    assert gemv(K=16384) == _lib.WISP_EINVAL  # K <= 8192
+    assert gemv(O=0, r1=0, r2=0) == _lib.WISP_EINVAL
+    assert gemv(r1=64, r2=32) == _lib.WISP_EINVAL  # r1 <= r2
+    assert gemv(r1=64, r2=128) == _lib.WISP_EINVAL  # rows [64, 128) need w1
+    assert gemv(r1=64, r2=64) == _lib.WISP_EINVAL  # rows [64, 128) need w2
+    assert gemv(b=FAKE) == _lib.WISP_EINVAL  # b, h_out, x_out only with the RMSNorm prologue
+    assert gemv(y=None) == _lib.WISP_EINVAL
+    assert gemv(a=ctypes.c_void_p(0x100008)) == _lib.WISP_EALIGN
+    assert gemv(w0=ctypes.c_void_p(0x100004)) == _lib.WISP_EALIGN
+
+    def rope(**kw):
+        a = dict(qkv=FAKE, qn=FAKE, kn=FAKE, eps=1e-6, cos=FAKE, sin=FAKE, pos=FAKE, hq=32, hk=4, d=128, kc=FAKE,
+                 vc=FAKE, hs=4096 * 128, qo=FAKE)
+        a.update(kw)
+        return L.wisp_dl_qk_rope(*a.values(), None)
+
+    assert rope(d=96) == _lib.WISP_EINVAL  # head dim 64, 128 or 256
+    assert rope(hk=0) == _lib.WISP_EINVAL
+    assert rope(hs=64) == _lib.WISP_EINVAL  # head stride >= d
+    assert rope(pos=None) == _lib.WISP_EINVAL
+
+    def rt(**kw):
+        a = dict(logits=FAKE, E=128, k=8, norm=1, row=FAKE, host_row=None, host_flag=None, seq=None)
+        a.update(kw)
+        return L.wisp_dl_route(*a.values(), None)
+
+    assert rt(E=0) == _lib.WISP_EINVAL
+    assert rt(E=2048) == _lib.WISP_EINVAL  # E <= 1024
+    assert rt(k=17) == _lib.WISP_EINVAL  # k <= 16
+    assert rt(E=4, k=5) == _lib.WISP_EINVAL  # k <= E
+    assert rt(host_row=FAKE) == _lib.WISP_EINVAL  # host_row, host_flag and seq go together
+    assert rt(host_row=FAKE, host_flag=FAKE) == _lib.WISP_EINVAL
+    assert rt(row=None) == _lib.WISP_EINVAL
+
+
 def test_expert_cache_needs_a_gpu():
     """The slot pool is device memory: without a GPU the cache refuses to build (no host pool)."""
     if torch.cuda.is_available():

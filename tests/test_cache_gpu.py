@@ -239,3 +239,32 @@ def test_page_kernel_needs_a_pinned_store():
     c = ExpertCache(st, 2, copy="auto")  # falls back to the DMA copies
     assert c.copy == "dma"
     c.free()
+
+
+@pytest.mark.parametrize("copy", ["dma", "kernel"])
+def test_signaled_step_waits_pages_and_writes_meta(copy):
+    """wisp_cache_prepare_signaled: a flag that never moves times out (host-side spin only); a
+    moved flag is taken at once with the row's ids and weights; bad ids are refused."""
+    st = _store(1, 6, 4, seed=21)
+    c = ExpertCache(st, 4, copy=copy)
+    row = torch.zeros(16, dtype=torch.float32, pin_memory=True)
+    flag = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    meta_host = torch.zeros(8, dtype=torch.float32, pin_memory=True)
+    meta_dev = torch.full((8,), -1.0, dtype=torch.float32, device="cuda")
+    with pytest.raises(RuntimeError, match="timed out"):
+        c.prepare_signaled(row, flag, 0, 0, 4, 6, None, meta_host, meta_dev, timeout_ms=50)
+    row[:4] = torch.tensor([5.0, 1.0, 2.0, 3.0])
+    row[4:8] = torch.tensor([0.5, 0.25, 0.125, 0.125])
+    flag[0] = 1
+    assert c.prepare_signaled(row, flag, 0, 0, 4, 6, None, meta_host, meta_dev) == 1
+    torch.cuda.synchronize()
+    slots = meta_dev[:4].cpu().long().tolist()
+    assert meta_dev[4:].cpu().tolist() == [0.5, 0.25, 0.125, 0.125]
+    got = _rows(c, slots)
+    for j, key in enumerate([5, 1, 2, 3]):
+        assert torch.equal(got[j], st.host[key]), key
+    flag[0] = 2
+    row[0] = 6.0  # outside [0, n_ids)
+    with pytest.raises(RuntimeError):
+        c.prepare_signaled(row, flag, 1, 0, 4, 6, None, meta_host, meta_dev)
+    c.free()
