@@ -538,6 +538,18 @@ def run_c5(a) -> dict:
     }
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (the baseline depends on it)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -697,14 +709,25 @@ def main():
         routes = [(s_cpu[i].tolist(), w_cpu[i].float().tolist()) for i in range(64)]
         xcpu = [W.xs[i % W.layers].cpu() for i in range(8)]
         med, cnt, thr = CB.time_layers(rows, routes, xcpu, H, I, bits, G, budget_s=a.cpu_budget)
+        # the same layer on one thread, and C1 (one expert at weight 1), on smaller samples
+        med1, cnt1, _ = CB.time_layers(rows, routes, xcpu, H, I, bits, G, budget_s=a.cpu_budget / 3, warm=1, threads=1)
+        one = [([r], [1.0]) for r in range(96)]
+        medc1, cntc1, _ = CB.time_layers(rows, one, xcpu, H, I, bits, G, budget_s=a.cpu_budget / 5, threads=thr)
+        torch.set_num_threads(thr)
+        cpu = _cpu_model()
         res["cpu_baseline"] = {
             "value": round(layer_b / med / 1e9, 3),
             "unit": "GB/s",
             "cores": thr,
             "kind": "port",
             "sample": f"{cnt} MoE layers (8 of 96 distinct experts each, rotated), median; torch dequant->bf16 "
-                      f"F.linear on {thr} threads; {round(med * 1e6, 1)} us/layer; cpu={platform.processor() or 'x86_64'}",
+                      f"F.linear on {thr} threads; {round(med * 1e6, 1)} us/layer; cpu={cpu}",
             "us_per_layer": round(med * 1e6, 1),
+            "us_per_layer_1_thread": round(med1 * 1e6, 1),
+            "samples_1_thread": cnt1,
+            "c1_us_per_expert": round(medc1 * 1e6, 1),
+            "samples_c1": cntc1,
+            "cpu_model": cpu,
         }
     print(json.dumps(res))
 

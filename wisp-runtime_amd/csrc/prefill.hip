@@ -187,7 +187,10 @@ __device__ __forceinline__ void pf_stage_scales(const uint16_t* sc, int64_t mn_o
 template <int BITS>
 __device__ __forceinline__ void pf_bfrag(const uint32_t* cd, uint32_t sm, uint4* b) {
     uint32_t v[16];
-    dequant_chunk<BITS>(cd, h2f((uint16_t)(sm & 0xFFFFu)), h2f((uint16_t)(sm >> 16)), v);
+    if constexpr (BITS == 3)
+        dequant_chunk<BITS>(cd, h2f((uint16_t)(sm & 0xFFFFu)), h2f((uint16_t)(sm >> 16)), v);
+    else
+        dequant32<BITS>(cd, sm, v);
 #pragma unroll
     for (int s = 0; s < 4; ++s) b[s] = make_uint4(v[4 * s], v[4 * s + 1], v[4 * s + 2], v[4 * s + 3]);
 }

@@ -8,7 +8,9 @@
 //    q*s is exact in binary32 (q < 256, s an fp16 value: at most 8 + 11
 //    significant bits), so rounding it changes nothing; the kernels are
 //    written with plain operators under `#pragma clang fp contract(off)`,
-//    which keeps mul and add separate in the ISA.
+//    which keeps mul and add separate in the ISA. The 4- and 2-bit chunk
+//    path instead uses dequant32 (wisp_device.hpp), one fused multiply-add
+//    with the exact product q*s: the same single rounding of q*s + m.
 //  * quantize: binary32 sub/div with __fsub_rn/__fdiv_rn (IEEE, correctly
 //    rounded), round-half-even (rintf), fp16 RTNE conversion with subnormals.
 // Dequant is HBM-bound: it reads nbytes and writes 6n bytes per expert.
@@ -57,15 +59,21 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ row
     const int64_t ng = N / G;
     const int64_t g = (c * 32) / G;
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(buf + ncode);
-    const float s = h2f(sc[g]), m = h2f(sc[ng + g]);
-    uint32_t q[32];
-    unpack32<BITS>(buf, c, q);
     uint32_t w[16];
+    if constexpr (BITS == 4 || BITS == 2) {  // the same routine as the prefill kernels' B fragments
+        uint32_t d[BITS];
+        load_chunk<BITS>(buf + c * 4 * BITS, d);
+        dequant32<BITS>(d, (uint32_t)sc[g] | ((uint32_t)sc[ng + g] << 16), w);
+    } else {
+        const float s = h2f(sc[g]), m = h2f(sc[ng + g]);
+        uint32_t q[32];
+        unpack32<BITS>(buf, c, q);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float a = (float)q[2 * i] * s + m;
-        const float bb = (float)q[2 * i + 1] * s + m;
-        w[i] = pack_bf16x2(a, bb);
+        for (int i = 0; i < 16; ++i) {
+            const float a = (float)q[2 * i] * s + m;
+            const float bb = (float)q[2 * i + 1] * s + m;
+            w[i] = pack_bf16x2(a, bb);
+        }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
