@@ -135,9 +135,10 @@ __device__ __forceinline__ int group_state(const Prefill& F, int u, int& slot, i
 // A wave's weight row tiles: the lane's code and scale pointers for tile 0
 // (its row and chunk) and the tiles' offsets from them (wave-uniform).
 // Scale/min table of a workgroup's 256 weight rows, staged in LDS when a row has
-// at most kPfSmSteps quant groups (K <= 2048): entry [local row][K step] =
-// s | m << 16 (fp16 bits).
-constexpr int kPfSmSteps = 16;
+// at most kPfSmSteps quant groups (K <= 2048): entry [K step][local row] =
+// s | m << 16 (fp16 bits). K-step major, so the 16 rows of a tile that one read
+// touches are 16 consecutive words (distinct banks).
+constexpr int kPfSmSteps = 16, kPfSmRows = 256;
 
 struct PfRows {
     const uint8_t* rc;   // codes of tile 0 at the lane's row and chunk
@@ -145,7 +146,7 @@ struct PfRows {
     int64_t mn_off;      // mins - scales, in fp16 elements
     int64_t code_off[kPfMaxTiles], scale_off[kPfMaxTiles];
     const uint32_t* sml;  // LDS table at tile 0's row (nullptr: read sp/mn from global memory)
-    int sml_off[kPfMaxTiles];  // per-tile offsets in the LDS table, entries
+    int sml_off[kPfMaxTiles];  // per-tile local row offsets in the LDS table
 };
 
 // One K step's codes and fp16 scale/min (packed s | m << 16) of a lane's row in tile j.
@@ -153,17 +154,17 @@ template <int BITS>
 __device__ __forceinline__ void pf_load(const PfRows& R, int j, int kc, uint32_t* cd, uint32_t& sm) {
     load_chunk<BITS>(R.rc + R.code_off[j] + (int64_t)kc * 16 * BITS, cd);  // 128 codes per K step
     if (R.sml) {
-        sm = R.sml[R.sml_off[j] + kc];
+        sm = R.sml[R.sml_off[j] + kc * kPfSmRows];
     } else {
         const uint16_t* s = R.sp + R.scale_off[j] + kc;
         sm = (uint32_t)s[0] | ((uint32_t)s[R.mn_off] << 16);
     }
 }
 
-// Stage nrows * nk scale/min pairs (two contiguous fp16 runs, scales at `sc`,
-// mins at sc + mn_off) into sml[local0 * nk ...] packed s | m << 16, with
-// 16-byte loads (nrows * nk a multiple of 8; both runs 16-byte aligned). All
-// threads of the workgroup take part.
+// Stage nrows * nk scale/min pairs (two contiguous fp16 runs, [row][K step],
+// scales at `sc`, mins at sc + mn_off) into sml[kc * kPfSmRows + local0 + row]
+// packed s | m << 16, with 16-byte loads (nrows * nk a multiple of 8; both runs
+// 16-byte aligned). All threads of the workgroup take part.
 __device__ __forceinline__ void pf_stage_scales(const uint16_t* sc, int64_t mn_off, int nrows, int nk, int local0,
                                                 uint32_t* sml) {
     const int total = nrows * nk;  // entries, 8 per 16-byte load
@@ -171,15 +172,17 @@ __device__ __forceinline__ void pf_stage_scales(const uint16_t* sc, int64_t mn_o
         const uint4 vs = *reinterpret_cast<const uint4*>(sc + e);
         const uint4 vm = *reinterpret_cast<const uint4*>(sc + mn_off + e);
         const uint32_t s4[4] = {vs.x, vs.y, vs.z, vs.w}, m4[4] = {vm.x, vm.y, vm.z, vm.w};
-        uint32_t o[8];
+        int r = e / nk, kc = e - r * nk;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            o[2 * i] = (s4[i] & 0xFFFFu) | (m4[i] << 16);
-            o[2 * i + 1] = (s4[i] >> 16) | (m4[i] & 0xFFFF0000u);
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t sv = i & 1 ? s4[i >> 1] >> 16 : s4[i >> 1] & 0xFFFFu;
+            const uint32_t mv = i & 1 ? m4[i >> 1] & 0xFFFF0000u : m4[i >> 1] << 16;
+            sml[kc * kPfSmRows + local0 + r] = sv | mv;
+            if (++kc == nk) {
+                kc = 0;
+                ++r;
+            }
         }
-        uint4* dst = reinterpret_cast<uint4*>(sml + local0 * nk + e);
-        dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
-        dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
     }
 }
 
@@ -374,7 +377,7 @@ template <int BITS, int MT, int NW>
 __global__ __launch_bounds__(64 * NW) void k_pf_gate_up(const Prefill F) {
     constexpr int TPW = 16 / NW, HT = TPW / 2, CW = 8 * TPW;
     __shared__ uint4 lds[2 * MT * 16 * kArs];
-    __shared__ uint32_t sml[256 * kPfSmSteps];
+    __shared__ uint32_t sml[kPfSmRows * kPfSmSteps];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int c0 = blockIdx.x * 128 + wv * CW, u = blockIdx.y;
@@ -401,14 +404,14 @@ __global__ __launch_bounds__(64 * NW) void k_pf_gate_up(const Prefill F) {
         const int mat = j / HT, dr = (j % HT) * 16;
         R.code_off[j] = mat * F.nmb + dr * rowb;
         R.scale_off[j] = (int64_t)mat * F.NGM + (int64_t)dr * nk;
-        R.sml_off[j] = (mat * 128 + dr) * nk;  // local rows: gate 0..127, up 128..255
+        R.sml_off[j] = mat * 128 + dr;  // local rows: gate 0..127, up 128..255
     }
     if (nk <= kPfSmSteps) {  // the workgroup's 128 gate and 128 up rows' scale/min, once
         const int r0 = blockIdx.x * 128;
         pf_stage_scales(sc + (int64_t)r0 * nk, mn - sc, 128, nk, 0, sml);
         pf_stage_scales(sc + F.NGM + (int64_t)r0 * nk, mn - sc, 128, nk, 128, sml);
         __syncthreads();
-        R.sml = sml + (wv * CW + n) * nk;
+        R.sml = sml + wv * CW + n;
     }
     constexpr int MB = MT * 16;
     for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
@@ -429,7 +432,7 @@ template <int BITS, int MT, int NW>
 __global__ __launch_bounds__(64 * NW) void k_pf_down(const Prefill F) {
     constexpr int TPW = 16 / NW, RW = 16 * TPW;
     __shared__ uint4 lds[2 * MT * 16 * kArs];
-    __shared__ uint32_t sml[256 * kPfSmSteps];
+    __shared__ uint32_t sml[kPfSmRows * kPfSmSteps];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int h0 = blockIdx.x * 256 + wv * RW, u = blockIdx.y;
@@ -455,13 +458,13 @@ __global__ __launch_bounds__(64 * NW) void k_pf_down(const Prefill F) {
     for (int j = 0; j < TPW; ++j) {  // tiles h0 + 16j
         R.code_off[j] = (int64_t)j * 16 * rowb;
         R.scale_off[j] = (int64_t)j * 16 * nk;
-        R.sml_off[j] = j * 16 * nk;
+        R.sml_off[j] = j * 16;
     }
     if (nk <= kPfSmSteps) {  // the workgroup's 256 rows' scale/min, once
         const int hb = blockIdx.x * 256;
         pf_stage_scales(sc + 2 * (int64_t)F.NGM + (int64_t)hb * nk, mn - sc, 256, nk, 0, sml);
         __syncthreads();
-        R.sml = sml + (wv * RW + n) * nk;
+        R.sml = sml + wv * RW + n;
     }
     constexpr int MB = MT * 16;
     for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
