@@ -303,6 +303,59 @@ def summarize_stats(stats_csv: str, title: str, cmd: str, bench_line: str, top: 
     return "\n".join(lines) + "\n"
 
 
+SQ_PASSES = ("SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_ACTIVE_INST_VMEM "
+             "SQ_WAIT_INST_LDS SQ_VALU_MFMA_BUSY_CYCLES SQ_WAIT_ANY",
+             "SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT SQ_INSTS_VMEM_RD SQ_INSTS_SALU "
+             "SQ_WAIT_INST_ANY SQ_LDS_DATA_FIFO_FULL")
+
+
+def summarize_sq(runs) -> str:
+    """Shader-sequencer counters of the prefill kernels from two rocprofv3 --pmc passes per
+    token count: runs = [(T, csv_pass_a, csv_pass_b)]. Counters are summed over the chip;
+    issue shares assume 1,024 SIMDs at 2.4 GHz, 4 cycles per wave64 VALU instruction and 16
+    per v_mfma_f32_16x16x32_bf16."""
+    import csv as _csv
+    import collections
+
+    lines = ["# SQ counters, grouped prefill, C5 4-bit (rocprofv3 --pmc)", "",
+             "Commands (from the repository root on the GPU box), two passes per token count T:", "", "```"]
+    for t, _, _ in runs:
+        for i, pas in enumerate(SQ_PASSES):
+            lines.append(f"cd /tmp && TMPDIR=/tmp timeout -s KILL 150 rocprofv3 --pmc {pas} --output-format csv -d "
+                         f"$REPO/gpurun_out/pmc_c5{'ab'[i]}_{t} -o c5 -- python3 $REPO/bench.py --workload c5 "
+                         f"--c5-tokens {t} --c5-reps 3 --no-cpu-baseline")
+    lines.append("python3 bench.py --summarize-sq " + " ".join(
+        f"{t}:gpurun_out/pmc_c5a_{t}/c5_counter_collection.csv:gpurun_out/pmc_c5b_{t}/c5_counter_collection.csv"
+        for t, _, _ in runs))
+    lines += ["```", "",
+              "Averages per dispatch. VALU share = SQ_INSTS_VALU x 4 / (1,024 x cycles); MFMA share = "
+              "SQ_VALU_MFMA_BUSY_CYCLES / (1,024 x cycles); cycles = dispatch duration x 2.4 GHz (durations "
+              "include the profiler's per-dispatch overhead). SQ_INSTS_VALU counts the MFMA instructions too.", "",
+              "| T | kernel | us | VALU insts | MFMA insts | LDS insts | LDS bank-conflict cycles | VALU share "
+              "| MFMA share | wait / wave cycles |",
+              "|---|---|---|---|---|---|---|---|---|---|"]
+    for t, ca, cb in runs:
+        d = collections.defaultdict(lambda: collections.defaultdict(list))
+        for path in (ca, cb):
+            with open(path) as f:
+                for r in _csv.DictReader(f):
+                    name = r["Kernel_Name"]
+                    if "k_pf_" not in name:
+                        continue
+                    k = name.split("(")[0].replace("void ", "")
+                    d[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
+                    if path == ca and r["Counter_Name"] == "SQ_WAVE_CYCLES":
+                        d[k]["_ns"].append(float(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+        for k, c in d.items():
+            av = {n: sum(v) / len(v) for n, v in c.items()}
+            cyc = 1024 * av["_ns"] * 2.4
+            lines.append(f"| {t} | `{k}` | {av['_ns'] / 1e3:.1f} | {av['SQ_INSTS_VALU'] / 1e6:.2f} M | "
+                         f"{av['SQ_INSTS_MFMA'] / 1e6:.2f} M | {av['SQ_INSTS_LDS'] / 1e6:.2f} M | "
+                         f"{av['SQ_LDS_BANK_CONFLICT'] / 1e6:.2f} M | {av['SQ_INSTS_VALU'] * 4 / cyc:.0%} | "
+                         f"{av['SQ_VALU_MFMA_BUSY_CYCLES'] / cyc:.0%} | {av['SQ_WAIT_ANY'] / av['SQ_WAVE_CYCLES']:.0%} |")
+    return "\n".join(lines) + "\n"
+
+
 def summarize_c5(runs, cmds) -> str:
     """Markdown table of the grouped-prefill kernels from rocprofv3 --stats CSVs of
     `bench.py --workload c5 --c5-tokens T` runs: runs = [(T, stats_csv, bench_log)].
@@ -577,12 +630,21 @@ def main():
                     help="how expert misses cross PCIe (ExpertCache copy=)")
     ap.add_argument("--summarize-c5", nargs="+", metavar="T:STATS_CSV:BENCH_LOG",
                     help="write profiles/moe_prefill_c5_q4_kernel_trace.md from per-T rocprofv3 --stats runs")
+    ap.add_argument("--summarize-sq", nargs="+", metavar="T:PASS_A_CSV:PASS_B_CSV",
+                    help="write profiles/moe_prefill_c5_q4_sq_counters.md from two rocprofv3 --pmc passes per T")
     ap.add_argument("--summarize-stats", nargs=4, metavar=("STATS_CSV", "BENCH_LOG", "TITLE", "NAME"),
                     help="write profiles/NAME.md from a rocprofv3 --stats CSV (command text from --pmc-command)")
     ap.add_argument("--summarize-trace", nargs=3, metavar=("TRACE_CSV", "STATS_CSV", "BENCH_JSON"),
                     help="write the kernel-trace summary under profiles/ from a rocprofv3 run of bench.py")
     a = ap.parse_args()
 
+    if a.summarize_sq:
+        runs = [tuple(int(v) if i == 0 else v for i, v in enumerate(spec.split(":"))) for spec in a.summarize_sq]
+        text = summarize_sq(runs)
+        with open(os.path.join(PROFILES, "moe_prefill_c5_q4_sq_counters.md"), "w") as f:
+            f.write(text)
+        print(text)
+        return
     if a.summarize_c5:
         runs = []
         for spec in a.summarize_c5:
