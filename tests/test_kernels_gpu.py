@@ -481,3 +481,24 @@ def test_moe_prefill_any_group_partition(bits, chunk, monkeypatch):
     got = _run_prefill(pool, x, sel, rw, H, I, bits).float()
     print(f"prefill partition chunk={chunk} bits={bits}: max |diff| {float((got - base).abs().max()):.3e}")
     assert torch.equal(got, base)
+
+
+def test_empty_inputs_are_no_ops():
+    """Empty work (the reference's loops over zero tokens or zero experts) returns empty or
+    zero results without a launch: T = 0 tokens, tokens whose experts are all absent from
+    the slot map (output zeros; with acc, acc unchanged), and zero dequant rows."""
+    E, H, I, bits = 4, 256, 128, 4
+    pool, x, sel, rw = _prefill_case(E, H, I, 5, 2, bits, seed=77)
+    pt = torch.from_numpy(pool).to(DEV)
+    x0 = torch.empty((0, H), dtype=torch.bfloat16, device=DEV)
+    out = kernels.moe_prefill(pt, {e: e for e in range(E)}, x0, torch.empty((0, 2), dtype=torch.int64),
+                              torch.empty((0, 2), dtype=torch.float32, device=DEV), H * I, H, I, bits)
+    assert out.shape == (0, H)
+    none = _run_prefill(pool, x, sel, rw, H, I, bits, slots={})
+    assert none.shape == (5, H) and not none.float().abs().any()
+    acc = torch.full((5, H), 0.5, dtype=torch.float32, device=DEV)
+    _run_prefill(pool, x, sel, rw, H, I, bits, slots={}, acc=acc)
+    assert torch.equal(acc, torch.full_like(acc, 0.5))
+    rows = quant.dequant(pt[:0], H * I, bits)
+    torch.cuda.synchronize()
+    assert rows.shape == (0, 3, H * I)

@@ -83,6 +83,8 @@ def dequant(buf: torch.Tensor, n: int, bits: int, group: int = 128) -> torch.Ten
     if buf.dim() != 2 or buf.stride(1) != 1:
         buf = buf.reshape(B, -1).contiguous()
     out = torch.empty((B, 3, n), dtype=torch.bfloat16, device=dev)
+    if B == 0:  # an empty batch dequantizes to an empty tensor, as the reference's torch ops do
+        return out
     _lib.check(
         _lib.lib().wisp_dequant(
             _lib.ptr(buf), buf.stride(0), None, B, B, n, bits, group, _lib.ptr(out), _lib.stream(dev)
