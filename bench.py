@@ -591,6 +591,102 @@ def run_c5(a) -> dict:
     }
 
 
+def run_gptoss(a) -> dict:
+    """gpt-oss-20b-shaped expert layer at decode batch 1: PagedGptOssBlock's decode step
+    (gptoss.py:116-131) through the package's three gpt-oss launches. H = I = 2880, 32
+    experts, top-4 by router logits ~N(0,1) with the softmax over the selected logits
+    (gptoss.py:117-118, weights bf16), random-init experts (std 0.02) quantized on the GPU in
+    the store format (group 128, gptoss.py:67), bf16 biases. Slot pools of --gptoss-pools
+    layers are rotated past the Infinity Cache and refreshed from 8 routings per replay; the
+    layers are captured in one graph and timed with HIP events on the replay stream."""
+    dev = torch.device("cuda:0")
+    GH = GI = 2880
+    GE, GK = 32, 4
+    n = GH * GI
+    bits = a.bits
+    nb = expert_nbytes(n, bits, G)
+    P_ = a.gptoss_pools
+    gen = torch.Generator(device=dev).manual_seed(11)
+    print(f"[bench] gptoss: quantizing {GE} experts ({bits}-bit, {nb} B each) on the GPU", file=sys.stderr, flush=True)
+    base = torch.empty((GE, nb), dtype=torch.uint8, device=dev)
+    for e in range(GE):
+        base[e].copy_(quantize(torch.randn((3, n), generator=gen, device=dev) * 0.02, bits, G))
+    pool = torch.empty((P_ * GE, nb), dtype=torch.uint8, device=dev)
+    for l in range(P_):
+        pool[l * GE : (l + 1) * GE].copy_(base)
+    del base
+    gub = (torch.randn((GE, 2 * GI), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    db = (torch.randn((GE, GH), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    logits = torch.randn((ROUNDS, P_, GE), generator=gen, device=dev).to(torch.bfloat16)
+    tv, ti = torch.topk(logits, GK, dim=-1)
+    sc = torch.softmax(tv, dim=-1, dtype=torch.bfloat16).float()
+    slots = ti + (torch.arange(P_, device=dev) * GE).view(1, P_, 1)
+    metas = torch.cat([slots.float(), sc, ti.float()], -1).contiguous()  # [slot ids | weights | expert ids]
+    meta_live = metas[0].clone()
+    xs = torch.randn((P_, GH), generator=gen, device=dev).to(torch.bfloat16)
+    L = _lib.lib()
+    wsb = L.wisp_gptoss_ws_bytes(GK, GH, GI)
+    wstride = (wsb + 255) // 256 * 256
+    ws = torch.empty((P_, wstride), dtype=torch.uint8, device=dev)
+    out = torch.empty((P_, GH), dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.Stream(dev)
+    sp = _lib.ptr
+
+    def launch(l, st):
+        _lib.check(L.wisp_gptoss_decode(sp(pool), nb, pool.shape[0], sp(meta_live[l]), GK, GH, GI, bits, G, sp(xs[l]),
+                                        sp(gub), sp(db), GE, 1.702, 7.0, sp(ws[l]), sp(out[l]), st), "gptoss_decode")
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        st = _lib.stream(dev)
+        for l in range(P_):
+            launch(l, st)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            st = _lib.stream(dev)
+            for l in range(P_):
+                launch(l, st)
+    torch.cuda.synchronize()
+
+    def run(reps):
+        with torch.cuda.stream(stream):
+            for r in range(reps):
+                meta_live.copy_(metas[r % ROUNDS], non_blocking=True)
+                g.replay()
+
+    run(4)
+    reps = max(1, a.gptoss_reps)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    run(reps)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / (reps * P_)
+    byts = GK * nb + 2 * GH + GK * (2 * GI + GH) * 2 + 2 * GH + 3 * GK * 4
+    gbs = byts / t / 1e9
+    return {
+        "metric": "us per gpt-oss MoE layer + achieved HBM GB/s, 4-bit top-4 of 32, batch 1",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": reps * P_,
+        "warmup": 4 * P_,
+        "ms_per_step": round(t * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": f"gpt-oss-20b expert layer: H=I=2880, top-{GK} of {GE}, {bits}-bit group-{G}, "
+                               f"bf16 biases, {P_} layer pools rotated",
+                   "bytes_per_layer": byts, "workspace_bytes": wsb,
+                   "path": "three kernel launches per layer (wisp_gptoss_decode / kernels.gptoss_decode)"},
+        "us_per_layer": round(t * 1e6, 3),
+        "pct_hbm_peak": round(gbs / PEAK_HBM_GBS * 100, 2),
+    }
+
+
 def _cpu_model() -> str:
     """The host CPU's model name (the baseline depends on it)."""
     try:
@@ -617,9 +713,11 @@ def main():
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write the PMC traffic summary under profiles/ from two counter_collection.csv files")
     ap.add_argument("--pmc-command", default="", help="command text recorded in the PMC summary")
-    ap.add_argument("--workload", default="c2", choices=["c2", "c4", "c5"], help="c2: one MoE layer (default); "
+    ap.add_argument("--workload", default="c2", choices=["c2", "c4", "c5", "gptoss"], help="c2: one MoE layer (default); "
                     "c4: full decode steps through the graph decoder and the expert cache; c5: grouped prefill")
     ap.add_argument("--c5-tokens", default="64,256,512")
+    ap.add_argument("--gptoss-pools", type=int, default=8, help="gpt-oss layer pools rotated (32 experts each)")
+    ap.add_argument("--gptoss-reps", type=int, default=50, help="timed replays of the rotated layers")
     ap.add_argument("--c5-pools", type=int, default=8)
     ap.add_argument("--c5-reps", type=int, default=10)
     ap.add_argument("--c4-layers", type=int, default=48)
@@ -706,6 +804,9 @@ def main():
         return
     if a.workload == "c5":
         print(json.dumps(run_c5(a)))
+        return
+    if a.workload == "gptoss":
+        print(json.dumps(run_gptoss(a)))
         return
 
     bits = a.bits

@@ -159,17 +159,25 @@ __device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int
     for (int i = 0; i < 32; ++i) acc[i] = 0.f;
 #pragma unroll
     for (int p = 0; p < kGoPairs; ++p) {
-        uint32_t q0[32], q1[32];
-        chunk_codes<BITS>(cd[p][0], q0);
-        chunk_codes<BITS>(cd[p][1], q1);
-        const float s0 = h2f((uint16_t)sv[p][0][0]), m0 = h2f((uint16_t)sv[p][0][1]);
-        const float s1 = h2f((uint16_t)sv[p][1][0]), m1 = h2f((uint16_t)sv[p][1][1]);
+        // the two rows' bf16 weights (RTNE of fp32(q*s) + m, q*s exact), one dot2
+        float w0[32], w1[32];
+        if constexpr (BITS == 3) {
+            uint32_t q0[32], q1[32];
+            chunk_codes<BITS>(cd[p][0], q0);
+            chunk_codes<BITS>(cd[p][1], q1);
+            const float s0 = h2f((uint16_t)sv[p][0][0]), m0 = h2f((uint16_t)sv[p][0][1]);
+            const float s1 = h2f((uint16_t)sv[p][1][0]), m1 = h2f((uint16_t)sv[p][1][1]);
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            // the two rows' bf16 weights (RTNE of fp32(q*s) + m, q*s exact), one dot2
-            const uint32_t w = pack_bf16x2(__builtin_fmaf((float)q0[i], s0, m0), __builtin_fmaf((float)q1[i], s1, m1));
-            acc[i] = dot2(w, xp[p], acc[i]);
+            for (int i = 0; i < 32; ++i) {
+                w0[i] = __builtin_fmaf((float)q0[i], s0, m0);
+                w1[i] = __builtin_fmaf((float)q1[i], s1, m1);
+            }
+        } else {
+            dequant32_f32<BITS>(cd[p][0], sv[p][0][0] | (sv[p][0][1] << 16), w0);
+            dequant32_f32<BITS>(cd[p][1], sv[p][1][0] | (sv[p][1][1] << 16), w1);
         }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) acc[i] = dot2(pack_bf16x2(w0[i], w1[i]), xp[p], acc[i]);
     }
     // partial vectors [16][32 lanes x 33]: slot = 2w + h, column 32*cl + i at cl*33 + i
     float* mine = red + (2 * wv + h) * kGoRedStride + cl * 33;
@@ -251,21 +259,54 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
                      L.p2 + ((int64_t)j * L.S2 + blockIdx.y) * L.H + blockIdx.x * kGoCols, slot < 0);
 }
 
-// out[h] = bf16( sum_j bf16( w_j * bf16( bf16(sum_s p2[j][s][h]) + db[e_j][h] ) ) ), j ascending
-__global__ __launch_bounds__(256) void k_go_out(const GoLayer L) {
-    const int h = blockIdx.x * 256 + threadIdx.x;
-    if (h >= L.H) return;
+// out[h] = bf16( sum_j bf16( w_j * bf16( bf16(sum_s p2[j][s][h]) + db[e_j][h] ) ) ), j ascending.
+// A workgroup takes kGoOutCols columns and splits each column's S2 partial sums
+// into kGoOutSlices slices, one per wave. Every lane requests the partials of
+// up to kGoOutBatch experts before adding any (the sums are latency-bound);
+// the slice sums are added in slice order through LDS.
+constexpr int kGoOutCols = 64, kGoOutSlices = 4, kGoOutBatch = 8, kGoOutUnroll = 8;
+__global__ __launch_bounds__(64 * kGoOutSlices) void k_go_out(const GoLayer L) {
+    __shared__ float part[kGoOutSlices][kGoOutBatch][kGoOutCols];
+    const int c = threadIdx.x & (kGoOutCols - 1), sl = threadIdx.x / kGoOutCols;
+    const int h = blockIdx.x * kGoOutCols + c, hh = min(h, L.H - 1);
+    const int per = (L.S2 + kGoOutSlices - 1) / kGoOutSlices, s0 = sl * per, s1 = min(L.S2, s0 + per);
     float y = 0.f;
-    for (int j = 0; j < L.k; ++j) {
-        const int ex = go_expert(L, j);
-        const float* p = L.p2 + (int64_t)j * L.S2 * L.H + h;
-        float v = 0.f;
-        for (int s = 0; s < L.S2; ++s) v += p[(int64_t)s * L.H];
-        const float w = bf16r(L.meta[L.k + j]);
-        const float o = ex >= 0 ? bf16r(bf16r(v) + bf16_to_f32(L.db[(int64_t)ex * L.H + h])) : __builtin_nanf("");
-        y += bf16r(o * w);
+    for (int j0 = 0; j0 < L.k; j0 += kGoOutBatch) {
+        float v[kGoOutBatch];
+#pragma unroll
+        for (int jj = 0; jj < kGoOutBatch; ++jj) v[jj] = 0.f;
+        for (int sb = s0; sb < s1; sb += kGoOutUnroll) {
+            float t[kGoOutBatch][kGoOutUnroll];
+#pragma unroll
+            for (int jj = 0; jj < kGoOutBatch; ++jj)
+#pragma unroll
+                for (int u = 0; u < kGoOutUnroll; ++u) {
+                    const int j = min(j0 + jj, L.k - 1), s = min(sb + u, s1 - 1);
+                    t[jj][u] = L.p2[((int64_t)j * L.S2 + s) * L.H + hh];
+                }
+#pragma unroll
+            for (int jj = 0; jj < kGoOutBatch; ++jj)
+#pragma unroll
+                for (int u = 0; u < kGoOutUnroll; ++u)
+                    if (sb + u < s1) v[jj] += t[jj][u];
+        }
+#pragma unroll
+        for (int jj = 0; jj < kGoOutBatch; ++jj) part[sl][jj][c] = v[jj];
+        __syncthreads();
+        if (sl == 0) {
+            for (int jj = 0; jj < kGoOutBatch && j0 + jj < L.k; ++jj) {
+                const int j = j0 + jj, ex = go_expert(L, j);
+                float sum = part[0][jj][c];
+#pragma unroll
+                for (int q = 1; q < kGoOutSlices; ++q) sum += part[q][jj][c];
+                const float w = bf16r(L.meta[L.k + j]);
+                const float o = ex >= 0 ? bf16r(bf16r(sum) + bf16_to_f32(L.db[(int64_t)ex * L.H + hh])) : __builtin_nanf("");
+                y += bf16r(o * w);
+            }
+        }
+        __syncthreads();
     }
-    L.out[h] = f32_to_bf16(y);
+    if (sl == 0 && h < L.H) L.out[h] = f32_to_bf16(y);
 }
 
 template <int BITS>
@@ -275,7 +316,7 @@ static void launch_go(const GoLayer& L, hipStream_t st) {
                        st, L);
     hipLaunchKernelGGL(k_go_down<BITS>, dim3((L.H + kGoCols - 1) / kGoCols, L.S2, L.k), dim3(64 * kGoWaves), 0, st,
                        L);
-    hipLaunchKernelGGL(k_go_out, dim3((L.H + 255) / 256), dim3(256), 0, st, L);
+    hipLaunchKernelGGL(k_go_out, dim3((L.H + kGoOutCols - 1) / kGoOutCols), dim3(64 * kGoOutSlices), 0, st, L);
 }
 
 }  // namespace wisp

@@ -258,52 +258,57 @@ __device__ __forceinline__ float half_hi_f(uint32_t x) {
 
 // Dequantize one chunk of 32 codes (BITS = 4 or 2; BITS dwords d, element i at
 // bit BITS*i) of a group whose fp16 scale s and min m are packed in
-// sm = s | m << 16, into 16 bf16 pairs in element order: bf16(q*s + m)
-// (quant.py:76-87; q*s is exact in binary32, so that is q*s + m rounded once).
-// No code is converted to float: a code masked in place at bit p < 8 of a
+// sm = s | m << 16, into 32 binary32 values in element order: q*s + m rounded
+// once, the value quant.py:76-87 computes (q*s is exact in binary32) before its
+// bf16 rounding. No code is converted to float: a code masked in place at bit p < 8 of a
 // 16-bit half is the fp16 subnormal q * 2^(p-24), and fma(q * 2^(p-24),
 // s * 2^(24-p), m) has the exact product q*s and one rounding. s * 2^(24-p) is
 // exact (a power-of-two scaling of an fp16 value stays in binary32 range).
 // The results are 0 or at least 2^-24 in magnitude (s and m are multiples of
 // 2^-24), so no binary32 subnormal arises. One mask yields a code of each half.
 template <int BITS>
-__device__ __forceinline__ void dequant32(const uint32_t* d, uint32_t sm, uint32_t* out) {
+__device__ __forceinline__ void dequant32_f32(const uint32_t* d, uint32_t sm, float* v) {
     const float s = h2f((uint16_t)sm), m = h2f((uint16_t)(sm >> 16));
     if constexpr (BITS == 4) {
         const float s0 = s * 0x1p24f, s4 = s * 0x1p20f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            // codes 8w+i at bits 4i: a = (8w, 8w+4), b = 16*(8w+1, 8w+5), c = (8w+2, 8w+6), e = 16*(8w+3, 8w+7)
             const uint32_t x = d[w], y = x >> 8;
             const uint32_t a = x & 0x000F000Fu, b = x & 0x00F000F0u, c = y & 0x000F000Fu, e = y & 0x00F000F0u;
-            out[4 * w + 0] = pack_bf16x2(__builtin_fmaf(half_lo_f(a), s0, m), __builtin_fmaf(half_lo_f(b), s4, m));
-            out[4 * w + 1] = pack_bf16x2(__builtin_fmaf(half_lo_f(c), s0, m), __builtin_fmaf(half_lo_f(e), s4, m));
-            out[4 * w + 2] = pack_bf16x2(__builtin_fmaf(half_hi_f(a), s0, m), __builtin_fmaf(half_hi_f(b), s4, m));
-            out[4 * w + 3] = pack_bf16x2(__builtin_fmaf(half_hi_f(c), s0, m), __builtin_fmaf(half_hi_f(e), s4, m));
+            v[8 * w + 0] = __builtin_fmaf(half_lo_f(a), s0, m);
+            v[8 * w + 1] = __builtin_fmaf(half_lo_f(b), s4, m);
+            v[8 * w + 2] = __builtin_fmaf(half_lo_f(c), s0, m);
+            v[8 * w + 3] = __builtin_fmaf(half_lo_f(e), s4, m);
+            v[8 * w + 4] = __builtin_fmaf(half_hi_f(a), s0, m);
+            v[8 * w + 5] = __builtin_fmaf(half_hi_f(b), s4, m);
+            v[8 * w + 6] = __builtin_fmaf(half_hi_f(c), s0, m);
+            v[8 * w + 7] = __builtin_fmaf(half_hi_f(e), s4, m);
         }
     } else {
-        static_assert(BITS == 2, "dequant32: 4 or 2 bits");
-        const float s0 = s * 0x1p24f, s2 = s * 0x1p22f, s4 = s * 0x1p20f, s6 = s * 0x1p18f;
+        static_assert(BITS == 2, "dequant32_f32: 4 or 2 bits");
+        const float sk[4] = {s * 0x1p24f, s * 0x1p22f, s * 0x1p20f, s * 0x1p18f};
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
-            // codes 16w+i at bits 2i; x's low byte per half holds codes (0..3, 8..11), y's (4..7, 12..15)
             const uint32_t x = d[w], y = x >> 8;
-            uint32_t a[4], b[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                a[k] = x & (0x00030003u << (2 * k));
-                b[k] = y & (0x00030003u << (2 * k));
+                const uint32_t a = x & (0x00030003u << (2 * k)), b = y & (0x00030003u << (2 * k));
+                v[16 * w + k] = __builtin_fmaf(half_lo_f(a), sk[k], m);
+                v[16 * w + 4 + k] = __builtin_fmaf(half_lo_f(b), sk[k], m);
+                v[16 * w + 8 + k] = __builtin_fmaf(half_hi_f(a), sk[k], m);
+                v[16 * w + 12 + k] = __builtin_fmaf(half_hi_f(b), sk[k], m);
             }
-            out[8 * w + 0] = pack_bf16x2(__builtin_fmaf(half_lo_f(a[0]), s0, m), __builtin_fmaf(half_lo_f(a[1]), s2, m));
-            out[8 * w + 1] = pack_bf16x2(__builtin_fmaf(half_lo_f(a[2]), s4, m), __builtin_fmaf(half_lo_f(a[3]), s6, m));
-            out[8 * w + 2] = pack_bf16x2(__builtin_fmaf(half_lo_f(b[0]), s0, m), __builtin_fmaf(half_lo_f(b[1]), s2, m));
-            out[8 * w + 3] = pack_bf16x2(__builtin_fmaf(half_lo_f(b[2]), s4, m), __builtin_fmaf(half_lo_f(b[3]), s6, m));
-            out[8 * w + 4] = pack_bf16x2(__builtin_fmaf(half_hi_f(a[0]), s0, m), __builtin_fmaf(half_hi_f(a[1]), s2, m));
-            out[8 * w + 5] = pack_bf16x2(__builtin_fmaf(half_hi_f(a[2]), s4, m), __builtin_fmaf(half_hi_f(a[3]), s6, m));
-            out[8 * w + 6] = pack_bf16x2(__builtin_fmaf(half_hi_f(b[0]), s0, m), __builtin_fmaf(half_hi_f(b[1]), s2, m));
-            out[8 * w + 7] = pack_bf16x2(__builtin_fmaf(half_hi_f(b[2]), s4, m), __builtin_fmaf(half_hi_f(b[3]), s6, m));
         }
     }
+}
+
+// dequant32_f32 rounded to bf16 (RTNE), as 16 pairs in element order.
+template <int BITS>
+__device__ __forceinline__ void dequant32(const uint32_t* d, uint32_t sm, uint32_t* out) {
+    float v[32];
+    dequant32_f32<BITS>(d, sm, v);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) out[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
 }
 
 // bf16 pair (2^elo(P), 2^ehi(P)): dot2 of a stored operand pair with it gives
