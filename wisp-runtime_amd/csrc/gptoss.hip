@@ -124,11 +124,13 @@ __device__ __forceinline__ int go_expert(const GoLayer& L, int j) {
 // h = l/32, the row pairs r0 + 16w + 8h + 2p (p < 4). xpair(r) returns the bf16
 // pair (x[r], x[r+1]) of the operand. Rows past R and columns past C read
 // clamped (in-bounds) weights and contribute nothing (zero operand / no
-// store). The partial sums of the 16 half-waves are reduced through LDS in a
-// fixed order and stored as dst[c - col0] for c < C.
-template <int BITS, typename XPair>
+// store). pre() runs after the weight loads are issued and before the first
+// xpair() (the down kernel forms its operand there). The partial sums of the 16
+// half-waves are reduced through LDS in a fixed order and stored as
+// dst[c - col0] for c < C.
+template <int BITS, typename XPair, typename Pre>
 __device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int64_t e0, int R, int C, int G,
-                                           int64_t scale_off, int64_t NG, int r0, int col0, XPair xpair,
+                                           int64_t scale_off, int64_t NG, int r0, int col0, XPair xpair, Pre pre,
                                            float* red, float* __restrict__ dst, bool poison) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, h = lane >> 5, cl = lane & 31;
     const int c = col0 + 32 * cl;
@@ -152,7 +154,12 @@ __device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int
             sv[p][t][0] = sc[g];
             sv[p][t][1] = mn[g];
         }
-        xp[p] = row_on ? xpair(r) : 0u;
+    }
+    pre();  // runs while the weight loads are in flight
+#pragma unroll
+    for (int p = 0; p < kGoPairs; ++p) {
+        const int r = r0 + 16 * wv + 8 * h + 2 * p;
+        xp[p] = r < R ? xpair(r) : 0u;
     }
     float acc[32];
 #pragma unroll
@@ -202,8 +209,8 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_gate_up(const GoLayer L
     const uint8_t* base = L.pool + (int64_t)(slot >= 0 ? slot : 0) * L.slot_bytes;
     const int C = 2 * L.I, col0 = blockIdx.x * kGoCols, r0 = blockIdx.y * kGoRows;
     const uint32_t* xw = reinterpret_cast<const uint32_t*>(L.x);
-    go_colgemv<BITS>(base, 0, L.H, C, L.G, L.scale_off, L.NG, r0, col0, [&](int r) { return xw[r >> 1]; }, red,
-                     L.p1 + ((int64_t)j * L.S1 + blockIdx.y) * C + col0, slot < 0);
+    go_colgemv<BITS>(base, 0, L.H, C, L.G, L.scale_off, L.NG, r0, col0, [&](int r) { return xw[r >> 1]; },
+                     [] {}, red, L.p1 + ((int64_t)j * L.S1 + blockIdx.y) * C + col0, slot < 0);
 }
 
 // grid (ceil(H / 1024), S2 = ceil(I / 128), k)
@@ -211,51 +218,71 @@ template <int BITS>
 __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
     __shared__ float red[2 * kGoWaves * kGoRedStride];
     __shared__ float gu[2 * kGoRows];
+    __shared__ float half_sum[2][2 * kGoRows];
     __shared__ uint32_t actp[kGoRows / 2];
+    static_assert(64 * kGoWaves == 4 * kGoRows, "two threads per gate_up column");
     const int j = blockIdx.z;
     const int slot = go_slot(L, j), ex = go_expert(L, j);
     const int I2 = 2 * L.I, i0 = blockIdx.y * kGoRows;
-    // gate_up outputs of activation rows i0 .. i0+127: gu = bf16(bf16(x . W) + bias)
-    for (int t = threadIdx.x; t < 2 * kGoRows; t += 64 * kGoWaves) {
+    auto prologue = [&] {
+        // gate_up outputs of activation rows i0 .. i0+127: gu = bf16(bf16(x . W) + bias). The S1
+        // partial sums of a column are split between two threads, each requesting 8 at a time.
+        const int t = threadIdx.x & (2 * kGoRows - 1), hf = threadIdx.x / (2 * kGoRows);
         const int c = 2 * i0 + t;
+        const int per = (L.S1 + 1) / 2, s0 = hf * per, s1 = min(L.S1, s0 + per);
         float v = 0.f;
         if (c < I2) {
             const float* p = L.p1 + (int64_t)j * L.S1 * I2 + c;
-            for (int s = 0; s < L.S1; ++s) v += p[(int64_t)s * I2];
-            v = ex >= 0 ? bf16r(bf16r(v) + bf16_to_f32(L.gub[(int64_t)ex * I2 + c])) : __builtin_nanf("");
-        }
-        gu[t] = v;
-    }
-    __syncthreads();
-    // clamped SwiGLU, each step rounded to bf16 as the reference's bf16 tensor ops do
-    // (gptoss.py:120-122): gate = min(g, limit), up = clamp(u, -limit, limit),
-    // act = (up + 1) * (gate * sigmoid(gate * alpha))
-    for (int t = threadIdx.x; t < kGoRows / 2; t += 64 * kGoWaves) {
-        float a2[2];
+            for (int sb = s0; sb < s1; sb += 8) {
+                float u8[8];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int i = i0 + 2 * t + q;
-            float a = 0.f;
-            if (i < L.I) {
-                const float g = fminf(gu[4 * t + 2 * q], L.limit);
-                const float u = fmaxf(fminf(gu[4 * t + 2 * q + 1], L.limit), -L.limit);
-                const float ga = bf16r(g * L.alpha);
-                const float sg = bf16r(1.f / (1.f + expf(-ga)));
-                const float glu = bf16r(g * sg);
-                a = bf16r(bf16r(u + 1.f) * glu);
-                // a NaN gate/up (invalid expert or slot) stays NaN through fminf/fmaxf only
-                // if both operands are NaN, so carry it explicitly
-                if (gu[4 * t + 2 * q] != gu[4 * t + 2 * q] || gu[4 * t + 2 * q + 1] != gu[4 * t + 2 * q + 1])
-                    a = __builtin_nanf("");
+                for (int u = 0; u < 8; ++u) u8[u] = p[(int64_t)min(sb + u, s1 - 1) * I2];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (sb + u < s1) v += u8[u];
             }
-            a2[q] = a;
         }
-        actp[t] = pack_bf16x2(a2[0], a2[1]);
-    }
-    __syncthreads();
+        half_sum[hf][t] = v;
+        __syncthreads();
+        if (threadIdx.x < 2 * kGoRows) {
+            float g = 0.f;
+            if (c < I2) {
+                g = half_sum[0][t] + half_sum[1][t];
+                g = ex >= 0 ? bf16r(bf16r(g) + bf16_to_f32(L.gub[(int64_t)ex * I2 + c])) : __builtin_nanf("");
+            }
+            gu[t] = g;
+        }
+        __syncthreads();
+        // clamped SwiGLU, each step rounded to bf16 as the reference's bf16 tensor ops do
+        // (gptoss.py:120-122): gate = min(g, limit), up = clamp(u, -limit, limit),
+        // act = (up + 1) * (gate * sigmoid(gate * alpha))
+        for (int t2 = threadIdx.x; t2 < kGoRows / 2; t2 += 64 * kGoWaves) {
+            float a2[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int i = i0 + 2 * t2 + q;
+                float a = 0.f;
+                if (i < L.I) {
+                    const float gg = fminf(gu[4 * t2 + 2 * q], L.limit);
+                    const float uu = fmaxf(fminf(gu[4 * t2 + 2 * q + 1], L.limit), -L.limit);
+                    const float ga = bf16r(gg * L.alpha);
+                    const float sg = bf16r(1.f / (1.f + expf(-ga)));
+                    const float glu = bf16r(gg * sg);
+                    a = bf16r(bf16r(uu + 1.f) * glu);
+                    // a NaN gate/up (invalid expert or slot) stays NaN through fminf/fmaxf only
+                    // if both operands are NaN, so carry it explicitly
+                    if (gu[4 * t2 + 2 * q] != gu[4 * t2 + 2 * q] || gu[4 * t2 + 2 * q + 1] != gu[4 * t2 + 2 * q + 1])
+                        a = __builtin_nanf("");
+                }
+                a2[q] = a;
+            }
+            actp[t2] = pack_bf16x2(a2[0], a2[1]);
+        }
+        __syncthreads();
+    };
     const uint8_t* base = L.pool + (int64_t)(slot >= 0 ? slot : 0) * L.slot_bytes;
     go_colgemv<BITS>(base, 2 * L.n, L.I, L.H, L.G, L.scale_off, L.NG, i0, blockIdx.x * kGoCols,
-                     [&](int r) { return actp[(r - i0) >> 1]; }, red,
+                     [&](int r) { return actp[(r - i0) >> 1]; }, prologue, red,
                      L.p2 + ((int64_t)j * L.S2 + blockIdx.y) * L.H + blockIdx.x * kGoCols, slot < 0);
 }
 
