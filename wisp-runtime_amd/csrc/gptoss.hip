@@ -81,8 +81,8 @@ __global__ __launch_bounds__(256) void k_mxfp4(const uint8_t* __restrict__ block
 // ---------------------------------------------------------------------------
 // Decode layer.
 
-constexpr int kGoWaves = 8;         // waves per workgroup
-constexpr int kGoRows = 128;        // input rows per workgroup (8 waves x 16)
+constexpr int kGoWaves = 4;         // waves per workgroup
+constexpr int kGoRows = 64;         // input rows per workgroup (4 waves x 16)
 constexpr int kGoCols = 1024;       // output columns per workgroup (32 lanes x 32)
 constexpr int kGoPairs = 4;         // row pairs per half-wave (16 rows per wave)
 constexpr int kGoRedStride = 1056;  // LDS floats per partial vector (32 x 33: conflict-free transpose)
