@@ -11,9 +11,9 @@
 //
 // Kernels:
 //   k_mxfp4      MXFP4 blocks + power-of-two scales -> bf16 (gptoss.py:22-29)
-//   k_go_gate_up partial gate_up GEMV: per expert, column block and block of 128
-//                input rows, fp32 partial sums of x . W_gu (bf16 weights)
-//   k_go_down    sums the gate_up partials of its 128 activation rows, adds the
+//   k_go_gate_up partial gate_up GEMV: per expert, column block and block of
+//                kGoRows input rows, fp32 partial sums of x . W_gu (bf16 weights)
+//   k_go_down    sums the gate_up partials of its kGoRows activation rows, adds the
 //                bias and applies the clamped SwiGLU with the reference's bf16
 //                rounding steps, then the partial down GEMV over those rows
 //   k_go_out     sums the down partials, adds the bias and the weighted sum over
@@ -118,14 +118,14 @@ __device__ __forceinline__ int go_expert(const GoLayer& L, int j) {
     return (f >= 0.f && f < (float)L.E && (float)e == f) ? e : -1;
 }
 
-// The workgroup's column GEMV over rows [r0, r0 + 128) of a [R, C] input-major
+// The workgroup's column GEMV over rows [r0, r0 + kGoRows) of a [R, C] input-major
 // matrix whose element (r, c) is flat element e0 + r*C + c of the expert.
 // Lane l of wave w owns columns col0 + 32*(l%32) .. +31 and, with half
 // h = l/32, the row pairs r0 + 16w + 8h + 2p (p < 4). xpair(r) returns the bf16
 // pair (x[r], x[r+1]) of the operand. Rows past R and columns past C read
 // clamped (in-bounds) weights and contribute nothing (zero operand / no
 // store). pre() runs after the weight loads are issued and before the first
-// xpair() (the down kernel forms its operand there). The partial sums of the 16
+// xpair() (the down kernel forms its operand there). The partial sums of the 2*kGoWaves
 // half-waves are reduced through LDS in a fixed order and stored as
 // dst[c - col0] for c < C.
 template <int BITS, typename XPair, typename Pre>
@@ -186,7 +186,7 @@ __device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int
 #pragma unroll
         for (int i = 0; i < 32; ++i) acc[i] = dot2(pack_bf16x2(w0[i], w1[i]), xp[p], acc[i]);
     }
-    // partial vectors [16][32 lanes x 33]: slot = 2w + h, column 32*cl + i at cl*33 + i
+    // partial vectors [2*kGoWaves][32 lanes x 33]: slot = 2w + h, column 32*cl + i at cl*33 + i
     float* mine = red + (2 * wv + h) * kGoRedStride + cl * 33;
 #pragma unroll
     for (int i = 0; i < 32; ++i) mine[i] = acc[i];
@@ -200,7 +200,7 @@ __device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int
     }
 }
 
-// grid (ceil(2I / 1024), S1 = ceil(H / 128), k)
+// grid (ceil(2I / kGoCols), S1 = ceil(H / kGoRows), k)
 template <int BITS>
 __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_gate_up(const GoLayer L) {
     __shared__ float red[2 * kGoWaves * kGoRedStride];
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_gate_up(const GoLayer L
                      [] {}, red, L.p1 + ((int64_t)j * L.S1 + blockIdx.y) * C + col0, slot < 0);
 }
 
-// grid (ceil(H / 1024), S2 = ceil(I / 128), k)
+// grid (ceil(H / kGoCols), S2 = ceil(I / kGoRows), k)
 template <int BITS>
 __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
     __shared__ float red[2 * kGoWaves * kGoRedStride];
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
     const int slot = go_slot(L, j), ex = go_expert(L, j);
     const int I2 = 2 * L.I, i0 = blockIdx.y * kGoRows;
     auto prologue = [&] {
-        // gate_up outputs of activation rows i0 .. i0+127: gu = bf16(bf16(x . W) + bias). The S1
+        // gate_up outputs of activation rows i0 .. i0+kGoRows-1: gu = bf16(bf16(x . W) + bias). The S1
         // partial sums of a column are split between two threads, each requesting 8 at a time.
         const int t = threadIdx.x & (2 * kGoRows - 1), hf = threadIdx.x / (2 * kGoRows);
         const int c = 2 * i0 + t;
