@@ -291,7 +291,7 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
 // into kGoOutSlices slices, one per wave. Every lane requests the partials of
 // up to kGoOutBatch experts before adding any (the sums are latency-bound);
 // the slice sums are added in slice order through LDS.
-constexpr int kGoOutCols = 64, kGoOutSlices = 4, kGoOutBatch = 8, kGoOutUnroll = 8;
+constexpr int kGoOutCols = 64, kGoOutSlices = 8, kGoOutBatch = 8, kGoOutUnroll = 8;
 __global__ __launch_bounds__(64 * kGoOutSlices) void k_go_out(const GoLayer L) {
     __shared__ float part[kGoOutSlices][kGoOutBatch][kGoOutCols];
     const int c = threadIdx.x & (kGoOutCols - 1), sl = threadIdx.x / kGoOutCols;
