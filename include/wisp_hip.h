@@ -40,7 +40,16 @@ extern "C" {
 #define WISP_EINVAL (-1)
 #define WISP_EALIGN (-2)
 
-#define WISP_ABI_VERSION 1
+#define WISP_ABI_VERSION 2
+
+/* Float types of x and of the layer output (the reference kernels take any
+ * float x and return x.dtype, wisp/kernels.py:132-137, 196-203, 315-322). */
+#define WISP_DT_BF16 0
+#define WISP_DT_F16 1
+#define WISP_DT_F32 2
+
+/* Largest k (experts per token) the decode entry points take. */
+#define WISP_MAX_K 8192
 
 /* ABI version of the loaded library (WISP_ABI_VERSION). No reference
  * counterpart: lets a binding check it loaded the library it was written for. */
@@ -81,17 +90,22 @@ int wisp_dequant(const uint8_t* rows, int64_t row_stride, const int64_t* row_ind
 /* Kernel 1 of a batch-1 MoE layer: for each of the k experts in meta and each
  * row r < I, a[j,r] = silu(Wg_j[r].x) * (Wu_j[r].x), fp32 accumulation,
  * written to the workspace `act` (wisp_act_bytes(k, I) bytes, internal
- * layout; wisp_act_read decodes it). x: H bf16 values. bits in {4,3,2}.
+ * layout; wisp_act_read decodes it). x: H values of type x_dtype
+ * (WISP_DT_BF16, WISP_DT_F16 or WISP_DT_F32; a non-bf16 x is used to ~17
+ * significant bits: exact for fp16, within 2^-17 relative for fp32), 16-byte
+ * aligned. bits in {4,3,2}; 1 <= k <= WISP_MAX_K.
  * Replaces wisp/kernels.py:20-69 (_gate_up_kernel, 4-bit) and 220-263
  * (_gate_up_kernel3, 3-bit); the 2-bit variant has no reference kernel. */
 int wisp_moe_gate_up(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
-                     const uint16_t* x, int64_t H, int64_t I, int bits, int64_t group, uint32_t* act, void* stream);
+                     const void* x, int x_dtype, int64_t H, int64_t I, int bits, int64_t group, uint32_t* act,
+                     void* stream);
 
 /* Kernel 2, weighted sum: out[h] = sum_{j=0..k-1} w_j * (Wd_j[h].a_j), fp32,
- * experts reduced in order, stored once as bf16. Replaces
+ * experts reduced in order, rounded once (to nearest even) to out_dtype
+ * (WISP_DT_BF16, WISP_DT_F16 or WISP_DT_F32). Replaces
  * wisp/kernels.py:140-185 (_down_sum_kernel) and 266-307 (_down_sum_kernel3). */
 int wisp_moe_down_sum(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
-                      const uint32_t* act, int64_t H, int64_t I, int bits, int64_t group, uint16_t* out,
+                      const uint32_t* act, int64_t H, int64_t I, int bits, int64_t group, void* out, int out_dtype,
                       void* stream);
 
 /* Kernel 2, per expert: y[j,h] = Wd_j[h].a_j (fp32 [k, H]).
@@ -101,10 +115,11 @@ int wisp_moe_down(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const
 
 /* Both kernels of one layer (gate_up, then down_sum) on `stream`.
  * Replaces wisp/kernels.py:188-203 (moe_decode_q4_fast) and 310-322
- * (moe_decode_q3_fast). act: caller-owned workspace of wisp_act_bytes(k, I). */
+ * (moe_decode_q3_fast), which return x.dtype: pass out_dtype = x_dtype.
+ * act: caller-owned workspace of wisp_act_bytes(k, I). */
 int wisp_moe_decode(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
-                    const uint16_t* x, int64_t H, int64_t I, int bits, int64_t group, uint32_t* act, uint16_t* out,
-                    void* stream);
+                    const void* x, int x_dtype, int64_t H, int64_t I, int bits, int64_t group, uint32_t* act,
+                    void* out, int out_dtype, void* stream);
 
 /* Rotary embedding of one decode token, q and k heads in one launch:
  * out[i] = x[i]*cos[i] + sign(i)*x[(i + d/2) mod d]*sin[i], sign = -1 for
@@ -349,6 +364,24 @@ int wisp_set_tuning(int gu_rows, int gu_waves, int dn_iters);
  * No reference counterpart (the reference's `a` is already fp32); used by
  * tests to check kernel 1 on its own. */
 int wisp_act_read(const uint32_t* act, int k, int64_t I, int bits, float* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Measurement probes (no reference counterpart): the floors the decode
+ * kernels are measured against (bench.py --workload floor). Not used by the
+ * product path.
+ * ------------------------------------------------------------------------ */
+
+/* An empty kernel (one wave): the cost of one launch inside a graph. */
+int wisp_probe_empty(void* stream);
+
+/* A plain streaming read of `bytes` (a multiple of 16) from base with 16-byte
+ * non-temporal loads over `workgroups` workgroups of 256 threads; nothing is
+ * written to `sink` (a device buffer of `workgroups` uint32, kept so the loads
+ * are not removed). With `slot` non-null (device float), the read starts at
+ * base + s*stride, s = *slot when it is an integer in [0, nslots), else 0:
+ * the caller guarantees base + (nslots-1)*stride + bytes is in bounds. */
+int wisp_probe_read(const uint8_t* base, const float* slot, int64_t stride, int64_t nslots, int64_t bytes,
+                    int workgroups, uint32_t* sink, void* stream);
 
 #ifdef __cplusplus
 }

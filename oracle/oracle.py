@@ -54,6 +54,8 @@ def lib() -> ctypes.CDLL:
         L.wo_dequant.restype, L.wo_dequant.argtypes = i32, [vp, i64, i32, i64, vp]
         L.wo_moe_layer_f64.restype = i32
         L.wo_moe_layer_f64.argtypes = [vp, i64, i64, vp, vp, i32, vp, i64, i64, i32, i64, vp, vp, vp]
+        L.wo_moe_layer_f64x.restype = i32
+        L.wo_moe_layer_f64x.argtypes = [vp, i64, i64, vp, vp, i32, vp, i64, i64, i32, i64, vp, vp, vp]
         L.wo_rope.restype, L.wo_rope.argtypes = i32, [vp, i64, i32, vp, vp, vp]
         _lib = L
     return _lib
@@ -152,19 +154,27 @@ def dequant(buf: np.ndarray, n: int, bits: int, group: int = 128) -> np.ndarray:
 def moe_layer_f64(pool: np.ndarray, slots, w, x_bf16: np.ndarray, H: int, I: int, bits: int, group: int = 128):
     """Binary64 statement of one batch-1 MoE layer with the fused kernels' semantics
     (kernels.py:12, 20-69, 72-112, 140-185, 220-307): returns (a [k,I], y [k,H], out [H]),
-    all float64 and unrounded. `w` are the routing weights the kernels read (float32 values)."""
+    all float64 and unrounded. `w` are the routing weights the kernels read (float32 values).
+    x_bf16: uint16 bf16 bit patterns, or x as float16/float32/float64 values (the reference
+    kernels widen any float x exactly, kernels.py:51-52)."""
     pool = np.ascontiguousarray(pool, dtype=np.uint8)
     slots = np.ascontiguousarray(slots, dtype=np.int64).ravel()
     w = np.ascontiguousarray(w, dtype=np.float32).ravel()
-    x = np.ascontiguousarray(x_bf16, dtype=np.uint16).ravel()
+    xin = np.asarray(x_bf16)
     k = slots.size
-    assert w.size == k and x.size == H
+    assert w.size == k and xin.size == H
     a = np.empty((k, I), dtype=np.float64)
     y = np.empty((k, H), dtype=np.float64)
     out = np.empty(H, dtype=np.float64)
-    rc = lib().wo_moe_layer_f64(
-        _p(pool), pool.shape[1], pool.shape[0], _p(slots), _p(w), k, _p(x), H, I, bits, group, _p(a), _p(y), _p(out)
-    )
+    if xin.dtype == np.uint16:
+        x = np.ascontiguousarray(xin).ravel()
+        fn = lib().wo_moe_layer_f64
+    else:
+        assert xin.dtype in (np.float16, np.float32, np.float64), xin.dtype
+        x = np.ascontiguousarray(xin, dtype=np.float64).ravel()
+        fn = lib().wo_moe_layer_f64x
+    rc = fn(_p(pool), pool.shape[1], pool.shape[0], _p(slots), _p(w), k, _p(x), H, I, bits, group, _p(a), _p(y),
+            _p(out))
     if rc != 0:
         raise ValueError("bad arguments to moe_layer_f64")
     return a, y, out

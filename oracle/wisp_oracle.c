@@ -341,23 +341,23 @@ static double row_dot(const uint8_t* buf, int64_t n, int bits, int64_t group, in
  *   out[h] = sum_j w_j * y[j,h]   (j in order 0..k-1)             (140-185)
  * pool: nslots rows of slot_bytes; slots[k]; w[k] routing weights as the
  * kernels see them (fp32 values of the bf16-rounded weights, moe.py:72);
- * x: H bf16 bit patterns. Outputs (any may be NULL): a [k*I], y [k*H],
- * out [H], all binary64 and unrounded. Returns 0, or -1 on bad arguments. */
-WO_EXPORT int wo_moe_layer_f64(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const int64_t* slots,
-                               const float* w, int k, const uint16_t* x, int64_t H, int64_t I, int bits,
-                               int64_t group, double* a_out, double* y_out, double* out) {
+ * xd: H values of x in binary64 (the reference kernels widen x of any float
+ * type to fp32 exactly, kernels.py:51-52). Outputs (any may be NULL): a [k*I],
+ * y [k*H], out [H], all binary64 and unrounded. Returns 0, or -1 on bad
+ * arguments. */
+WO_EXPORT int wo_moe_layer_f64x(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const int64_t* slots,
+                                const float* w, int k, const double* xd, int64_t H, int64_t I, int bits,
+                                int64_t group, double* a_out, double* y_out, double* out) {
     if (!(bits == 8 || bits == 4 || bits == 3 || bits == 2)) return -1;
     if (H <= 0 || I <= 0 || H % group || I % group) return -1;
     int64_t n = H * I;
     if (wo_expert_nbytes(n, bits, group) < 0 || wo_expert_nbytes(n, bits, group) > slot_bytes) return -1;
-    double* xd = (double*)malloc(sizeof(double) * (size_t)H);
     double* ad = (double*)malloc(sizeof(double) * (size_t)I);
-    if (!xd || !ad) { free(xd); free(ad); return -1; }
-    for (int64_t i = 0; i < H; i++) xd[i] = (double)wo_bf16_to_f32(x[i]);
+    if (!ad) return -1;
     if (out)
         for (int64_t h = 0; h < H; h++) out[h] = 0.0;
     for (int j = 0; j < k; j++) {
-        if (slots[j] < 0 || slots[j] >= nslots) { free(xd); free(ad); return -1; }
+        if (slots[j] < 0 || slots[j] >= nslots) { free(ad); return -1; }
         const uint8_t* buf = pool + slots[j] * slot_bytes;
         for (int64_t r = 0; r < I; r++) {
             double g = row_dot(buf, n, bits, group, 0, r, H, xd);
@@ -372,9 +372,21 @@ WO_EXPORT int wo_moe_layer_f64(const uint8_t* pool, int64_t slot_bytes, int64_t 
             if (out) out[h] += (double)w[j] * y;
         }
     }
-    free(xd);
     free(ad);
     return 0;
+}
+
+/* wo_moe_layer_f64x with x given as H bf16 bit patterns. */
+WO_EXPORT int wo_moe_layer_f64(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const int64_t* slots,
+                               const float* w, int k, const uint16_t* x, int64_t H, int64_t I, int bits,
+                               int64_t group, double* a_out, double* y_out, double* out) {
+    if (H <= 0) return -1;
+    double* xd = (double*)malloc(sizeof(double) * (size_t)H);
+    if (!xd) return -1;
+    for (int64_t i = 0; i < H; i++) xd[i] = (double)wo_bf16_to_f32(x[i]);
+    int rc = wo_moe_layer_f64x(pool, slot_bytes, nslots, slots, w, k, xd, H, I, bits, group, a_out, y_out, out);
+    free(xd);
+    return rc;
 }
 
 /* ------------------------------------------------------------------------ */

@@ -77,7 +77,8 @@ FAKE = ctypes.c_void_p(0x100000)  # never dereferenced: every call below fails v
     [
         (dict(bits=5), b"bits"),
         (dict(k=0), b"k must"),
-        (dict(k=17), b"k must"),
+        (dict(k=8193), b"k must"),
+        (dict(x_dtype=3), b"x_dtype"),
         (dict(H=2000), b"multiples of group"),
         (dict(group=64 + 16, H=2080 // 1, I=80 * 9), b"multiple of 32"),
         (dict(slot_bytes=1000), b"smaller than one expert"),
@@ -87,22 +88,39 @@ FAKE = ctypes.c_void_p(0x100000)  # never dereferenced: every call below fails v
 )
 def test_layer_argument_validation(args, needle):
     L = _lib.lib()
-    a = dict(pool=FAKE, slot_bytes=2506752, nslots=128, meta=FAKE, k=8, x=FAKE, H=2048, I=768, bits=4, group=128,
-             act=FAKE, stream=None)
+    a = dict(pool=FAKE, slot_bytes=2506752, nslots=128, meta=FAKE, k=8, x=FAKE, x_dtype=_lib.WISP_DT_BF16, H=2048,
+             I=768, bits=4, group=128, act=FAKE, stream=None)
     a.update(args)
     rc = L.wisp_moe_gate_up(*a.values())
     assert rc == _lib.WISP_EINVAL, rc
     assert needle in L.wisp_last_error()
+    if "x_dtype" in args:
+        return
     d = (a["pool"], a["slot_bytes"], a["nslots"], a["meta"], a["k"], FAKE, a["H"], a["I"], a["bits"], a["group"])
-    assert L.wisp_moe_down_sum(*d, FAKE, None) == _lib.WISP_EINVAL
+    assert L.wisp_moe_down_sum(*d, FAKE, _lib.WISP_DT_BF16, None) == _lib.WISP_EINVAL
     assert L.wisp_moe_down(*d, FAKE, None) == _lib.WISP_EINVAL
+    x = (FAKE, _lib.WISP_DT_BF16)
+    assert L.wisp_moe_decode(*d[:5], *x, *d[6:], FAKE, FAKE, _lib.WISP_DT_BF16, None) == _lib.WISP_EINVAL
+
+
+def test_output_dtype_validation():
+    L = _lib.lib()
+    d = (FAKE, 2506752, 128, FAKE, 8, FAKE, 2048, 768, 4, 128)
+    assert L.wisp_moe_down_sum(*d, FAKE, 7, None) == _lib.WISP_EINVAL
+    assert b"out_dtype" in L.wisp_last_error()
+    assert L.wisp_moe_down_sum(*d, None, _lib.WISP_DT_F32, None) == _lib.WISP_EINVAL
+    assert b"null out" in L.wisp_last_error()
 
 
 def test_alignment_validation():
     L = _lib.lib()
-    rc = L.wisp_moe_gate_up(ctypes.c_void_p(0x100004), 2506752, 128, FAKE, 8, FAKE, 2048, 768, 4, 128, FAKE, None)
+    bf = _lib.WISP_DT_BF16
+    rc = L.wisp_moe_gate_up(ctypes.c_void_p(0x100004), 2506752, 128, FAKE, 8, FAKE, bf, 2048, 768, 4, 128, FAKE, None)
     assert rc == _lib.WISP_EALIGN
-    rc = L.wisp_moe_gate_up(FAKE, 2506752 + 4, 128, FAKE, 8, FAKE, 2048, 768, 4, 128, FAKE, None)
+    rc = L.wisp_moe_gate_up(FAKE, 2506752 + 4, 128, FAKE, 8, FAKE, bf, 2048, 768, 4, 128, FAKE, None)
+    assert rc == _lib.WISP_EALIGN
+    rc = L.wisp_moe_gate_up(FAKE, 2506752, 128, FAKE, 8, ctypes.c_void_p(0x100008), _lib.WISP_DT_F32, 2048, 768, 4,
+                            128, FAKE, None)
     assert rc == _lib.WISP_EALIGN
 
 
@@ -227,6 +245,14 @@ def test_no_cpu_fallback():
     # the reference's shape assertion (kernels.py:191) comes first
     with pytest.raises(AssertionError):
         kernels.moe_decode_q4_fast(pool, meta, torch.zeros(256, dtype=torch.bfloat16), 2, 256 * 128, 250, 128)
+    # k beyond WISP_MAX_K is refused before any device work
+    with pytest.raises(AssertionError, match="k must"):
+        kernels.moe_decode_q4_fast(pool, meta, torch.zeros(256), 8193, 256 * 128, 256, 128)
+    # x of a non-float dtype is refused; float64 x would be rounded to fp32 (no CPU path either way)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        kernels.moe_decode_q4_fast(pool, meta, torch.zeros(256, dtype=torch.float64), 2, 256 * 128, 256, 128)
+    with pytest.raises(TypeError, match="float"):
+        kernels._prep_x_any(torch.zeros(256, dtype=torch.int32))
 
 
 def test_meta_layout_helpers():

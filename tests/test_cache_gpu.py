@@ -143,6 +143,22 @@ def test_resize_keeps_hottest_and_recopies():
     c.free()
 
 
+def test_failed_resize_reports_the_missing_pool():
+    """A resize whose new pool cannot be allocated leaves the cache without a pool: the
+    calls that would touch it return an error instead of dereferencing it."""
+    st = _store(1, 6, 4, seed=9)
+    c = ExpertCache(st, 4)
+    assert c.ensure([0, 1]) == [0, 1]
+    huge = 1 << 23  # 2^23 slots of ~61 KB (512 GB): past the device memory
+    with pytest.raises((RuntimeError, ValueError)):
+        c.resize(huge)
+    assert _lib.lib().wisp_cache_pool(c._h) is None
+    with pytest.raises(RuntimeError, match="pool not allocated"):
+        c.ensure([2, 3])
+    assert not _lib.lib().wisp_cache_pool_dlpack(c._h)
+    c.free()
+
+
 def test_prefetch_and_admit_async_issue_copies():
     st = _store(1, 8, 4, seed=9)
     c = ExpertCache(st, 4, admit_after=0.5)

@@ -1,0 +1,229 @@
+"""GPU parity of the drop-in surface beyond the bf16 / k <= 8 case, the pool sizes the
+benchmark uses, and negative controls that show the parity bar discriminates.
+
+* x of any float dtype, output in x.dtype (reference wisp/kernels.py:132-137, 196-203,
+  315-322: x is loaded and widened with `.to(tl.float32)`, `out` is allocated in x.dtype).
+* any k (the reference's `_down_sum_kernel` loops over a constexpr K, kernels.py:166-184).
+* a slot pool past 4 GiB of offsets with the routed experts in its top slots
+  (`pool + slot * NBYTES`, kernels.py:39) -- the 48 x 128-slot pool of the benchmark.
+* sabotage: a swapped slot, swapped weights and a shifted scale table each miss the
+  1e-3 bar by more than 10x (the reference's own control: shuffled experts must fail,
+  tests/test_paged_moe.py:114-126).
+All checks are against the binary64 oracle of the fused semantics (oracle/).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from wisp import kernels
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 1e-3
+
+
+def _pool(E, H, I, bits, group, seed):
+    rng = np.random.default_rng(seed)
+    n = H * I
+    return np.stack([O.quantize((rng.standard_normal(3 * n) * 0.02).astype(np.float32), bits, group)
+                     for _ in range(E)])
+
+
+def _route(rng, E, k):
+    sel, rw = O.route(rng.standard_normal((1, E)).astype(np.float32), k)
+    return sel[0], rw[0]
+
+
+def _rel_l2(got, ref):
+    return float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+
+
+def _f64(t):
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+def _round_to(ref, dtype):
+    """The binary64 oracle rounded once to the output dtype (the kernels store once)."""
+    if dtype == torch.float32:
+        return ref.astype(np.float32).astype(np.float64)
+    if dtype == torch.float16:
+        return ref.astype(np.float16).astype(np.float64)
+    return O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.astype(np.float32))).astype(np.float64)
+
+
+_FNS = {4: kernels.moe_decode_q4_fast, 3: kernels.moe_decode_q3_fast, 2: kernels.moe_decode_q2_fast}
+
+
+# ---------------------------------------------------------------- x dtype, output dtype
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.float64])
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("H,I,group,E,k", [(2048, 768, 128, 10, 8), (256, 128, 128, 6, 3), (4096, 256, 128, 3, 2)])
+def test_float_x_parity_and_output_dtype(dtype, bits, H, I, group, E, k):
+    rng = np.random.default_rng(hash((bits, H, str(dtype))) % 2**32)
+    pool = _pool(E, H, I, bits, group, seed=bits + H)
+    sel, rw = _route(rng, E, k)
+    xt = torch.randn(H, generator=torch.Generator().manual_seed(H + bits), dtype=torch.float64).to(dtype)
+    # the oracle sees x exactly as stored (float64 x reaches the kernels rounded to fp32)
+    x_np = xt.to(torch.float32).numpy() if dtype == torch.float64 else xt.numpy()
+    _, _, ref = O.moe_layer_f64(pool, sel, rw, x_np, H, I, bits, group)
+    got = _FNS[bits](torch.from_numpy(pool).to(DEV), torch.from_numpy(O.meta(sel, rw)).to(DEV), xt.to(DEV),
+                     k, H * I, H, I, group)
+    torch.cuda.synchronize()
+    assert got.dtype == dtype and got.shape == (H,)
+    err = _rel_l2(_f64(got), _round_to(ref, torch.float32 if dtype == torch.float64 else dtype))
+    print(f"x {dtype} bits={bits} H={H} I={I} k={k}: rel-L2 {err:.3e}")
+    assert err <= TOL, err
+    if dtype == torch.float32:
+        # the fp32 path keeps x to ~17 bits: far tighter than the bar (bf16 x alone would not be)
+        assert err <= 1e-4, err
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_float_x_activation(dtype):
+    H, I, group, E, k, bits = 2048, 768, 128, 4, 3, 4
+    rng = np.random.default_rng(5)
+    pool = _pool(E, H, I, bits, group, seed=5)
+    sel, rw = _route(rng, E, k)
+    xt = torch.randn(H, generator=torch.Generator().manual_seed(6)).to(dtype)
+    a_ref, _, _ = O.moe_layer_f64(pool, sel, rw, xt.numpy(), H, I, bits, group)
+    a = kernels.gate_up_act(torch.from_numpy(pool).to(DEV), torch.from_numpy(O.meta(sel, rw)).to(DEV), xt.to(DEV),
+                            k, H * I, H, I, bits, group)
+    err = _rel_l2(a.cpu().numpy().astype(np.float64), a_ref)
+    print(f"gate_up x {dtype}: rel-L2 {err:.3e}")
+    assert err <= 2e-5, err
+
+
+def test_per_expert_path_float_x():
+    """moe_decode_q4 (kernels.py:115-137) with fp32 x returns fp32."""
+    H, I, group, E, k = 256, 128, 128, 6, 3
+    rng = np.random.default_rng(8)
+    pool = _pool(E, H, I, 4, group, seed=8)
+    sel, rw = _route(rng, E, k)
+    xt = torch.randn(H, generator=torch.Generator().manual_seed(9))
+    _, _, ref = O.moe_layer_f64(pool, sel, rw, xt.numpy(), H, I, 4, group)
+    got = kernels.moe_decode_q4(torch.from_numpy(pool).to(DEV), torch.from_numpy(sel).to(DEV), xt.to(DEV),
+                                torch.from_numpy(rw).to(DEV), H * I, H, I, group)
+    assert got.dtype == torch.float32
+    assert _rel_l2(_f64(got), ref) <= 1e-4
+
+
+# ---------------------------------------------------------------- any k
+@pytest.mark.parametrize("bits", [4, 3])
+@pytest.mark.parametrize("H,I,group,E,k", [(256, 128, 128, 40, 17), (256, 128, 128, 40, 33), (512, 384, 128, 24, 24),
+                                           (2048, 768, 128, 20, 20), (64, 32, 32, 70, 64)])
+def test_more_than_16_experts(bits, H, I, group, E, k):
+    rng = np.random.default_rng(k * 3 + bits)
+    pool = _pool(E, H, I, bits, group, seed=k + bits)
+    sel, rw = _route(rng, E, k)
+    x = O.f32_to_bf16_bits(rng.standard_normal(H).astype(np.float32))
+    _, _, ref = O.moe_layer_f64(pool, sel, rw, x, H, I, bits, group)
+    got = _FNS[bits](torch.from_numpy(pool).to(DEV), torch.from_numpy(O.meta(sel, rw)).to(DEV),
+                     torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV), k, H * I, H, I, group)
+    torch.cuda.synchronize()
+    err = _rel_l2(_f64(got), _round_to(ref, torch.bfloat16))
+    print(f"k={k} bits={bits} H={H} I={I}: rel-L2 {err:.3e}")
+    assert err <= TOL, err
+
+
+def test_more_than_16_experts_per_expert_y_and_invalid_slot():
+    H, I, group, E, k = 256, 128, 128, 24, 20
+    rng = np.random.default_rng(21)
+    pool = _pool(E, H, I, 4, group, seed=21)
+    sel, rw = _route(rng, E, k)
+    x = O.f32_to_bf16_bits(rng.standard_normal(H).astype(np.float32))
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV)
+    _, _, ref = O.moe_layer_f64(pool, sel, rw, x, H, I, 4, group)
+    got = kernels.moe_decode_q4(torch.from_numpy(pool).to(DEV), torch.from_numpy(sel).to(DEV), xt,
+                                torch.from_numpy(rw).to(DEV), H * I, H, I, group)
+    assert _rel_l2(_f64(got), _round_to(ref, torch.bfloat16)) <= TOL
+    meta = torch.from_numpy(O.meta(sel, rw)).to(DEV)
+    meta[k - 1] = float(E + 5)  # the last expert's slot out of range: NaN rows, no fault
+    bad = kernels.moe_decode_q4_fast(torch.from_numpy(pool).to(DEV), meta, xt, k, H * I, H, I, group)
+    assert torch.isnan(bad.float()).all()
+
+
+# ---------------------------------------------------------------- the benchmark's pool: > 4 GiB of offsets
+def test_pool_past_4gib_top_slots():
+    """The C2 benchmark's pool: 48 layer pools x 128 experts = 6,144 slots of 2,506,752 B
+    (15.4 GB). Experts are written into slots whose byte offsets lie far past 2^32, and the
+    layer is checked against the oracle on those rows; the rest of the pool stays unwritten."""
+    H, I, group, bits, k = 2048, 768, 128, 4, 8
+    n = H * I
+    nb = O.expert_nbytes(n, bits, group)
+    nslots = 48 * 128
+    rows = _pool(12, H, I, bits, group, seed=123)
+    pool = torch.empty((nslots, nb), dtype=torch.uint8, device=DEV)
+    top = np.array([nslots - 1, nslots - 2, nslots - 3, 5000, 4100, 3000, 1714, 1713, 2, 0, 6100, 5555])
+    assert (top[:8] * nb > 2**32).all()
+    for i, s in enumerate(top):
+        pool[int(s)].copy_(torch.from_numpy(rows[i]))
+    rng = np.random.default_rng(124)
+    for it in range(3):
+        pick = rng.choice(12, k, replace=False) if it else np.arange(k)
+        _, rw = _route(rng, 12, k)
+        sel_rows = rows[pick]
+        x = O.f32_to_bf16_bits(rng.standard_normal(H).astype(np.float32))
+        _, _, ref = O.moe_layer_f64(sel_rows, np.arange(k), rw, x, H, I, bits, group)
+        meta = torch.from_numpy(O.meta(top[pick], rw)).to(DEV)
+        got = kernels.moe_decode_q4_fast(pool, meta, torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV),
+                                         k, n, H, I, group)
+        torch.cuda.synchronize()
+        err = _rel_l2(_f64(got), _round_to(ref, torch.bfloat16))
+        print(f"pool 15.4 GB, slots {top[pick].tolist()}: rel-L2 {err:.3e}")
+        assert err <= TOL, err
+    del pool
+    torch.cuda.empty_cache()
+
+
+# ---------------------------------------------------------------- negative controls
+@pytest.fixture(scope="module")
+def c2_case():
+    H, I, group, bits, E, k = 2048, 768, 128, 4, 12, 8
+    rng = np.random.default_rng(99)
+    pool = _pool(E, H, I, bits, group, seed=99)
+    sel, rw = _route(rng, E, k)
+    x = O.f32_to_bf16_bits(rng.standard_normal(H).astype(np.float32))
+    _, _, ref = O.moe_layer_f64(pool, sel, rw, x, H, I, bits, group)
+    return dict(H=H, I=I, group=group, bits=bits, pool=pool, sel=sel, rw=rw, x=x, ref=_round_to(ref, torch.bfloat16))
+
+
+def _run(c, pool, meta):
+    xt = torch.from_numpy(c["x"].view(np.int16)).view(torch.bfloat16).to(DEV)
+    H, I = c["H"], c["I"]
+    out = kernels.moe_decode_q4_fast(torch.from_numpy(pool).to(DEV), torch.from_numpy(meta).to(DEV), xt,
+                                     len(c["sel"]), H * I, H, I, c["group"])
+    return _f64(out)
+
+
+def test_control_clean_case_passes(c2_case):
+    c = c2_case
+    err = _rel_l2(_run(c, c["pool"], O.meta(c["sel"], c["rw"])), c["ref"])
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("sabotage", ["swap_slots", "swap_weights", "shift_down_scales", "shift_gate_mins"])
+def test_control_sabotage_fails_by_10x(c2_case, sabotage):
+    """Each plausible kernel mistake, planted in the kernel's inputs, must miss the bar by
+    more than 10x, so a bar of 1e-3 cannot be met by a wrong kernel."""
+    c = c2_case
+    sel, rw, pool = c["sel"].copy(), c["rw"].copy(), c["pool"].copy()
+    n, bits, group = c["H"] * c["I"], c["bits"], c["group"]
+    ncode, ng = 3 * n * bits // 8, 3 * n // group
+    if sabotage == "swap_slots":  # experts 0 and 5 trade places, their weights do not
+        sel[[0, 5]] = sel[[5, 0]]
+    elif sabotage == "swap_weights":
+        rw[[0, 7]] = rw[[7, 0]]
+    elif sabotage == "shift_down_scales":  # the down matrix of the top expert reads group g+1's scale
+        e = int(sel[0])
+        sc = pool[e, ncode:ncode + 2 * ng].view(np.uint16)
+        d0 = 2 * (n // group)
+        sc[d0:ng - 1] = sc[d0 + 1:ng].copy()
+    else:  # the gate matrix of the top expert reads group g+1's min
+        e = int(sel[0])
+        mn = pool[e, ncode + 2 * ng:ncode + 4 * ng].view(np.uint16)
+        mn[: n // group - 1] = mn[1: n // group].copy()
+    err = _rel_l2(_run(c, pool, O.meta(sel, rw)), c["ref"])
+    print(f"sabotage {sabotage}: rel-L2 {err:.3e}")
+    assert err > 10 * TOL, (sabotage, err)

@@ -206,7 +206,10 @@ def test_dequant_matches_numpy_float32_semantics():
 # ---------------------------------------------------------------- fused layer semantics
 def _dense_layer(pool, slots, w, x_bits, H, I, bits, group):
     n = H * I
-    xf = O.bf16_bits_to_f32(x_bits).astype(np.float64)
+    if x_bits.dtype == np.uint16:
+        xf = O.bf16_bits_to_f32(x_bits).astype(np.float64)
+    else:
+        xf = x_bits.astype(np.float64)
     out = np.zeros(H)
     a_all, y_all = [], []
     for s, wj in zip(slots, w):
@@ -238,6 +241,25 @@ def test_fused_oracle_matches_dense_matvec(bits, H, I, group):
     assert np.allclose(a, a2, rtol=1e-10, atol=1e-12)
     assert np.allclose(y, y2, rtol=1e-10, atol=1e-12)
     assert np.allclose(out, out2, rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("xdt", [np.float32, np.float16])
+def test_fused_oracle_float_x(xdt):
+    # x given as float values (the reference loads any float x and widens it, kernels.py:51-52):
+    # the same dense unfolded form, and the bf16 entry point agrees on bf16-representable x
+    rng = np.random.default_rng(31)
+    H, I, group, bits, n = 256, 128, 128, 4, 256 * 128
+    pool = np.stack([O.quantize((rng.standard_normal(3 * n) * 0.05).astype(np.float32), bits, group) for _ in range(4)])
+    slots, w = [3, 1], np.array([0.75, 0.25], np.float32)
+    x = rng.standard_normal(H).astype(xdt)
+    a, y, out = O.moe_layer_f64(pool, slots, w, x, H, I, bits, group)
+    a2, y2, out2 = _dense_layer(pool, slots, w, x, H, I, bits, group)
+    assert np.allclose(out, out2, rtol=1e-10, atol=1e-12) and np.allclose(a, a2, rtol=1e-10, atol=1e-12)
+    xb = O.f32_to_bf16_bits(x.astype(np.float32))
+    _, _, out3 = O.moe_layer_f64(pool, slots, w, O.bf16_bits_to_f32(xb), H, I, bits, group)
+    _, _, out4 = O.moe_layer_f64(pool, slots, w, xb, H, I, bits, group)
+    assert np.array_equal(out3, out4)
+    assert not np.allclose(out, out4, rtol=1e-6, atol=0)  # x's low bits reach the result
 
 
 # ---------------------------------------------------------------- routing (moe.py:67-72)

@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 OBJDIR = os.path.join(HERE, "lib", "obj")
 LIB = os.path.join(LIBDIR, "libwisp_hip.so")
-SOURCES = ["abi.hip", "quant_kernels.hip", "moe_decode.hip", "rope.hip", "cache.hip", "attention.hip", "prefill.hip", "gptoss.hip", "decode_layer.hip"]
+SOURCES = ["abi.hip", "quant_kernels.hip", "moe_decode.hip", "rope.hip", "cache.hip", "attention.hip", "prefill.hip", "gptoss.hip", "decode_layer.hip", "probe.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -221,6 +221,10 @@ static int hip_fail(hipError_t e, const char* what) {
     return (int)e;
 }
 
+// A resize whose new pool could not be allocated leaves the cache without one;
+// every entry point that would touch the pool reports it instead.
+static int no_pool() { return fail_inval("pool not allocated: the last resize failed to allocate it"); }
+
 static int alloc_pool(Cache& c) {
     PoolBlock* b = new (std::nothrow) PoolBlock();
     if (!b) return fail_inval("out of host memory");
@@ -297,6 +301,7 @@ static int page_on_stream(Cache& c, const int64_t* keys, const int64_t* slots, i
     for (int64_t i = 0; i < n; ++i)
         if (keys[i] < 0 || keys[i] >= c.host_rows || slots[i] < 0 || slots[i] >= c.nslots)
             return fail_inval("key outside the host store or slot outside the pool");
+    if (!c.pool) return no_pool();
     uint8_t* pool = static_cast<uint8_t*>(c.pool->ptr);
     const int64_t row16 = c.row_bytes / 16, slot16 = c.slot_bytes / 16;
     const int64_t per = ((row16 + kPageSplit - 1) / kPageSplit + 1023) / 1024 * 1024;
@@ -326,6 +331,7 @@ static int issue(Cache& c, const int64_t* keys, const int64_t* slots, int64_t n,
     for (int64_t i = 0; i < n; ++i)
         if (keys[i] < 0 || keys[i] >= c.host_rows || slots[i] < 0 || slots[i] >= c.nslots)
             return fail_inval("key outside the host store or slot outside the pool");
+    if (!c.pool) return no_pool();
     hipError_t e = hipEventRecord(c.order, compute);
     if (e == hipSuccess) e = hipStreamWaitEvent(c.copy, c.order, 0);
     if (e != hipSuccess) return hip_fail(e, "ordering the copy stream");
@@ -660,7 +666,10 @@ extern "C" void wisp_cache_destroy(void* h) {
 }
 
 extern "C" void* wisp_cache_core(void* h) { return as_cache(h)->core; }
-extern "C" void* wisp_cache_pool(void* h) { return as_cache(h)->pool->ptr; }
+extern "C" void* wisp_cache_pool(void* h) {
+    Cache* c = as_cache(h);
+    return c->pool ? c->pool->ptr : nullptr;
+}
 extern "C" void* wisp_cache_copy_stream(void* h) { return as_cache(h)->copy; }
 
 extern "C" void wisp_cache_counters(void* h, int64_t* bytes_h2d, int64_t* n_loads) {
@@ -672,6 +681,10 @@ extern "C" void wisp_cache_counters(void* h, int64_t* bytes_h2d, int64_t* n_load
 // view holds a reference, so the memory outlives the cache while it is used.
 extern "C" void* wisp_cache_pool_dlpack(void* h) {
     Cache* c = as_cache(h);
+    if (!c->pool) {
+        no_pool();
+        return nullptr;
+    }
     PoolView* v = new (std::nothrow) PoolView();
     if (!v) return nullptr;
     c->pool->refs.fetch_add(1);

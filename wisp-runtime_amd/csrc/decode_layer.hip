@@ -385,11 +385,12 @@ __global__ __launch_bounds__(64) void k_dl_route(const uint16_t* __restrict__ lo
         if (host_row) __hip_atomic_store(host_row + lane, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     if (host_row) {
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this lane's row store has completed
-        __builtin_amdgcn_wave_barrier();     // ... and every other lane's (one wave)
+        // the barrier makes every lane's row store happen-before lane 0's flag store,
+        // and the system-scope release orders them before the flag for the host
+        __syncthreads();
         if (lane == 0) {
             *seq = seq0 + 1;
-            __hip_atomic_store(host_flag, seq0 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(host_flag, seq0 + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
 }

@@ -46,7 +46,66 @@ struct Layer {
     int gsh;      // log2(G/32) when G/32 is a power of two, else -1
     int spr_gu;   // chunks per gate/up row, H/32
     int spr_dn;   // chunks per down row, I/32
+    int odt;      // output dtype of the weighted sum: WISP_DT_BF16, WISP_DT_F16 or WISP_DT_F32
 };
+
+// out[h] = v rounded once (round to nearest even) to the caller's dtype
+__device__ __forceinline__ void store_out(void* out, int odt, int h, float v) {
+    if (odt == WISP_DT_F32)
+        reinterpret_cast<float*>(out)[h] = v;
+    else if (odt == WISP_DT_F16)
+        reinterpret_cast<__half*>(out)[h] = __float2half_rn(v);
+    else
+        reinterpret_cast<uint16_t*>(out)[h] = f32_to_bf16(v);
+}
+
+// ---------------------------------------------------------------------------
+// x in any of the three float types. XT: WISP_DT_BF16 (the native operand),
+// WISP_DT_F16 or WISP_DT_F32. A non-bf16 x is carried as a bf16 hi/lo split,
+// x = hi + lo (hi = bf16(x), lo = bf16(x - hi)): exact for fp16 x, within
+// 2^-17 relative for fp32 x, so the kernels' dot products see x to ~17 bits
+// as the reference's fp32 loads of x do (kernels.py:51-52).
+// ---------------------------------------------------------------------------
+template <int XT>
+struct XWords {
+    static constexpr int n = XT == WISP_DT_F32 ? 32 : 16;  // dwords of 32 values
+};
+
+// raw dwords of the 32 x values of chunk c
+template <int XT>
+__device__ __forceinline__ void load_x_raw(const void* x, int c, uint32_t* w) {
+    const uint4* q = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(x) +
+                                                    (int64_t)c * 32 * (XT == WISP_DT_F32 ? 4 : 2));
+#pragma unroll
+    for (int i = 0; i < XWords<XT>::n / 4; ++i) {
+        const uint4 v = q[i];
+        w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    }
+}
+
+// raw dwords -> 16 bf16 hi dwords (+ 16 lo dwords for a non-bf16 x)
+template <int XT>
+__device__ __forceinline__ void split_x(const uint32_t* w, uint32_t* hi, uint32_t* lo) {
+    if constexpr (XT == WISP_DT_BF16) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) hi[i] = w[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float a, b;
+            if constexpr (XT == WISP_DT_F32) {
+                a = __uint_as_float(w[2 * i]);
+                b = __uint_as_float(w[2 * i + 1]);
+            } else {
+                a = half_lo_f(w[i]);
+                b = half_hi_f(w[i]);
+            }
+            hi[i] = pack_bf16x2(a, b);
+            lo[i] = pack_bf16x2(a - bf16_lo(hi[i]), b - bf16_hi(hi[i]));
+        }
+    }
+}
+
 
 // slot id from the meta buffer: -1 unless an exact integer in [0, nslots)
 __device__ __forceinline__ int slot_from(float f, int nslots) {
@@ -76,18 +135,22 @@ __device__ __forceinline__ void write_act(uint32_t* act, int j, int I, int r, fl
     a16[2 * (16 + P) + half] = lo;
 }
 
-// x operand of chunk c: pairs, sum of stored values, sum of true values
-template <int BITS>
-__device__ __forceinline__ void load_x_operand(const uint16_t* x, int c, uint32_t* xp, float& vsum, float& xsum) {
-    const uint4* xq = reinterpret_cast<const uint4*>(x + 32 * c);
-    uint32_t w[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint4 q = xq[i];
-        w[4 * i] = q.x; w[4 * i + 1] = q.y; w[4 * i + 2] = q.z; w[4 * i + 3] = q.w;
-    }
-    operand_pairs<BITS>(w, xp);
+// x operand of chunk c: hi (and lo) pairs, sum of stored values, sum of true values
+template <int BITS, int XT>
+__device__ __forceinline__ void load_x_operand(const void* x, int c, uint32_t* xp, uint32_t* xq, float& vsum,
+                                               float& xsum) {
+    uint32_t w[XWords<XT>::n], h[16], l[16];
+    load_x_raw<XT>(x, c, w);
+    split_x<XT>(w, h, l);
+    operand_pairs<BITS>(h, xp);
     operand_sums<BITS>(xp, vsum, xsum);
+    if constexpr (XT != WISP_DT_BF16) {
+        float vl, tl;
+        operand_pairs<BITS>(l, xq);
+        operand_sums<BITS>(xq, vl, tl);
+        vsum += vl;
+        xsum += tl;
+    }
 }
 
 // activation operand of segment s of expert j: hi and lo pairs and their sums
@@ -174,12 +237,13 @@ __device__ __forceinline__ int lanes_per_sum(int NQ) {
 //      16-bit load per lane and shares them with DPP broadcasts.
 // part: this wave's LDS scratch, T*2*64 floats.
 // ===========================================================================
-template <int BITS, int SPR_T, int T, bool QSC>
-// The lanes' x words (xw, chunk `seg` of x) are loaded by the caller before the
-// slot id is known; `ok` false (invalid slot id) reads slot 0 and writes NaN rows.
+template <int BITS, int SPR_T, int T, bool QSC, bool HL>
+// The lanes' x words (xw, chunk `seg` of x; HL: x = xw + xl as bf16 hi/lo) are
+// loaded by the caller before the slot id is known; `ok` false (invalid slot
+// id) reads slot 0 and writes NaN rows.
 __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __restrict__ base, bool ok,
-                                             const uint32_t (&xw)[16], uint32_t* __restrict__ act, int j, int r0,
-                                             float* part) {
+                                             const uint32_t (&xw)[16], const uint32_t (&xl)[16],
+                                             uint32_t* __restrict__ act, int j, int r0, float* part) {
     const int SPR = SPR_T ? SPR_T : L.spr_gu;
     const int RPI = 64 / SPR;
     const int lane = threadIdx.x & 63;
@@ -211,17 +275,30 @@ __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __re
             sv[t][3 % (QSC ? 1 : 4)] = mn[L.NGM + gidx];
         }
     }
-    uint32_t xp[16];
+    uint32_t xp[16], xq[HL ? 16 : 1];
     operand_pairs<BITS>(xw, xp);
     float vs, xs;
     operand_sums<BITS>(xp, vs, xs);
+    if constexpr (HL) {
+        float vl, tl;
+        operand_pairs<BITS>(xl, xq);
+        operand_sums<BITS>(xq, vl, tl);
+        vs += vl;
+        xs += tl;
+    }
     const float bias = -kBiasF * vs;
     const uint32_t B = bias_vgpr();
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const bool ok = lane_on && (r0 + t * RPI + rr < L.I);
-        const float dg = chunk_dot<BITS>(cg[t], xp, bias, B);
-        const float du = chunk_dot<BITS>(cu[t], xp, bias, B);
+        float dg, du;
+        if constexpr (HL) {
+            dg = chunk_dot_hl<BITS>(cg[t], xp, xq, bias, B);
+            du = chunk_dot_hl<BITS>(cu[t], xp, xq, bias, B);
+        } else {
+            dg = chunk_dot<BITS>(cg[t], xp, bias, B);
+            du = chunk_dot<BITS>(cu[t], xp, bias, B);
+        }
         uint32_t s_g, m_g, s_u, m_u;
         if (QSC) {
             s_g = quad_bcast<0>(sv[t][0]);
@@ -273,10 +350,10 @@ __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __re
 // preloading, built with -amdgpu-kernarg-preload-count): the slot-id read and
 // the x loads need no kernel-argument fetch first, so the only memory round
 // trip before the weight loads is the slot id itself.
-template <int BITS, int SPR_T, int T, int NW, bool QSC>
+template <int BITS, int SPR_T, int T, int NW, bool QSC, int XT>
 __global__ __launch_bounds__(64 * NW) void k_gate_up(const float* __restrict__ meta,
                                                       const uint8_t* __restrict__ pool, int64_t slot_bytes,
-                                                      int nslots, const uint16_t* __restrict__ x,
+                                                      int nslots, const void* __restrict__ x,
                                                       uint32_t* __restrict__ act, const Layer L) {
     __shared__ float part[NW][T * 2 * 64];
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -285,27 +362,22 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up(const float* __restrict__ m
     // together; the scheduling barrier keeps every use (and so every wait) after them
     const float f = meta[j];
     const Layer Lc = L;
-    uint32_t xw[16];
-    {
-        const int seg = (threadIdx.x & 63) % (SPR_T ? SPR_T : Lc.spr_gu);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint4 q = reinterpret_cast<const uint4*>(x + 32 * seg)[i];
-            xw[4 * i] = q.x; xw[4 * i + 1] = q.y; xw[4 * i + 2] = q.z; xw[4 * i + 3] = q.w;
-        }
-    }
+    uint32_t xr[XWords<XT>::n];
+    load_x_raw<XT>(x, (threadIdx.x & 63) % (SPR_T ? SPR_T : Lc.spr_gu), xr);
     __builtin_amdgcn_sched_barrier(0);
     const int slot = __builtin_amdgcn_readfirstlane(slot_from(f, nslots));
     const bool ok = slot >= 0;
     const uint8_t* base = pool + (int64_t)(ok ? slot : 0) * slot_bytes;
     const int RPI = 64 / (SPR_T ? SPR_T : Lc.spr_gu);
     const int r0 = (blockIdx.x * NW + wv) * (T * RPI);
-    gate_up_rows<BITS, SPR_T, T, QSC>(Lc, base, ok, xw, act, j, r0, part[wv]);
+    uint32_t xw[16], xl[16];
+    split_x<XT>(xr, xw, xl);
+    gate_up_rows<BITS, SPR_T, T, QSC, XT != WISP_DT_BF16>(Lc, base, ok, xw, xl, act, j, r0, part[wv]);
 }
 
 // Kernel 1 (generic): any H, G; one wave per (row, expert).
-template <int BITS>
-__global__ __launch_bounds__(64) void k_gate_up_generic(const Layer L, const uint16_t* __restrict__ x,
+template <int BITS, int XT>
+__global__ __launch_bounds__(64) void k_gate_up_generic(const Layer L, const void* __restrict__ x,
                                                         uint32_t* __restrict__ act) {
     const int lane = threadIdx.x;
     const int r = blockIdx.x, j = blockIdx.y;
@@ -317,16 +389,24 @@ __global__ __launch_bounds__(64) void k_gate_up_generic(const Layer L, const uin
         const uint16_t* mn = sc + 3 * L.NGM;
         const uint32_t B = bias_vgpr();
         for (int c = lane; c < L.spr_gu; c += 64) {
-            uint32_t cg[BITS], cu[BITS], xp[16];
+            uint32_t cg[BITS], cu[BITS], xp[16], xq[16];
             const uint8_t* rp = base + (int64_t)r * L.rowb_gu + c * (4 * BITS);
             load_chunk<BITS>(rp, cg);
             load_chunk<BITS>(rp + L.nmb, cu);
             float vs, xs;
-            load_x_operand<BITS>(x, c, xp, vs, xs);
+            load_x_operand<BITS, XT>(x, c, xp, xq, vs, xs);
             const float bias = -kBiasF * vs;
             const int gidx = r * L.gpr_gu + (c * 32) / L.G;
-            pg += h2f(sc[gidx]) * chunk_dot<BITS>(cg, xp, bias, B) + h2f(mn[gidx]) * xs;
-            pu += h2f(sc[L.NGM + gidx]) * chunk_dot<BITS>(cu, xp, bias, B) + h2f(mn[L.NGM + gidx]) * xs;
+            float dg, du;
+            if constexpr (XT != WISP_DT_BF16) {
+                dg = chunk_dot_hl<BITS>(cg, xp, xq, bias, B);
+                du = chunk_dot_hl<BITS>(cu, xp, xq, bias, B);
+            } else {
+                dg = chunk_dot<BITS>(cg, xp, bias, B);
+                du = chunk_dot<BITS>(cu, xp, bias, B);
+            }
+            pg += h2f(sc[gidx]) * dg + h2f(mn[gidx]) * xs;
+            pu += h2f(sc[L.NGM + gidx]) * du + h2f(mn[L.NGM + gidx]) * xs;
         }
         pg = wave_sum(pg);
         pu = wave_sum(pu);
@@ -357,7 +437,7 @@ template <int BITS, int SPR_T, int T, bool WSUM, bool QSC>
 // yields NaN partials.
 __device__ __forceinline__ void down_rows(const Layer& L, const float* meta,
                                           const uint8_t* __restrict__ pool, int64_t slot_bytes, int nslots, int k,
-                                          int I, const uint32_t* __restrict__ act, uint16_t* __restrict__ out,
+                                          int I, const uint32_t* __restrict__ act, void* __restrict__ out,
                                           float* __restrict__ y, int h0, float* lds) {
     static_assert(!QSC || T % 2 == 0, "quad-shared scales cover two rows per load");
     const int SPR = SPR_T ? SPR_T : L.spr_dn;
@@ -481,7 +561,7 @@ __device__ __forceinline__ void down_rows(const Layer& L, const float* meta,
             if (h < L.H) {
                 float acc = 0.f;
                 for (int jj = 0; jj < k; ++jj) acc += rows[jj * RW + q];
-                out[h] = f32_to_bf16(acc);
+                store_out(out, L.odt, h, acc);
             }
         }
     }
@@ -494,50 +574,57 @@ template <int BITS, int SPR_T, int T, bool WSUM, bool QSC>
 // k_gate_up.
 __global__ __launch_bounds__(1024) void k_down(const float* meta, const uint8_t* __restrict__ pool,
                                                int64_t slot_bytes, int nslots, int k, int I,
-                                               const uint32_t* __restrict__ act, uint16_t* __restrict__ out,
+                                               const uint32_t* __restrict__ act, void* __restrict__ out,
                                                float* __restrict__ y, const Layer L) {
     extern __shared__ float lds[];
     const int RW = T * (64 / (SPR_T ? SPR_T : L.spr_dn));
     down_rows<BITS, SPR_T, T, WSUM, QSC>(L, meta, pool, slot_bytes, nslots, k, I, act, out, y, blockIdx.x * RW, lds);
 }
 
-// Kernel 2 (generic): any I, G; one workgroup (k waves) per output row.
+// Kernel 2 (generic): any I, G and k; one workgroup of min(k, 16) waves per
+// output row, wave w takes experts w, w + 16, ...; the k expert sums meet in
+// LDS (dynamic, k floats) and are combined in expert order.
 template <int BITS, bool WSUM>
 __global__ __launch_bounds__(1024) void k_down_generic(const Layer L, const uint32_t* __restrict__ act,
-                                                       uint16_t* __restrict__ out, float* __restrict__ y) {
-    __shared__ float rows[16];
+                                                       void* __restrict__ out, float* __restrict__ y) {
+    extern __shared__ float rows[];
     const int lane = threadIdx.x & 63;
-    const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = blockDim.x >> 6;
     const int h = blockIdx.x;
-    const int slot = __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots));
-    float v = 0.f;
-    if (slot >= 0) {
-        const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
-        const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb) + 2 * L.NGM;
-        const uint16_t* mn = sc + 3 * L.NGM;
-        const uint32_t B = bias_vgpr();
-        for (int c = lane; c < L.spr_dn; c += 64) {
-            uint32_t cd[BITS], AH[16], AL[16];
-            load_chunk<BITS>(base + 2 * L.nmb + (int64_t)h * L.rowb_dn + c * (4 * BITS), cd);
-            float vs, as;
-            load_act_operand<BITS>(act, j, L.I, c, AH, AL, vs, as);
-            const int gidx = h * L.gpr_dn + (c * 32) / L.G;
-            v += h2f(sc[gidx]) * chunk_dot_hl<BITS>(cd, AH, AL, -kBiasF * vs, B) + h2f(mn[gidx]) * as;
+    for (int j = w; j < L.k; j += nw) {
+        const int slot = __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots));
+        float v = 0.f;
+        if (slot >= 0) {
+            const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
+            const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb) + 2 * L.NGM;
+            const uint16_t* mn = sc + 3 * L.NGM;
+            const uint32_t B = bias_vgpr();
+            for (int c = lane; c < L.spr_dn; c += 64) {
+                uint32_t cd[BITS], AH[16], AL[16];
+                load_chunk<BITS>(base + 2 * L.nmb + (int64_t)h * L.rowb_dn + c * (4 * BITS), cd);
+                float vs, as;
+                load_act_operand<BITS>(act, j, L.I, c, AH, AL, vs, as);
+                const int gidx = h * L.gpr_dn + (c * 32) / L.G;
+                v += h2f(sc[gidx]) * chunk_dot_hl<BITS>(cd, AH, AL, -kBiasF * vs, B) + h2f(mn[gidx]) * as;
+            }
+            v = wave_sum(v);
+        } else {
+            v = __builtin_nanf("");
         }
-        v = wave_sum(v);
-    } else {
-        v = __builtin_nanf("");
+        if (WSUM) {
+            if (lane == 0) rows[j] = v;
+        } else if (lane == 0) {
+            y[(int64_t)j * L.H + h] = v;
+        }
     }
     if (WSUM) {
-        if (lane == 0) rows[j] = v;
         __syncthreads();
         if (threadIdx.x == 0) {
             float acc = 0.f;
             for (int jj = 0; jj < L.k; ++jj) acc += L.meta[L.k + jj] * rows[jj];
-            out[h] = f32_to_bf16(acc);
+            store_out(out, L.odt, h, acc);
         }
-    } else if (lane == 0) {
-        y[(int64_t)j * L.H + h] = v;
     }
 }
 
@@ -561,7 +648,7 @@ static int make_layer(Layer& L, const uint8_t* pool, int64_t slot_bytes, int64_t
                       int64_t H, int64_t I, int bits, int64_t group) {
     if (!pool || !meta) return fail_inval("null pool or meta");
     if (!(bits == 4 || bits == 3 || bits == 2)) return fail_inval("bits must be 4, 3 or 2 for the fused kernels");
-    if (k < 1 || k > 16) return fail_inval("k must be in [1, 16]");
+    if (k < 1 || k > WISP_MAX_K) return fail_inval("k must be in [1, WISP_MAX_K = 8192]");
     if (H <= 0 || I <= 0 || group <= 0 || H % group || I % group)
         return fail_inval("H and I must be positive multiples of group (kernels.py:118)");
     if (group % 32) return fail_inval("group must be a multiple of 32");
@@ -593,44 +680,53 @@ static int make_layer(Layer& L, const uint8_t* pool, int64_t slot_bytes, int64_t
     L.gsh = (cpg & (cpg - 1)) ? -1 : __builtin_ctz(cpg);
     L.spr_gu = (int)(H / 32);
     L.spr_dn = (int)(I / 32);
+    L.odt = WISP_DT_BF16;
     return WISP_OK;
 }
 
-template <int BITS, int SPR, int T, int NW, bool QSC>
-static void launch_gu(const Layer& L, const uint16_t* x, uint32_t* act, hipStream_t st) {
+static bool valid_dtype(int dt) { return dt == WISP_DT_BF16 || dt == WISP_DT_F16 || dt == WISP_DT_F32; }
+
+template <int BITS, int SPR, int T, int NW, bool QSC, int XT>
+static void launch_gu(const Layer& L, const void* x, uint32_t* act, hipStream_t st) {
     const int RPI = 64 / L.spr_gu;
     const int rows_wg = NW * T * RPI;
     const dim3 grid((L.I + rows_wg - 1) / rows_wg, L.k);
-    hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW, QSC>), grid, dim3(64 * NW), 0, st, L.meta, L.pool, L.slot_bytes,
-                       L.nslots, x, act, L);
+    hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW, QSC, XT>), grid, dim3(64 * NW), 0, st, L.meta, L.pool,
+                       L.slot_bytes, L.nslots, x, act, L);
 }
 
-template <int BITS>
-static int gate_up_bits(const Layer& L, const uint16_t* x, uint32_t* act, hipStream_t st) {
+template <int BITS, int XT>
+static int gate_up_bits(const Layer& L, const void* x, uint32_t* act, hipStream_t st) {
     if (L.spr_gu > 64 || L.gsh < 0) {
-        hipLaunchKernelGGL((k_gate_up_generic<BITS>), dim3(L.I, L.k), dim3(64), 0, st, L, x, act);
+        hipLaunchKernelGGL((k_gate_up_generic<BITS, XT>), dim3(L.I, L.k), dim3(64), 0, st, L, x, act);
         return check_launch("k_gate_up_generic");
     }
     if (L.spr_gu != 64 || L.gsh < 2) {
-        launch_gu<BITS, 0, 2, 4, false>(L, x, act, st);
+        launch_gu<BITS, 0, 2, 4, false, XT>(L, x, act, st);
         return check_launch("k_gate_up");
     }
-    const Tuning& tu = tuning();
-#define WISP_GU(TT, WW)                                      \
-    if (tu.gu_rows == TT && tu.gu_waves == WW) {             \
-        launch_gu<BITS, 64, TT, WW, (bool)WISP_QSC>(L, x, act, st);    \
-        return check_launch("k_gate_up");                    \
+    if constexpr (XT != WISP_DT_BF16) {
+        // fp16 / fp32 x: the default launch shape only
+        launch_gu<BITS, 64, 2, 4, (bool)WISP_QSC, XT>(L, x, act, st);
+        return check_launch("k_gate_up");
+    } else {
+        const Tuning& tu = tuning();
+#define WISP_GU(TT, WW)                                                 \
+    if (tu.gu_rows == TT && tu.gu_waves == WW) {                        \
+        launch_gu<BITS, 64, TT, WW, (bool)WISP_QSC, XT>(L, x, act, st); \
+        return check_launch("k_gate_up");                               \
     }
-    WISP_GU(2, 4)
-    WISP_GU(4, 4)
-    WISP_GU(8, 4)
-    WISP_GU(1, 4)
-    WISP_GU(4, 2)
-    WISP_GU(2, 8)
-    WISP_GU(4, 1)
-    WISP_GU(8, 1)
+        WISP_GU(2, 4)
+        WISP_GU(4, 4)
+        WISP_GU(8, 4)
+        WISP_GU(1, 4)
+        WISP_GU(4, 2)
+        WISP_GU(2, 8)
+        WISP_GU(4, 1)
+        WISP_GU(8, 1)
 #undef WISP_GU
-    return fail_inval("unsupported tuning (gu_rows, gu_waves)");
+        return fail_inval("unsupported tuning (gu_rows, gu_waves)");
+    }
 }
 
 // dynamic LDS of the fast kernel 2 with T row iterations (see down_rows)
@@ -640,7 +736,7 @@ static size_t dn_lds_bytes(const Layer& L, int T) {
 }
 
 template <int BITS, int SPR, int T, bool WSUM, bool QSC>
-static void launch_dn(const Layer& L, const uint32_t* act, uint16_t* out, float* y, hipStream_t st) {
+static void launch_dn(const Layer& L, const uint32_t* act, void* out, float* y, hipStream_t st) {
     const int RW = T * (64 / L.spr_dn);
     const size_t lds = dn_lds_bytes(L, T);
     hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM, QSC>), dim3((L.H + RW - 1) / RW), dim3(64 * L.k), lds, st, L.meta,
@@ -648,11 +744,14 @@ static void launch_dn(const Layer& L, const uint32_t* act, uint16_t* out, float*
 }
 
 template <int BITS, bool WSUM>
-static int down_bits(const Layer& L, const uint32_t* act, uint16_t* out, float* y, hipStream_t st) {
-    // the fast path stages k*I activation dwords in LDS: keep the whole LDS within 64 KB
+static int down_bits(const Layer& L, const uint32_t* act, void* out, float* y, hipStream_t st) {
+    // the fast path has one wave per expert (k <= 16) and stages k*I activation
+    // dwords in LDS: keep the whole LDS within 64 KB
     const bool tuned = L.spr_dn == 24 && L.gsh >= 2;
-    if (L.spr_dn > 64 || L.gsh < 0 || dn_lds_bytes(L, tuned ? tuning().dn_iters : 4) > 65536) {
-        hipLaunchKernelGGL((k_down_generic<BITS, WSUM>), dim3(L.H), dim3(64 * L.k), 0, st, L, act, out, y);
+    if (L.k > 16 || L.spr_dn > 64 || L.gsh < 0 || dn_lds_bytes(L, tuned ? tuning().dn_iters : 4) > 65536) {
+        const int nw = L.k < 16 ? L.k : 16;
+        hipLaunchKernelGGL((k_down_generic<BITS, WSUM>), dim3(L.H), dim3(64 * nw), WSUM ? sizeof(float) * L.k : 0, st,
+                           L, act, out, y);
         return check_launch("k_down_generic");
     }
     if (!tuned) {
@@ -669,51 +768,26 @@ static int down_bits(const Layer& L, const uint32_t* act, uint16_t* out, float* 
     return check_launch("k_down");
 }
 
-// ---------------------------------------------------------------------------
-// single-launch layer
-// ---------------------------------------------------------------------------
-}  // namespace wisp
-
-using namespace wisp;
-
-extern "C" int64_t wisp_act_bytes(int k, int64_t I) {
-    if (k < 1 || I <= 0) return -1;
-    return (int64_t)k * I * 4;
-}
-
-extern "C" int wisp_moe_gate_up(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
-                                const uint16_t* x, int64_t H, int64_t I, int bits, int64_t group, uint32_t* act,
-                                void* stream) {
-    clear_error();
-    Layer L;
-    const int rc = make_layer(L, pool, slot_bytes, nslots, meta, k, H, I, bits, group);
-    if (rc) return rc;
-    if (!x || !act) return fail_inval("null x or act");
-    if (!aligned(x, 16) || !aligned(act, 16)) {
-        set_error("x and act must be 16-byte aligned");
-        return WISP_EALIGN;
-    }
-    hipStream_t st = (hipStream_t)stream;
+template <int XT>
+static int gate_up_xt(const Layer& L, int bits, const void* x, uint32_t* act, hipStream_t st) {
     switch (bits) {
-    case 4: return gate_up_bits<4>(L, x, act, st);
-    case 3: return gate_up_bits<3>(L, x, act, st);
-    default: return gate_up_bits<2>(L, x, act, st);
+    case 4: return gate_up_bits<4, XT>(L, x, act, st);
+    case 3: return gate_up_bits<3, XT>(L, x, act, st);
+    default: return gate_up_bits<2, XT>(L, x, act, st);
     }
 }
 
-static int down_common(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
-                       const uint32_t* act, int64_t H, int64_t I, int bits, int64_t group, uint16_t* out, float* y,
-                       void* stream) {
-    clear_error();
-    Layer L;
-    const int rc = make_layer(L, pool, slot_bytes, nslots, meta, k, H, I, bits, group);
-    if (rc) return rc;
-    if (!act) return fail_inval("null act");
-    if (!aligned(act, 16)) {
-        set_error("act must be 16-byte aligned");
-        return WISP_EALIGN;
+// kernel 1 of a validated layer
+static int gate_up_launch(const Layer& L, int bits, const void* x, int x_dtype, uint32_t* act, hipStream_t st) {
+    switch (x_dtype) {
+    case WISP_DT_F16: return gate_up_xt<WISP_DT_F16>(L, bits, x, act, st);
+    case WISP_DT_F32: return gate_up_xt<WISP_DT_F32>(L, bits, x, act, st);
+    default: return gate_up_xt<WISP_DT_BF16>(L, bits, x, act, st);
     }
-    hipStream_t st = (hipStream_t)stream;
+}
+
+// kernel 2 of a validated layer: weighted sum into out (L.odt) when out, else per-expert y
+static int down_launch(const Layer& L, int bits, const uint32_t* act, void* out, float* y, hipStream_t st) {
     if (out) {
         switch (bits) {
         case 4: return down_bits<4, true>(L, act, out, nullptr, st);
@@ -728,26 +802,78 @@ static int down_common(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, 
     }
 }
 
+static int check_x(const void* x, int x_dtype) {
+    if (!x) return fail_inval("null x");
+    if (!valid_dtype(x_dtype)) return fail_inval("x_dtype must be WISP_DT_BF16, WISP_DT_F16 or WISP_DT_F32");
+    if (!aligned(x, 16)) {
+        set_error("x must be 16-byte aligned");
+        return WISP_EALIGN;
+    }
+    return WISP_OK;
+}
+
+static int check_act(const void* act) {
+    if (!act) return fail_inval("null act");
+    if (!aligned(act, 16)) {
+        set_error("act must be 16-byte aligned");
+        return WISP_EALIGN;
+    }
+    return WISP_OK;
+}
+
+}  // namespace wisp
+
+using namespace wisp;
+
+extern "C" int64_t wisp_act_bytes(int k, int64_t I) {
+    if (k < 1 || I <= 0) return -1;
+    return (int64_t)k * I * 4;
+}
+
+extern "C" int wisp_moe_gate_up(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
+                                const void* x, int x_dtype, int64_t H, int64_t I, int bits, int64_t group,
+                                uint32_t* act, void* stream) {
+    clear_error();
+    Layer L;
+    int rc = make_layer(L, pool, slot_bytes, nslots, meta, k, H, I, bits, group);
+    if (!rc) rc = check_x(x, x_dtype);
+    if (!rc) rc = check_act(act);
+    if (rc) return rc;
+    return gate_up_launch(L, bits, x, x_dtype, act, (hipStream_t)stream);
+}
+
 extern "C" int wisp_moe_down_sum(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
-                                 const uint32_t* act, int64_t H, int64_t I, int bits, int64_t group, uint16_t* out,
-                                 void* stream) {
+                                 const uint32_t* act, int64_t H, int64_t I, int bits, int64_t group, void* out,
+                                 int out_dtype, void* stream) {
+    clear_error();
+    Layer L;
+    int rc = make_layer(L, pool, slot_bytes, nslots, meta, k, H, I, bits, group);
+    if (!rc) rc = check_act(act);
+    if (rc) return rc;
     if (!out) return fail_inval("null out");
-    return down_common(pool, slot_bytes, nslots, meta, k, act, H, I, bits, group, out, nullptr, stream);
+    if (!valid_dtype(out_dtype)) return fail_inval("out_dtype must be WISP_DT_BF16, WISP_DT_F16 or WISP_DT_F32");
+    L.odt = out_dtype;
+    return down_launch(L, bits, act, out, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int wisp_moe_down(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
                              const uint32_t* act, int64_t H, int64_t I, int bits, int64_t group, float* y,
                              void* stream) {
+    clear_error();
+    Layer L;
+    int rc = make_layer(L, pool, slot_bytes, nslots, meta, k, H, I, bits, group);
+    if (!rc) rc = check_act(act);
+    if (rc) return rc;
     if (!y) return fail_inval("null y");
-    return down_common(pool, slot_bytes, nslots, meta, k, act, H, I, bits, group, nullptr, y, stream);
+    return down_launch(L, bits, act, nullptr, y, (hipStream_t)stream);
 }
 
 extern "C" int wisp_moe_decode(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
-                               const uint16_t* x, int64_t H, int64_t I, int bits, int64_t group, uint32_t* act,
-                               uint16_t* out, void* stream) {
-    const int rc = wisp_moe_gate_up(pool, slot_bytes, nslots, meta, k, x, H, I, bits, group, act, stream);
+                               const void* x, int x_dtype, int64_t H, int64_t I, int bits, int64_t group,
+                               uint32_t* act, void* out, int out_dtype, void* stream) {
+    const int rc = wisp_moe_gate_up(pool, slot_bytes, nslots, meta, k, x, x_dtype, H, I, bits, group, act, stream);
     if (rc) return rc;
-    return wisp_moe_down_sum(pool, slot_bytes, nslots, meta, k, act, H, I, bits, group, out, stream);
+    return wisp_moe_down_sum(pool, slot_bytes, nslots, meta, k, act, H, I, bits, group, out, out_dtype, stream);
 }
 
 extern "C" int wisp_act_read(const uint32_t* act, int k, int64_t I, int bits, float* a, void* stream) {

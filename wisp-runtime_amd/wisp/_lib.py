@@ -15,9 +15,11 @@ import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
 
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_ROOT, "lib", "libwisp_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 WISP_OK, WISP_EINVAL, WISP_EALIGN = 0, -1, -2
+WISP_DT_BF16, WISP_DT_F16, WISP_DT_F32 = 0, 1, 2
+WISP_MAX_K = 8192
 
 _i64, _i32, _vp, _f64 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_double
 
@@ -31,10 +33,10 @@ SIGNATURES = {
     "wisp_pack": (_i32, [_vp, _i64, _i32, _vp, _vp]),
     "wisp_unpack": (_i32, [_vp, _i64, _i32, _vp, _vp]),
     "wisp_dequant": (_i32, [_vp, _i64, _vp, _i64, _i64, _i64, _i32, _i64, _vp, _vp]),
-    "wisp_moe_gate_up": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp]),
-    "wisp_moe_down_sum": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp]),
+    "wisp_moe_gate_up": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i32, _i64, _i64, _i32, _i64, _vp, _vp]),
+    "wisp_moe_down_sum": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _i32, _vp]),
     "wisp_moe_down": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp]),
-    "wisp_moe_decode": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp, _vp]),
+    "wisp_moe_decode": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i32, _i64, _i64, _i32, _i64, _vp, _vp, _i32, _vp]),
     "wisp_rope_decode": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "wisp_attn_ws_bytes": (_i64, [_i32, _i32, _i32]),
     "wisp_attn_decode": (_i32, [_vp, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, ctypes.c_float, _vp, _vp, _vp]),
@@ -83,6 +85,8 @@ SIGNATURES = {
     "wisp_cache_resize": (_i32, [_vp, _i64]),
     "wisp_set_tuning": (_i32, [_i32, _i32, _i32]),
     "wisp_act_read": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp]),
+    "wisp_probe_empty": (_i32, [_vp]),
+    "wisp_probe_read": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -22,13 +22,28 @@ import torch
 from . import _lib
 
 
-def _prep_x(x: torch.Tensor) -> torch.Tensor:
-    if x.dtype != torch.bfloat16:
-        raise TypeError(f"x must be bfloat16 (got {x.dtype})")
+_X_DTYPES = {torch.bfloat16: _lib.WISP_DT_BF16, torch.float16: _lib.WISP_DT_F16, torch.float32: _lib.WISP_DT_F32}
+
+
+def _prep_x(x: torch.Tensor, dtypes=(torch.bfloat16,)) -> torch.Tensor:
+    if x.dtype not in dtypes:
+        raise TypeError(f"x must be one of {dtypes} (got {x.dtype})")
     x = x.reshape(-1).contiguous()
     if x.data_ptr() % 16:
         x = x.clone()
     return x
+
+
+def _prep_x_any(x: torch.Tensor):
+    """x of any float dtype, as the reference kernels load it (`.to(tl.float32)`,
+    kernels.py:51-52): bf16, fp16 and fp32 go to the kernels as they are, float64 is
+    rounded to fp32 first. Returns (x, its WISP_DT_* code)."""
+    if not x.is_floating_point():
+        raise TypeError(f"x must be a float tensor (got {x.dtype})")
+    if x.dtype not in _X_DTYPES:
+        x = x.to(torch.float32)
+    x = _prep_x(x, tuple(_X_DTYPES))
+    return x, _X_DTYPES[x.dtype]
 
 
 def _check_pool(pool: torch.Tensor) -> None:
@@ -39,30 +54,32 @@ def _check_pool(pool: torch.Tensor) -> None:
 
 def _layer(pool, meta, x, k, n, H, I, group, bits):
     assert H % group == 0 and I % group == 0 and n == H * I
+    assert 1 <= k <= _lib.WISP_MAX_K, f"k must be in [1, {_lib.WISP_MAX_K}]"
     _check_pool(pool)
     dev = _lib.require_gpu(pool, meta, x, what=f"moe_decode (bits={bits})")
     assert meta.dtype == torch.float32 and meta.numel() >= 2 * k, "meta must be float32 [2k]"
     meta = meta.contiguous()
-    x = _prep_x(x)
-    assert x.numel() == H
+    xk, xdt = _prep_x_any(x)
+    assert xk.numel() == H
     act = torch.empty((k, I), dtype=torch.float32, device=dev).view(torch.int32)
-    return dev, meta, x, act
+    return dev, meta, xk, xdt, act
 
 
 def moe_decode_fast(pool, meta, x, k, n, H, I, bits, group=128):
     """One batch-1 MoE layer: gate_up+SiLU, then down + routing-weighted sum, as two
     kernel launches (kernels.py:197-202). meta: float32 [2k] on the GPU =
-    [slot_0..slot_{k-1}, w_0..w_{k-1}]. Returns [H] in x.dtype."""
-    dev, meta, x, act = _layer(pool, meta, x, k, n, H, I, group, bits)
-    out = torch.empty((H,), dtype=x.dtype, device=dev)
+    [slot_0..slot_{k-1}, w_0..w_{k-1}]; x: [H] of any float dtype. Returns [H] in
+    x.dtype (the fp32 sum rounded once; float64 via fp32, as a Triton store would)."""
+    dev, meta, xk, xdt, act = _layer(pool, meta, x, k, n, H, I, group, bits)
+    out = torch.empty((H,), dtype=xk.dtype, device=dev)
     _lib.check(
         _lib.lib().wisp_moe_decode(
-            _lib.ptr(pool), pool.stride(0), pool.shape[0], _lib.ptr(meta), k, _lib.ptr(x), H, I, bits, group,
-            _lib.ptr(act), _lib.ptr(out), _lib.stream(dev),
+            _lib.ptr(pool), pool.stride(0), pool.shape[0], _lib.ptr(meta), k, _lib.ptr(xk), xdt, H, I, bits, group,
+            _lib.ptr(act), _lib.ptr(out), xdt, _lib.stream(dev),
         ),
         "moe_decode",
     )
-    return out
+    return out if out.dtype == x.dtype else out.to(x.dtype)
 
 
 def moe_decode_q4_fast(pool, meta, x, k, n, H, I, group=128, block_gu=32, block_down=8, num_warps=4):
@@ -84,15 +101,16 @@ def moe_decode_q2_fast(pool, meta, x, k, n, H, I, group=128, block_gu=8, block_d
 
 def moe_decode_q4(pool, slots, x, w, n, H, I, group=128, block_r=32, num_warps=4):
     """kernels.py:115-137. pool: [nslots, nbytes] uint8 (4-bit experts); slots: int64 [k];
-    x: [H] (bf16); w: [k] routing weights. Per-expert y[k, H] from the kernels, then the
+    x: [H] of any float dtype; w: [k] routing weights. Per-expert y[k, H] from the kernels, then the
     weighted sum in fp32 and the cast to x.dtype, as the reference does."""
     k = slots.numel()
     meta = torch.cat([slots.reshape(-1).to(torch.float32), w.reshape(-1).to(torch.float32)])
-    dev, meta, x, act = _layer(pool, meta, x, k, n, H, I, group, 4)
+    dev, meta, xk, xdt, act = _layer(pool, meta, x, k, n, H, I, group, 4)
     L = _lib.lib()
     st = _lib.stream(dev)
     args = (_lib.ptr(pool), pool.stride(0), pool.shape[0], _lib.ptr(meta), k)
-    _lib.check(L.wisp_moe_gate_up(*args, _lib.ptr(x), H, I, 4, group, _lib.ptr(act), st), "moe_decode_q4 gate_up")
+    _lib.check(L.wisp_moe_gate_up(*args, _lib.ptr(xk), xdt, H, I, 4, group, _lib.ptr(act), st),
+               "moe_decode_q4 gate_up")
     y = torch.empty((k, H), dtype=torch.float32, device=dev)
     _lib.check(L.wisp_moe_down(*args, _lib.ptr(act), H, I, 4, group, _lib.ptr(y), st), "moe_decode_q4 down")
     return (y * w.float().unsqueeze(1)).sum(0).to(x.dtype)
@@ -100,12 +118,12 @@ def moe_decode_q4(pool, slots, x, w, n, H, I, group=128, block_r=32, num_warps=4
 
 def gate_up_act(pool, meta, x, k, n, H, I, bits, group=128) -> torch.Tensor:
     """Kernel 1 alone, decoded to fp32 a [k, I] (for checks of the first kernel)."""
-    dev, meta, x, act = _layer(pool, meta, x, k, n, H, I, group, bits)
+    dev, meta, xk, xdt, act = _layer(pool, meta, x, k, n, H, I, group, bits)
     L = _lib.lib()
     st = _lib.stream(dev)
     _lib.check(
         L.wisp_moe_gate_up(
-            _lib.ptr(pool), pool.stride(0), pool.shape[0], _lib.ptr(meta), k, _lib.ptr(x), H, I, bits, group,
+            _lib.ptr(pool), pool.stride(0), pool.shape[0], _lib.ptr(meta), k, _lib.ptr(xk), xdt, H, I, bits, group,
             _lib.ptr(act), st,
         ),
         "gate_up",
