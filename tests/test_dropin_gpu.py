@@ -155,8 +155,9 @@ def test_pool_past_4gib_top_slots():
     nslots = 48 * 128
     rows = _pool(12, H, I, bits, group, seed=123)
     pool = torch.empty((nslots, nb), dtype=torch.uint8, device=DEV)
-    top = np.array([nslots - 1, nslots - 2, nslots - 3, 5000, 4100, 3000, 1714, 1713, 2, 0, 6100, 5555])
-    assert (top[:8] * nb > 2**32).all()
+    # the first eight slots start past 2^32 bytes (slot 1714 is the first), the rest straddle it
+    top = np.array([nslots - 1, nslots - 2, nslots - 3, 5000, 4100, 3000, 1714, 1800, 1713, 2, 0, 6100])
+    assert (top[:8] * nb > 2**32).all() and top[8] * nb < 2**32
     for i, s in enumerate(top):
         pool[int(s)].copy_(torch.from_numpy(rows[i]))
     rng = np.random.default_rng(124)

@@ -77,7 +77,11 @@ def _run_decode(pool, slots, gub, db, x, ex, sc, H, I, bits, group, meta_overrid
 @pytest.mark.parametrize("E,H,I,k,group", [(8, 64, 64, 2, 64),      # the reference's test shape
                                            (6, 256, 256, 4, 128),
                                            (5, 2880, 2880, 4, 128),  # gpt-oss-20b: down rows straddle groups
-                                           (4, 320, 160, 3, 32)])    # H != I (kernel-level), partial blocks
+                                           (4, 320, 160, 3, 32),     # H != I (kernel-level), partial blocks
+                                           (20, 96, 48, 12, 32),     # H % 64 == 32: a partial gate_up row block;
+                                                                     # k > 8: several batches of 8 experts
+                                           (18, 256, 256, 9, 128),
+                                           (18, 256, 256, 16, 128)])
 def test_gptoss_decode_matches_oracle(bits, E, H, I, k, group):
     pool, slots, gub, db, x, ex, sc = _gptoss_case(E, H, I, k, bits, group, seed=H + bits)
     got = _run_decode(pool, slots, gub, db, x, ex, sc, H, I, bits, group)

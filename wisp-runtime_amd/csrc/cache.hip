@@ -232,6 +232,7 @@ static int alloc_pool(Cache& c) {
     const hipError_t e = hipMalloc(&b->ptr, (size_t)(c.nslots * c.slot_bytes));
     if (e != hipSuccess) {
         delete b;
+        (void)hipGetLastError();  // consume it here: a later launch check must not report it
         return hip_fail(e, "hipMalloc(slot pool)");
     }
     c.pool = b;
