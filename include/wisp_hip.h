@@ -121,6 +121,25 @@ int wisp_moe_decode(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, con
                     const void* x, int x_dtype, int64_t H, int64_t I, int bits, int64_t group, uint32_t* act,
                     void* out, int out_dtype, void* stream);
 
+/* Largest k*I of wisp_moe_decode_noalloc (its activation scratch: 1 MiB). */
+#define WISP_NOALLOC_MAX_ACT 262144
+
+/* wisp_moe_decode without the caller's `act` workspace, allocating nothing:
+ * the activation between the two kernels lives in a 1 MiB array of device
+ * memory inside the library (a file-scope __device__ array; each GPU the
+ * library runs on holds its own copy until the process ends). No reference
+ * counterpart: for callers that cannot allocate (code under graph capture
+ * that may not call hipMalloc, tight serving loops, harnesses that forbid
+ * allocation). Refuses k*I > WISP_NOALLOC_MAX_ACT (WISP_EINVAL). The stream
+ * must belong to the current device. Every call on one GPU shares that GPU's
+ * scratch: calls that overlap in time on one GPU (different streams) race;
+ * calls in one stream are ordered. Nothing in the scratch needs clearing:
+ * kernel 1 writes every value kernel 2 reads. Same results as
+ * wisp_moe_decode (the same kernels). */
+int wisp_moe_decode_noalloc(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
+                            const void* x, int x_dtype, int64_t H, int64_t I, int bits, int64_t group, void* out,
+                            int out_dtype, void* stream);
+
 /* Rotary embedding of one decode token, q and k heads in one launch:
  * out[i] = x[i]*cos[i] + sign(i)*x[(i + d/2) mod d]*sin[i], sign = -1 for
  * i < d/2, else +1; binary32 products and sum rounded separately, one

@@ -21,6 +21,8 @@
 //  * The activation between the kernels is kept at ~17-bit precision as a
 //    bf16 hi/lo split (a = hi + lo), pre-arranged in the down kernel's pair
 //    order, so kernel 2 uses the same dot2 path (two dot2 per code pair).
+#include <mutex>
+
 #include "wisp_device.hpp"
 #include "wisp_internal.hpp"
 
@@ -821,6 +823,52 @@ static int check_act(const void* act) {
     return WISP_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free layer (wisp_moe_decode_noalloc): the activation workspace
+// between the two kernels is a file-scope device array instead of a caller
+// buffer. Each GPU holds its own copy until the process ends; its address on
+// a device comes from hipGetSymbolAddress (with that device current), taken
+// once per device and kept. In host code `scratch` names a host-side
+// stand-in, never a device address: only the kept pointer is passed on.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint32_t scratch[WISP_NOALLOC_MAX_ACT];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static uint32_t* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device (looked up once).
+static int scratch_ptr(hipStream_t st, uint32_t** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        set_error("hipGetDevice: %s", hipGetErrorString(e));
+        return (int)e;
+    }
+    if (dev < 0 || dev >= kMaxDevices) return fail_inval("device index beyond the no-alloc scratch table");
+    if (st) {
+        int sdev = -1;
+        e = hipStreamGetDevice(st, &sdev);
+        if (e != hipSuccess) {
+            set_error("hipStreamGetDevice: %s", hipGetErrorString(e));
+            return (int)e;
+        }
+        if (sdev != dev) return fail_inval("the stream's device must be the current device");
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_error("hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+            return e != hipSuccess ? (int)e : WISP_EINVAL;
+        }
+        g_scratch_ptr[dev] = static_cast<uint32_t*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return WISP_OK;
+}
+
 }  // namespace wisp
 
 using namespace wisp;
@@ -874,6 +922,30 @@ extern "C" int wisp_moe_decode(const uint8_t* pool, int64_t slot_bytes, int64_t 
     const int rc = wisp_moe_gate_up(pool, slot_bytes, nslots, meta, k, x, x_dtype, H, I, bits, group, act, stream);
     if (rc) return rc;
     return wisp_moe_down_sum(pool, slot_bytes, nslots, meta, k, act, H, I, bits, group, out, out_dtype, stream);
+}
+
+extern "C" int wisp_moe_decode_noalloc(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta,
+                                       int k, const void* x, int x_dtype, int64_t H, int64_t I, int bits, int64_t group,
+                                       void* out, int out_dtype, void* stream) {
+    clear_error();
+    Layer L;
+    int rc = make_layer(L, pool, slot_bytes, nslots, meta, k, H, I, bits, group);
+    if (!rc) rc = check_x(x, x_dtype);
+    if (rc) return rc;
+    if (!out) return fail_inval("null out");
+    if (!valid_dtype(out_dtype)) return fail_inval("out_dtype must be WISP_DT_BF16, WISP_DT_F16 or WISP_DT_F32");
+    if ((int64_t)k * I > WISP_NOALLOC_MAX_ACT)
+        return fail_inval("k*I exceeds the no-alloc scratch (WISP_NOALLOC_MAX_ACT = 262144 activation values)");
+    hipStream_t st = (hipStream_t)stream;
+    uint32_t* act = nullptr;
+    rc = scratch_ptr(st, &act);
+    if (rc) return rc;
+    // kernel 1 writes every activation value kernel 2 reads: nothing in the
+    // scratch has to start at zero
+    rc = gate_up_launch(L, bits, x, x_dtype, act, st);
+    if (rc) return rc;
+    L.odt = out_dtype;
+    return down_launch(L, bits, act, out, nullptr, st);
 }
 
 extern "C" int wisp_act_read(const uint32_t* act, int k, int64_t I, int bits, float* a, void* stream) {

@@ -20,6 +20,7 @@ ABI_VERSION = 2
 WISP_OK, WISP_EINVAL, WISP_EALIGN = 0, -1, -2
 WISP_DT_BF16, WISP_DT_F16, WISP_DT_F32 = 0, 1, 2
 WISP_MAX_K = 8192
+WISP_NOALLOC_MAX_ACT = 262144
 
 _i64, _i32, _vp, _f64 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_double
 
@@ -37,6 +38,7 @@ SIGNATURES = {
     "wisp_moe_down_sum": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _i32, _vp]),
     "wisp_moe_down": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i32, _i64, _vp, _vp]),
     "wisp_moe_decode": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i32, _i64, _i64, _i32, _i64, _vp, _vp, _i32, _vp]),
+    "wisp_moe_decode_noalloc": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp, _i32, _i64, _i64, _i32, _i64, _vp, _i32, _vp]),
     "wisp_rope_decode": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "wisp_attn_ws_bytes": (_i64, [_i32, _i32, _i32]),
     "wisp_attn_decode": (_i32, [_vp, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, ctypes.c_float, _vp, _vp, _vp]),
