@@ -150,14 +150,21 @@ def timed_steps(stream, warm, timed, steps: int):
     return e0.elapsed_time(e1) * 1e-3 / steps
 
 
+def setup_pass(W: Layers):
+    """Set-up, not a step: one eager layer on every pool with the last routing round (the
+    timed steps start at round 0), so module loading and the first touch of each pool's
+    pages happen before the warm-up steps, as in a decoder that runs every layer per token."""
+    with torch.cuda.stream(W.stream):
+        st = _lib.stream(W.dev)
+        for l in range(W.layers):
+            W.layer((ROUNDS - 1) * W.layers + l, st)
+    torch.cuda.synchronize()
+
+
 def measure(W: Layers, steps: int, warmup: int):
     """Seconds per layer (both kernels) and per kernel alone over exactly `steps` steps after
     `warmup` untimed ones: graph replays, HIP events on the replay stream."""
-    with torch.cuda.stream(W.stream):  # eager warm-up of the launches (module load, first-touch)
-        st = _lib.stream(W.dev)
-        for i in range(min(W.layers, max(warmup, 1))):
-            W.layer(i, st)
-    torch.cuda.synchronize()
+    setup_pass(W)
     res = dict(steps=steps, warmup=warmup)
     for name, body in (("layer", W.layer), ("gu", W.gate_up), ("dn", W.down)):
         warm = capture_steps(W.stream, body, 0, warmup) if warmup else []
@@ -204,6 +211,7 @@ def run_floor(a) -> dict:
               ("read_down_bytes_after_slot_read", reader(dn_b, True), dn_b),
               ("c2_layer", W.layer, gu_b + dn_b), ("c2_gate_up", W.gate_up, gu_b), ("c2_down", W.down, dn_b)]
     rows = {}
+    setup_pass(W)
     for name, body, nbytes in probes:
         with torch.cuda.stream(W.stream):
             st = _lib.stream(dev)
@@ -401,6 +409,71 @@ def summarize_stats(stats_csv: str, title: str, cmd: str, bench_line: str, top: 
                      f"{float(r['AverageNs']):.0f} | {r['MinNs']} | {r['MaxNs']} | {float(r['Percentage']):.2f} |")
     lines += ["", "bench.py's own line from the profiled process (the profiler adds per-dispatch overhead, so its "
               "times are not the figures of record):", "", "```", bench_line.strip(), "```"]
+    return "\n".join(lines) + "\n"
+
+
+FLOOR_PROBES = ("empty_kernel", "read_gate_up_bytes", "read_down_bytes", "read_gate_up_bytes_after_slot_read",
+                "read_down_bytes_after_slot_read", "c2_layer", "c2_gate_up", "c2_down")
+
+
+def summarize_floor(trace_csv: str, log: str, cmd: str) -> str:
+    """Markdown summary of a rocprofv3 --kernel-trace run of `bench.py --workload floor`: the
+    kernel durations of each probe's timed launches (the probes run in FLOOR_PROBES order,
+    each as warm-up then timed graph replays), beside the unprofiled-style in-graph times the
+    profiled process printed."""
+    import csv
+    import statistics as stt
+
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Dispatch_Id"]))
+
+    def kind(n):
+        return ("probe_empty" if "k_probe_empty" in n else "probe_read" if "k_probe_read" in n else
+                "k_gate_up" if "k_gate_up" in n else "k_down" if "k_down" in n else None)
+
+    runs = []  # consecutive dispatches of one kernel, split at any other kernel (e.g. the sleep before timing)
+    sep = True
+    for r in rows:
+        k = kind(r["Kernel_Name"])
+        if k is None:
+            sep = True
+            continue
+        d = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        if not sep and runs[-1][2] == r["Kernel_Name"]:
+            runs[-1][1].append(d)
+        else:
+            runs.append([k, [d], r["Kernel_Name"]])
+        sep = False
+    with open(log) as f:
+        res = json.loads([ln for ln in f if ln.startswith("{")][-1])
+    steps, warm = res["steps"], res["warmup"]
+    timed = [r for r in runs if len(r[1]) >= steps]
+    lines = ["# Floor probes beside the C2 layer, 4-bit (rocprofv3 kernel trace)", "",
+             "Command (from the repository root on the GPU box):", "", "```", cmd, "```", "",
+             f"Each probe runs {warm} warm-up then {steps} timed launches as graph replays over the 48 layer pools "
+             "(the C2 rotation). Kernel durations are the trace's end - start per dispatch of the timed replays; "
+             "the in-graph time is bench.py's HIP-event time per launch in the same profiled process (the "
+             "profiler serialises dispatches, so it is not the figure of record; the unprofiled figures are in "
+             "DESIGN's measurement section).", "",
+             "| probe | kernel | bytes | dispatches | median ns | mean ns | min ns | GB/s at mean |",
+             "|---|---|---|---|---|---|---|---|"]
+    names = [p for p in FLOOR_PROBES]
+    # the c2_layer probe alternates k_gate_up / k_down dispatches: one run of each per replay
+    i = 0
+    for name in names:
+        nbytes = res["floors"][name]["bytes"]
+        if name == "c2_layer":
+            continue
+        while i < len(runs) and len(runs[i][1]) < steps:
+            i += 1
+        if i >= len(runs):
+            break
+        k, v, full = runs[i]
+        mean = stt.mean(v[-steps:])
+        gbs = f"{nbytes / mean:.0f}" if nbytes else "—"
+        lines.append(f"| {name} | `{k}` | {nbytes} | {len(v[-steps:])} | {stt.median(v[-steps:]):.0f} | {mean:.0f} "
+                     f"| {min(v[-steps:])} | {gbs} |")
+        i += 1
+    lines += ["", "bench.py's line from the profiled process:", "", "```", json.dumps(res), "```"]
     return "\n".join(lines) + "\n"
 
 
@@ -818,6 +891,8 @@ def main():
                     help="write profiles/moe_prefill_c5_q4_sq_counters.md from two rocprofv3 --pmc passes per T")
     ap.add_argument("--summarize-stats", nargs=4, metavar=("STATS_CSV", "BENCH_LOG", "TITLE", "NAME"),
                     help="write profiles/NAME.md from a rocprofv3 --stats CSV (command text from --pmc-command)")
+    ap.add_argument("--summarize-floor", nargs=2, metavar=("TRACE_CSV", "BENCH_LOG"),
+                    help="write profiles/floor_c2_q4_kernel_trace.md from a rocprofv3 run of --workload floor")
     ap.add_argument("--summarize-trace", nargs=3, metavar=("TRACE_CSV", "STATS_CSV", "BENCH_JSON"),
                     help="write the kernel-trace summary under profiles/ from a rocprofv3 run of bench.py")
     a = ap.parse_args()
@@ -850,6 +925,13 @@ def main():
             bench_line = [ln for ln in f if ln.startswith("{")][-1]
         text = summarize_stats(a.summarize_stats[0], a.summarize_stats[2], a.pmc_command, bench_line)
         with open(os.path.join(PROFILES, a.summarize_stats[3] + ".md"), "w") as f:
+            f.write(text)
+        print(text)
+        return
+
+    if a.summarize_floor:
+        text = summarize_floor(a.summarize_floor[0], a.summarize_floor[1], a.pmc_command)
+        with open(os.path.join(PROFILES, f"floor_c2_q{a.bits}_kernel_trace.md"), "w") as f:
             f.write(text)
         print(text)
         return
@@ -941,7 +1023,8 @@ def main():
             "gate_up_bytes": gu_b,
             "down_bytes": dn_b,
             "timing": "HIP events on the replay stream around graph replays of exactly `steps` layer steps "
-                      "(pool i % 48); per-launch averages include the in-graph launch gaps",
+                      "(pool i % 48, routing round i // 48 % 8) after `warmup` untimed ones and one set-up "
+                      "layer per pool; per-launch averages include the in-graph launch gaps",
         },
         "roofline": {
             "bound": "hbm",
