@@ -580,7 +580,13 @@ __global__ __launch_bounds__(1024) void k_down(const float* meta, const uint8_t*
                                                float* __restrict__ y, const Layer L) {
     extern __shared__ float lds[];
     const int RW = T * (64 / (SPR_T ? SPR_T : L.spr_dn));
-    down_rows<BITS, SPR_T, T, WSUM, QSC>(L, meta, pool, slot_bytes, nslots, k, I, act, out, y, blockIdx.x * RW, lds);
+    // XCD-aware row blocks: the dispatcher deals workgroups to the 8 XCDs in turn, so
+    // workgroup b runs on XCD b % 8; give each XCD one contiguous range of row blocks,
+    // so the scale/min lines neighbouring blocks share are fetched into one L2 only
+    int rb = blockIdx.x;
+    const int G = gridDim.x;
+    if ((G & 7) == 0) rb = (rb & 7) * (G >> 3) + (rb >> 3);
+    down_rows<BITS, SPR_T, T, WSUM, QSC>(L, meta, pool, slot_bytes, nslots, k, I, act, out, y, rb * RW, lds);
 }
 
 // Kernel 2 (generic): any I, G and k; one workgroup of min(k, 16) waves per

@@ -1,115 +1,65 @@
-"""gpt-oss adapter (openai/gpt-oss-20b and -120b) on the WiSP expert store, cache and
-slot pool. Same interface as the reference's wisp/gptoss.py (gptoss.py:1-183).
+"""gpt-oss experts (openai/gpt-oss-20b and -120b) on this package's expert store, cache and
+slot pool. Reference interface: wisp/gptoss.py (mxfp4_to_bf16 :22-29, expert_w3 :32-37,
+PagedGptOssBlock :92-143).
 
-An expert is gate_up [H, 2I] (gate and up interleaved on the last axis), down [I, H],
-plus two biases. With I == H both halves of gate_up and down are n = H*I elements, so
-an expert fits the flat [3, n] layout [gate_up.flat[:n] | gate_up.flat[n:] | down.flat]
-(gptoss.py:32-37) and the store, cache and quantizer are reused unchanged; the biases
-stay on the GPU for all experts.
+Expert format. A gpt-oss expert is gate_up [H, 2I] (gate and up interleaved along the last
+axis), down [I, H], and bf16 biases gate_up [2I] and down [H]. gpt-oss has I == H, so each
+half of gate_up and the down matrix hold n = H*I elements, and an expert is stored in the
+flat [3, n] format every other expert of this package uses:
+    [ gate_up.flat[:n] | gate_up.flat[n:] | down.flat ]
+so the quantizer, store, cache and page kernel serve it unchanged. The biases of all
+experts stay on the GPU in the block.
 
-Execution of PagedGptOssBlock.forward (all on the GPU; there is no CPU path):
-  * one token, 4/3/2-bit experts: the three gfx950 decode kernels of
-    kernels.gptoss_decode on the slot pool (bf16 weights dequantized in registers, the
-    reference's bf16 rounding of every intermediate, one host sync per layer);
-  * otherwise (several tokens, 16/8-bit stores, decode-on-load): the reference's
-    dequantize-then-matmul path (bit-exact dequant kernel + bf16 GEMMs).
-MXFP4 checkpoint tensors are decoded by a HIP kernel (kernels.mxfp4_to_bf16).
+PagedGptOssBlock.forward:
+  * routing: router logits (with bias), the k largest, softmax over those k in the
+    activation dtype; the scores are returned beside the output, as transformers does;
+  * one token with 2/3/4-bit experts in the pool: the three gfx950 decode launches of
+    kernels.gptoss_decode (weights dequantized in registers, the reference's bf16
+    rounding of every intermediate);
+  * any other case (several tokens, 8/16-bit stores, decode-on-load): every routed
+    (token, expert) pair exactly once, grouped per expert by one stable sort of the routing;
+    experts are paged rt.chunk at a time and run as bf16 GEMMs on their bit-exactly
+    dequantized weights.
+Reading gpt-oss checkpoints (their MXFP4 safetensors) is outside this build's scope; the
+MXFP4 decode itself is a HIP kernel (kernels.mxfp4_to_bf16).
 """
 
 from __future__ import annotations
-
-import json
-import os
-import time
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .store import ExpertStore
-
-# e2m1 code -> value (gptoss.py:19)
+# e2m1 code -> value (gptoss.py:19); the decode kernel holds the same table
 FP4 = [+0.0, +0.5, +1.0, +1.5, +2.0, +3.0, +4.0, +6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
 
 
 def mxfp4_to_bf16(blocks, scales):
-    """gptoss.py:22-29: blocks [..., G, 16] uint8 (two fp4 per byte, low nibble first),
-    scales [..., G] uint8 (power-of-two exponents, bias 127) -> [..., G*32] bfloat16."""
-    from .kernels import mxfp4_to_bf16 as _k
+    """blocks [..., G, 16] uint8 (two e2m1 codes per byte, low nibble first), scales [..., G]
+    uint8 (power-of-two exponents, bias 127) -> [..., G*32] bfloat16, on the GPU."""
+    from .kernels import mxfp4_to_bf16 as decode
 
-    return _k(blocks, scales)
+    return decode(blocks, scales)
 
 
 def expert_w3(gate_up, down):
-    """gate_up [H, 2I], down [I, H] -> [3, n] (n = H*I), gptoss.py:32-37."""
-    H, I2 = gate_up.shape
-    n = H * (I2 // 2)
-    f = gate_up.reshape(-1)
-    return torch.stack([f[:n], f[n:], down.reshape(-1)])
+    """gate_up [H, 2I] and down [I, H] of one expert -> the flat [3, n] rows, n = H*I."""
+    half = gate_up.numel() // 2
+    flat = gate_up.reshape(-1)
+    return torch.stack([flat[:half], flat[half:], down.reshape(-1)])
 
 
-def _layer_tensors(get, has, l, E, device):
-    """Dequantized gate_up [E, H, 2I], down [E, I, H], biases, for one layer (MXFP4 or
-    plain bf16 checkpoints), gptoss.py:40-49."""
-    p = f"model.layers.{l}.mlp.experts."
-    if has(p + "gate_up_proj_blocks"):
-        gu = mxfp4_to_bf16(get(p + "gate_up_proj_blocks").to(device), get(p + "gate_up_proj_scales").to(device))
-        dn = mxfp4_to_bf16(get(p + "down_proj_blocks").to(device), get(p + "down_proj_scales").to(device))
-        gu, dn = gu.transpose(1, 2).contiguous(), dn.transpose(1, 2).contiguous()  # [E,out,K] -> [E,K,out]
-    else:
-        gu, dn = get(p + "gate_up_proj").to(device), get(p + "down_proj").to(device)
-    return gu, dn, get(p + "gate_up_proj_bias"), get(p + "down_proj_bias")
-
-
-def _reader(model_dir):
-    """Tensor getter over model.safetensors.index.json (gptoss.py:52-63)."""
-    from safetensors import safe_open
-
-    with open(os.path.join(model_dir, "model.safetensors.index.json")) as f:
-        idx = json.load(f)["weight_map"]
-    handles = {}
-
-    def get(name):
-        fn = idx[name]
-        if fn not in handles:
-            handles[fn] = safe_open(os.path.join(model_dir, fn), framework="pt", device="cpu")
-        return handles[fn].get_tensor(name)
-
-    return get, (lambda name: name in idx), idx
-
-
-def build_store(model_dir, cfg, bits, group=128, device="cuda", cache_dir=None, pin=True):
-    """All experts of a gpt-oss checkpoint, quantized on the GPU into an ExpertStore, cached
-    on disk as raw rows under cache_dir (gptoss.py:66-89)."""
-    L, E, H, I = cfg.num_hidden_layers, cfg.num_local_experts, cfg.hidden_size, cfg.intermediate_size
-    if H != I:
-        raise ValueError("the gpt-oss adapter needs intermediate_size == hidden_size (true for gpt-oss)")
-    n = H * I
-    st = ExpertStore(L, E, n, bits, group, pin)
-    path = None
-    if cache_dir and bits < 16:
-        os.makedirs(cache_dir, exist_ok=True)
-        path = os.path.join(cache_dir, f"store_gptoss_b{bits}_g{group}_{L}x{E}x{n}.u8")
-        if os.path.exists(path) and os.path.getsize(path) == st.host.numel():
-            st._load(path)
-            return st
-    get, has, _ = _reader(model_dir)
-    t0 = time.time()
-    for l in range(L):
-        gu, dn, _, _ = _layer_tensors(get, has, l, E, device)
-        for e in range(E):
-            st.put(l, e, expert_w3(gu[e], dn[e]), device)
-        del gu, dn
-        if l % 4 == 3 or l == L - 1:
-            print(f"[store] gpt-oss bits={bits} layer {l + 1}/{L}  {time.time() - t0:.0f}s", flush=True)
-    if path:
-        st._save(path)
-    return st
+def clamped_swiglu(gu, alpha: float, limit: float):
+    """gpt-oss's activation on interleaved gate/up columns (gptoss.py:120-122): gate clamped
+    from above at `limit`, up clamped to [-limit, limit], (up + 1) * gate * sigmoid(alpha*gate)."""
+    gate = torch.clamp(gu[..., 0::2], max=limit)
+    up = torch.clamp(gu[..., 1::2], -limit, limit)
+    return (up + 1) * (gate * torch.sigmoid(gate * alpha))
 
 
 class PagedGptOssBlock(nn.Module):
-    """Drop-in for GptOssMLP: the router stays resident, the experts are paged
-    (gptoss.py:92-143). Returns (output, router_scores) like transformers."""
+    """Drop-in for transformers' GptOssMLP: the router stays resident, the experts are paged
+    from the store. Returns (output [B, T, H], router scores [B*T, k])."""
 
     def __init__(self, router, layer_idx, rt, cfg, device="cuda"):
         super().__init__()
@@ -117,17 +67,15 @@ class PagedGptOssBlock(nn.Module):
         self.E, self.top_k = cfg.num_local_experts, cfg.num_experts_per_tok
         self.H, self.I = cfg.hidden_size, cfg.intermediate_size
         self.alpha, self.limit = 1.702, float(getattr(cfg, "swiglu_limit", 7.0))
-        self.register_buffer(
-            "gub", torch.zeros(self.E, 2 * self.I, dtype=torch.bfloat16, device=device), persistent=False
-        )
-        self.register_buffer("db", torch.zeros(self.E, self.H, dtype=torch.bfloat16, device=device), persistent=False)
+        bf = dict(dtype=torch.bfloat16, device=device)
+        self.register_buffer("gub", torch.zeros(self.E, 2 * self.I, **bf), persistent=False)
+        self.register_buffer("db", torch.zeros(self.E, self.H, **bf), persistent=False)
 
     def _act(self, gu):
-        """Clamped SwiGLU on interleaved gate/up (gptoss.py:120-122)."""
-        gate, up = gu[..., ::2].clamp(max=self.limit), gu[..., 1::2].clamp(min=-self.limit, max=self.limit)
-        return (up + 1) * (gate * torch.sigmoid(gate * self.alpha))
+        return clamped_swiglu(gu, self.alpha, self.limit)
 
     def _fused_ok(self, cache):
+        """Whether one token can take the fused decode kernels on this cache's pool."""
         st = cache.store
         return (st.bits in (2, 3, 4) and not cache.decode_on_load and self.H % 32 == 0 and self.I % 16 == 0
                 and st.group % 32 == 0)
@@ -136,89 +84,67 @@ class PagedGptOssBlock(nn.Module):
         rt, cache = self.rt, self.rt.cache
         B, T, H = hidden_states.shape
         x = hidden_states.reshape(-1, H)
-        N, k, I = x.shape[0], self.top_k, self.I
-        logits = F.linear(x, self.router.weight, self.router.bias)
-        tv, ti = torch.topk(logits, k, dim=-1)
-        sc = F.softmax(tv, dim=1, dtype=tv.dtype)
-        base = self.layer_idx * self.E
+        k = self.top_k
+        top_logits, ids = torch.topk(F.linear(x, self.router.weight, self.router.bias), k, dim=-1)
+        scores = F.softmax(top_logits, dim=1, dtype=top_logits.dtype)
         rt.stats["layer_calls"] += 1
-        if N == 1 and self._fused_ok(cache):
-            row = torch.cat([ti.float(), sc.float()], 1).cpu()[0]  # the single sync of this layer
-            ex = row[:k].to(torch.int64)
-            if rt.recorder is not None:
-                rt.recorder.append((self.layer_idx, ex.view(1, k).numpy().copy()))
-            slots = cache.ensure([base + int(e) for e in ex])
-            meta = torch.cat([torch.tensor(slots, dtype=torch.float32), row[k:], row[:k]]).pin_memory()
-            meta = meta.to(x.device, non_blocking=True)
-            from .kernels import gptoss_decode
+        if x.shape[0] == 1 and self._fused_ok(cache):
+            y = self._decode_fused(x, ids, scores)
+        else:
+            y = self._grouped(x, ids, scores)
+        return y.view(B, T, H), scores
 
-            st = cache.store
-            y = gptoss_decode(cache.gpu, meta, x[0], self.gub, self.db, k, st.n, H, I, st.bits, st.group,
-                              self.alpha, self.limit).view(1, H)
-            rt.stats["gpu_experts"] += k
-        elif N == 1:  # decode through the reference's dequantize + 2 bmm path
-            if rt.recorder is not None:
-                rt.recorder.append((self.layer_idx, ti.cpu().numpy().copy()))
-            ex = ti[0].tolist()
-            slots = cache.ensure([base + e for e in ex])
-            W = cache.weights_batched(torch.as_tensor(slots, device=x.device))  # [k, 3, n]
-            # contiguous operands: bf16 batched products on strided views are avoided on this platform
-            xk = x.unsqueeze(0).expand(k, 1, H).contiguous()
-            gu = torch.bmm(xk, W[:, :2].reshape(k, H, 2 * I).contiguous()) + self.gub[ti[0]].unsqueeze(1)
-            out = torch.bmm(self._act(gu).contiguous(), W[:, 2].reshape(k, I, H).contiguous()) + self.db[ti[0]].unsqueeze(1)
-            y = (out[:, 0] * sc[0].unsqueeze(-1)).sum(0, keepdim=True)
-            rt.stats["gpu_experts"] += k
-        else:  # prefill: group tokens per expert, page in chunks
-            if rt.recorder is not None:
-                rt.recorder.append((self.layer_idx, ti.cpu().numpy().copy()))
-            y = torch.zeros_like(x)
-            uniq = torch.unique(ti).tolist()
-            for i in range(0, len(uniq), rt.chunk):
-                ce = uniq[i : i + rt.chunk]
-                Ws = cache.weights(cache.ensure([base + e for e in ce]))
-                for e, W3 in zip(ce, Ws, strict=True):
-                    tok, pos = torch.where(ti == e)
-                    gu = x[tok] @ torch.cat([W3[0], W3[1]]).view(H, 2 * I) + self.gub[e]
-                    out = self._act(gu) @ W3[2].view(I, H) + self.db[e]
-                    y.index_add_(0, tok, (out * sc[tok, pos, None]).to(x.dtype))
-                    rt.stats["gpu_experts"] += 1
-        return y.view(B, T, H), sc
+    def _record(self, ids_cpu):
+        if self.rt.recorder is not None:
+            self.rt.recorder.append((self.layer_idx, ids_cpu.numpy().copy()))
 
+    def _decode_fused(self, x, ids, scores):
+        """One token: page the k experts, then the three decode launches read them in place."""
+        rt, cache, k = self.rt, self.rt.cache, self.top_k
+        row = torch.cat([ids.float(), scores.float()], 1).cpu()[0]  # the layer's one host sync
+        ex = row[:k].to(torch.int64)
+        self._record(ex.view(1, k))
+        slots = cache.ensure([self.layer_idx * self.E + int(e) for e in ex])
+        # meta [slot ids | routing weights | expert ids] (the kernels index the biases by id)
+        meta = torch.cat([torch.tensor(slots, dtype=torch.float32), row[k:], row[:k]]).pin_memory()
+        meta = meta.to(x.device, non_blocking=True)
+        from .kernels import gptoss_decode
 
-def load_skeleton_gptoss(model_dir, rt, device="cuda"):
-    """Meta-init the transformers gpt-oss model, swap every MLP for a paged block, load all
-    non-expert tensors and the expert biases (gptoss.py:146-183)."""
-    from transformers import AutoConfig, AutoModelForCausalLM
-    from safetensors import safe_open
+        st = cache.store
+        y = gptoss_decode(cache.gpu, meta, x[0], self.gub, self.db, k, st.n, self.H, self.I, st.bits, st.group,
+                          self.alpha, self.limit)
+        rt.stats["gpu_experts"] += k
+        return y.view(1, self.H)
 
-    from .model import nbytes_of
-
-    cfg = AutoConfig.from_pretrained(model_dir)
-    with torch.device("meta"):
-        model = AutoModelForCausalLM.from_config(cfg, torch_dtype=torch.bfloat16)
-    blocks = []
-    for i, layer in enumerate(model.model.layers):
-        blk = PagedGptOssBlock(layer.mlp.router, i, rt, cfg, device)
-        layer.mlp = blk
-        blocks.append(blk)
-    get, has, idx = _reader(model_dir)
-    wanted = {k: f for k, f in idx.items() if ".mlp.experts." not in k}
-    sd, t0 = {}, time.time()
-    for fn in sorted(set(wanted.values())):
-        with safe_open(os.path.join(model_dir, fn), framework="pt", device=str(device)) as h:
-            for key in h.keys():
-                if key in wanted:
-                    sd[key] = h.get_tensor(key)
-    res = model.load_state_dict(sd, strict=False, assign=True)
-    bad = [key for key in res.missing_keys if "rotary" not in key]
-    if bad:
-        raise RuntimeError(f"missing keys: {bad[:5]}")
-    for l, blk in enumerate(blocks):
-        p = f"model.layers.{l}.mlp.experts."
-        blk.gub.copy_(get(p + "gate_up_proj_bias").to(device))
-        blk.db.copy_(get(p + "down_proj_bias").to(device))
-    model.model.rotary_emb = type(model.model.rotary_emb)(config=cfg, device=device)
-    model.eval()
-    print(f"[model] gpt-oss non-expert weights on {device}: {nbytes_of(model) / 2**30:.2f} GiB "
-          f"({time.time() - t0:.0f}s)", flush=True)
-    return model, cfg
+    def _grouped(self, x, ids, scores):
+        """Every (token, expert) pair once: pairs sorted by expert (stable, so tokens stay in
+        order within an expert), experts paged rt.chunk at a time and dequantized bit-exactly,
+        then per expert gate_up GEMM + bias, activation, down GEMM + bias, and the weighted rows
+        added to their tokens (the reference's bf16 rounding points, gptoss.py:131-143)."""
+        rt, cache, k, H, I = self.rt, self.rt.cache, self.top_k, self.H, self.I
+        N = x.shape[0]
+        flat = ids.reshape(-1)
+        order = torch.argsort(flat, stable=True)
+        experts, counts = torch.unique_consecutive(flat[order], return_counts=True)
+        experts, counts = experts.tolist(), counts.tolist()  # the layer's one host sync
+        self._record(ids.cpu())
+        tok_of_pair = order // k
+        w_of_pair = scores.reshape(-1)[order]
+        y = torch.zeros_like(x)
+        starts = [0]
+        for c in counts:
+            starts.append(starts[-1] + c)
+        base = self.layer_idx * self.E
+        for c0 in range(0, len(experts), max(1, rt.chunk)):
+            batch = experts[c0 : c0 + max(1, rt.chunk)]
+            W = cache.weights(cache.ensure([base + e for e in batch]))
+            for j, e in enumerate(batch):
+                lo, hi = starts[c0 + j], starts[c0 + j + 1]
+                tok = tok_of_pair[lo:hi]
+                w_gu = W[j][:2].reshape(H, 2 * I)  # contiguous rows of the [3, n] expert
+                w_dn = W[j][2].reshape(I, H)
+                gu = x.index_select(0, tok) @ w_gu + self.gub[e]
+                out = self._act(gu) @ w_dn + self.db[e]
+                y.index_add_(0, tok, (out * w_of_pair[lo:hi, None]).to(x.dtype))
+                rt.stats["gpu_experts"] += 1
+        return y

@@ -1,13 +1,12 @@
 """Qwen3-MoE model skeletons whose experts live in an ExpertStore: only the non-expert
-weights are on the GPU. Same entry points as the reference's wisp/model.py
-(load_skeleton, make_runtime, configure: model.py:20-95), plus a random-initialised
-skeleton for synthetic benchmarks (no checkpoint is needed).
+weights are on the GPU. Runtime set-up entry points as the reference's wisp/model.py
+(make_runtime, configure: model.py:58-95) and a random-initialised skeleton of any
+Qwen3-MoE config for the synthetic workloads. Loading a checkpoint (the reference's
+load_skeleton, model.py:20-55) is outside this build's scope: no checkpoint reaches this
+path, and the synthetic skeletons carry the same module structure.
 """
 
 from __future__ import annotations
-
-import json
-import os
 
 import torch
 import torch.nn as nn
@@ -38,43 +37,6 @@ def _fresh_rotary(model, cfg, device):
 def _gates_with_storage(model, cfg, device, dtype):
     for layer in model.model.layers:  # real storage, so attach() keeps a real router module
         layer.mlp.gate = nn.Linear(cfg.hidden_size, cfg.num_experts, bias=False, device=device, dtype=dtype)
-
-
-def load_skeleton(model_dir, rt, device="cuda", dtype=torch.bfloat16):
-    """Meta-initialise the model, attach paged MoE blocks, then load every NON-expert tensor of
-    the checkpoint in `model_dir` (model.safetensors.index.json or a single model.safetensors)
-    straight to `device` (model.py:20-55)."""
-    from safetensors import safe_open
-    from transformers import AutoConfig
-
-    cfg = AutoConfig.from_pretrained(model_dir)
-    if cfg.model_type == "gpt_oss":  # model.py:25-28
-        from .gptoss import load_skeleton_gptoss
-
-        return load_skeleton_gptoss(model_dir, rt, device)
-    model = _meta_model(cfg, dtype)
-    _gates_with_storage(model, cfg, device, dtype)
-    attach(model, rt)
-    index = os.path.join(model_dir, "model.safetensors.index.json")
-    if os.path.exists(index):
-        with open(index) as f:
-            where = json.load(f)["weight_map"]
-    else:
-        with safe_open(os.path.join(model_dir, "model.safetensors"), framework="pt", device="cpu") as h:
-            where = {k: "model.safetensors" for k in h.keys()}
-    wanted = {k: f for k, f in where.items() if ".mlp.experts." not in k}
-    sd = {}
-    for fn in sorted(set(wanted.values())):
-        with safe_open(os.path.join(model_dir, fn), framework="pt", device=str(device)) as h:
-            for k in h.keys():
-                if k in wanted:
-                    sd[k] = h.get_tensor(k).to(dtype)
-    missing = model.load_state_dict(sd, strict=False, assign=True)
-    bad = [k for k in missing.missing_keys if "rotary" not in k]
-    assert not bad, f"missing keys: {bad[:5]}"
-    _fresh_rotary(model, cfg, device)
-    model.eval()
-    return model, cfg
 
 
 @torch.no_grad()

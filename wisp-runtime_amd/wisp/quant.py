@@ -54,17 +54,23 @@ def _unpack(c: torch.Tensor, bits: int) -> torch.Tensor:
 
 
 @torch.no_grad()
-def quantize(w3: torch.Tensor, bits: int, group: int = 128) -> torch.Tensor:
-    """w3: [3, n] (any float dtype) on the GPU -> flat uint8 buffer (quant.py:60-73), bit-exact."""
+def quantize(w3: torch.Tensor, bits: int, group: int = 128, out: torch.Tensor | None = None) -> torch.Tensor:
+    """w3: [3, n] (any float dtype) on the GPU -> flat uint8 buffer (quant.py:60-73), bit-exact.
+    out: an optional contiguous uint8 device buffer of expert_nbytes(n, bits, group) to write."""
     dev = _lib.require_gpu(w3, what="quantize")
     if bits == 16:
-        return w3.to(torch.bfloat16).contiguous().view(torch.uint8).reshape(-1)
+        b = w3.to(torch.bfloat16).contiguous().view(torch.uint8).reshape(-1)
+        return b if out is None else out.copy_(b)
     w = w3.reshape(-1)
     if w.dtype not in (torch.float32, torch.bfloat16):
         w = w.float()  # the reference's .float(): exact for fp16, RTNE for fp64
     w = w.contiguous()
     n = w.numel() // 3
-    out = torch.empty(expert_nbytes(n, bits, group), dtype=torch.uint8, device=dev)
+    nb = expert_nbytes(n, bits, group)
+    if out is None:
+        out = torch.empty(nb, dtype=torch.uint8, device=dev)
+    assert out.dtype == torch.uint8 and out.is_contiguous() and out.numel() == nb and out.device == dev, (
+        "out must be a contiguous uint8 buffer of expert_nbytes on w3's device")
     _lib.check(
         _lib.lib().wisp_quantize(
             _lib.ptr(w), 1 if w.dtype == torch.bfloat16 else 0, n, bits, group, _lib.ptr(out), _lib.stream(dev)

@@ -1,110 +1,157 @@
-"""Host-side store of all experts, quantized to `bits`, in pinned RAM.
+"""The quantized experts of every layer, in pinned host memory: the source the expert cache
+pages from. Reference interface: wisp/store.py:12-110 (ExpertStore: L, E, n, bits, group,
+nbytes, host, pinned, total_gib, key, put, from_experts, _save, _load); same row format.
 
-Same interface as the reference's wisp/store.py (store.py:12-110): one row of
-expert_nbytes per (layer, expert), key = layer * n_experts + expert, built by
-quantizing on the GPU (this package's bit-exact kernels) and copying to the host,
-cached on disk as raw rows (`.u8`, row after row, no header).
+Layout. One row of `nbytes = expert_nbytes(n, bits, group)` bytes per (layer, expert) at
+row `key = layer * E + expert`, all rows in ONE page-locked allocation, so a cache miss is
+a single contiguous read of `nbytes` at `key * nbytes` -- by a DMA copy or by the GPU's
+page kernel reading the pinned rows directly over PCIe.
+
+Filling. `fill` quantizes experts on the GPU with the package's bit-exact kernel into a
+ring of device staging rows and copies each finished row to its pinned row on a side
+stream, so the PCIe transfer of one expert overlaps the quantization of the next ones;
+the host never waits per expert.
+
+Persistence. A `.u8` file is the rows back to back with no header (its size identifies the
+shape: L * E * nbytes). `save` writes through a temporary file renamed into place; both
+directions stream 64 MiB at a time, so a 15 GB store never needs a second copy in memory.
 """
 
 from __future__ import annotations
 
-import json
 import os
 import time
+from typing import Iterable
 
 import torch
 
 from .quant import expert_nbytes, quantize
+
+_IO_PIECE = 64 << 20  # bytes per read/write call of save/load
+
+
+def _host_rows(nrows: int, nbytes: int, pin: bool):
+    """[nrows, nbytes] uint8 on the host, page-locked when `pin` and the runtime allows it.
+    Returns (tensor, pinned). A pageable store still works with DMA copies; the page
+    kernel (ExpertCache copy="kernel") needs a pinned one."""
+    if pin:
+        try:
+            return torch.empty((nrows, nbytes), dtype=torch.uint8, pin_memory=True), True
+        except RuntimeError as err:
+            print(f"[store] page-locked allocation refused ({err}); the store is pageable", flush=True)
+    return torch.empty((nrows, nbytes), dtype=torch.uint8), False
 
 
 class ExpertStore:
     def __init__(self, n_layers, n_experts, n, bits, group=128, pin=True):
         self.L, self.E, self.n, self.bits, self.group = n_layers, n_experts, n, bits, group
         self.nbytes = expert_nbytes(n, bits, group)
-        t = time.time()
-        try:
-            self.host = torch.empty((n_layers * n_experts, self.nbytes), dtype=torch.uint8, pin_memory=pin)
-            self.pinned = pin
-        except RuntimeError as e:  # pinning refused: pageable rows still work, copies are slower
-            print(f"[store] pin_memory failed ({e}); using pageable memory", flush=True)
-            self.host = torch.empty((n_layers * n_experts, self.nbytes), dtype=torch.uint8)
-            self.pinned = False
-        print(f"[store] allocated {self.host.numel() / 2**30:.1f} GiB host (pinned={self.pinned}) "
-              f"in {time.time() - t:.1f}s", flush=True)
+        t0 = time.time()
+        self.host, self.pinned = _host_rows(n_layers * n_experts, self.nbytes, pin)
+        print(f"[store] {n_layers}x{n_experts} experts, {self.total_gib:.1f} GiB host (pinned={self.pinned}) "
+              f"in {time.time() - t0:.1f}s", flush=True)
 
     @property
-    def total_gib(self):
+    def total_gib(self) -> float:
         return self.host.numel() / 2**30
 
-    def key(self, l, e):
+    @property
+    def rows(self) -> int:
+        return self.host.shape[0]
+
+    def key(self, l: int, e: int) -> int:
+        """Row of expert e of layer l (the key the cache and the graph decoder use)."""
         return l * self.E + e
 
+    # ---------------------------------------------------------------- filling
     @torch.no_grad()
-    def put(self, l, e, w3, device):
-        """Quantize expert (l, e) from w3 [3, n] on `device` and store its row."""
-        buf = quantize(w3.to(device), self.bits, self.group)
-        self.host[self.key(l, e)].copy_(buf.cpu())
+    def fill(self, items: Iterable, device="cuda", ring: int = 4) -> int:
+        """Quantize experts into their rows. items: iterable of (key, w3) with w3 [3, n] of any
+        float dtype (on any device; moved to `device`). Up to `ring` rows are in flight: row i
+        is quantized into staging slot i % ring on the current stream, then copied to the pinned
+        row on a side stream that waits only for that quantization. Returns the row count."""
+        side = None
+        count = 0
+        for key, w3 in items:
+            if not 0 <= key < self.rows:
+                raise IndexError(f"expert row {key} outside the store's {self.rows} rows")
+            if side is None:  # device state on the first row (the quantizer has no CPU path)
+                dev = torch.device(device)
+                if dev.type != "cuda":
+                    raise RuntimeError("ExpertStore.fill quantizes on a ROCm device; no CPU path is provided")
+                if dev.index is None:
+                    dev = torch.device("cuda", torch.cuda.current_device())
+                compute = torch.cuda.current_stream(dev)
+                side = torch.cuda.Stream(dev)
+                staging = torch.empty((ring, self.nbytes), dtype=torch.uint8, device=dev)
+                free = [torch.cuda.Event() for _ in range(ring)]  # copy of slot s done: it may be rewritten
+                used = [False] * ring
+            s = count % ring
+            if used[s]:
+                compute.wait_event(free[s])
+            quantize(w3.to(dev), self.bits, self.group, out=staging[s])
+            done = torch.cuda.Event()
+            done.record(compute)
+            side.wait_event(done)
+            with torch.cuda.stream(side):
+                self.host[key].copy_(staging[s], non_blocking=self.pinned)
+                free[s].record(side)
+            used[s] = True
+            count += 1
+        if side is not None:
+            side.synchronize()
+        return count
 
-    # ---- builders -------------------------------------------------------
+    def put(self, l, e, w3, device="cuda"):
+        """Quantize expert (l, e) from w3 [3, n] on `device` into its row."""
+        self.fill([(self.key(l, e), w3)], device, ring=1)
+
     @classmethod
     def from_experts(cls, layers, bits, group=128, device="cuda", pin=True):
-        """layers: per layer, a list of (gate_w, up_w, down_w) tensors."""
-        L, E = len(layers), len(layers[0])
+        """layers: per layer, a list of (gate_w, up_w, down_w) weight tensors of one shape."""
         n = layers[0][0][0].numel()
-        st = cls(L, E, n, bits, group, pin)
-        for l, exps in enumerate(layers):
-            for e, (g, u, d) in enumerate(exps):
-                st.put(l, e, torch.stack([g.reshape(-1), u.reshape(-1), d.reshape(-1)]), device)
+        st = cls(len(layers), len(layers[0]), n, bits, group, pin)
+        st.fill(((st.key(l, e), torch.stack([g.reshape(-1), u.reshape(-1), d.reshape(-1)]))
+                 for l, exps in enumerate(layers) for e, (g, u, d) in enumerate(exps)), device)
         return st
 
-    @classmethod
-    def from_safetensors(cls, model_dir, cfg, bits, group=128, device="cuda", cache_dir=None, pin=True):
-        """Experts of a Qwen3-MoE checkpoint (`model.layers.{l}.mlp.experts.{e}.{gate,up,down}_proj.weight`),
-        read through model.safetensors.index.json; cached as raw rows under cache_dir."""
-        from safetensors import safe_open
+    # ---------------------------------------------------------------- persistence
+    @staticmethod
+    def cache_file(cache_dir: str, bits: int, group: int, L: int, E: int, n: int) -> str:
+        """Where a store of this shape is cached (the reference's file name, store.py:62)."""
+        return os.path.join(cache_dir, f"store_b{bits}_g{group}_{L}x{E}x{n}.u8")
 
-        L, E = cfg.num_hidden_layers, cfg.num_experts
-        n = cfg.moe_intermediate_size * cfg.hidden_size
-        st = cls(L, E, n, bits, group, pin)
-        path = None
-        if cache_dir and bits < 16:
-            os.makedirs(cache_dir, exist_ok=True)
-            path = os.path.join(cache_dir, f"store_b{bits}_g{group}_{L}x{E}x{n}.u8")
-            if os.path.exists(path) and os.path.getsize(path) == st.host.numel():
-                st._load(path)
-                return st
-        with open(os.path.join(model_dir, "model.safetensors.index.json")) as f:
-            where = json.load(f)["weight_map"]
-        files = {}
+    def _flat(self) -> memoryview:
+        return memoryview(self.host.numpy()).cast("B")
 
-        def tensor(name):
-            fn = where[name]
-            if fn not in files:
-                files[fn] = safe_open(os.path.join(model_dir, fn), framework="pt", device="cpu")
-            return files[fn].get_tensor(name)
+    def save(self, path: str) -> None:
+        """Write the rows back to back (no header) to `path`, atomically (temp file + rename)."""
+        buf = self._flat()
+        tmp = path + ".tmp"
+        with open(tmp, "wb") as f:
+            for off in range(0, len(buf), _IO_PIECE):
+                f.write(buf[off : off + _IO_PIECE])
+        os.replace(tmp, path)
 
-        t0 = time.time()
-        for l in range(L):
-            for e in range(E):
-                p = f"model.layers.{l}.mlp.experts.{e}."
-                w3 = torch.stack([tensor(p + m + "_proj.weight").reshape(-1) for m in ("gate", "up", "down")])
-                st.put(l, e, w3, device)
-            if l % 4 == 3 or l == L - 1:
-                print(f"[store] bits={bits} layer {l + 1}/{L}  {time.time() - t0:.0f}s", flush=True)
-        if path:
-            st._save(path)
-        return st
-
-    # ---- persistence ----------------------------------------------------
-    def _save(self, path, rows=256):
-        a = self.host.numpy()
-        with open(path + ".tmp", "wb") as f:
-            for i in range(0, a.shape[0], rows):
-                f.write(memoryview(a[i : i + rows]))
-        os.replace(path + ".tmp", path)
-
-    def _load(self, path, rows=256):
-        a = self.host.numpy()
+    def load(self, path: str) -> None:
+        """Read a file written by `save` (or the reference's `_save`) into the rows. The file
+        must hold exactly L * E * nbytes bytes."""
+        size = os.path.getsize(path)
+        if size != self.host.numel():
+            raise ValueError(f"{path}: {size} bytes, this store holds {self.host.numel()} "
+                             f"({self.rows} rows of {self.nbytes})")
+        buf = self._flat()
         with open(path, "rb") as f:
-            for i in range(0, a.shape[0], rows):
-                f.readinto(memoryview(a[i : i + rows]))
+            off = 0
+            while off < len(buf):
+                got = f.readinto(buf[off : off + _IO_PIECE])
+                if not got:
+                    raise IOError(f"{path}: short read at byte {off}")
+                off += got
+
+    # the reference's names (store.py:96-110)
+    def _save(self, path, rows=None):
+        self.save(path)
+
+    def _load(self, path, rows=None):
+        self.load(path)
