@@ -140,7 +140,7 @@ def timed_steps(stream, warm, timed, steps: int):
         for g, reps in warm:
             for _ in range(reps):
                 g.replay()
-        torch.cuda._sleep(2_000_000)
+        torch.cuda._sleep(200_000)
         e0.record(stream)
         for g, reps in timed:
             for _ in range(reps):
@@ -151,13 +151,17 @@ def timed_steps(stream, warm, timed, steps: int):
 
 
 def setup_pass(W: Layers):
-    """Set-up, not a step: one eager layer on every pool with the last routing round (the
-    timed steps start at round 0), so module loading and the first touch of each pool's
-    pages happen before the warm-up steps, as in a decoder that runs every layer per token."""
-    with torch.cuda.stream(W.stream):
-        st = _lib.stream(W.dev)
-        for l in range(W.layers):
-            W.layer((ROUNDS - 1) * W.layers + l, st)
+    """Set-up, not a step: one layer for every (pool, routing round) of the rotation, replayed
+    from a graph, so module loading, the first graph launch of the process and the first
+    touch of every expert page the steps will read happen before the warm-up steps -- the
+    state of a decoder that has been running."""
+    with torch.cuda.stream(W.stream):  # one eager layer loads the code, the rest runs as a graph replay
+        W.layer(0, _lib.stream(W.dev))
+    torch.cuda.synchronize()
+    for g, reps in capture_steps(W.stream, W.layer, 0, ROUNDS * W.layers):
+        with torch.cuda.stream(W.stream):
+            for _ in range(reps):
+                g.replay()
     torch.cuda.synchronize()
 
 
@@ -1041,7 +1045,7 @@ def main():
             "down_bytes": dn_b,
             "timing": "HIP events on the replay stream around graph replays of exactly `steps` layer steps "
                       "(pool i % 48, routing round i // 48 % 8) after `warmup` untimed ones and one set-up "
-                      "layer per pool; per-launch averages include the in-graph launch gaps",
+                      "layer per pool and routing round; per-launch averages include the in-graph launch gaps",
         },
         "roofline": {
             "bound": "hbm",

@@ -51,6 +51,41 @@ struct Layer {
     int odt;      // output dtype of the weighted sum: WISP_DT_BF16, WISP_DT_F16 or WISP_DT_F32
 };
 
+// The layer constants as the kernels use them: with C2 (the Qwen3-30B-A3B expert shape,
+// H = 2048, I = 768, G = 128) every shape-derived field is a compile-time constant, so the
+// kernels read no Layer field from kernel-argument memory before their weight loads (the
+// runtime fields come from the preloaded scalar arguments); otherwise the Layer as passed.
+constexpr int kC2H = 2048, kC2I = 768, kC2G = 128;
+
+template <int BITS, bool C2>
+__device__ __forceinline__ Layer layer_of(const Layer& L, const uint8_t* pool, const float* meta, int64_t slot_bytes,
+                                          int nslots) {
+    if constexpr (C2) {
+        Layer c;
+        c.pool = pool;
+        c.meta = meta;
+        c.slot_bytes = slot_bytes;
+        c.nmb = (int64_t)kC2H * kC2I * BITS / 8;
+        c.nslots = nslots;
+        c.k = 0;  // taken from the kernel's own argument where needed
+        c.H = kC2H;
+        c.I = kC2I;
+        c.G = kC2G;
+        c.rowb_gu = kC2H * BITS / 8;
+        c.rowb_dn = kC2I * BITS / 8;
+        c.gpr_gu = kC2H / kC2G;
+        c.gpr_dn = kC2I / kC2G;
+        c.NGM = kC2H * kC2I / kC2G;
+        c.gsh = 2;  // log2(G / 32)
+        c.spr_gu = kC2H / 32;
+        c.spr_dn = kC2I / 32;
+        c.odt = L.odt;  // read only at the output store
+        return c;
+    } else {
+        return L;
+    }
+}
+
 // out[h] = v rounded once (round to nearest even) to the caller's dtype
 __device__ __forceinline__ void store_out(void* out, int odt, int h, float v) {
     if (odt == WISP_DT_F32)
@@ -352,7 +387,7 @@ __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __re
 // preloading, built with -amdgpu-kernarg-preload-count): the slot-id read and
 // the x loads need no kernel-argument fetch first, so the only memory round
 // trip before the weight loads is the slot id itself.
-template <int BITS, int SPR_T, int T, int NW, bool QSC, int XT>
+template <int BITS, int SPR_T, int T, int NW, bool QSC, int XT, bool C2>
 __global__ __launch_bounds__(64 * NW) void k_gate_up(const float* __restrict__ meta,
                                                       const uint8_t* __restrict__ pool, int64_t slot_bytes,
                                                       int nslots, const void* __restrict__ x,
@@ -363,7 +398,7 @@ __global__ __launch_bounds__(64 * NW) void k_gate_up(const float* __restrict__ m
     // issue the slot-id read, the remaining kernel-argument reads and the x loads
     // together; the scheduling barrier keeps every use (and so every wait) after them
     const float f = meta[j];
-    const Layer Lc = L;
+    const Layer Lc = layer_of<BITS, C2>(L, pool, meta, slot_bytes, nslots);
     uint32_t xr[XWords<XT>::n];
     load_x_raw<XT>(x, (threadIdx.x & 63) % (SPR_T ? SPR_T : Lc.spr_gu), xr);
     __builtin_amdgcn_sched_barrier(0);
@@ -558,7 +593,7 @@ __device__ __forceinline__ void down_rows(const Layer& L, const float* meta,
     }
     if (WSUM) {
         __syncthreads();
-        for (int q = threadIdx.x; q < RW; q += blockDim.x) {
+        for (int q = threadIdx.x; q < RW; q += 64 * k) {  // the block is k waves
             const int h = h0 + q;
             if (h < L.H) {
                 float acc = 0.f;
@@ -571,20 +606,22 @@ __device__ __forceinline__ void down_rows(const Layer& L, const float* meta,
 
 // Kernel 2 (fast path), two-kernel form.
 // grid = ceil(H / (T*RPI)), block = 64*k, dynamic LDS as for down_rows.
-template <int BITS, int SPR_T, int T, bool WSUM, bool QSC>
+template <int BITS, int SPR_T, int T, bool WSUM, bool QSC, bool C2>
 // The leading scalar arguments are preloaded into SGPRs at dispatch, as for
 // k_gate_up.
 __global__ __launch_bounds__(1024) void k_down(const float* meta, const uint8_t* __restrict__ pool,
                                                int64_t slot_bytes, int nslots, int k, int I,
                                                const uint32_t* __restrict__ act, void* __restrict__ out,
-                                               float* __restrict__ y, const Layer L) {
+                                               float* __restrict__ y, const Layer L0) {
     extern __shared__ float lds[];
+    const Layer L = layer_of<BITS, C2>(L0, pool, meta, slot_bytes, nslots);
     const int RW = T * (64 / (SPR_T ? SPR_T : L.spr_dn));
     // XCD-aware row blocks: the dispatcher deals workgroups to the 8 XCDs in turn, so
     // workgroup b runs on XCD b % 8; give each XCD one contiguous range of row blocks,
     // so the scale/min lines neighbouring blocks share are fetched into one L2 only
+    // (the grid size from the shape: gridDim would be a kernel-argument memory read)
     int rb = blockIdx.x;
-    const int G = gridDim.x;
+    const int G = (L.H + RW - 1) / RW;
     if ((G & 7) == 0) rb = (rb & 7) * (G >> 3) + (rb >> 3);
     down_rows<BITS, SPR_T, T, WSUM, QSC>(L, meta, pool, slot_bytes, nslots, k, I, act, out, y, rb * RW, lds);
 }
@@ -694,13 +731,19 @@ static int make_layer(Layer& L, const uint8_t* pool, int64_t slot_bytes, int64_t
 
 static bool valid_dtype(int dt) { return dt == WISP_DT_BF16 || dt == WISP_DT_F16 || dt == WISP_DT_F32; }
 
+static bool is_c2(const Layer& L) { return L.H == kC2H && L.I == kC2I && L.G == kC2G; }
+
 template <int BITS, int SPR, int T, int NW, bool QSC, int XT>
 static void launch_gu(const Layer& L, const void* x, uint32_t* act, hipStream_t st) {
     const int RPI = 64 / L.spr_gu;
     const int rows_wg = NW * T * RPI;
     const dim3 grid((L.I + rows_wg - 1) / rows_wg, L.k);
-    hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW, QSC, XT>), grid, dim3(64 * NW), 0, st, L.meta, L.pool,
-                       L.slot_bytes, L.nslots, x, act, L);
+    if (SPR == 64 && is_c2(L))
+        hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW, QSC, XT, true>), grid, dim3(64 * NW), 0, st, L.meta, L.pool,
+                           L.slot_bytes, L.nslots, x, act, L);
+    else
+        hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW, QSC, XT, false>), grid, dim3(64 * NW), 0, st, L.meta,
+                           L.pool, L.slot_bytes, L.nslots, x, act, L);
 }
 
 template <int BITS, int XT>
@@ -747,8 +790,13 @@ template <int BITS, int SPR, int T, bool WSUM, bool QSC>
 static void launch_dn(const Layer& L, const uint32_t* act, void* out, float* y, hipStream_t st) {
     const int RW = T * (64 / L.spr_dn);
     const size_t lds = dn_lds_bytes(L, T);
-    hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM, QSC>), dim3((L.H + RW - 1) / RW), dim3(64 * L.k), lds, st, L.meta,
-                       L.pool, L.slot_bytes, L.nslots, L.k, L.I, act, out, y, L);
+    const dim3 grid((L.H + RW - 1) / RW), block(64 * L.k);
+    if (SPR == 24 && is_c2(L))
+        hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM, QSC, true>), grid, block, lds, st, L.meta, L.pool,
+                           L.slot_bytes, L.nslots, L.k, L.I, act, out, y, L);
+    else
+        hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM, QSC, false>), grid, block, lds, st, L.meta, L.pool,
+                           L.slot_bytes, L.nslots, L.k, L.I, act, out, y, L);
 }
 
 template <int BITS, bool WSUM>
