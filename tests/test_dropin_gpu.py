@@ -144,6 +144,25 @@ def test_more_than_16_experts_per_expert_y_and_invalid_slot():
     assert torch.isnan(bad.float()).all()
 
 
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("k", [8, 5, 1])
+def test_c2_shape_invalid_slot_poisons_every_row(bits, k):
+    """At the Qwen3 shape (the row-per-wave down kernel for k <= 8) an out-of-range slot id
+    makes every output row NaN and reads nothing out of bounds; valid ids give finite rows."""
+    H, I, group, E = 2048, 768, 128, 9
+    rng = np.random.default_rng(bits * 10 + k)
+    pool = torch.from_numpy(_pool(E, H, I, bits, group, seed=bits + k)).to(DEV)
+    sel, rw = _route(rng, E, k)
+    x = torch.randn(H, device=DEV).to(torch.bfloat16)
+    meta = torch.from_numpy(O.meta(sel, rw)).to(DEV)
+    ok = _FNS[bits](pool, meta, x, k, H * I, H, I, group)
+    assert torch.isfinite(ok.float()).all()
+    meta[k - 1] = float(E + 3)
+    bad = _FNS[bits](pool, meta, x, k, H * I, H, I, group)
+    torch.cuda.synchronize()
+    assert torch.isnan(bad.float()).all()
+
+
 # ---------------------------------------------------------------- the benchmark's pool: > 4 GiB of offsets
 def test_pool_past_4gib_top_slots():
     """The C2 benchmark's pool: 48 layer pools x 128 experts = 6,144 slots of 2,506,752 B

@@ -604,6 +604,148 @@ __device__ __forceinline__ void down_rows(const Layer& L, const float* meta,
     }
 }
 
+// ===========================================================================
+// Kernel 2 for the Qwen3-30B-A3B shape (I = 768, k <= 8, launched for 4-bit
+// codes; 3- and 2-bit measure faster on k_down), weighted sum: one wave
+// computes RPW whole output rows over all k experts. Lane l takes the (expert,
+// chunk) pairs l, l + 64 and l + 128 of a row's k x 24 pairs, so all 64 lanes
+// work, each lane keeps its three activation chunks in registers for the wave's
+// rows, and a row total is one in-register reduction (DPP within 16-lane rows,
+// then the four rows) -- no exchange between waves, and every wave stores its
+// own rows as soon as they are done. Sum order: the three pairs of a lane, then
+// the lanes; the k expert weights are applied per pair.
+// The activations of all k experts are staged in LDS once per workgroup.
+// ===========================================================================
+template <int BITS, int RPW, int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_down_rows(const float* meta, const uint8_t* __restrict__ pool,
+                                                        int64_t slot_bytes, int nslots, int k,
+                                                        const uint32_t* __restrict__ act, void* __restrict__ out,
+                                                        const Layer L0) {
+    constexpr int SEG = kC2I / 32, NC = 3, ROWB = kC2I * BITS / 8;
+    constexpr int64_t NMB = (int64_t)kC2H * kC2I * BITS / 8;
+    constexpr int NGM = kC2H * kC2I / kC2G, GPR = kC2I / kC2G;
+    constexpr int ROWS_WG = RPW * NWV, NB = kC2H / ROWS_WG;
+    constexpr bool QS = (RPW % 2) == 0;
+    __shared__ uint4 stage[8 * SEG * 9];  // per (expert, chunk): 8 uint4 of hi|lo pairs + 1 pad
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int rb = blockIdx.x;
+    if ((NB & 7) == 0) rb = (rb & 7) * (NB >> 3) + (rb >> 3);
+    const int h0 = rb * ROWS_WG + wv * RPW;
+
+    // the activations of all k experts (k * 192 uint4) -> registers, then LDS
+    constexpr int APT = (8 * SEG * 8 + 64 * NWV - 1) / (64 * NWV);
+    const int na = k * SEG * 8;
+    // lane i < 2k holds meta[i] (slot ids, then weights); issued before the activation
+    // loads, so waiting for it does not wait for them
+    const float mv = meta[min(lane & 15, 2 * k - 1)];
+    const uint4* a4 = reinterpret_cast<const uint4*>(act);
+    uint4 ap[APT];
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+        const int idx = threadIdx.x + i * 64 * NWV;
+        ap[i] = a4[min(idx, na - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    int ec[NC], sg[NC];
+    bool on[NC], okc[NC];
+    const uint8_t* bc[NC];
+    float wc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int combo = lane + 64 * c;
+        ec[c] = combo / SEG;
+        sg[c] = combo - ec[c] * SEG;
+        on[c] = ec[c] < k;
+        const int e = on[c] ? ec[c] : 0;
+        const float f = __shfl(mv, e, 64);
+        const int slot = slot_from(f, nslots);
+        okc[c] = slot >= 0;
+        bc[c] = pool + (int64_t)(okc[c] ? slot : 0) * slot_bytes;
+        const float w = __shfl(mv, k + e, 64);
+        wc[c] = on[c] ? w : 0.f;
+    }
+    uint32_t cd[RPW][NC][BITS];
+    uint32_t sv[QS ? RPW / 2 : RPW][NC];
+#pragma unroll
+    for (int t = 0; t < RPW; ++t) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const uint8_t* row = bc[c] + 2 * NMB + (int64_t)(h0 + t) * ROWB + sg[c] * (4 * BITS);
+            load_chunk<BITS>(row, cd[t][c]);
+            const uint16_t* sc = reinterpret_cast<const uint16_t*>(bc[c] + 3 * NMB) + 2 * NGM;
+            const uint16_t* mn = sc + 3 * NGM;
+            const int g = sg[c] >> 2;
+            if constexpr (QS) {
+                if (t % 2 == 0) {
+                    const int w = lane & 3;
+                    const int hh = h0 + t + ((w >> 1) & 1);
+                    sv[t / 2][c] = ((w & 1) ? mn : sc)[hh * GPR + g];
+                }
+            } else {
+                sv[t][c] = (uint32_t)sc[(h0 + t) * GPR + g] | ((uint32_t)mn[(h0 + t) * GPR + g] << 16);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+        // every thread stores (clamped: duplicates rewrite the same value), halves swapped so the
+        // compiler cannot fold the load and this store into a copy placed here
+        const int idx = min((int)threadIdx.x + i * 64 * NWV, na - 1);
+        const uint4 a = ap[i];
+        stage[(idx >> 3) * 9 + (idx & 7)] = make_uint4(a.z, a.w, a.x, a.y);
+    }
+    __syncthreads();
+    uint32_t AH[NC][16], AL[NC][16];
+    float as[NC], bias[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int e = on[c] ? ec[c] : 0;
+        const uint4* q = stage + (e * SEG + sg[c]) * 9;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 h = q[i], l = q[4 + i];  // halves swapped in the stage
+            AH[c][4 * i] = h.z; AH[c][4 * i + 1] = h.w; AH[c][4 * i + 2] = h.x; AH[c][4 * i + 3] = h.y;
+            AL[c][4 * i] = l.z; AL[c][4 * i + 1] = l.w; AL[c][4 * i + 2] = l.x; AL[c][4 * i + 3] = l.y;
+        }
+        float vh, th, vl, tl;
+        operand_sums<BITS>(AH[c], vh, th);
+        operand_sums<BITS>(AL[c], vl, tl);
+        as[c] = th + tl;
+        bias[c] = -kBiasF * (vh + vl);
+    }
+    const uint32_t B = bias_vgpr();
+#pragma unroll
+    for (int t = 0; t < RPW; ++t) {
+        float p = 0.f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const float d = chunk_dot_hl<BITS>(cd[t][c], AH[c], AL[c], bias[c], B);
+            uint32_t s_, m_;
+            if constexpr (QS) {
+                const uint32_t v2 = sv[t / 2][c];
+                s_ = (t & 1) ? quad_bcast<2>(v2) : quad_bcast<0>(v2);
+                m_ = (t & 1) ? quad_bcast<3>(v2) : quad_bcast<1>(v2);
+            } else {
+                s_ = sv[t][c] & 0xFFFFu;
+                m_ = sv[t][c] >> 16;
+            }
+            const float v = h2f((uint16_t)s_) * d + h2f((uint16_t)m_) * as[c];
+            p += !okc[c] && on[c] ? __builtin_nanf("") : wc[c] * v;
+        }
+        // row sums by DPP within each 16-lane row, then the four rows through readlane
+        p += dpp_f<0xB1>(p);
+        p += dpp_f<0x4E>(p);
+        p += dpp_f<0x141>(p);
+        p += dpp_f<0x140>(p);
+        const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 0)) +
+                          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 16)) +
+                          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 32)) +
+                          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 48));
+        if (lane == 0) store_out(out, L0.odt, h0 + t, tot);
+    }
+}
+
 // Kernel 2 (fast path), two-kernel form.
 // grid = ceil(H / (T*RPI)), block = 64*k, dynamic LDS as for down_rows.
 template <int BITS, int SPR_T, int T, bool WSUM, bool QSC, bool C2>
@@ -817,7 +959,17 @@ static int down_bits(const Layer& L, const uint32_t* act, void* out, float* y, h
     switch (tuning().dn_iters) {
     case 1: launch_dn<BITS, 24, 1, WSUM, false>(L, act, out, y, st); break;
     case 2: launch_dn<BITS, 24, 2, WSUM, (bool)WISP_QSC>(L, act, out, y, st); break;
-    case 4: launch_dn<BITS, 24, 4, WSUM, (bool)WISP_QSC>(L, act, out, y, st); break;
+    case 4:
+        if constexpr (BITS == 4) {  // 3- and 2-bit codes measure faster on the per-expert waves
+            if (WSUM && is_c2(L) && L.k <= 8) {  // the default tuning of the C2 shape
+                constexpr int RPW = 2, NWV = 4;
+                hipLaunchKernelGGL((k_down_rows<BITS, RPW, NWV>), dim3(kC2H / (RPW * NWV)), dim3(64 * NWV), 0, st,
+                                   L.meta, L.pool, L.slot_bytes, L.nslots, L.k, act, out, L);
+                return check_launch("k_down_rows");
+            }
+        }
+        launch_dn<BITS, 24, 4, WSUM, (bool)WISP_QSC>(L, act, out, y, st);
+        break;
     case 8: launch_dn<BITS, 24, 8, WSUM, (bool)WISP_QSC>(L, act, out, y, st); break;
     default: return fail_inval("unsupported tuning dn_iters");
     }
