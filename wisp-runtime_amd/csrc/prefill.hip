@@ -35,9 +35,14 @@
 // MFMA 16x16x32 bf16 lane layout (lane l): A[row l%16][k 8*(l/16) + 0..7],
 // B[k 8*(l/16) + 0..7][col l%16], D[row 4*(l/16) + 0..3][col l%16].
 // With the weights read once per expert the path is HBM-bound for T <= 512.
+// 4-bit codes with an even number of K groups (the Qwen3 shapes) take the LDS-DMA
+// form of the two GEMMs (k_pf_gate_up_dma / k_pf_down_dma, described at
+// pf_gemm_dma): the codes of a K step arrive as whole 128-byte lines straight into
+// LDS, two steps ahead, and the scales with them.
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "wisp_device.hpp"
 #include "wisp_internal.hpp"
@@ -138,7 +143,7 @@ __device__ __forceinline__ int group_state(const Prefill& F, int u, int& slot, i
 // at most kPfSmSteps quant groups (K <= 2048): entry [K step][local row] =
 // s | m << 16 (fp16 bits). K-step major, so the 16 rows of a tile that one read
 // touches are 16 consecutive words (distinct banks).
-constexpr int kPfSmSteps = 16, kPfSmRows = 256;
+constexpr int kPfSmSteps = 16;
 
 struct PfRows {
     const uint8_t* rc;   // codes of tile 0 at the lane's row and chunk
@@ -150,11 +155,14 @@ struct PfRows {
 };
 
 // One K step's codes and fp16 scale/min (packed s | m << 16) of a lane's row in tile j.
-template <int BITS>
+// SMR > 0: the scale/min come from the workgroup's LDS table (row stride SMR); SMR == 0:
+// from global memory. A compile-time choice: a run-time one compiled to a divergent branch
+// whose loads made the compiler drain every outstanding load at the step loop's head.
+template <int BITS, int SMR>
 __device__ __forceinline__ void pf_load(const PfRows& R, int j, int kc, uint32_t* cd, uint32_t& sm) {
     load_chunk<BITS>(R.rc + R.code_off[j] + (int64_t)kc * 16 * BITS, cd);  // 128 codes per K step
-    if (R.sml) {
-        sm = R.sml[R.sml_off[j] + kc * kPfSmRows];
+    if constexpr (SMR > 0) {  // the LDS table (row stride SMR)
+        sm = R.sml[R.sml_off[j] + kc * SMR];
     } else {
         const uint16_t* s = R.sp + R.scale_off[j] + kc;
         sm = (uint32_t)s[0] | ((uint32_t)s[R.mn_off] << 16);
@@ -166,7 +174,7 @@ __device__ __forceinline__ void pf_load(const PfRows& R, int j, int kc, uint32_t
 // packed s | m << 16, with 16-byte loads (nrows * nk a multiple of 8; both runs
 // 16-byte aligned). All threads of the workgroup take part.
 __device__ __forceinline__ void pf_stage_scales(const uint16_t* sc, int64_t mn_off, int nrows, int nk, int local0,
-                                                uint32_t* sml) {
+                                                uint32_t* sml, int smr) {
     const int total = nrows * nk;  // entries, 8 per 16-byte load
     for (int e = (int)threadIdx.x * 8; e < total; e += (int)blockDim.x * 8) {
         const uint4 vs = *reinterpret_cast<const uint4*>(sc + e);
@@ -177,7 +185,7 @@ __device__ __forceinline__ void pf_stage_scales(const uint16_t* sc, int64_t mn_o
         for (int i = 0; i < 8; ++i) {
             const uint32_t sv = i & 1 ? s4[i >> 1] >> 16 : s4[i >> 1] & 0xFFFFu;
             const uint32_t mv = i & 1 ? m4[i >> 1] & 0xFFFF0000u : m4[i >> 1] << 16;
-            sml[kc * kPfSmRows + local0 + r] = sv | mv;
+            sml[kc * smr + local0 + r] = sv | mv;
             if (++kc == nk) {
                 kc = 0;
                 ++r;
@@ -226,10 +234,10 @@ struct PfStep {
     uint32_t cd[2][2][BITS], sm[2][2];  // [row tile of the step][group of the pair]: codes, s | m << 16
 };
 
-template <int BITS, int NT, int NW>
+template <int BITS, int NT, int NW, int TPW, int SMR>
 __device__ __forceinline__ void pf_gemm(const PfRows& R, const uint4* const* crow, uint4* lds, int nk,
-                                        f32x4_t (*acc)[16 / NW]) {
-    constexpr int TPW = 16 / NW, TP = TPW / 2;  // row tiles per wave, steps per group pair
+                                        f32x4_t (*acc)[TPW]) {
+    constexpr int TP = TPW / 2;  // steps per group pair
     constexpr int RPT = 8 * NT / NW;           // A pieces per thread and pair
     constexpr int BUF = NT * 16 * kArs;
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
@@ -246,8 +254,8 @@ __device__ __forceinline__ void pf_gemm(const PfRows& R, const uint4* const* cro
         const int k0 = min(2 * q, nk - 1), k1 = min(2 * q + 1, nk - 1);
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
-            pf_load<BITS>(R, t0 + jj, k0, S.cd[jj][0], S.sm[jj][0]);
-            pf_load<BITS>(R, t0 + jj, k1, S.cd[jj][1], S.sm[jj][1]);
+            pf_load<BITS, SMR>(R, t0 + jj, k0, S.cd[jj][0], S.sm[jj][0]);
+            pf_load<BITS, SMR>(R, t0 + jj, k1, S.cd[jj][1], S.sm[jj][1]);
         }
     };
     auto load_a = [&](u32x4_t* av, int q) {
@@ -302,21 +310,24 @@ __device__ __forceinline__ void pf_gemm(const PfRows& R, const uint4* const* cro
     load_a(an, 0);
     load_step(S0, 0);
     put_a(an, 0);
-    for (int st = 0;; st += 2) {
+    // whole rounds of two steps, then the odd one: no exit from inside a round, so the
+    // compiler's load counting is the same on every path into the loop head (an exit
+    // mid-round made it drain every load there, prefetch included)
+    int st = 0;
+    for (const int nr = nsteps & ~1; st < nr; st += 2) {
         step(S0, S1, an, st);
-        if (st + 1 >= nsteps) break;
         step(S1, S0, an, st + 1);
-        if (st + 2 >= nsteps) break;
     }
+    if (st < nsteps) step(S0, S1, an, st);
 }
 
 // One pass of kernel gate_up over NT 16-token tiles starting at pair mb of the
 // group: A rows are the pairs' tokens (rows past cnt repeat the last pair).
 // The wave's tiles j < TPW/2 are gate rows c0 + 16j, the others the same up rows.
-template <int BITS, int NT, int NW>
+template <int BITS, int NT, int NW, int TPW, int SMR>
 __device__ __forceinline__ void pf_gate_up_pass(const Prefill& F, const PfRows& R, int nk, int c0, int p0, int cnt,
                                                 int mb, uint4* lds) {
-    constexpr int TPW = 16 / NW, HT = TPW / 2, RPT = 8 * NT / NW;
+    constexpr int HT = TPW / 2, RPT = 8 * NT / NW;
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const uint4* crow[RPT];
 #pragma unroll
@@ -326,7 +337,7 @@ __device__ __forceinline__ void pf_gate_up_pass(const Prefill& F, const PfRows& 
         crow[k] = reinterpret_cast<const uint4*>(F.x + (int64_t)t * F.H) + (threadIdx.x & 15);
     }
     f32x4_t acc[NT][TPW];
-    pf_gemm<BITS, NT, NW>(R, crow, lds, nk, acc);
+    pf_gemm<BITS, NT, NW, TPW, SMR>(R, crow, lds, nk, acc);
     // D layout: acc[mt][j][i] = token mb + mt*16 + 4g + i, row tile j column n
 #pragma unroll
     for (int mt = 0; mt < NT; ++mt)
@@ -342,10 +353,10 @@ __device__ __forceinline__ void pf_gate_up_pass(const Prefill& F, const PfRows& 
 }
 
 // One pass of kernel down (A rows: the pairs' activations), stores w * y.
-template <int BITS, int NT, int NW>
+template <int BITS, int NT, int NW, int TPW, int SMR>
 __device__ __forceinline__ void pf_down_pass(const Prefill& F, const PfRows& R, int nk, int h0, int p0, int cnt,
                                              int mb, uint4* lds) {
-    constexpr int TPW = 16 / NW, RPT = 8 * NT / NW;
+    constexpr int RPT = 8 * NT / NW;
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const uint4* crow[RPT];
 #pragma unroll
@@ -354,7 +365,7 @@ __device__ __forceinline__ void pf_down_pass(const Prefill& F, const PfRows& R, 
         crow[k] = reinterpret_cast<const uint4*>(F.act + (int64_t)(p0 + m) * F.I) + (threadIdx.x & 15);
     }
     f32x4_t acc[NT][TPW];
-    pf_gemm<BITS, NT, NW>(R, crow, lds, nk, acc);
+    pf_gemm<BITS, NT, NW, TPW, SMR>(R, crow, lds, nk, acc);
 #pragma unroll
     for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
@@ -373,14 +384,15 @@ __device__ __forceinline__ void pf_down_pass(const Prefill& F, const PfRows& R, 
 // gate_up: act[p][r] = bf16(silu(g) * u), g/u = x[tok[p]] . W{gate,up}[r]
 // grid (I/128, U, Z), NW waves; wave w of workgroup x owns act columns
 // c0 = x*128 + w*8*TPW .. +8*TPW-1: row tiles {gate c0 + 16j, up c0 + 16j}.
-template <int BITS, int MT, int NW>
-__global__ __launch_bounds__(64 * NW) void k_pf_gate_up(const Prefill F) {
-    constexpr int TPW = 16 / NW, HT = TPW / 2, CW = 8 * TPW;
+template <int BITS, int MT, int NW, int RWG, bool SML>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gate_up(const Prefill F) {
+    constexpr int SMR = SML ? RWG : 0;
+    constexpr int TPW = RWG / (16 * NW), HT = TPW / 2, CW = 8 * TPW, HR = RWG / 2;
     __shared__ uint4 lds[2 * MT * 16 * kArs];
-    __shared__ uint32_t sml[kPfSmRows * kPfSmSteps];
+    __shared__ uint32_t sml[RWG * kPfSmSteps];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int c0 = blockIdx.x * 128 + wv * CW, u = blockIdx.y;
+    const int c0 = blockIdx.x * HR + wv * CW, u = blockIdx.y;
     int slot, p0, cnt;
     const int gs = group_state(F, u, slot, p0, cnt);
     if (gs == 0) return;
@@ -404,22 +416,22 @@ __global__ __launch_bounds__(64 * NW) void k_pf_gate_up(const Prefill F) {
         const int mat = j / HT, dr = (j % HT) * 16;
         R.code_off[j] = mat * F.nmb + dr * rowb;
         R.scale_off[j] = (int64_t)mat * F.NGM + (int64_t)dr * nk;
-        R.sml_off[j] = mat * 128 + dr;  // local rows: gate 0..127, up 128..255
+        R.sml_off[j] = mat * HR + dr;  // local rows: gate 0..HR-1, up HR..RWG-1
     }
-    if (nk <= kPfSmSteps) {  // the workgroup's 128 gate and 128 up rows' scale/min, once
-        const int r0 = blockIdx.x * 128;
-        pf_stage_scales(sc + (int64_t)r0 * nk, mn - sc, 128, nk, 0, sml);
-        pf_stage_scales(sc + F.NGM + (int64_t)r0 * nk, mn - sc, 128, nk, 128, sml);
+    if constexpr (SML) {  // the workgroup's HR gate and HR up rows' scale/min, once (nk <= kPfSmSteps)
+        const int r0 = blockIdx.x * HR;
+        pf_stage_scales(sc + (int64_t)r0 * nk, mn - sc, HR, nk, 0, sml, RWG);
+        pf_stage_scales(sc + F.NGM + (int64_t)r0 * nk, mn - sc, HR, nk, HR, sml, RWG);
         __syncthreads();
         R.sml = sml + wv * CW + n;
     }
     constexpr int MB = MT * 16;
     for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
         const int nt = min(MT, (cnt - mb + 15) / 16);  // 16-token tiles in this pass (workgroup-uniform)
-        if (MT >= 4 && nt >= 4) pf_gate_up_pass<BITS, (MT >= 4 ? 4 : 1), NW>(F, R, nk, c0, p0, cnt, mb, lds);
-        else if (MT >= 3 && nt == 3) pf_gate_up_pass<BITS, (MT >= 3 ? 3 : 1), NW>(F, R, nk, c0, p0, cnt, mb, lds);
-        else if (MT >= 2 && nt == 2) pf_gate_up_pass<BITS, (MT >= 2 ? 2 : 1), NW>(F, R, nk, c0, p0, cnt, mb, lds);
-        else pf_gate_up_pass<BITS, 1, NW>(F, R, nk, c0, p0, cnt, mb, lds);
+        if (MT >= 4 && nt >= 4) pf_gate_up_pass<BITS, (MT >= 4 ? 4 : 1), NW, TPW, SMR>(F, R, nk, c0, p0, cnt, mb, lds);
+        else if (MT >= 3 && nt == 3) pf_gate_up_pass<BITS, (MT >= 3 ? 3 : 1), NW, TPW, SMR>(F, R, nk, c0, p0, cnt, mb, lds);
+        else if (MT >= 2 && nt == 2) pf_gate_up_pass<BITS, (MT >= 2 ? 2 : 1), NW, TPW, SMR>(F, R, nk, c0, p0, cnt, mb, lds);
+        else pf_gate_up_pass<BITS, 1, NW, TPW, SMR>(F, R, nk, c0, p0, cnt, mb, lds);
         __syncthreads();  // the next pass restages LDS buffer 0
     }
 }
@@ -428,14 +440,15 @@ __global__ __launch_bounds__(64 * NW) void k_pf_gate_up(const Prefill F) {
 // down: y[p][h] = w[p] * (act[p] . Wdown[h]), fp32
 // grid (H/256, U, Z), NW waves; wave w of workgroup x owns rows
 // x*256 + w*16*TPW .. +16*TPW-1.
-template <int BITS, int MT, int NW>
-__global__ __launch_bounds__(64 * NW) void k_pf_down(const Prefill F) {
-    constexpr int TPW = 16 / NW, RW = 16 * TPW;
+template <int BITS, int MT, int NW, int RWG, bool SML>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_down(const Prefill F) {
+    constexpr int SMR = SML ? RWG : 0;
+    constexpr int TPW = RWG / (16 * NW), RW = 16 * TPW;
     __shared__ uint4 lds[2 * MT * 16 * kArs];
-    __shared__ uint32_t sml[kPfSmRows * kPfSmSteps];
+    __shared__ uint32_t sml[RWG * kPfSmSteps];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int h0 = blockIdx.x * 256 + wv * RW, u = blockIdx.y;
+    const int h0 = blockIdx.x * RWG + wv * RW, u = blockIdx.y;
     int slot, p0, cnt;
     const int gs = group_state(F, u, slot, p0, cnt);
     if (gs == 0) return;
@@ -460,21 +473,309 @@ __global__ __launch_bounds__(64 * NW) void k_pf_down(const Prefill F) {
         R.scale_off[j] = (int64_t)j * 16 * nk;
         R.sml_off[j] = j * 16;
     }
-    if (nk <= kPfSmSteps) {  // the workgroup's 256 rows' scale/min, once
-        const int hb = blockIdx.x * 256;
-        pf_stage_scales(sc + 2 * (int64_t)F.NGM + (int64_t)hb * nk, mn - sc, 256, nk, 0, sml);
+    if constexpr (SML) {  // the workgroup's RWG rows' scale/min, once (nk <= kPfSmSteps)
+        const int hb = blockIdx.x * RWG;
+        pf_stage_scales(sc + 2 * (int64_t)F.NGM + (int64_t)hb * nk, mn - sc, RWG, nk, 0, sml, RWG);
         __syncthreads();
         R.sml = sml + wv * RW + n;
     }
     constexpr int MB = MT * 16;
     for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
         const int nt = min(MT, (cnt - mb + 15) / 16);
-        if (MT >= 4 && nt >= 4) pf_down_pass<BITS, (MT >= 4 ? 4 : 1), NW>(F, R, nk, h0, p0, cnt, mb, lds);
-        else if (MT >= 3 && nt == 3) pf_down_pass<BITS, (MT >= 3 ? 3 : 1), NW>(F, R, nk, h0, p0, cnt, mb, lds);
-        else if (MT >= 2 && nt == 2) pf_down_pass<BITS, (MT >= 2 ? 2 : 1), NW>(F, R, nk, h0, p0, cnt, mb, lds);
-        else pf_down_pass<BITS, 1, NW>(F, R, nk, h0, p0, cnt, mb, lds);
+        if (MT >= 4 && nt >= 4) pf_down_pass<BITS, (MT >= 4 ? 4 : 1), NW, TPW, SMR>(F, R, nk, h0, p0, cnt, mb, lds);
+        else if (MT >= 3 && nt == 3) pf_down_pass<BITS, (MT >= 3 ? 3 : 1), NW, TPW, SMR>(F, R, nk, h0, p0, cnt, mb, lds);
+        else if (MT >= 2 && nt == 2) pf_down_pass<BITS, (MT >= 2 ? 2 : 1), NW, TPW, SMR>(F, R, nk, h0, p0, cnt, mb, lds);
+        else pf_down_pass<BITS, 1, NW, TPW, SMR>(F, R, nk, h0, p0, cnt, mb, lds);
         __syncthreads();
     }
+}
+
+// ===========================================================================
+// LDS-DMA form (4-bit codes, an even number nk <= kPfSmSteps of K groups).
+// A K step is one pair of groups (256 K): for each of a wave's two 16-row tiles
+// the step's codes are one whole 128-byte line per row. Every line is fetched
+// by ONE request: global_load_lds_dwordx4 moves 64 lanes x 16 bytes = 8 rows x
+// 128 bytes straight into LDS (no VGPRs held while in flight), where each lane
+// then reads its MFMA fragment chunk. (Loads into registers in the fragment
+// layout can only cover 16 rows x 64 bytes per instruction, i.e. every line
+// in two halves, which measured 23 % slower in a loads-only run.)
+//   * codes: per wave a private ring of 2 slots x 4 KB (32 rows x 128 bytes);
+//     slot s holds step st (st % 2 == s); it is read into registers at the
+//     step's start and refilled at once with step st + 2, so two steps of
+//     codes are in flight while the step computes.
+//   * tokens (A): per pair the NT*16 rows x 512 bytes, double-buffered, loaded
+//     by all waves (DMA as well) and published by the step's barrier.
+//   * in LDS, piece p (16 bytes) of row r is stored at position p ^ (r & 7):
+//     the 8 lanes of a 128-bit LDS read phase (rows n..n+7, one piece) then hit
+//     8 different bank groups.
+// The compiler neither emits nor counts these loads, so every wait for them is
+// an explicit s_waitcnt vmcnt(n), n = the number of DMA instructions this wave
+// issued after the awaited ones (vector memory loads complete in order), and
+// nothing else in the loop issues vector memory loads.
+// ===========================================================================
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
+// 64 lanes x 16 bytes from the lanes' global addresses to LDS [lds, lds + 1024)
+__device__ __forceinline__ void dma16(uint32_t lds, const void* g) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
+                 : "memory");
+}
+// s_waitcnt vmcnt(n) (expcnt and lgkmcnt not waited for), gfx9 encoding
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | 0xF00 | ((N >> 4) << 14));
+    asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("" ::: "memory");
+}
+
+// base (SGPR pair) + per-lane 32-bit offset forms: no 64-bit address arithmetic per lane
+__device__ __forceinline__ void dma16s(uint32_t lds, const void* sbase, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(lds), "v"(voff), "s"(sbase)
+                 : "memory");
+}
+__device__ __forceinline__ void dma4s(uint32_t lds, const void* sbase, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
+                 :
+                 : "s"(lds), "v"(voff), "s"(sbase)
+                 : "memory");
+}
+__device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const uint8_t*>((uintptr_t)(((uint64_t)hi << 32) | lo));
+}
+
+// One wave's view of a tile for the LDS-DMA GEMM (all byte offsets).
+struct PfDma {
+    const uint8_t* cb[2];  // code base of row tile jj (its first row, pair 0), wave-uniform
+    const uint8_t* sb;     // scale base: fp16 scales of the wave's row 0, pair 0, wave-uniform
+    int64_t rowb;          // code bytes of one row
+    uint32_t voc;          // lane code offset: row lane>>3 of an 8-row block, piece (lane&7)^(lane>>3)
+    uint32_t vos;          // lane scale offset: lanes 0-31 scale pair, 32-63 min pair of the wave's row lane&31
+};
+
+// per wave: ring of 2 slots x (4 KB codes + 256 B scales); abuf: 2 x NT*16 rows x 512 B
+constexpr int kDmaSlot = 4096 + 256;
+
+// NT token tiles, NW waves of two 16-row tiles each. asrc: uniform A base (pair 0),
+// avo[k]: the lane's A offset for its k-th piece.
+template <int NT, int NW>
+__device__ __forceinline__ void pf_gemm_dma(const PfDma& R, const uint8_t* abase, const uint32_t* avo, uint8_t* abuf,
+                                            uint8_t* ring, int nk, f32x4_t (*acc)[2]
+                                            ) {
+    constexpr int RPT = 8 * NT / NW;   // A DMA instructions per wave and pair
+    constexpr int ABUF = NT * 16 * 512;
+    constexpr int CS = 5;              // code + scale DMA instructions per step
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nsteps = nk >> 1;
+#pragma unroll
+    for (int mt = 0; mt < NT; ++mt) acc[mt][0] = acc[mt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const uint32_t ring_l = lds_addr(ring), abuf_l = lds_addr(abuf);
+    auto issue_cs = [&](int st) {
+        const uint32_t dst = ring_l + (st & 1) * kDmaSlot;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            dma16s(dst + i * 1024, R.cb[i >> 1] + (i & 1) * 8 * R.rowb + (int64_t)st * 128, R.voc);
+        dma4s(dst + 4096, R.sb + st * 4, R.vos);
+    };
+    auto issue_a = [&](int q) {
+        const uint32_t dst = abuf_l + (q & 1) * ABUF;
+#pragma unroll
+        for (int k = 0; k < RPT; ++k) dma16s(dst + 1024 * (wv + NW * k), abase + q * 512, avo[k]);
+    };
+    // lane-invariant LDS read offsets
+    const uint32_t co0 = 128 * n + 16 * ((0 + g) ^ (n & 7)), co1 = 128 * n + 16 * ((4 + g) ^ (n & 7));
+    issue_cs(0);
+    if (nsteps > 1) issue_cs(1);
+    issue_a(0);
+    for (int st = 0; st < nsteps; ++st) {
+        // (a) this step's codes and scales: issued after them are A(st-1) (or CS(1)), CS(st+1) if any, A(st)
+        if (st == 0) {
+            if (nsteps > 1) wait_vm<CS + RPT>(); else wait_vm<RPT>();
+        } else {
+            if (st + 1 < nsteps) wait_vm<2 * RPT + CS>(); else wait_vm<2 * RPT>();
+        }
+        uint32_t cd[2][2][4], sm[2][2];
+        const uint8_t* slot = ring + (st & 1) * kDmaSlot;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            const uint4 v0 = *reinterpret_cast<const uint4*>(slot + 2048 * jj + co0);
+            const uint4 v1 = *reinterpret_cast<const uint4*>(slot + 2048 * jj + co1);
+            cd[jj][0][0] = v0.x; cd[jj][0][1] = v0.y; cd[jj][0][2] = v0.z; cd[jj][0][3] = v0.w;
+            cd[jj][1][0] = v1.x; cd[jj][1][1] = v1.y; cd[jj][1][2] = v1.z; cd[jj][1][3] = v1.w;
+            const uint32_t sp = *reinterpret_cast<const uint32_t*>(slot + 4096 + 4 * (16 * jj + n));
+            const uint32_t mp = *reinterpret_cast<const uint32_t*>(slot + 4096 + 128 + 4 * (16 * jj + n));
+            sm[jj][0] = __builtin_amdgcn_perm(mp, sp, 0x05040100u);  // s0 | m0 << 16
+            sm[jj][1] = __builtin_amdgcn_perm(mp, sp, 0x07060302u);  // s1 | m1 << 16
+        }
+        // (b) the slot is read: refill it with step st + 2
+        wait_lgkm0();
+        if (st + 2 < nsteps) issue_cs(st + 2);
+        // (c) this wave's part of A(st) has landed (issued after it: CS(st+2) if any);
+        // the barrier publishes every wave's part and ends every read of buffer (st+1)&1
+        if (st + 2 < nsteps) wait_vm<CS>(); else wait_vm<0>();
+        __syncthreads();
+        if (st + 1 < nsteps) issue_a(st + 1);
+        // (d) the MFMAs of the pair
+        const uint8_t* A = abuf + (st & 1) * ABUF;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint4 xa[NT][4];
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    xa[mt][s] = *reinterpret_cast<const uint4*>(A + 512 * (16 * mt + n) + 16 * ((16 * h + 4 * g + s) ^ (n & 7)));
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                uint4 b[4];
+                pf_bfrag<4>(cd[jj][h], sm[jj][h], b);
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int mt = 0; mt < NT; ++mt) acc[mt][jj] = mfma16(xa[mt][s], b[s], acc[mt][jj]);
+            }
+        }
+    }
+}
+
+template <int MT, int NW, bool GATE_UP, class Epi>
+__device__ __forceinline__ void pf_dma_passes(const Prefill& F, const PfDma& R, int p0, int cnt, uint8_t* ab,
+                                              uint8_t* ringw, int nk, Epi epi) {
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int MB = MT * 16;
+    for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
+        const int nt = min(MT, (cnt - mb + 15) / 16);
+        auto pass = [&](auto NTc) {
+            constexpr int NT = decltype(NTc)::value, RPT = 8 * NT / NW;
+            uint32_t avo[RPT];
+            const uint8_t* abase;
+            if constexpr (GATE_UP) {
+                abase = uniform_ptr(F.x);
+#pragma unroll
+                for (int k = 0; k < RPT; ++k) {
+                    const int r = 2 * (wv + NW * k) + (lane >> 5);
+                    int t = F.tok[p0 + min(mb + r, cnt - 1)];
+                    t = min(max(t, 0), F.T - 1);
+                    avo[k] = (uint32_t)t * (uint32_t)F.H * 2u + 16u * ((lane & 31) ^ (r & 7));
+                }
+            } else {
+                abase = uniform_ptr(F.act + (int64_t)p0 * F.I);
+#pragma unroll
+                for (int k = 0; k < RPT; ++k) {
+                    const int r = 2 * (wv + NW * k) + (lane >> 5);
+                    const int m = min(mb + r, cnt - 1);
+                    avo[k] = (uint32_t)m * (uint32_t)F.I * 2u + 16u * ((lane & 31) ^ (r & 7));
+                }
+            }
+            f32x4_t acc[NT][2];
+            pf_gemm_dma<NT, NW>(R, abase, avo, ab, ringw, nk, acc);
+            epi(acc, mb);
+        };
+        if (MT >= 4 && nt >= 4) pass(std::integral_constant<int, (MT >= 4 ? 4 : 1)>{});
+        else if (MT >= 3 && nt == 3) pass(std::integral_constant<int, (MT >= 3 ? 3 : 1)>{});
+        else if (MT >= 2 && nt == 2) pass(std::integral_constant<int, (MT >= 2 ? 2 : 1)>{});
+        else pass(std::integral_constant<int, 1>{});
+        __syncthreads();  // the next pass reuses the A buffers and the ring
+    }
+}
+
+// gate_up with the LDS-DMA form: grid (I / (RWG/2), U, Z), NW waves of 2 tiles,
+// RWG = 32*NW rows (RWG/2 gate + RWG/2 up act columns).
+template <int MT, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gate_up_dma(const Prefill F) {
+    constexpr int RWG = 32 * NW, HR = RWG / 2, CW = 16;
+    __shared__ uint4 abuf[2 * MT * 16 * 32];
+    __shared__ uint4 ring[NW * 2 * kDmaSlot / 16];
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int c0 = blockIdx.x * HR + wv * CW, u = blockIdx.y;
+    int slot, p0, cnt;
+    const int gs = group_state(F, u, slot, p0, cnt);
+    if (gs == 0) return;
+    if (gs == 1) {
+        for (int i = lane; i < cnt * CW; i += 64)
+            F.act[(int64_t)(p0 + i / CW) * F.I + c0 + (i % CW)] = 0x7FC0;  // bf16 NaN
+        return;
+    }
+    const uint8_t* base = F.pool + (int64_t)slot * F.slot_bytes;
+    const int nk = F.H / 128;
+    PfDma R;
+    R.rowb = (int64_t)F.H / 2;
+    R.cb[0] = uniform_ptr(base + (int64_t)c0 * R.rowb);           // gate rows c0 .. c0 + 15
+    R.cb[1] = uniform_ptr(base + F.nmb + (int64_t)c0 * R.rowb);   // up rows c0 .. c0 + 15
+    R.voc = (uint32_t)((lane >> 3) * R.rowb + 16 * ((lane & 7) ^ (lane >> 3)));
+    const uint8_t* sc = base + 3 * F.nmb;                           // fp16 scales, then mins at + 3*NGM
+    R.sb = uniform_ptr(sc + (int64_t)c0 * nk * 2);
+    R.vos = (uint32_t)((lane >= 32 ? 3 * (int64_t)F.NGM * 2 : 0) + ((lane & 31) >> 4) * (int64_t)F.NGM * 2 +
+                       (lane & 15) * nk * 2);
+    uint8_t* ringw = reinterpret_cast<uint8_t*>(ring) + wv * 2 * kDmaSlot;
+    uint8_t* ab = reinterpret_cast<uint8_t*>(abuf);
+    pf_dma_passes<MT, NW, true>(F, R, p0, cnt, ab, ringw, nk, [&](auto& acc, int mb) {
+        constexpr int NT = sizeof(acc) / sizeof(acc[0]);
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = mb + mt * 16 + 4 * g + i;
+                if (m < cnt) F.act[(int64_t)(p0 + m) * F.I + c0 + n] = f32_to_bf16(silu_mul(acc[mt][0][i], acc[mt][1][i]));
+            }
+    });
+}
+
+// down with the LDS-DMA form: grid (H / RWG, U, Z), RWG = 32*NW rows.
+template <int MT, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_down_dma(const Prefill F) {
+    constexpr int RWG = 32 * NW, RW = 32;
+    __shared__ uint4 abuf[2 * MT * 16 * 32];
+    __shared__ uint4 ring[NW * 2 * kDmaSlot / 16];
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int h0 = blockIdx.x * RWG + wv * RW, u = blockIdx.y;
+    int slot, p0, cnt;
+    const int gs = group_state(F, u, slot, p0, cnt);
+    if (gs == 0) return;
+    if (gs == 1) {
+        for (int i = lane; i < cnt * RW; i += 64)
+            F.y[(int64_t)(p0 + i / RW) * F.H + h0 + (i % RW)] = __builtin_nanf("");
+        return;
+    }
+    const uint8_t* base = F.pool + (int64_t)slot * F.slot_bytes;
+    const int nk = F.I / 128;
+    PfDma R;
+    R.rowb = (int64_t)F.I / 2;
+    R.cb[0] = uniform_ptr(base + 2 * F.nmb + (int64_t)h0 * R.rowb);
+    R.cb[1] = uniform_ptr(base + 2 * F.nmb + (int64_t)(h0 + 16) * R.rowb);
+    R.voc = (uint32_t)((lane >> 3) * R.rowb + 16 * ((lane & 7) ^ (lane >> 3)));
+    const uint8_t* sc = base + 3 * F.nmb;
+    R.sb = uniform_ptr(sc + (2 * (int64_t)F.NGM + (int64_t)h0 * nk) * 2);
+    R.vos = (uint32_t)((lane >= 32 ? 3 * (int64_t)F.NGM * 2 : 0) + (lane & 31) * nk * 2);
+    uint8_t* ringw = reinterpret_cast<uint8_t*>(ring) + wv * 2 * kDmaSlot;
+    uint8_t* ab = reinterpret_cast<uint8_t*>(abuf);
+    pf_dma_passes<MT, NW, false>(F, R, p0, cnt, ab, ringw, nk, [&](auto& acc, int mb) {
+        constexpr int NT = sizeof(acc) / sizeof(acc[0]);
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = mb + mt * 16 + 4 * g + i;
+                if (m < cnt) {
+                    const float wp = F.w[p0 + m];
+                    float* dst = F.y + (int64_t)(p0 + m) * F.H + h0 + n;
+                    dst[0] = wp * acc[mt][0][i];
+                    dst[16] = wp * acc[mt][1][i];
+                }
+            }
+    });
 }
 
 // s = sum_j y[back[t*k + j]][h], j in ascending expert id (back = -1: no pair in
@@ -520,12 +821,33 @@ __global__ __launch_bounds__(256) void k_pf_combine(const float* __restrict__ y,
 // share a larger group's passes
 template <int BITS, int MT>
 static void launch_pf_mt(const Prefill& F, int ngroups, int max_group, hipStream_t st) {
-    constexpr int NW = MT >= 4 ? 8 : 4;
+    constexpr int NW = MT >= 4 ? 8 : 4, RWG = 256;
     const unsigned z = (unsigned)std::min(64, std::max(1, (max_group + MT * 16 - 1) / (MT * 16)));
-    hipLaunchKernelGGL((k_pf_gate_up<BITS, MT, NW>), dim3((unsigned)(F.I / 128), (unsigned)ngroups, z),
-                       dim3(64 * NW), 0, st, F);
-    hipLaunchKernelGGL((k_pf_down<BITS, MT, NW>), dim3((unsigned)(F.H / 256), (unsigned)ngroups, z), dim3(64 * NW),
-                       0, st, F);
+    if constexpr (BITS == 4) {
+        // the LDS-DMA form: an even number of K groups in both GEMMs, at most kPfSmSteps, and
+        // x and act addressable with 32-bit offsets
+        const int nkg = F.H / 128, nkd = F.I / 128;
+        const bool off32 = (int64_t)F.T * F.H * 2 < (int64_t(1) << 31) && (int64_t)F.P * F.I * 2 < (int64_t(1) << 31);
+        if (nkg % 2 == 0 && nkd % 2 == 0 && nkg <= kPfSmSteps && nkd <= kPfSmSteps && off32) {
+            constexpr int NWD = MT >= 4 ? 8 : 4, RWD = 32 * NWD;
+            if (F.I % (RWD / 2) == 0 && F.H % RWD == 0) {
+                hipLaunchKernelGGL((k_pf_gate_up_dma<MT, NWD>), dim3((unsigned)(F.I / (RWD / 2)), (unsigned)ngroups, z),
+                                   dim3(64 * NWD), 0, st, F);
+                hipLaunchKernelGGL((k_pf_down_dma<MT, NWD>), dim3((unsigned)(F.H / RWD), (unsigned)ngroups, z),
+                                   dim3(64 * NWD), 0, st, F);
+                return;
+            }
+        }
+    }
+    const dim3 ggu((unsigned)(F.I / (RWG / 2)), (unsigned)ngroups, z), gdn((unsigned)(F.H / RWG), (unsigned)ngroups, z);
+    if (F.H / 128 <= kPfSmSteps)
+        hipLaunchKernelGGL((k_pf_gate_up<BITS, MT, NW, RWG, true>), ggu, dim3(64 * NW), 0, st, F);
+    else
+        hipLaunchKernelGGL((k_pf_gate_up<BITS, MT, NW, RWG, false>), ggu, dim3(64 * NW), 0, st, F);
+    if (F.I / 128 <= kPfSmSteps)
+        hipLaunchKernelGGL((k_pf_down<BITS, MT, NW, RWG, true>), gdn, dim3(64 * NW), 0, st, F);
+    else
+        hipLaunchKernelGGL((k_pf_down<BITS, MT, NW, RWG, false>), gdn, dim3(64 * NW), 0, st, F);
 }
 template <int BITS>
 static void launch_pf(const Prefill& F, int ngroups, int max_group, hipStream_t st) {
