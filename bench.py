@@ -930,7 +930,7 @@ def main():
         for spec in a.summarize_c5:
             t, st_csv, log = spec.split(":")
             runs.append((int(t), st_csv, log))
-        cmds = [f"cd /tmp && TMPDIR=/tmp rocprofv3 --kernel-trace --stats --output-format csv -d "
+        cmds = [f"cd /tmp && TMPDIR=/tmp timeout -s KILL 200 rocprofv3 --kernel-trace --stats --output-format csv -d "
                 f"$REPO/gpurun_out/prof_c5_t{t} -o c5 -- python3 $REPO/bench.py --workload c5 --c5-tokens {t} "
                 f"--no-cpu-baseline > $REPO/gpurun_out/prof_c5_t{t}.log" for t, _, _ in runs]
         cmds.append("python3 bench.py --summarize-c5 " + " ".join(
