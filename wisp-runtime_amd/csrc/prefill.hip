@@ -36,8 +36,8 @@
 // B[k 8*(l/16) + 0..7][col l%16], D[row 4*(l/16) + 0..3][col l%16].
 // With the weights read once per expert the path is HBM-bound for T <= 512.
 // 4-bit codes with an even number of K groups (the Qwen3 shapes) take the LDS-DMA
-// form of the two GEMMs (k_pf_gate_up_dma / k_pf_down_dma, described at
-// pf_gemm_dma): the codes of a K step arrive as whole 128-byte lines straight into
+// form of the two GEMMs (k_pf_gate_up_dmag / k_pf_down_dmag, described at
+// pf_gemm_dmag): the codes of a K step arrive as whole 128-byte lines straight into
 // LDS, two steps ahead, and the scales with them.
 #include <math.h>
 
@@ -491,36 +491,38 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
 }
 
 // ===========================================================================
-// LDS-DMA form (4-bit codes, an even number nk <= kPfSmSteps of K groups).
-// A K step is one pair of groups (256 K): for each of a wave's two 16-row tiles
-// the step's codes are one whole 128-byte line per row. Every line is fetched
-// by ONE request: global_load_lds_dwordx4 moves 64 lanes x 16 bytes = 8 rows x
-// 128 bytes straight into LDS (no VGPRs held while in flight), where each lane
-// then reads its MFMA fragment chunk. (Loads into registers in the fragment
-// layout can only cover 16 rows x 64 bytes per instruction, i.e. every line
-// in two halves, which measured 23 % slower in a loads-only run.)
-//   * codes: per wave a private ring of 2 slots x 4 KB (32 rows x 128 bytes);
-//     slot s holds step st (st % 2 == s); it is read into registers at the
-//     step's start and refilled at once with step st + 2, so two steps of
-//     codes are in flight while the step computes.
-//   * tokens (A): per pair the NT*16 rows x 512 bytes, double-buffered, loaded
-//     by all waves (DMA as well) and published by the step's barrier.
+// LDS-DMA form (4-bit codes, an even number nk <= kPfSmSteps of K groups):
+// pf_gemm_dmag, k_pf_gate_up_dmag, k_pf_down_dmag.
+// A workgroup of 4 waves owns 128 weight rows, a wave 32 (two 16-row tiles).
+// A K step is one pair of groups (256 K): for each row the step's codes are one
+// whole 128-byte line, and every line is fetched by ONE request:
+// global_load_lds_dwordx4 moves 64 lanes x 16 bytes = 8 rows x 128 bytes
+// straight into LDS (no VGPRs held while in flight), where each lane then reads
+// its MFMA fragment chunk. (Loads into registers in the fragment layout can only
+// cover 16 rows x 64 bytes per instruction, i.e. every line in two halves, which
+// measured 23 % slower in a loads-only run.)
+//   * codes: per wave a private ring of 2 slots x (4 KB codes + 256 B of the
+//     rows' fp16 scale and min pairs); slot s holds step st (st % 2 == s); it
+//     is read into registers at the step's start and refilled with step st + 2,
+//     so two steps of codes are in flight while the step computes.
+//   * tokens (A): the NT*16 rows x 256 bytes of one quant group, double-
+//     buffered, loaded by all waves (DMA as well) and published by a barrier
+//     per group. Staging per group keeps a workgroup at 2 x NT*16*256 + 34 KB of
+//     LDS, so two (NT = 4) or three workgroups share a CU and one's start-up runs
+//     beside the others' steps.
+//   * the step's codes are issued in two parts, tile 0 after the first group's
+//     A and tile 1 + scales after the second's, so every A wait has a later DMA
+//     behind it and never drains the code prefetch.
 //   * in LDS, piece p (16 bytes) of row r is stored at position p ^ (r & 7):
 //     the 8 lanes of a 128-bit LDS read phase (rows n..n+7, one piece) then hit
 //     8 different bank groups.
 // The compiler neither emits nor counts these loads, so every wait for them is
 // an explicit s_waitcnt vmcnt(n), n = the number of DMA instructions this wave
 // issued after the awaited ones (vector memory loads complete in order), and
-// nothing else in the loop issues vector memory loads.
+// nothing else in the loop issues vector memory loads. Where fewer DMAs follow
+// near the end of a tile the count is smaller: waiting longer is always safe.
 // ===========================================================================
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
-// 64 lanes x 16 bytes from the lanes' global addresses to LDS [lds, lds + 1024)
-__device__ __forceinline__ void dma16(uint32_t lds, const void* g) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :
-                 : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
-                 : "memory");
-}
 // s_waitcnt vmcnt(n) (expcnt and lgkmcnt not waited for), gfx9 encoding
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -533,7 +535,8 @@ __device__ __forceinline__ void wait_lgkm0() {
     asm volatile("" ::: "memory");
 }
 
-// base (SGPR pair) + per-lane 32-bit offset forms: no 64-bit address arithmetic per lane
+// 64 lanes x 16 (dma16s) or 4 (dma4s) bytes from sbase + each lane's 32-bit offset to
+// LDS [lds, lds + 64*size): the base in an SGPR pair, no 64-bit address arithmetic per lane
 __device__ __forceinline__ void dma16s(uint32_t lds, const void* sbase, uint32_t voff) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                  :
@@ -561,47 +564,57 @@ struct PfDma {
     uint32_t vos;          // lane scale offset: lanes 0-31 scale pair, 32-63 min pair of the wave's row lane&31
 };
 
-// per wave: ring of 2 slots x (4 KB codes + 256 B scales); abuf: 2 x NT*16 rows x 512 B
+// per wave: ring of 2 slots x (4 KB codes + 256 B scales)
 constexpr int kDmaSlot = 4096 + 256;
 
-// NT token tiles, NW waves of two 16-row tiles each. asrc: uniform A base (pair 0),
-// avo[k]: the lane's A offset for its k-th piece.
+// NT token tiles, NW waves of two 16-row tiles each; abase: uniform A base (group 0),
+// avo[k]: the lane's A offset for its k-th piece; abuf: 2 x NT*16 rows x 256 B;
+// ring: this wave's 2 slots.
 template <int NT, int NW>
-__device__ __forceinline__ void pf_gemm_dma(const PfDma& R, const uint8_t* abase, const uint32_t* avo, uint8_t* abuf,
-                                            uint8_t* ring, int nk, f32x4_t (*acc)[2]
-                                            ) {
-    constexpr int RPT = 8 * NT / NW;   // A DMA instructions per wave and pair
-    constexpr int ABUF = NT * 16 * 512;
-    constexpr int CS = 5;              // code + scale DMA instructions per step
+__device__ __forceinline__ void pf_gemm_dmag(const PfDma& R, const uint8_t* abase, const uint32_t* avo, uint8_t* abuf,
+                                             uint8_t* ring, int nk, f32x4_t (*acc)[2]) {
+    constexpr int RPTG = 4 * NT / NW;  // A DMA instructions per wave and group
+    static_assert(RPTG >= 1 && (4 * NT) % NW == 0, "A pieces per wave");
+    constexpr int ABUF = NT * 16 * 256;
+    constexpr int CA = 2, CB = 3;      // code DMAs of tile 0; of tile 1 + scales
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nsteps = nk >> 1;
 #pragma unroll
     for (int mt = 0; mt < NT; ++mt) acc[mt][0] = acc[mt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const uint32_t ring_l = lds_addr(ring), abuf_l = lds_addr(abuf);
-    auto issue_cs = [&](int st) {
+    auto issue_ca = [&](int st) {
         const uint32_t dst = ring_l + (st & 1) * kDmaSlot;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            dma16s(dst + i * 1024, R.cb[i >> 1] + (i & 1) * 8 * R.rowb + (int64_t)st * 128, R.voc);
+        for (int i = 0; i < 2; ++i) dma16s(dst + i * 1024, R.cb[0] + i * 8 * R.rowb + (int64_t)st * 128, R.voc);
+    };
+    auto issue_cb = [&](int st) {
+        const uint32_t dst = ring_l + (st & 1) * kDmaSlot;
+#pragma unroll
+        for (int i = 2; i < 4; ++i) dma16s(dst + i * 1024, R.cb[1] + (i & 1) * 8 * R.rowb + (int64_t)st * 128, R.voc);
         dma4s(dst + 4096, R.sb + st * 4, R.vos);
     };
-    auto issue_a = [&](int q) {
-        const uint32_t dst = abuf_l + (q & 1) * ABUF;
+    auto issue_a = [&](int G) {
+        const uint32_t dst = abuf_l + (G & 1) * ABUF;
 #pragma unroll
-        for (int k = 0; k < RPT; ++k) dma16s(dst + 1024 * (wv + NW * k), abase + q * 512, avo[k]);
+        for (int k = 0; k < RPTG; ++k) dma16s(dst + 1024 * (wv + NW * k), abase + G * 256, avo[k]);
     };
-    // lane-invariant LDS read offsets
     const uint32_t co0 = 128 * n + 16 * ((0 + g) ^ (n & 7)), co1 = 128 * n + 16 * ((4 + g) ^ (n & 7));
-    issue_cs(0);
-    if (nsteps > 1) issue_cs(1);
+    issue_ca(0);
+    issue_cb(0);
+    if (nsteps > 1) {
+        issue_ca(1);
+        issue_cb(1);
+    }
     issue_a(0);
     for (int st = 0; st < nsteps; ++st) {
-        // (a) this step's codes and scales: issued after them are A(st-1) (or CS(1)), CS(st+1) if any, A(st)
+        // (a) this step's codes and scales (the later part, CB(st), is the one waited for)
         if (st == 0) {
-            if (nsteps > 1) wait_vm<CS + RPT>(); else wait_vm<RPT>();
+            if (nsteps > 1) wait_vm<CA + CB + RPTG>(); else wait_vm<RPTG>();
+        } else if (st == 1) {
+            if (nsteps > 2) wait_vm<3 * RPTG + CA + CB>(); else wait_vm<3 * RPTG>();
         } else {
-            if (st + 1 < nsteps) wait_vm<2 * RPT + CS>(); else wait_vm<2 * RPT>();
+            if (st + 1 < nsteps) wait_vm<2 * RPTG + CA + CB>(); else wait_vm<2 * RPTG>();
         }
         uint32_t cd[2][2][4], sm[2][2];
         const uint8_t* slot = ring + (st & 1) * kDmaSlot;
@@ -613,27 +626,31 @@ __device__ __forceinline__ void pf_gemm_dma(const PfDma& R, const uint8_t* abase
             cd[jj][1][0] = v1.x; cd[jj][1][1] = v1.y; cd[jj][1][2] = v1.z; cd[jj][1][3] = v1.w;
             const uint32_t sp = *reinterpret_cast<const uint32_t*>(slot + 4096 + 4 * (16 * jj + n));
             const uint32_t mp = *reinterpret_cast<const uint32_t*>(slot + 4096 + 128 + 4 * (16 * jj + n));
-            sm[jj][0] = __builtin_amdgcn_perm(mp, sp, 0x05040100u);  // s0 | m0 << 16
-            sm[jj][1] = __builtin_amdgcn_perm(mp, sp, 0x07060302u);  // s1 | m1 << 16
+            sm[jj][0] = __builtin_amdgcn_perm(mp, sp, 0x05040100u);
+            sm[jj][1] = __builtin_amdgcn_perm(mp, sp, 0x07060302u);
         }
-        // (b) the slot is read: refill it with step st + 2
-        wait_lgkm0();
-        if (st + 2 < nsteps) issue_cs(st + 2);
-        // (c) this wave's part of A(st) has landed (issued after it: CS(st+2) if any);
-        // the barrier publishes every wave's part and ends every read of buffer (st+1)&1
-        if (st + 2 < nsteps) wait_vm<CS>(); else wait_vm<0>();
-        __syncthreads();
-        if (st + 1 < nsteps) issue_a(st + 1);
-        // (d) the MFMAs of the pair
-        const uint8_t* A = abuf + (st & 1) * ABUF;
+        wait_lgkm0();  // the slot is read: it may be refilled below
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
+            const int G = 2 * st + h;
+            // A(G): issued after it are CB(st+1) (h = 0, st >= 1) or CA(st+2) (h = 1), if any
+            if (h == 0) {
+                if (st >= 1 && st + 1 < nsteps) wait_vm<CB>(); else wait_vm<0>();
+            } else {
+                if (st + 2 < nsteps) wait_vm<CA>(); else wait_vm<0>();
+            }
+            __syncthreads();  // every wave's part of A(G) landed; every read of buffer (G+1)&1 ended
+            if (G + 1 < nk) issue_a(G + 1);
+            if (st + 2 < nsteps) {
+                if (h == 0) issue_ca(st + 2); else issue_cb(st + 2);
+            }
+            const uint8_t* A = abuf + (G & 1) * ABUF;
             uint4 xa[NT][4];
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
-                    xa[mt][s] = *reinterpret_cast<const uint4*>(A + 512 * (16 * mt + n) + 16 * ((16 * h + 4 * g + s) ^ (n & 7)));
+                    xa[mt][s] = *reinterpret_cast<const uint4*>(A + 256 * (16 * mt + n) + 16 * ((4 * g + s) ^ (n & 7)));
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
                 uint4 b[4];
@@ -648,53 +665,51 @@ __device__ __forceinline__ void pf_gemm_dma(const PfDma& R, const uint8_t* abase
 }
 
 template <int MT, int NW, bool GATE_UP, class Epi>
-__device__ __forceinline__ void pf_dma_passes(const Prefill& F, const PfDma& R, int p0, int cnt, uint8_t* ab,
-                                              uint8_t* ringw, int nk, Epi epi) {
+__device__ __forceinline__ void pf_dmag_passes(const Prefill& F, const PfDma& R, int p0, int cnt, uint8_t* ab,
+                                               uint8_t* ringw, int nk, Epi epi) {
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     constexpr int MB = MT * 16;
     for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
         const int nt = min(MT, (cnt - mb + 15) / 16);
         auto pass = [&](auto NTc) {
-            constexpr int NT = decltype(NTc)::value, RPT = 8 * NT / NW;
-            uint32_t avo[RPT];
+            constexpr int NT = decltype(NTc)::value, RPTG = 4 * NT / NW;
+            uint32_t avo[RPTG];
             const uint8_t* abase;
             if constexpr (GATE_UP) {
                 abase = uniform_ptr(F.x);
 #pragma unroll
-                for (int k = 0; k < RPT; ++k) {
-                    const int r = 2 * (wv + NW * k) + (lane >> 5);
+                for (int k = 0; k < RPTG; ++k) {
+                    const int r = 4 * (wv + NW * k) + (lane >> 4);
                     int t = F.tok[p0 + min(mb + r, cnt - 1)];
                     t = min(max(t, 0), F.T - 1);
-                    avo[k] = (uint32_t)t * (uint32_t)F.H * 2u + 16u * ((lane & 31) ^ (r & 7));
+                    avo[k] = (uint32_t)t * (uint32_t)F.H * 2u + 16u * ((lane & 15) ^ (r & 7));
                 }
             } else {
                 abase = uniform_ptr(F.act + (int64_t)p0 * F.I);
 #pragma unroll
-                for (int k = 0; k < RPT; ++k) {
-                    const int r = 2 * (wv + NW * k) + (lane >> 5);
+                for (int k = 0; k < RPTG; ++k) {
+                    const int r = 4 * (wv + NW * k) + (lane >> 4);
                     const int m = min(mb + r, cnt - 1);
-                    avo[k] = (uint32_t)m * (uint32_t)F.I * 2u + 16u * ((lane & 31) ^ (r & 7));
+                    avo[k] = (uint32_t)m * (uint32_t)F.I * 2u + 16u * ((lane & 15) ^ (r & 7));
                 }
             }
             f32x4_t acc[NT][2];
-            pf_gemm_dma<NT, NW>(R, abase, avo, ab, ringw, nk, acc);
+            pf_gemm_dmag<NT, NW>(R, abase, avo, ab, ringw, nk, acc);
             epi(acc, mb);
         };
         if (MT >= 4 && nt >= 4) pass(std::integral_constant<int, (MT >= 4 ? 4 : 1)>{});
         else if (MT >= 3 && nt == 3) pass(std::integral_constant<int, (MT >= 3 ? 3 : 1)>{});
         else if (MT >= 2 && nt == 2) pass(std::integral_constant<int, (MT >= 2 ? 2 : 1)>{});
         else pass(std::integral_constant<int, 1>{});
-        __syncthreads();  // the next pass reuses the A buffers and the ring
+        __syncthreads();
     }
 }
 
-// gate_up with the LDS-DMA form: grid (I / (RWG/2), U, Z), NW waves of 2 tiles,
-// RWG = 32*NW rows (RWG/2 gate + RWG/2 up act columns).
 template <int MT, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gate_up_dma(const Prefill F) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gate_up_dmag(const Prefill F) {
     constexpr int RWG = 32 * NW, HR = RWG / 2, CW = 16;
-    __shared__ uint4 abuf[2 * MT * 16 * 32];
+    __shared__ uint4 abuf[2 * MT * 16 * 16];
     __shared__ uint4 ring[NW * 2 * kDmaSlot / 16];
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
@@ -704,23 +719,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     if (gs == 0) return;
     if (gs == 1) {
         for (int i = lane; i < cnt * CW; i += 64)
-            F.act[(int64_t)(p0 + i / CW) * F.I + c0 + (i % CW)] = 0x7FC0;  // bf16 NaN
+            F.act[(int64_t)(p0 + i / CW) * F.I + c0 + (i % CW)] = 0x7FC0;
         return;
     }
     const uint8_t* base = F.pool + (int64_t)slot * F.slot_bytes;
     const int nk = F.H / 128;
     PfDma R;
     R.rowb = (int64_t)F.H / 2;
-    R.cb[0] = uniform_ptr(base + (int64_t)c0 * R.rowb);           // gate rows c0 .. c0 + 15
-    R.cb[1] = uniform_ptr(base + F.nmb + (int64_t)c0 * R.rowb);   // up rows c0 .. c0 + 15
+    R.cb[0] = uniform_ptr(base + (int64_t)c0 * R.rowb);
+    R.cb[1] = uniform_ptr(base + F.nmb + (int64_t)c0 * R.rowb);
     R.voc = (uint32_t)((lane >> 3) * R.rowb + 16 * ((lane & 7) ^ (lane >> 3)));
-    const uint8_t* sc = base + 3 * F.nmb;                           // fp16 scales, then mins at + 3*NGM
+    const uint8_t* sc = base + 3 * F.nmb;
     R.sb = uniform_ptr(sc + (int64_t)c0 * nk * 2);
     R.vos = (uint32_t)((lane >= 32 ? 3 * (int64_t)F.NGM * 2 : 0) + ((lane & 31) >> 4) * (int64_t)F.NGM * 2 +
                        (lane & 15) * nk * 2);
     uint8_t* ringw = reinterpret_cast<uint8_t*>(ring) + wv * 2 * kDmaSlot;
     uint8_t* ab = reinterpret_cast<uint8_t*>(abuf);
-    pf_dma_passes<MT, NW, true>(F, R, p0, cnt, ab, ringw, nk, [&](auto& acc, int mb) {
+    pf_dmag_passes<MT, NW, true>(F, R, p0, cnt, ab, ringw, nk, [&](auto& acc, int mb) {
         constexpr int NT = sizeof(acc) / sizeof(acc[0]);
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt)
@@ -732,11 +747,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     });
 }
 
-// down with the LDS-DMA form: grid (H / RWG, U, Z), RWG = 32*NW rows.
 template <int MT, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_down_dma(const Prefill F) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_down_dmag(const Prefill F) {
     constexpr int RWG = 32 * NW, RW = 32;
-    __shared__ uint4 abuf[2 * MT * 16 * 32];
+    __shared__ uint4 abuf[2 * MT * 16 * 16];
     __shared__ uint4 ring[NW * 2 * kDmaSlot / 16];
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
@@ -761,7 +775,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     R.vos = (uint32_t)((lane >= 32 ? 3 * (int64_t)F.NGM * 2 : 0) + (lane & 31) * nk * 2);
     uint8_t* ringw = reinterpret_cast<uint8_t*>(ring) + wv * 2 * kDmaSlot;
     uint8_t* ab = reinterpret_cast<uint8_t*>(abuf);
-    pf_dma_passes<MT, NW, false>(F, R, p0, cnt, ab, ringw, nk, [&](auto& acc, int mb) {
+    pf_dmag_passes<MT, NW, false>(F, R, p0, cnt, ab, ringw, nk, [&](auto& acc, int mb) {
         constexpr int NT = sizeof(acc) / sizeof(acc[0]);
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt)
@@ -829,12 +843,14 @@ static void launch_pf_mt(const Prefill& F, int ngroups, int max_group, hipStream
         const int nkg = F.H / 128, nkd = F.I / 128;
         const bool off32 = (int64_t)F.T * F.H * 2 < (int64_t(1) << 31) && (int64_t)F.P * F.I * 2 < (int64_t(1) << 31);
         if (nkg % 2 == 0 && nkd % 2 == 0 && nkg <= kPfSmSteps && nkd <= kPfSmSteps && off32) {
-            constexpr int NWD = MT >= 4 ? 8 : 4, RWD = 32 * NWD;
-            if (F.I % (RWD / 2) == 0 && F.H % RWD == 0) {
-                hipLaunchKernelGGL((k_pf_gate_up_dma<MT, NWD>), dim3((unsigned)(F.I / (RWD / 2)), (unsigned)ngroups, z),
-                                   dim3(64 * NWD), 0, st, F);
-                hipLaunchKernelGGL((k_pf_down_dma<MT, NWD>), dim3((unsigned)(F.H / RWD), (unsigned)ngroups, z),
-                                   dim3(64 * NWD), 0, st, F);
+            // 4-wave workgroups of 128 rows, token tiles staged per quant group: two or three
+            // workgroups share a CU (measured on C5 against 8-wave workgroups with the tile
+            // staged per group pair, one per CU: T = 256 119.7 -> 114.3 us, 512 150.5 -> 142.3)
+            if (F.I % 64 == 0 && F.H % 128 == 0) {
+                hipLaunchKernelGGL((k_pf_gate_up_dmag<MT, 4>), dim3((unsigned)(F.I / 64), (unsigned)ngroups, z),
+                                   dim3(256), 0, st, F);
+                hipLaunchKernelGGL((k_pf_down_dmag<MT, 4>), dim3((unsigned)(F.H / 128), (unsigned)ngroups, z),
+                                   dim3(256), 0, st, F);
                 return;
             }
         }
