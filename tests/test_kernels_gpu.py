@@ -449,6 +449,36 @@ def test_moe_prefill_matches_oracle(bits, E, H, I, T, k, hot):
     assert np.max(np.abs(got - ref)) <= 2e-2 * np.max(np.abs(ref))
 
 
+# 4-bit with an even number (<= 16) of quant groups in both GEMMs takes the LDS-DMA form
+# (hand-counted waits): tiles of 1, 2, 4 and 8 K steps, single and several passes per group.
+@pytest.mark.parametrize("E,H,I,T,k,hot", [(5, 256, 256, 3, 2, False), (5, 512, 256, 33, 2, False),
+                                          (6, 1024, 512, 70, 3, False), (4, 512, 256, 150, 2, True),
+                                          (8, 2048, 1536, 24, 4, False), (3, 1024, 256, 1, 3, False)])
+def test_moe_prefill_lds_dma_shapes(E, H, I, T, k, hot):
+    pool, x, sel, rw = _prefill_case(E, H, I, T, k, 4, seed=E * 7 + T, hot=hot)
+    out = _run_prefill(pool, x, sel, rw, H, I, 4)
+    ref = O.moe_prefill_f64(pool, {e: e for e in range(E)}, x, sel, rw, H, I, 4)
+    r = O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.astype(np.float32))).reshape(ref.shape)
+    got = out.float().cpu().numpy()
+    err = np.linalg.norm(got - r) / np.linalg.norm(r)
+    print(f"prefill lds-dma H={H} I={I} T={T}: rel-L2 {err:.3e}")
+    assert err <= 1e-3, err
+
+
+@pytest.mark.parametrize("chunk", [1 << 20, 16, 48])
+def test_moe_prefill_lds_dma_any_partition_and_invalid_slot(chunk, monkeypatch):
+    E, H, I, T, k = 4, 512, 256, 200, 2
+    pool, x, sel, rw = _prefill_case(E, H, I, T, k, 4, seed=91, hot=True)
+    base = _run_prefill(pool, x, sel, rw, H, I, 4).float()
+    orig = kernels._prefill_chunks
+    monkeypatch.setattr(kernels, "_prefill_chunks", lambda u, f, c, chunk_=None: orig(u, f, c, chunk))
+    got = _run_prefill(pool, x, sel, rw, H, I, 4).float()
+    assert torch.equal(got, base)
+    bad = _run_prefill(pool, x, sel, rw, H, I, 4, slots={**{e: e for e in range(E)}, 1: 77}).float().cpu()
+    hit = torch.from_numpy((sel == 1).any(axis=1))
+    assert torch.isnan(bad[hit]).all() and torch.isfinite(bad[~hit]).all()
+
+
 def test_moe_prefill_expert_chunks_accumulate_and_invalid_slot():
     E, H, I, T, k, bits = 6, 256, 128, 24, 2, 4
     pool, x, sel, rw = _prefill_case(E, H, I, T, k, bits, seed=31)
