@@ -38,7 +38,7 @@
 // 4-bit codes with an even number of K groups (the Qwen3 shapes) take the LDS-DMA
 // form of the two GEMMs (k_pf_gate_up_dmag / k_pf_down_dmag, described at
 // pf_gemm_dmag): the codes of a K step arrive as whole 128-byte lines straight into
-// LDS, two steps ahead, and the scales with them.
+// LDS, one step ahead, and the scales with them.
 #include <math.h>
 
 #include <algorithm>
@@ -501,18 +501,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
 // its MFMA fragment chunk. (Loads into registers in the fragment layout can only
 // cover 16 rows x 64 bytes per instruction, i.e. every line in two halves, which
 // measured 23 % slower in a loads-only run.)
-//   * codes: per wave a private ring of 2 slots x (4 KB codes + 256 B of the
-//     rows' fp16 scale and min pairs); slot s holds step st (st % 2 == s); it
-//     is read into registers at the step's start and refilled with step st + 2,
-//     so two steps of codes are in flight while the step computes.
+//   * codes: per wave one private slot of 4 KB codes + 256 B of the rows' fp16
+//     scale and min pairs; it is read into registers at the step's start and
+//     then refilled with the next step's codes, which have the whole step to
+//     arrive.
 //   * tokens (A): the NT*16 rows x 256 bytes of one quant group, double-
 //     buffered, loaded by all waves (DMA as well) and published by a barrier
-//     per group. Staging per group keeps a workgroup at 2 x NT*16*256 + 34 KB of
-//     LDS, so two (NT = 4) or three workgroups share a CU and one's start-up runs
-//     beside the others' steps.
-//   * the step's codes are issued in two parts, tile 0 after the first group's
-//     A and tile 1 + scales after the second's, so every A wait has a later DMA
-//     behind it and never drains the code prefetch.
+//     per group. A workgroup holds 2 x NT*16*256 B + 17 KB of LDS, so three
+//     (NT = 4) or four (NT = 2) workgroups share a CU: measured on C5 at T = 512,
+//     three workgroups with one slot per wave beat two with two slots (125-129 µs
+//     against 142-145), the SIMDs' dequantisation, MFMA and LDS work then
+//     covering each other's waits.
+//   * A(2st+1) is issued before the step's code DMAs, so the step's one inner
+//     wait (for A(2st+1)) leaves the next step's codes in flight.
 //   * in LDS, piece p (16 bytes) of row r is stored at position p ^ (r & 7):
 //     the 8 lanes of a 128-bit LDS read phase (rows n..n+7, one piece) then hit
 //     8 different bank groups.
@@ -564,35 +565,33 @@ struct PfDma {
     uint32_t vos;          // lane scale offset: lanes 0-31 scale pair, 32-63 min pair of the wave's row lane&31
 };
 
-// per wave: ring of 2 slots x (4 KB codes + 256 B scales)
+// per wave: one slot of 4 KB codes + 256 B scales
 constexpr int kDmaSlot = 4096 + 256;
 
 // NT token tiles, NW waves of two 16-row tiles each; abase: uniform A base (group 0),
 // avo[k]: the lane's A offset for its k-th piece; abuf: 2 x NT*16 rows x 256 B;
-// ring: this wave's 2 slots.
+// ring: this wave's slot. Issue order of step st (C = the step's 5 code and scale DMAs,
+// A(G) = the RPTG token DMAs of group G):
+//   wait all, barrier | A(2st+1) | read the slot | C(st+1) | group 2st
+//   wait A(2st+1) (C(st+1) stays in flight), barrier | A(2st+2) | group 2st+1
 template <int NT, int NW>
 __device__ __forceinline__ void pf_gemm_dmag(const PfDma& R, const uint8_t* abase, const uint32_t* avo, uint8_t* abuf,
                                              uint8_t* ring, int nk, f32x4_t (*acc)[2]) {
     constexpr int RPTG = 4 * NT / NW;  // A DMA instructions per wave and group
     static_assert(RPTG >= 1 && (4 * NT) % NW == 0, "A pieces per wave");
     constexpr int ABUF = NT * 16 * 256;
-    constexpr int CA = 2, CB = 3;      // code DMAs of tile 0; of tile 1 + scales
+    constexpr int CN = 5;  // code and scale DMA instructions per step
     const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nsteps = nk >> 1;
 #pragma unroll
     for (int mt = 0; mt < NT; ++mt) acc[mt][0] = acc[mt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const uint32_t ring_l = lds_addr(ring), abuf_l = lds_addr(abuf);
-    auto issue_ca = [&](int st) {
-        const uint32_t dst = ring_l + (st & 1) * kDmaSlot;
+    auto issue_c = [&](int st) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) dma16s(dst + i * 1024, R.cb[0] + i * 8 * R.rowb + (int64_t)st * 128, R.voc);
-    };
-    auto issue_cb = [&](int st) {
-        const uint32_t dst = ring_l + (st & 1) * kDmaSlot;
-#pragma unroll
-        for (int i = 2; i < 4; ++i) dma16s(dst + i * 1024, R.cb[1] + (i & 1) * 8 * R.rowb + (int64_t)st * 128, R.voc);
-        dma4s(dst + 4096, R.sb + st * 4, R.vos);
+        for (int i = 0; i < 4; ++i)
+            dma16s(ring_l + i * 1024, R.cb[i >> 1] + (i & 1) * 8 * R.rowb + (int64_t)st * 128, R.voc);
+        dma4s(ring_l + 4096, R.sb + st * 4, R.vos);
     };
     auto issue_a = [&](int G) {
         const uint32_t dst = abuf_l + (G & 1) * ABUF;
@@ -600,49 +599,33 @@ __device__ __forceinline__ void pf_gemm_dmag(const PfDma& R, const uint8_t* abas
         for (int k = 0; k < RPTG; ++k) dma16s(dst + 1024 * (wv + NW * k), abase + G * 256, avo[k]);
     };
     const uint32_t co0 = 128 * n + 16 * ((0 + g) ^ (n & 7)), co1 = 128 * n + 16 * ((4 + g) ^ (n & 7));
-    issue_ca(0);
-    issue_cb(0);
-    if (nsteps > 1) {
-        issue_ca(1);
-        issue_cb(1);
-    }
+    issue_c(0);
     issue_a(0);
     for (int st = 0; st < nsteps; ++st) {
-        // (a) this step's codes and scales (the later part, CB(st), is the one waited for)
-        if (st == 0) {
-            if (nsteps > 1) wait_vm<CA + CB + RPTG>(); else wait_vm<RPTG>();
-        } else if (st == 1) {
-            if (nsteps > 2) wait_vm<3 * RPTG + CA + CB>(); else wait_vm<3 * RPTG>();
-        } else {
-            if (st + 1 < nsteps) wait_vm<2 * RPTG + CA + CB>(); else wait_vm<2 * RPTG>();
-        }
+        wait_vm<0>();     // C(st) and A(2st)
+        __syncthreads();  // every wave's part of A(2st) landed; every read of group 2st-1 ended
+        issue_a(2 * st + 1);
         uint32_t cd[2][2][4], sm[2][2];
-        const uint8_t* slot = ring + (st & 1) * kDmaSlot;
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
-            const uint4 v0 = *reinterpret_cast<const uint4*>(slot + 2048 * jj + co0);
-            const uint4 v1 = *reinterpret_cast<const uint4*>(slot + 2048 * jj + co1);
+            const uint4 v0 = *reinterpret_cast<const uint4*>(ring + 2048 * jj + co0);
+            const uint4 v1 = *reinterpret_cast<const uint4*>(ring + 2048 * jj + co1);
             cd[jj][0][0] = v0.x; cd[jj][0][1] = v0.y; cd[jj][0][2] = v0.z; cd[jj][0][3] = v0.w;
             cd[jj][1][0] = v1.x; cd[jj][1][1] = v1.y; cd[jj][1][2] = v1.z; cd[jj][1][3] = v1.w;
-            const uint32_t sp = *reinterpret_cast<const uint32_t*>(slot + 4096 + 4 * (16 * jj + n));
-            const uint32_t mp = *reinterpret_cast<const uint32_t*>(slot + 4096 + 128 + 4 * (16 * jj + n));
+            const uint32_t sp = *reinterpret_cast<const uint32_t*>(ring + 4096 + 4 * (16 * jj + n));
+            const uint32_t mp = *reinterpret_cast<const uint32_t*>(ring + 4096 + 128 + 4 * (16 * jj + n));
             sm[jj][0] = __builtin_amdgcn_perm(mp, sp, 0x05040100u);
             sm[jj][1] = __builtin_amdgcn_perm(mp, sp, 0x07060302u);
         }
-        wait_lgkm0();  // the slot is read: it may be refilled below
+        wait_lgkm0();  // the slot is read: it may be refilled
+        if (st + 1 < nsteps) issue_c(st + 1);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int G = 2 * st + h;
-            // A(G): issued after it are CB(st+1) (h = 0, st >= 1) or CA(st+2) (h = 1), if any
-            if (h == 0) {
-                if (st >= 1 && st + 1 < nsteps) wait_vm<CB>(); else wait_vm<0>();
-            } else {
-                if (st + 2 < nsteps) wait_vm<CA>(); else wait_vm<0>();
-            }
-            __syncthreads();  // every wave's part of A(G) landed; every read of buffer (G+1)&1 ended
-            if (G + 1 < nk) issue_a(G + 1);
-            if (st + 2 < nsteps) {
-                if (h == 0) issue_ca(st + 2); else issue_cb(st + 2);
+            if (h == 1) {
+                if (st + 1 < nsteps) wait_vm<CN>(); else wait_vm<0>();  // A(2st+1)
+                __syncthreads();  // every wave's part of A(2st+1) landed; every read of group 2st ended
+                if (G + 1 < nk) issue_a(G + 1);
             }
             const uint8_t* A = abuf + (G & 1) * ABUF;
             uint4 xa[NT][4];
@@ -710,7 +693,7 @@ template <int MT, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gate_up_dmag(const Prefill F) {
     constexpr int RWG = 32 * NW, HR = RWG / 2, CW = 16;
     __shared__ uint4 abuf[2 * MT * 16 * 16];
-    __shared__ uint4 ring[NW * 2 * kDmaSlot / 16];
+    __shared__ uint4 ring[NW * kDmaSlot / 16];
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
     const int c0 = blockIdx.x * HR + wv * CW, u = blockIdx.y;
@@ -733,7 +716,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     R.sb = uniform_ptr(sc + (int64_t)c0 * nk * 2);
     R.vos = (uint32_t)((lane >= 32 ? 3 * (int64_t)F.NGM * 2 : 0) + ((lane & 31) >> 4) * (int64_t)F.NGM * 2 +
                        (lane & 15) * nk * 2);
-    uint8_t* ringw = reinterpret_cast<uint8_t*>(ring) + wv * 2 * kDmaSlot;
+    uint8_t* ringw = reinterpret_cast<uint8_t*>(ring) + wv * kDmaSlot;
     uint8_t* ab = reinterpret_cast<uint8_t*>(abuf);
     pf_dmag_passes<MT, NW, true>(F, R, p0, cnt, ab, ringw, nk, [&](auto& acc, int mb) {
         constexpr int NT = sizeof(acc) / sizeof(acc[0]);
@@ -751,7 +734,7 @@ template <int MT, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_down_dmag(const Prefill F) {
     constexpr int RWG = 32 * NW, RW = 32;
     __shared__ uint4 abuf[2 * MT * 16 * 16];
-    __shared__ uint4 ring[NW * 2 * kDmaSlot / 16];
+    __shared__ uint4 ring[NW * kDmaSlot / 16];
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
     const int h0 = blockIdx.x * RWG + wv * RW, u = blockIdx.y;
@@ -773,7 +756,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     const uint8_t* sc = base + 3 * F.nmb;
     R.sb = uniform_ptr(sc + (2 * (int64_t)F.NGM + (int64_t)h0 * nk) * 2);
     R.vos = (uint32_t)((lane >= 32 ? 3 * (int64_t)F.NGM * 2 : 0) + (lane & 31) * nk * 2);
-    uint8_t* ringw = reinterpret_cast<uint8_t*>(ring) + wv * 2 * kDmaSlot;
+    uint8_t* ringw = reinterpret_cast<uint8_t*>(ring) + wv * kDmaSlot;
     uint8_t* ab = reinterpret_cast<uint8_t*>(abuf);
     pf_dmag_passes<MT, NW, false>(F, R, p0, cnt, ab, ringw, nk, [&](auto& acc, int mb) {
         constexpr int NT = sizeof(acc) / sizeof(acc[0]);
