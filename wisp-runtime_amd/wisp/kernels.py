@@ -222,14 +222,13 @@ def _prefill_chunks(uniq, first, count, chunk=None):
     largest first. Each item becomes one group of the launch, so every workgroup
     of the grid has work (a launch sized for the largest group would hold idle
     workgroups that wait for a free slot before they can exit) and the longest
-    items start first. Default chunk: 64 pairs (one pass of 4 token tiles) when
-    the experts average at least 8 pairs, else 32 (measured on C5 with 4-bit codes:
-    64 is 3 % faster at T = 256, where the experts average 16 pairs, and even at
-    T = 64, where they average 5)."""
+    items start first. Default chunk: 64 pairs, one pass of 4 token tiles (measured on
+    C5 with 4-bit codes against 16, 32, 48, 96 and 128: the fastest at T = 64, 256 and
+    512)."""
     import numpy as np
 
     if chunk is None:
-        chunk = 64 if count.sum() >= 8 * len(count) else 32
+        chunk = 64
     n = (count + chunk - 1) // chunk
     ex = np.repeat(uniq, n)
     start = np.repeat(first, n) + (np.arange(n.sum()) - np.repeat(np.cumsum(n) - n, n)) * chunk
