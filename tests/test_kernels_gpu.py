@@ -453,7 +453,9 @@ def test_moe_prefill_matches_oracle(bits, E, H, I, T, k, hot):
 # (hand-counted waits): tiles of 1, 2, 4 and 8 K steps, single and several passes per group.
 @pytest.mark.parametrize("E,H,I,T,k,hot", [(5, 256, 256, 3, 2, False), (5, 512, 256, 33, 2, False),
                                           (6, 1024, 512, 70, 3, False), (4, 512, 256, 150, 2, True),
-                                          (8, 2048, 1536, 24, 4, False), (3, 1024, 256, 1, 3, False)])
+                                          (8, 2048, 1536, 24, 4, False), (3, 1024, 256, 1, 3, False),
+                                          # the C2 expert shape with a 130-pair group: a 128-token pass
+                                          (6, 2048, 768, 130, 3, True)])
 def test_moe_prefill_lds_dma_shapes(E, H, I, T, k, hot):
     pool, x, sel, rw = _prefill_case(E, H, I, T, k, 4, seed=E * 7 + T, hot=hot)
     out = _run_prefill(pool, x, sel, rw, H, I, 4)
@@ -465,7 +467,9 @@ def test_moe_prefill_lds_dma_shapes(E, H, I, T, k, hot):
     assert err <= 1e-3, err
 
 
-@pytest.mark.parametrize("chunk", [1 << 20, 16, 48])
+# chunks of 80, 96 and 128 pairs make passes of 5-8 token tiles (the token tile staged half
+# a quant group at a time); whole experts (1 << 20) several such passes per group
+@pytest.mark.parametrize("chunk", [1 << 20, 16, 48, 80, 96, 128])
 def test_moe_prefill_lds_dma_any_partition_and_invalid_slot(chunk, monkeypatch):
     E, H, I, T, k = 4, 512, 256, 200, 2
     pool, x, sel, rw = _prefill_case(E, H, I, T, k, 4, seed=91, hot=True)

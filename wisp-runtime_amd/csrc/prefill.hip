@@ -647,6 +647,92 @@ __device__ __forceinline__ void pf_gemm_dmag(const PfDma& R, const uint8_t* abas
     }
 }
 
+// Passes of NT = 5..8 token tiles (items of 65-128 pairs) in the same LDS: the token
+// tile is staged half a quant group at a time (NT*16 rows x 128 bytes: the pieces of
+// K substeps 2hh and 2hh+1 of every lane group, 8 per row, piece p of row r at
+// p ^ (r & 7)), double-buffered with one barrier per half group, so a 128-token tile
+// needs no more LDS than a 64-token tile staged per group. Each group's codes are
+// dequantized once (both halves of the group use the same B fragments), so an item of
+// up to 128 pairs pays one dequantisation of its rows instead of two.
+// Issue order of step st (stages q = 4st .. 4st+3, stage q = half q&1 of group q>>1):
+//   wait all, barrier | A(4st+1) | read the slot | C(st+1) | stage 4st
+//   wait A(4st+1) (C(st+1) in flight), barrier | A(4st+2) | stage 4st+1
+//   wait all, barrier | A(4st+3) | stage 4st+2
+//   wait all, barrier | A(4st+4) | stage 4st+3
+// avo[k]: the lane's offset of its k-th A piece for group 0, half 0 (the lane's logical
+// piece p = 2g + s' maps to the group's byte 16 * (4g + 2hh + s')).
+template <int NT, int NW>
+__device__ __forceinline__ void pf_gemm_dmag_h(const PfDma& R, const uint8_t* abase, const uint32_t* avo,
+                                               uint8_t* abuf, uint8_t* ring, int nk, f32x4_t (*acc)[2]) {
+    constexpr int RPTS = 2 * NT / NW;  // A DMA instructions per wave and stage
+    static_assert(RPTS >= 1 && (2 * NT) % NW == 0, "A pieces per wave");
+    constexpr int SBUF = NT * 16 * 128;
+    constexpr int CN = 5;
+    const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nsteps = nk >> 1, nst = 2 * nk;
+#pragma unroll
+    for (int mt = 0; mt < NT; ++mt) acc[mt][0] = acc[mt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const uint32_t ring_l = lds_addr(ring), abuf_l = lds_addr(abuf);
+    auto issue_c = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            dma16s(ring_l + i * 1024, R.cb[i >> 1] + (i & 1) * 8 * R.rowb + (int64_t)st * 128, R.voc);
+        dma4s(ring_l + 4096, R.sb + st * 4, R.vos);
+    };
+    auto issue_a = [&](int q) {
+        const uint32_t dst = abuf_l + (q & 1) * SBUF;
+        const uint8_t* src = abase + (q >> 1) * 256 + (q & 1) * 32;
+#pragma unroll
+        for (int k = 0; k < RPTS; ++k) dma16s(dst + 1024 * (wv + NW * k), src, avo[k]);
+    };
+    const uint32_t co0 = 128 * n + 16 * ((0 + g) ^ (n & 7)), co1 = 128 * n + 16 * ((4 + g) ^ (n & 7));
+    issue_c(0);
+    issue_a(0);
+    for (int st = 0; st < nsteps; ++st) {
+        uint32_t cd[2][2][4], sm[2][2];
+        uint4 b[2][4];  // B fragments of the current group, kept across its half-group barrier
+#pragma unroll
+        for (int hq = 0; hq < 4; ++hq) {
+            const int q = 4 * st + hq, h = hq >> 1, hh = hq & 1;
+            if (hq == 1 && st + 1 < nsteps) wait_vm<CN>(); else wait_vm<0>();  // A(q) (and at hq 0, C(st))
+            __syncthreads();  // every wave's part of A(q) landed; every read of stage q-1 ended
+            if (q + 1 < nst) issue_a(q + 1);
+            if (hq == 0) {
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const uint4 v0 = *reinterpret_cast<const uint4*>(ring + 2048 * jj + co0);
+                    const uint4 v1 = *reinterpret_cast<const uint4*>(ring + 2048 * jj + co1);
+                    cd[jj][0][0] = v0.x; cd[jj][0][1] = v0.y; cd[jj][0][2] = v0.z; cd[jj][0][3] = v0.w;
+                    cd[jj][1][0] = v1.x; cd[jj][1][1] = v1.y; cd[jj][1][2] = v1.z; cd[jj][1][3] = v1.w;
+                    const uint32_t sp = *reinterpret_cast<const uint32_t*>(ring + 4096 + 4 * (16 * jj + n));
+                    const uint32_t mp = *reinterpret_cast<const uint32_t*>(ring + 4096 + 128 + 4 * (16 * jj + n));
+                    sm[jj][0] = __builtin_amdgcn_perm(mp, sp, 0x05040100u);
+                    sm[jj][1] = __builtin_amdgcn_perm(mp, sp, 0x07060302u);
+                }
+                wait_lgkm0();  // the slot is read: it may be refilled
+                if (st + 1 < nsteps) issue_c(st + 1);
+            }
+            const uint8_t* A = abuf + (q & 1) * SBUF;
+            if (hh == 0) {
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) pf_bfrag<4>(cd[jj][h], sm[jj][h], b[jj]);
+            }
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt) {
+                uint4 xa[2];
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    xa[s] = *reinterpret_cast<const uint4*>(A + 128 * (16 * mt + n) + 16 * ((2 * g + s) ^ (n & 7)));
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+#pragma unroll
+                    for (int jj = 0; jj < 2; ++jj) acc[mt][jj] = mfma16(xa[s], b[jj][2 * hh + s], acc[mt][jj]);
+            }
+        }
+    }
+}
+
 template <int MT, int NW, bool GATE_UP, class Epi>
 __device__ __forceinline__ void pf_dmag_passes(const Prefill& F, const PfDma& R, int p0, int cnt, uint8_t* ab,
                                                uint8_t* ringw, int nk, Epi epi) {
@@ -681,7 +767,40 @@ __device__ __forceinline__ void pf_dmag_passes(const Prefill& F, const PfDma& R,
             pf_gemm_dmag<NT, NW>(R, abase, avo, ab, ringw, nk, acc);
             epi(acc, mb);
         };
-        if (MT >= 4 && nt >= 4) pass(std::integral_constant<int, (MT >= 4 ? 4 : 1)>{});
+        // 5..8 tiles: staged half a group at a time (pf_gemm_dmag_h); lane l of A DMA
+        // instruction k covers row 8 (wv + NW k) + l/8 at LDS position l%8
+        auto pass_h = [&](auto NTc) {
+            constexpr int NT = decltype(NTc)::value, RPTS = 2 * NT / NW;
+            uint32_t avo[RPTS];
+            const uint8_t* abase;
+#pragma unroll
+            for (int k = 0; k < RPTS; ++k) {
+                const int r = 8 * (wv + NW * k) + (lane >> 3);
+                const int p = (lane & 7) ^ (r & 7);
+                const uint32_t piece = 16u * (uint32_t)(4 * (p >> 1) + (p & 1));
+                const int m = min(mb + r, cnt - 1);
+                if constexpr (GATE_UP) {
+                    int t = F.tok[p0 + m];
+                    t = min(max(t, 0), F.T - 1);
+                    avo[k] = (uint32_t)t * (uint32_t)F.H * 2u + piece;
+                } else {
+                    avo[k] = (uint32_t)m * (uint32_t)F.I * 2u + piece;
+                }
+            }
+            if constexpr (GATE_UP) abase = uniform_ptr(F.x);
+            else abase = uniform_ptr(F.act + (int64_t)p0 * F.I);
+            f32x4_t acc[NT][2];
+            pf_gemm_dmag_h<NT, NW>(R, abase, avo, ab, ringw, nk, acc);
+            epi(acc, mb);
+        };
+        bool half = false;
+        if constexpr (MT >= 8) {
+            half = nt >= 5;
+            if (nt >= 7) pass_h(std::integral_constant<int, 8>{});
+            else if (nt >= 5) pass_h(std::integral_constant<int, 6>{});
+        }
+        if (half) {
+        } else if (MT >= 4 && nt >= 4) pass(std::integral_constant<int, (MT >= 4 ? 4 : 1)>{});
         else if (MT >= 3 && nt == 3) pass(std::integral_constant<int, (MT >= 3 ? 3 : 1)>{});
         else if (MT >= 2 && nt == 2) pass(std::integral_constant<int, (MT >= 2 ? 2 : 1)>{});
         else pass(std::integral_constant<int, 1>{});
@@ -692,7 +811,7 @@ __device__ __forceinline__ void pf_dmag_passes(const Prefill& F, const PfDma& R,
 template <int MT, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_gate_up_dmag(const Prefill F) {
     constexpr int RWG = 32 * NW, HR = RWG / 2, CW = 16;
-    __shared__ uint4 abuf[2 * MT * 16 * 16];
+    __shared__ uint4 abuf[2 * (MT > 4 ? 4 : MT) * 16 * 16];  // 5..8 tiles: staged per half group
     __shared__ uint4 ring[NW * kDmaSlot / 16];
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
@@ -733,7 +852,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
 template <int MT, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_down_dmag(const Prefill F) {
     constexpr int RWG = 32 * NW, RW = 32;
-    __shared__ uint4 abuf[2 * MT * 16 * 16];
+    __shared__ uint4 abuf[2 * (MT > 4 ? 4 : MT) * 16 * 16];  // 5..8 tiles: staged per half group
     __shared__ uint4 ring[NW * kDmaSlot / 16];
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
@@ -818,9 +937,8 @@ __global__ __launch_bounds__(256) void k_pf_combine(const float* __restrict__ y,
 // share a larger group's passes
 template <int BITS, int MT>
 static void launch_pf_mt(const Prefill& F, int ngroups, int max_group, hipStream_t st) {
-    constexpr int NW = MT >= 4 ? 8 : 4, RWG = 256;
-    const unsigned z = (unsigned)std::min(64, std::max(1, (max_group + MT * 16 - 1) / (MT * 16)));
     if constexpr (BITS == 4) {
+        const unsigned z = (unsigned)std::min(64, std::max(1, (max_group + MT * 16 - 1) / (MT * 16)));
         // the LDS-DMA form: an even number of K groups in both GEMMs, at most kPfSmSteps, and
         // x and act addressable with 32-bit offsets
         const int nkg = F.H / 128, nkd = F.I / 128;
@@ -838,15 +956,22 @@ static void launch_pf_mt(const Prefill& F, int ngroups, int max_group, hipStream
             }
         }
     }
+    if constexpr (MT > 4) {
+        launch_pf_mt<BITS, 4>(F, ngroups, max_group, st);  // passes of more than 4 tiles: LDS-DMA form only
+        return;
+    }
+    constexpr int MTR = MT > 4 ? 4 : MT;  // the register form's tile count (MT <= 4 here)
+    constexpr int NW = MTR >= 4 ? 8 : 4, RWG = 256;
+    const unsigned z = (unsigned)std::min(64, std::max(1, (max_group + MTR * 16 - 1) / (MTR * 16)));
     const dim3 ggu((unsigned)(F.I / (RWG / 2)), (unsigned)ngroups, z), gdn((unsigned)(F.H / RWG), (unsigned)ngroups, z);
     if (F.H / 128 <= kPfSmSteps)
-        hipLaunchKernelGGL((k_pf_gate_up<BITS, MT, NW, RWG, true>), ggu, dim3(64 * NW), 0, st, F);
+        hipLaunchKernelGGL((k_pf_gate_up<BITS, MTR, NW, RWG, true>), ggu, dim3(64 * NW), 0, st, F);
     else
-        hipLaunchKernelGGL((k_pf_gate_up<BITS, MT, NW, RWG, false>), ggu, dim3(64 * NW), 0, st, F);
+        hipLaunchKernelGGL((k_pf_gate_up<BITS, MTR, NW, RWG, false>), ggu, dim3(64 * NW), 0, st, F);
     if (F.I / 128 <= kPfSmSteps)
-        hipLaunchKernelGGL((k_pf_down<BITS, MT, NW, RWG, true>), gdn, dim3(64 * NW), 0, st, F);
+        hipLaunchKernelGGL((k_pf_down<BITS, MTR, NW, RWG, true>), gdn, dim3(64 * NW), 0, st, F);
     else
-        hipLaunchKernelGGL((k_pf_down<BITS, MT, NW, RWG, false>), gdn, dim3(64 * NW), 0, st, F);
+        hipLaunchKernelGGL((k_pf_down<BITS, MTR, NW, RWG, false>), gdn, dim3(64 * NW), 0, st, F);
 }
 template <int BITS>
 static void launch_pf(const Prefill& F, int ngroups, int max_group, hipStream_t st) {
@@ -854,8 +979,10 @@ static void launch_pf(const Prefill& F, int ngroups, int max_group, hipStream_t 
         launch_pf_mt<BITS, 1>(F, ngroups, max_group, st);
     else if (max_group <= 32)
         launch_pf_mt<BITS, 2>(F, ngroups, max_group, st);
-    else
+    else if (max_group <= 64)
         launch_pf_mt<BITS, 4>(F, ngroups, max_group, st);
+    else
+        launch_pf_mt<BITS, 8>(F, ngroups, max_group, st);
 }
 
 }  // namespace wisp
