@@ -372,9 +372,19 @@ __global__ __launch_bounds__(64) void k_dl_route(const uint16_t* __restrict__ lo
         for (int t = 0; t < kRouteMaxPerLane; ++t)
             if (lane + 64 * t == bi) v[t] = -1.f;
     }
-    // every lane holds the same selection: lanes r < k store id r, lanes k + r weight r
-    float tot = 0.f;
-    for (int r = 0; r < k; ++r) tot += sel_v[r];
+    // every lane holds the same selection: lanes r < k store id r, lanes k + r weight r.
+    // The renormalising sum adds adjacent pairs level by level (an odd last entry carried
+    // up), which is the order torch's sum over the last dim takes for k = 1, 2, 4, 8 and 16
+    // (checked bit for bit on MI355X; for other k torch's order differs and the sum may
+    // differ in its last bit). The softmax above sums per lane in index order, then with the
+    // xor butterfly over the 64 lanes, as torch's warp softmax does.
+    float tree[16];
+    for (int r = 0; r < k; ++r) tree[r] = sel_v[r];
+    for (int n = k; n > 1; n = (n + 1) >> 1) {
+        for (int i = 0; i < (n >> 1); ++i) tree[i] = tree[2 * i] + tree[2 * i + 1];
+        if (n & 1) tree[n >> 1] = tree[n - 1];
+    }
+    const float tot = tree[0];
     float val = 0.f;
     for (int r = 0; r < k; ++r) {
         if (lane == r) val = (float)sel_i[r];
