@@ -1,5 +1,8 @@
 """The benchmark configurations at their own shapes, checked against the oracle.
 
+C3 -- all 128 experts of the layer at 3 and 2 bits: quantizer bytes and dequantized bf16
+bit-exact with the oracle.
+
 C5 -- grouped prefill, H=2048, I=768, 128 experts, top-8, T = 64 / 256 / 512 tokens routed
 by Zipf(1.1) as the benchmark draws them, against the binary64 restatement of the
 reference's per-expert dequant + F.linear path (moe.py:131-151, oracle.moe_prefill_f64).
@@ -46,6 +49,34 @@ def _gpu_pool(E_, bits, seed):
     for e in range(E_):
         quantize(torch.randn((3, H * I), generator=gen, device=DEV) * 0.02, bits, G, out=pool[e])
     return pool, pool.cpu().numpy()
+
+
+# ---------------------------------------------------------------- C3
+@pytest.mark.parametrize("bits", [3, 2])
+def test_c3_quantize_and_dequant_bit_exact_for_all_128_experts(bits):
+    """C3's check: 128 experts of the Qwen3 shape quantized on the GPU, every byte equal to
+    the oracle quantizer's (quant.py:60-73), and dequantized on the GPU, every bf16 equal to
+    the oracle's unpack and dequant (quant.py:76-87). Weights drawn on the GPU in blocks of
+    16 experts and copied to the host for the oracle."""
+    from wisp import quant
+
+    n = H * I
+    gen = torch.Generator(device=DEV).manual_seed(300 + bits)
+    nb = quant.expert_nbytes(n, bits, G)
+    for e0 in range(0, E, 16):
+        w = torch.randn((16, 3, n), generator=gen, device=DEV) * 0.02
+        rows = torch.empty((16, nb), dtype=torch.uint8, device=DEV)
+        for j in range(16):
+            quant.quantize(w[j], bits, G, out=rows[j])
+        got_rows = rows.cpu().numpy()
+        w_host = w.cpu().numpy()
+        for j in range(16):
+            assert np.array_equal(got_rows[j], O.quantize(w_host[j], bits, G)), (bits, e0 + j)
+        deq = quant.dequant(rows, n, bits, G)
+        torch.cuda.synchronize()
+        assert np.array_equal(deq.view(torch.int16).cpu().numpy().view(np.uint16), O.dequant(got_rows, n, bits, G)), \
+            (bits, e0)
+        del w, rows, deq
 
 
 # ---------------------------------------------------------------- C5
