@@ -291,8 +291,10 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
 // into kGoOutSlices slices, one per wave. Every lane requests the partials of
 // up to kGoOutBatch experts before adding any (the sums are latency-bound);
 // the slice sums are added in slice order through LDS.
-constexpr int kGoOutCols = 64, kGoOutSlices = 8, kGoOutBatch = 8, kGoOutUnroll = 8;
-__global__ __launch_bounds__(64 * kGoOutSlices) void k_go_out(const GoLayer L) {
+// 32 columns per workgroup (90 workgroups at H = 2880): measured 33.4 us per layer against
+// 34.1 with 64 (45 workgroups), the same as 16
+constexpr int kGoOutCols = 32, kGoOutSlices = 8, kGoOutBatch = 8, kGoOutUnroll = 8;
+__global__ __launch_bounds__(kGoOutCols * kGoOutSlices) void k_go_out(const GoLayer L) {
     __shared__ float part[kGoOutSlices][kGoOutBatch][kGoOutCols];
     const int c = threadIdx.x & (kGoOutCols - 1), sl = threadIdx.x / kGoOutCols;
     const int h = blockIdx.x * kGoOutCols + c, hh = min(h, L.H - 1);
@@ -343,7 +345,7 @@ static void launch_go(const GoLayer& L, hipStream_t st) {
                        st, L);
     hipLaunchKernelGGL(k_go_down<BITS>, dim3((L.H + kGoCols - 1) / kGoCols, L.S2, L.k), dim3(64 * kGoWaves), 0, st,
                        L);
-    hipLaunchKernelGGL(k_go_out, dim3((L.H + kGoOutCols - 1) / kGoOutCols), dim3(64 * kGoOutSlices), 0, st, L);
+    hipLaunchKernelGGL(k_go_out, dim3((L.H + kGoOutCols - 1) / kGoOutCols), dim3(kGoOutCols * kGoOutSlices), 0, st, L);
 }
 
 }  // namespace wisp
