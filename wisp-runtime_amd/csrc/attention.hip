@@ -9,15 +9,15 @@
 // (v_dot2_f32_bf16), the softmax and the weighted sum are fp32, and o is
 // rounded to bf16 once.
 //
-// Two launches (split-K over positions, then a combine):
-//  k_attn_partial: one wave per (64-position chunk, KV head). Phase 1, lane =
-//    position: the lane's K row (D bf16) against the G query rows held in LDS.
-//    Phase 2: per-head max and sum of exponentials across the wave. Phase 3,
-//    lane = D/64 dimensions: the exponentials (in LDS) times the V rows, read
-//    coalesced. Writes (m, l, o[D]) per head. Chunks beyond pos exit at once.
-//  k_attn_combine: one wave per query head merges the chunks' partials with
-//    the usual max-rescaling and stores bf16.
-// HBM-bound: reads 2 * (pos+1) * D * 2 bytes per KV head.
+// Two launches (split-K over positions, then a merge):
+//  k_attn_mfma: one workgroup of 4 waves per (64-position chunk, KV head); wave w
+//    owns positions p0 + 16w .. +15 and all G query heads of the KV head. Scores and
+//    the V sums run on the matrix cores; the waves' (m, l, o) are combined in LDS
+//    into one record per (chunk, head). Chunks beyond pos exit at once.
+//  k_attn_merge: one workgroup per query head merges the chunks' records with the
+//    usual max-rescaling and stores bf16.
+// HBM-bound in principle (2 * (pos+1) * D * 2 bytes per KV head); at decode sizes
+// the two launches' dependent round trips dominate.
 #include <math.h>
 
 #include "wisp_device.hpp"
@@ -25,368 +25,239 @@
 
 namespace wisp {
 
-constexpr int kChunk = 64;  // positions per partial workgroup (one wave)
+constexpr int kChunk = 64;  // positions per k_attn_mfma workgroup (4 waves of 16)
 
-template <int D>
-struct VRow;
-template <>
-struct VRow<64> {
-    static __device__ __forceinline__ void load(const uint16_t* p, float* v) { v[0] = __uint_as_float((uint32_t)p[0] << 16); }
-};
-template <>
-struct VRow<128> {
-    static __device__ __forceinline__ void load(const uint16_t* p, float* v) {
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
-        v[0] = __uint_as_float(w << 16);
-        v[1] = __uint_as_float(w & 0xFFFF0000u);
-    }
-};
-template <>
-struct VRow<256> {
-    static __device__ __forceinline__ void load(const uint16_t* p, float* v) {
-        const uint2 w = *reinterpret_cast<const uint2*>(p);
-        v[0] = __uint_as_float(w.x << 16);
-        v[1] = __uint_as_float(w.x & 0xFFFF0000u);
-        v[2] = __uint_as_float(w.y << 16);
-        v[3] = __uint_as_float(w.y & 0xFFFF0000u);
-    }
-};
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-// partial record of one (KV head, chunk, query head g): [m, l, o[0..D-1]]
-template <int G, int D>
-__global__ __launch_bounds__(64) void k_attn_partial(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-                                                     const uint16_t* __restrict__ vc, int64_t head_stride,
-                                                     const int64_t* __restrict__ pos_ptr, int tmax, float scale,
-                                                     float* __restrict__ part, int nsplit) {
-    constexpr int DPL = D / 64;  // dimensions per lane in phase 3
-    __shared__ uint4 qs[G][D / 8];
-    __shared__ float es[kChunk][G];
-    const int lane = threadIdx.x;
-    const int split = blockIdx.x, hk = blockIdx.y;
-    const int64_t pos = *pos_ptr;
-    const int p0 = split * kChunk;
-    if ((int64_t)p0 > pos) return;  // nothing valid here; the combine reads chunks <= pos only
-    const int nvalid = (int)min<int64_t>(min<int64_t>(kChunk, pos - p0 + 1), tmax - p0);
-
-    const uint4* qsrc = reinterpret_cast<const uint4*>(q + (int64_t)hk * G * D);
-    for (int i = lane; i < G * D / 8; i += 64) qs[i / (D / 8)][i % (D / 8)] = qsrc[i];
-    __syncthreads();
-
-    // phase 1: scores of this lane's position
-    const bool valid = lane < nvalid;
-    float s[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) s[g] = 0.f;
-    if (valid) {
-        const uint4* kr = reinterpret_cast<const uint4*>(kc + hk * head_stride + (int64_t)(p0 + lane) * D);
-        uint4 kk[D / 8];
-#pragma unroll
-        for (int c = 0; c < D / 8; ++c) kk[c] = kr[c];
-#pragma unroll
-        for (int c = 0; c < D / 8; ++c) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const uint4 qq = qs[g][c];
-                s[g] = dot2(kk[c].x, qq.x, s[g]);
-                s[g] = dot2(kk[c].y, qq.y, s[g]);
-                s[g] = dot2(kk[c].z, qq.z, s[g]);
-                s[g] = dot2(kk[c].w, qq.w, s[g]);
-            }
-        }
-    }
-    // phase 2: per-head max and exponentials over the chunk
-    float m[G], l[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float v = valid ? s[g] * scale : -INFINITY;
-        m[g] = wave_max(v);
-        const float e = valid ? expf(v - m[g]) : 0.f;
-        es[lane][g] = e;
-        l[g] = wave_sum(e);
-    }
-    __syncthreads();
-
-    // phase 3: o[g][d] = sum_j e[j][g] v[j][d], in batches of VB rows whose loads
-    // are all issued first (rows past the valid ones repeat the last valid row,
-    // with weight 0)
-    constexpr int VB = 64 / DPL;
-    const uint16_t* vbase = vc + hk * head_stride + (int64_t)p0 * D + lane * DPL;
-    float o[G][DPL];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int t = 0; t < DPL; ++t) o[g][t] = 0.f;
-    for (int j0 = 0; j0 < nvalid; j0 += VB) {
-        float vv[VB][DPL];
-#pragma unroll
-        for (int j = 0; j < VB; ++j) VRow<D>::load(vbase + (int64_t)min(j0 + j, nvalid - 1) * D, vv[j]);
-#pragma unroll
-        for (int j = 0; j < VB; ++j) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float e = j0 + j < kChunk ? es[min(j0 + j, kChunk - 1)][g] : 0.f;
-#pragma unroll
-                for (int t = 0; t < DPL; ++t) o[g][t] += e * vv[j][t];
-            }
-        }
-    }
-    float* rec = part + ((int64_t)hk * nsplit + split) * G * (2 + D);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        if (lane == 0) {
-            rec[g * (2 + D)] = m[g];
-            rec[g * (2 + D) + 1] = l[g];
-        }
-#pragma unroll
-        for (int t = 0; t < DPL; ++t) rec[g * (2 + D) + 2 + lane * DPL + t] = o[g][t];
-    }
+// v_mfma_f32_16x16x32_bf16, lane l: A[row l%16][k 8*(l/16) + 0..7], B[k 8*(l/16) + 0..7][col l%16]
+__device__ __forceinline__ f32x4_t mfma_k32(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                    c, 0, 0, 0);
 }
-
-// one wave per query head h: merge the partials of chunks 0 .. pos/64
-template <int D>
-__global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ part, const int64_t* __restrict__ pos_ptr,
-                                                     int G, int nsplit, uint16_t* __restrict__ out) {
-    constexpr int DPL = D / 64;
-    constexpr int U = 8;  // partials loaded per step
-    const int lane = threadIdx.x;
-    const int h = blockIdx.x, hk = h / G, g = h - hk * G;
-    const int64_t pos = *pos_ptr;
-    const int nv = (int)min<int64_t>(nsplit, pos / kChunk + 1);
-    const float* base = part + ((int64_t)hk * nsplit * G + g) * (2 + D);
-    const int64_t stride = (int64_t)G * (2 + D);  // between chunks of this head
-    float M = -INFINITY;
-    for (int i = lane; i < nv; i += 64) M = fmaxf(M, base[i * stride]);
-    M = wave_max(M);
-    float L = 0.f;
-    for (int i = lane; i < nv; i += 64) L += base[i * stride + 1] * expf(base[i * stride] - M);
-    L = wave_sum(L);
-    float O[DPL];
-#pragma unroll
-    for (int t = 0; t < DPL; ++t) O[t] = 0.f;
-    for (int i0 = 0; i0 < nv; i0 += U) {
-        float w[U], ov[U][DPL];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i = min(i0 + u, nv - 1);
-            w[u] = (i0 + u < nv) ? expf(base[i * stride] - M) : 0.f;
-#pragma unroll
-            for (int t = 0; t < DPL; ++t) ov[u][t] = base[i * stride + 2 + lane * DPL + t];
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int t = 0; t < DPL; ++t) O[t] += w[u] * ov[u][t];
-    }
-    const float inv = 1.f / L;
-#pragma unroll
-    for (int t = 0; t < DPL; ++t) out[(int64_t)h * D + lane * DPL + t] = f32_to_bf16(O[t] * inv);
+// v_mfma_f32_16x16x16_bf16, lane l: A[row l%16][k 4*(l/16) + 0..3], B[k 4*(l/16) + 0..3][col l%16];
+// both forms: D[row 4*(l/16) + i][col l%16] in element i
+__device__ __forceinline__ f32x4_t mfma_k16(uint2 a, uint2 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4_t, a), __builtin_bit_cast(i16x4_t, b),
+                                                      c, 0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------
-// Wide form (D in {64, 128}, G <= 8): one workgroup of 4 waves per (64-position
-// chunk, KV head); wave w owns positions p0 + 16w .. +15.
-//  * Every K and V load of the wave is issued first. K: LPR = D/8 lanes per row,
-//    16 bytes each (a wave load reads RPI = 64/LPR whole rows); V: lane = D/64
-//    dimensions of every row.
-//  * Scores: 4 v_dot2 per (row, head) and lane, summed over the LPR lanes of a
-//    row with DPP row operations (every lane of the group gets the sum).
-//  * Softmax statistics and the V sums are combined across the 4 waves in LDS;
-//    the record (m, l, o[D]) per head has the layout of k_attn_partial.
+// k_attn_mfma (G <= 16 query heads per KV head, D in {64, 128, 256}); lane l,
+// n = l%16, r = l/16, wave w:
+//  * Scores S[pos][head] = K q^T, D/32 MFMAs of k = 32: A = the wave's 16 K rows
+//    (row n, dims D/4*r .. +D/4-1 as D/32 16-byte loads), B = the query rows (column
+//    n = head n; columns >= G repeat head G-1 and are masked). A and B take the dims
+//    in the same order, so each score is the plain dot product over the head dim
+//    (exact bf16 products, fp32 sums). The result holds S[pos 4r+i][head n]: a lane
+//    has four positions of one head, so the wave's maximum and sum of exponentials
+//    per head take two cross-lane steps for all heads at once.
+//  * o[head][d] = sum_pos p v, D/16 MFMAs of k = 16 per term: A = p split into two
+//    bf16 terms (p = hi + lo to 2^-17 relative), which is the score layout unchanged;
+//    B = V rows 4r+i at dim 32u + 2n + b for tile 2u + b (one 4-byte load per row
+//    covers both tiles of a pair). The product of two bf16 is exact and the sums are
+//    fp32, so o carries fp32 rounding only.
+//  * The four waves exchange their maxima through LDS before the exponentials, so
+//    the workgroup's record (m, l, o[D]) per head is a plain sum of theirs. The PV
+//    result of a lane is four heads of one dim: one 16-byte LDS store per tile.
 // ---------------------------------------------------------------------------
-template <int LPR>
-__device__ __forceinline__ float row_group_sum(float v) {
-    v += dpp_f<0xB1>(v);                  // quad_perm [1,0,3,2]
-    v += dpp_f<0x4E>(v);                  // quad_perm [2,3,0,1]
-    v += dpp_f<0x141>(v);                 // row_half_mirror: the two quads of 8 lanes
-    if (LPR >= 16) v += dpp_f<0x140>(v);  // row_mirror: the two halves of 16 lanes
-    return v;
-}
-
 template <int G, int D>
-__global__ __launch_bounds__(256) void k_attn_wide(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+__global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
                                                    const uint16_t* __restrict__ vc, int64_t head_stride,
                                                    const int64_t* __restrict__ pos_ptr, int tmax, float scale,
                                                    float* __restrict__ part, int nsplit) {
-    static_assert(D == 64 || D == 128, "wide attention takes head dim 64 or 128");
-    static_assert(G >= 1 && G <= 8, "wide attention takes at most 8 query heads per KV head");
-    constexpr int LPR = D / 8, RPI = 64 / LPR, RW = kChunk / 4, NK = RW / RPI, DPL = D / 64;
-    __shared__ uint4 qs[G][D / 8];
-    __shared__ float es[4][RW][G];
-    __shared__ float red_m[4][G], red_l[4][G];
-    __shared__ float red_o[4][G][D];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "1, 2, 4, 8 or 16 query heads per KV head");
+    static_assert(D == 64 || D == 128 || D == 256, "head dim 64, 128 or 256");
+    constexpr int KS = D / 32;  // score MFMAs = 16-byte K loads per lane
+    constexpr int NU = D / 32;  // V tile pairs
+    constexpr int HQ = (G + 3) / 4;  // lane groups r whose PV rows are real heads
+    __shared__ f32x4_t red_o[4][HQ][D];  // heads 4hq .. 4hq+3 of dim d
+    __shared__ float red_m[4][16], red_l[4][16];
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, r = lane >> 4;
     const int split = blockIdx.x, hk = blockIdx.y;
     const int64_t pos = *pos_ptr;
     const int p0 = split * kChunk;
     if ((int64_t)p0 > pos) return;  // the whole workgroup: chunks past pos are never read
-    const int nvalid = (int)min<int64_t>(min<int64_t>(kChunk, pos - p0 + 1), tmax - p0);
-    const int plast = p0 + nvalid - 1;
-    const int pw = p0 + wv * RW;
-    const int rg = lane / LPR, dg = lane - rg * LPR;
+    const int plast = (int)min<int64_t>(min<int64_t>(pos, (int64_t)p0 + kChunk - 1), (int64_t)tmax - 1);
+    const int pw = p0 + 16 * wv;
     const uint16_t* kh = kc + hk * head_stride;
     const uint16_t* vh = vc + hk * head_stride;
 
-    uint4 kk[NK];
+    // every load first: K rows (A), query rows (B), V pieces (rows past plast repeat
+    // row plast and are masked)
+    uint4 ka[KS], qb[KS];
+    {
+        const uint4* kr = reinterpret_cast<const uint4*>(kh + (int64_t)min(pw + n, plast) * D + (D / 4) * r);
+        const uint4* qr = reinterpret_cast<const uint4*>(q + ((int64_t)hk * G + min(n, G - 1)) * D + (D / 4) * r);
 #pragma unroll
-    for (int i = 0; i < NK; ++i) {
-        const int p = min(pw + rg + RPI * i, plast);
-        kk[i] = *reinterpret_cast<const uint4*>(kh + (int64_t)p * D + dg * 8);
-    }
-    uint32_t vv[RW];
+        for (int s = 0; s < KS; ++s) ka[s] = kr[s];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-        const int p = min(pw + r, plast);
-        vv[r] = DPL == 2 ? *reinterpret_cast<const uint32_t*>(vh + (int64_t)p * D + lane * 2)
-                         : (uint32_t)vh[(int64_t)p * D + lane];
+        for (int s = 0; s < KS; ++s) qb[s] = qr[s];
     }
-    const uint4* qsrc = reinterpret_cast<const uint4*>(q + (int64_t)hk * G * D);
-    for (int i = threadIdx.x; i < G * D / 8; i += 256) qs[i / (D / 8)][i % (D / 8)] = qsrc[i];
+    uint32_t vw[4][NU];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t* vr = reinterpret_cast<const uint32_t*>(vh + (int64_t)min(pw + 4 * r + i, plast) * D + 2 * n);
+#pragma unroll
+        for (int u = 0; u < NU; ++u) vw[i][u] = vr[16 * u];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the first wait
+
+    f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) sc = mfma_k32(ka[s], qb[s], sc);
+
+    // this wave's maximum and exponential sum per head
+    float sv[4], m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool ok = n < G && pw + 4 * r + i <= plast;
+        sv[i] = ok ? sc[i] * scale : -INFINITY;
+        m = fmaxf(m, sv[i]);
+    }
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    if (lane < 16) red_m[wv][n] = m;
+    __syncthreads();
+    // the workgroup's maximum (finite for n < G: position p0 <= pos is in wave 0)
+    m = fmaxf(fmaxf(red_m[0][n], red_m[1][n]), fmaxf(red_m[2][n], red_m[3][n]));
+    float pe[4], l = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        pe[i] = sv[i] == -INFINITY ? 0.f : expf(sv[i] - m);
+        l += pe[i];
+    }
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (lane < 16) red_l[wv][n] = l;
+
+    uint2 phi, plo;
+    phi.x = pack_bf16x2(pe[0], pe[1]);
+    phi.y = pack_bf16x2(pe[2], pe[3]);
+    plo.x = pack_bf16x2(pe[0] - bf16_lo(phi.x), pe[1] - bf16_hi(phi.x));
+    plo.y = pack_bf16x2(pe[2] - bf16_lo(phi.y), pe[3] - bf16_hi(phi.y));
+
+    f32x4_t o[2 * NU];
+#pragma unroll
+    for (int t = 0; t < 2 * NU; ++t) o[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        uint2 b0, b1;  // dims 32u + 2n (low halves) and 32u + 2n + 1 (high halves) of rows 4r .. 4r+3
+        b0.x = __builtin_amdgcn_perm(vw[1][u], vw[0][u], 0x05040100u);
+        b0.y = __builtin_amdgcn_perm(vw[3][u], vw[2][u], 0x05040100u);
+        b1.x = __builtin_amdgcn_perm(vw[1][u], vw[0][u], 0x07060302u);
+        b1.y = __builtin_amdgcn_perm(vw[3][u], vw[2][u], 0x07060302u);
+        o[2 * u] = mfma_k16(phi, b0, o[2 * u]);
+        o[2 * u + 1] = mfma_k16(phi, b1, o[2 * u + 1]);
+        o[2 * u] = mfma_k16(plo, b0, o[2 * u]);
+        o[2 * u + 1] = mfma_k16(plo, b1, o[2 * u + 1]);
+    }
+
+    // o[t][i] = O[head 4r + i][dim 32(t/2) + 2n + t%2]
+    if (r < HQ) {
+#pragma unroll
+        for (int t = 0; t < 2 * NU; ++t) red_o[wv][r][32 * (t >> 1) + 2 * n + (t & 1)] = o[t];
+    }
     __syncthreads();
 
-    // scores of this lane group's rows
-    float s[NK][G];
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-        const bool valid = pw + rg + RPI * i <= plast;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const uint4 qq = qs[g][dg];
-            float a = dot2(kk[i].x, qq.x, 0.f);
-            a = dot2(kk[i].y, qq.y, a);
-            a = dot2(kk[i].z, qq.z, a);
-            a = dot2(kk[i].w, qq.w, a);
-            a = row_group_sum<LPR>(a);
-            s[i][g] = valid ? a * scale : -INFINITY;
-        }
-    }
-    // softmax statistics of the workgroup's rows
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float m = s[0][g];
-#pragma unroll
-        for (int i = 1; i < NK; ++i) m = fmaxf(m, s[i][g]);
-        m = wave_max(m);
-        if (lane == 0) red_m[wv][g] = m;
-    }
-    __syncthreads();
-    float M[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) M[g] = fmaxf(fmaxf(red_m[0][g], red_m[1][g]), fmaxf(red_m[2][g], red_m[3][g]));
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float l = 0.f;
-#pragma unroll
-        for (int i = 0; i < NK; ++i) {
-            const bool valid = pw + rg + RPI * i <= plast;
-            const float e = valid ? expf(s[i][g] - M[g]) : 0.f;
-            if (dg == 0) es[wv][rg + RPI * i][g] = e;
-            l += dg == 0 ? e : 0.f;
-        }
-        l = wave_sum(l);
-        if (lane == 0) red_l[wv][g] = l;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // o[g][lane's dims] over the wave's rows
-    float o[G][DPL];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int t = 0; t < DPL; ++t) o[g][t] = 0.f;
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-        float vf[DPL];
-        vf[0] = __uint_as_float(vv[r] << 16);
-        if (DPL == 2) vf[DPL - 1] = __uint_as_float(vv[r] & 0xFFFF0000u);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float e = es[wv][r][g];
-#pragma unroll
-            for (int t = 0; t < DPL; ++t) o[g][t] += e * vf[t];
-        }
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int t = 0; t < DPL; ++t) red_o[wv][g][lane * DPL + t] = o[g][t];
-    __syncthreads();
     float* rec = part + ((int64_t)hk * nsplit + split) * G * (2 + D);
-    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-        const int g = idx / D, d = idx - g * D;
-        rec[g * (2 + D) + 2 + d] = red_o[0][g][d] + red_o[1][g][d] + red_o[2][g][d] + red_o[3][g][d];
+    for (int e = threadIdx.x; e < HQ * D; e += 256) {
+        const int hq = e / D, d = e - hq * D;
+        const f32x4_t v = (red_o[0][hq][d] + red_o[1][hq][d]) + (red_o[2][hq][d] + red_o[3][hq][d]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (4 * hq + j < G) rec[(4 * hq + j) * (2 + D) + 2 + d] = v[j];
     }
     if (threadIdx.x < G) {
-        const int g = threadIdx.x;
-        rec[g * (2 + D)] = M[g];
-        rec[g * (2 + D) + 1] = red_l[0][g] + red_l[1][g] + red_l[2][g] + red_l[3][g];
+        const int h = threadIdx.x;
+        rec[h * (2 + D)] = fmaxf(fmaxf(red_m[0][h], red_m[1][h]), fmaxf(red_m[2][h], red_m[3][h]));
+        rec[h * (2 + D) + 1] = (red_l[0][h] + red_l[1][h]) + (red_l[2][h] + red_l[3][h]);
     }
 }
 
+// Sum of (lanes 0..15: max) of v over the 16 lanes of row 0, read from lane 0.
+__device__ __forceinline__ float row0_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+}
+__device__ __forceinline__ float row0_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+}
+
 // One workgroup (4 waves) per query head: wave w merges chunks w, w+4, ... in
-// batches of 16 whose loads are issued before the block-wide maximum is known.
+// batches of 16 with a running maximum. Lane b < 16 reads the m and l of the batch's
+// chunk b and computes its weight (one exponential per chunk); the weights reach the
+// o sums of every lane through readlane. The four waves' sums are rescaled to the
+// common maximum in LDS.
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ part, const int64_t* __restrict__ pos_ptr,
                                                     int G, int nsplit, uint16_t* __restrict__ out) {
     constexpr int DPL = D / 64, B = 16;
-    __shared__ float red[4];
-    __shared__ float red_l[4];
+    __shared__ float red_m[4], red_l[4];
     __shared__ float red_o[4][D];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // chunk indices in SGPRs
     const int h = blockIdx.x, hk = h / G, g = h - hk * G;
     const int64_t pos = *pos_ptr;
     const int nv = (int)min<int64_t>(nsplit, pos / kChunk + 1);
     const float* base = part + ((int64_t)hk * nsplit * G + g) * (2 + D);
     const int64_t stride = (int64_t)G * (2 + D);
-    // first batch of this wave's chunks: o pieces and m, l
-    float ov[B][DPL], mv[B], lv[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-        const int c = min(wv + 4 * b, nv - 1);
-        mv[b] = base[c * stride];
-        lv[b] = base[c * stride + 1];
-#pragma unroll
-        for (int t = 0; t < DPL; ++t) ov[b][t] = base[c * stride + 2 + lane * DPL + t];
-    }
-    // block maximum over all chunks
-    float m = -INFINITY;
-    for (int c = threadIdx.x; c < nv; c += 256) m = fmaxf(m, base[c * stride]);
-    m = wave_max(m);
-    if (lane == 0) red[wv] = m;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float L = 0.f, O[DPL];
+    float M = -INFINITY, L = 0.f, O[DPL];
 #pragma unroll
     for (int t = 0; t < DPL; ++t) O[t] = 0.f;
-    for (int c0 = 0;; c0 += 4 * B) {
+    for (int c0 = 0; c0 < nv; c0 += 4 * B) {
+        float ov[B][DPL];
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const bool use = c0 + wv + 4 * b < nv;
-            const float w = use ? expf(mv[b] - M) : 0.f;
-            L += w * lv[b];
-#pragma unroll
-            for (int t = 0; t < DPL; ++t) O[t] += w * ov[b][t];
-        }
-        if (c0 + 4 * B >= nv) break;
-#pragma unroll
-        for (int b = 0; b < B; ++b) {  // next batch
-            const int c = min(c0 + 4 * B + wv + 4 * b, nv - 1);
-            mv[b] = base[c * stride];
-            lv[b] = base[c * stride + 1];
+            const int c = min(c0 + wv + 4 * b, nv - 1);
 #pragma unroll
             for (int t = 0; t < DPL; ++t) ov[b][t] = base[c * stride + 2 + lane * DPL + t];
         }
+        const int cl = c0 + wv + 4 * (lane & 15);
+        const bool have = lane < 16 && cl < nv;
+        const int cc = min(cl, nv - 1);
+        const float mc = have ? base[cc * stride] : -INFINITY;
+        const float lc = base[cc * stride + 1];
+        const float Mn = fmaxf(M, row0_max(mc));
+        const float f = M == -INFINITY ? 0.f : expf(M - Mn);  // rescale of the sums so far
+        const float w = have ? expf(mc - Mn) : 0.f;
+        L = L * f + row0_sum(w * lc);
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) O[t] *= f;
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float wb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), b));
+#pragma unroll
+            for (int t = 0; t < DPL; ++t) O[t] += wb * ov[b][t];
+        }
+        M = Mn;
     }
-    if (lane == 0) red_l[wv] = L;
+    if (lane == 0) {
+        red_m[wv] = M;
+        red_l[wv] = L;
+    }
 #pragma unroll
     for (int t = 0; t < DPL; ++t) red_o[wv][lane * DPL + t] = O[t];
     __syncthreads();
     if (threadIdx.x < D) {
         const int d = threadIdx.x;
-        const float inv = 1.f / (red_l[0] + red_l[1] + red_l[2] + red_l[3]);
-        const float v = red_o[0][d] + red_o[1][d] + red_o[2][d] + red_o[3][d];
-        out[(int64_t)h * D + d] = f32_to_bf16(v * inv);
+        const float Mx = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));  // finite: chunk 0 exists
+        float v = 0.f, Lt = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float f = red_m[w] == -INFINITY ? 0.f : expf(red_m[w] - Mx);
+            v += f * red_o[w][d];
+            Lt += f * red_l[w];
+        }
+        out[(int64_t)h * D + d] = f32_to_bf16(v / Lt);
     }
 }
 
@@ -394,15 +265,9 @@ template <int G, int D>
 static void launch_attn(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t hs, const int64_t* pos,
                         int hk, int tmax, float scale, float* part, uint16_t* out, hipStream_t st) {
     const int nsplit = (tmax + kChunk - 1) / kChunk;
-    if constexpr ((D == 64 || D == 128) && G <= 8) {
-        hipLaunchKernelGGL((k_attn_wide<G, D>), dim3(nsplit, hk), dim3(256), 0, st, q, kc, vc, hs, pos, tmax, scale,
-                           part, nsplit);
-        hipLaunchKernelGGL((k_attn_merge<D>), dim3(hk * G), dim3(256), 0, st, part, pos, G, nsplit, out);
-    } else {
-        hipLaunchKernelGGL((k_attn_partial<G, D>), dim3(nsplit, hk), dim3(64), 0, st, q, kc, vc, hs, pos, tmax,
-                           scale, part, nsplit);
-        hipLaunchKernelGGL((k_attn_combine<D>), dim3(hk * G), dim3(64), 0, st, part, pos, G, nsplit, out);
-    }
+    hipLaunchKernelGGL((k_attn_mfma<G, D>), dim3(nsplit, hk), dim3(256), 0, st, q, kc, vc, hs, pos, tmax, scale, part,
+                       nsplit);
+    hipLaunchKernelGGL((k_attn_merge<D>), dim3(hk * G), dim3(256), 0, st, part, pos, G, nsplit, out);
 }
 
 }  // namespace wisp

@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) void k_dl_gemv(const GemvArgs g) {
             s0 = dot2(wr[r][c].z, xv[c].z, s0);
             s1 = dot2(wr[r][c].w, xv[c].w, s1);
         }
-        acc[r] = wave_sum(s0 + s1);
+        acc[r] = wave_sum_dpp(s0 + s1);
     }
     if (lane < R) {
         float v = acc[0];
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256) void k_dl_gemv_any(const GemvArgs g) {
             s0 = dot2(wq.z, xq.z, s0);
             s1 = dot2(wq.w, xq.w, s1);
         }
-        acc[r] = wave_sum(s0 + s1);
+        acc[r] = wave_sum_dpp(s0 + s1);
     }
     if (lane < R) {
         float v = acc[0];
