@@ -315,6 +315,37 @@ __global__ __launch_bounds__(64) void k_dl_qkrope(const uint16_t* __restrict__ q
 // for the row by watching host_flag instead of synchronising the stream.
 // EPL = logits per lane (a power of two >= E/64): every load is issued before
 // any use (addresses clamped into range, the extra values masked afterwards).
+// (value, index) maximum with equal values going to the lower index: a total order, so
+// every reduction order selects the same entry. Wave-wide with DPP inside each 16-lane
+// row (xor 1, xor 2, row_half_mirror, row_mirror), then the four row winners through
+// readlane; the result is wave-uniform.
+__device__ __forceinline__ void best_of(float& bv, int& bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+    }
+}
+template <int CTRL>
+__device__ __forceinline__ void best_dpp(float& bv, int& bi) {
+    const float ov = dpp_f<CTRL>(bv);
+    const int oi = __builtin_amdgcn_update_dpp(0, bi, CTRL, 0xF, 0xF, true);
+    best_of(bv, bi, ov, oi);
+}
+__device__ __forceinline__ void wave_best(float& bv, int& bi) {
+    best_dpp<0xB1>(bv, bi);
+    best_dpp<0x4E>(bv, bi);
+    best_dpp<0x141>(bv, bi);
+    best_dpp<0x140>(bv, bi);
+    float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), 0));
+    int i = __builtin_amdgcn_readlane(bi, 0);
+#pragma unroll
+    for (int r = 16; r < 64; r += 16)
+        best_of(v, i, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bv), r)),
+                __builtin_amdgcn_readlane(bi, r));
+    bv = v;
+    bi = i;
+}
+
 template <int EPL>
 __global__ __launch_bounds__(64) void k_dl_route(const uint16_t* __restrict__ logits, int E, int k, int norm,
                                                  float* __restrict__ row, float* host_row, uint32_t* host_flag,
@@ -334,7 +365,7 @@ __global__ __launch_bounds__(64) void k_dl_route(const uint16_t* __restrict__ lo
         v[t] = i < E ? bf(raw[t]) : -INFINITY;
         mx = fmaxf(mx, v[t]);
     }
-    mx = wave_max(mx);
+    mx = wave_max_dpp(mx);  // exact in any order
     float sum = 0.f;
 #pragma unroll
     for (int t = 0; t < kRouteMaxPerLane; ++t) {
@@ -357,15 +388,7 @@ __global__ __launch_bounds__(64) void k_dl_route(const uint16_t* __restrict__ lo
                 bv = v[t];
                 bi = lane + 64 * t;
             }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
+        wave_best(bv, bi);
         sel_v[r] = bv;
         sel_i[r] = bi;
 #pragma unroll
