@@ -165,6 +165,15 @@ int64_t wisp_attn_ws_bytes(int hq, int d, int tmax);
 int wisp_attn_decode(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t kv_head_stride,
                      const int64_t* pos, int hq, int hk, int d, int tmax, float scale, void* ws, uint16_t* out,
                      void* stream);
+/* graphdec.py:163-174 at batch 1 in one pair of launches: wisp_dl_qk_rope's per-head
+ * RMSNorm of the q and k heads of qkv = [q (hq*d) | k (hk*d) | v (hk*d)], rope at *pos,
+ * k and v stored into kc/vc at *pos, then wisp_attn_decode of those q heads; the same
+ * bits as the two calls in sequence (the q heads never leave the attention workgroups).
+ * Same shapes, alignment and workspace as wisp_attn_decode. */
+int wisp_attn_decode_qk(const uint16_t* qkv, const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
+                        const uint16_t* cos, const uint16_t* sin, const int64_t* pos, int hq, int hk, int d,
+                        uint16_t* kc, uint16_t* vc, int64_t kv_head_stride, int tmax, float scale, void* ws,
+                        uint16_t* out, void* stream);
 
 /* Workspace bytes of wisp_moe_prefill: act bf16 [pairs, I] (rounded up to 256)
  * followed by y fp32 [pairs, H]. */

@@ -138,6 +138,36 @@ def test_qk_rope_matches_modules(Hq, Hk, D):
     assert kc[0][:, others].abs().sum().item() == 0 and vc[0][:, others].abs().sum().item() == 0
 
 
+@pytest.mark.parametrize("Hq,Hk,D,T", [(32, 4, 128, 4096), (32, 4, 128, 300), (8, 8, 64, 130), (4, 1, 256, 70),
+                                       (32, 2, 128, 64), (16, 4, 128, 200), (4, 2, 64, 65)])
+def test_qk_rope_attn_equals_the_two_calls(Hq, Hk, D, T):
+    """The fused launch pair (q/k head norm + rope + K/V store inside the attention
+    workgroups) against dl_qk_rope then attn_decode: the output, the K and V written at pos
+    and every other cache row equal bit for bit, at chunk edges and the last position."""
+    g = torch.Generator(device=DEV).manual_seed(Hq * D + T)
+    qn = (1.0 + 0.2 * torch.randn(D, generator=g, device=DEV)).to(torch.bfloat16)
+    kn = (1.0 + 0.2 * torch.randn(D, generator=g, device=DEV)).to(torch.bfloat16)
+    ang = torch.arange(T, device=DEV)[:, None] * (1.0 / 1e4 ** (torch.arange(0, D, 2, device=DEV) / D))[None]
+    ang = torch.cat([ang, ang], 1)
+    cos, sin = ang.cos().to(torch.bfloat16).contiguous(), ang.sin().to(torch.bfloat16).contiguous()
+    kc0 = _bf(1, Hk, T, D, gen=g)
+    vc0 = _bf(1, Hk, T, D, gen=g)
+    scale = D ** -0.5
+    for pos in sorted(p for p in {0, 1, 63, 64, 127, T // 2, T - 1} if p < T):
+        qkv = _bf((Hq + 2 * Hk) * D, gen=g)
+        p = torch.tensor([pos], dtype=torch.int64, device=DEV)
+        ka, va = kc0.clone(), vc0.clone()
+        qo = torch.empty(Hq * D, dtype=torch.bfloat16, device=DEV)
+        kernels.dl_qk_rope(qkv, qn, kn, 1e-6, cos, sin, p, Hq, Hk, D, ka, va, qo)
+        ref = kernels.attn_decode(qo.view(Hq, D), ka, va, p, scale)
+        kb, vb = kc0.clone(), vc0.clone()
+        got = kernels.dl_qk_rope_attn(qkv, qn, kn, 1e-6, cos, sin, p, Hq, Hk, D, kb, vb, scale)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), pos
+        assert torch.equal(kb.view(torch.int16), ka.view(torch.int16)), pos
+        assert torch.equal(vb.view(torch.int16), va.view(torch.int16)), pos
+
+
 @pytest.mark.parametrize("E,k,norm", [(128, 8, True), (128, 8, False), (8, 2, True), (60, 4, True), (512, 10, True),
                                       (128, 16, True), (64, 1, True), (256, 8, True)])
 def test_route_matches_moe_route(E, k, norm):

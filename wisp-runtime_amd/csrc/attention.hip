@@ -61,12 +61,29 @@ __device__ __forceinline__ f32x4_t mfma_k16(uint2 a, uint2 b, f32x4_t c) {
 //  * The four waves exchange their maxima through LDS before the exponentials, so
 //    the workgroup's record (m, l, o[D]) per head is a plain sum of theirs. The PV
 //    result of a lane is four heads of one dim: one 16-byte LDS store per tile.
+//  * QK (the decoder's q/k head norm + rope + K/V store folded in, graphdec.py:163-172):
+//    q is not read ready-made; every workgroup forms its G query heads from the raw
+//    qkv with head_norm_rope (wave w: heads w, w+4, ...; the same arithmetic as
+//    k_dl_qkrope) into LDS. The workgroup whose chunk holds pos also forms the new K row
+//    (head_norm_rope) and copies the V row, stores both into the caches at pos and puts
+//    them into its own operands for that row (its loads of row pos read the old cache).
 // ---------------------------------------------------------------------------
-template <int G, int D>
-__global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-                                                   const uint16_t* __restrict__ vc, int64_t head_stride,
+struct QkPrep {
+    const uint16_t* qkv;  // [q (Hq heads) | k (Hk) | v (Hk)] of D
+    const uint16_t* qnw;
+    const uint16_t* knw;
+    const uint16_t* cos_t;  // [tmax, D]
+    const uint16_t* sin_t;
+    uint16_t* kc_w;  // the caches attention reads, written at pos
+    uint16_t* vc_w;
+    float eps;
+    int hq, hk;
+};
+template <int G, int D, bool QK>
+__global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ q, const uint16_t* kc,
+                                                   const uint16_t* vc, int64_t head_stride,
                                                    const int64_t* __restrict__ pos_ptr, int tmax, float scale,
-                                                   float* __restrict__ part, int nsplit) {
+                                                   float* __restrict__ part, int nsplit, const QkPrep qp) {
     static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "1, 2, 4, 8 or 16 query heads per KV head");
     static_assert(D == 64 || D == 128 || D == 256, "head dim 64, 128 or 256");
     constexpr int KS = D / 32;  // score MFMAs = 16-byte K loads per lane
@@ -90,11 +107,14 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
     uint4 ka[KS], qb[KS];
     {
         const uint4* kr = reinterpret_cast<const uint4*>(kh + (int64_t)min(pw + n, plast) * D + (D / 4) * r);
-        const uint4* qr = reinterpret_cast<const uint4*>(q + ((int64_t)hk * G + min(n, G - 1)) * D + (D / 4) * r);
 #pragma unroll
         for (int s = 0; s < KS; ++s) ka[s] = kr[s];
+        if constexpr (!QK) {
+            const uint4* qr =
+                reinterpret_cast<const uint4*>(q + ((int64_t)hk * G + min(n, G - 1)) * D + (D / 4) * r);
 #pragma unroll
-        for (int s = 0; s < KS; ++s) qb[s] = qr[s];
+            for (int s = 0; s < KS; ++s) qb[s] = qr[s];
+        }
     }
     uint32_t vw[4][NU];
 #pragma unroll
@@ -104,6 +124,51 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
         for (int u = 0; u < NU; ++u) vw[i][u] = vr[16 * u];
     }
     __builtin_amdgcn_sched_barrier(0);  // all loads in flight before the first wait
+    if constexpr (QK) {
+        __shared__ __align__(16) uint16_t q_l[G][D];
+        __shared__ __align__(16) uint16_t kv_l[2][D];  // the new K and V rows (chunk of pos)
+        const bool own = pos <= (int64_t)plast;  // this chunk holds position pos
+        const uint16_t* cs = qp.cos_t + pos * D;
+        const uint16_t* sn = qp.sin_t + pos * D;
+#pragma unroll
+        for (int j = 0; j < (G + 3) / 4; ++j) {
+            const int g = wv + 4 * j;
+            if (g < G)
+                head_norm_rope<D>(qp.qkv + ((int64_t)hk * G + g) * D, qp.qnw, qp.eps, cs, sn, &q_l[g][0], nullptr,
+                                  lane);
+        }
+        if (own) {
+            const int64_t at = hk * head_stride + pos * D;
+            if (wv == (G & 3)) {  // a wave with the fewest q heads
+                head_norm_rope<D>(qp.qkv + ((int64_t)qp.hq + hk) * D, qp.knw, qp.eps, cs, sn, &kv_l[0][0],
+                                  qp.kc_w + at, lane);
+            } else if (wv == ((G + 1) & 3)) {
+                const uint16_t* xv = qp.qkv + ((int64_t)qp.hq + qp.hk + hk) * D;
+                for (int i = lane; i < D; i += 64) {
+                    const uint16_t v = xv[i];
+                    kv_l[1][i] = v;
+                    qp.vc_w[at + i] = v;
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            qb[s] = *reinterpret_cast<const uint4*>(&q_l[min(n, G - 1)][(D / 4) * r + 8 * s]);
+        if (own) {  // the row at pos from the values just formed
+            if (pw + n == (int)pos) {
+#pragma unroll
+                for (int s = 0; s < KS; ++s) ka[s] = *reinterpret_cast<const uint4*>(&kv_l[0][(D / 4) * r + 8 * s]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (pw + 4 * r + i == (int)pos) {
+#pragma unroll
+                    for (int u = 0; u < NU; ++u)
+                        vw[i][u] = *reinterpret_cast<const uint32_t*>(&kv_l[1][32 * u + 2 * n]);
+                }
+        }
+    }
 
     f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -263,11 +328,43 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ pa
 
 template <int G, int D>
 static void launch_attn(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t hs, const int64_t* pos,
-                        int hk, int tmax, float scale, float* part, uint16_t* out, hipStream_t st) {
+                        int hk, int tmax, float scale, float* part, uint16_t* out, const QkPrep* qp, hipStream_t st) {
     const int nsplit = (tmax + kChunk - 1) / kChunk;
-    hipLaunchKernelGGL((k_attn_mfma<G, D>), dim3(nsplit, hk), dim3(256), 0, st, q, kc, vc, hs, pos, tmax, scale, part,
-                       nsplit);
+    if (qp)
+        hipLaunchKernelGGL((k_attn_mfma<G, D, true>), dim3(nsplit, hk), dim3(256), 0, st, q, kc, vc, hs, pos, tmax,
+                           scale, part, nsplit, *qp);
+    else
+        hipLaunchKernelGGL((k_attn_mfma<G, D, false>), dim3(nsplit, hk), dim3(256), 0, st, q, kc, vc, hs, pos, tmax,
+                           scale, part, nsplit, QkPrep{});
     hipLaunchKernelGGL((k_attn_merge<D>), dim3(hk * G), dim3(256), 0, st, part, pos, G, nsplit, out);
+}
+
+static int attn_dispatch(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t kv_head_stride,
+                         const int64_t* pos, int hq, int hk, int d, int tmax, float scale, void* ws, uint16_t* out,
+                         const QkPrep* qp, void* stream) {
+    const int G = hq / hk;
+    hipStream_t st = (hipStream_t)stream;
+    float* part = static_cast<float*>(ws);
+#define WISP_ATTN(GG, DD)                                                                         \
+    if (G == GG && d == DD) {                                                                     \
+        launch_attn<GG, DD>(q, kc, vc, kv_head_stride, pos, hk, tmax, scale, part, out, qp, st);  \
+        return check_launch("k_attn");                                                            \
+    }
+    WISP_ATTN(8, 128)
+    WISP_ATTN(4, 128)
+    WISP_ATTN(2, 128)
+    WISP_ATTN(1, 128)
+    WISP_ATTN(16, 128)
+    WISP_ATTN(8, 64)
+    WISP_ATTN(4, 64)
+    WISP_ATTN(2, 64)
+    WISP_ATTN(1, 64)
+    WISP_ATTN(8, 256)
+    WISP_ATTN(4, 256)
+    WISP_ATTN(2, 256)
+    WISP_ATTN(1, 256)
+#undef WISP_ATTN
+    return fail_inval("supported: head dim 64/128/256 with 1, 2, 4, 8 (and 16 at d=128) query heads per KV head");
 }
 
 }  // namespace wisp
@@ -291,27 +388,25 @@ extern "C" int wisp_attn_decode(const uint16_t* q, const uint16_t* kc, const uin
         set_error("q, kc, vc and the KV head stride must be 16-byte aligned");
         return WISP_EALIGN;
     }
-    const int G = hq / hk;
-    hipStream_t st = (hipStream_t)stream;
-    float* part = static_cast<float*>(ws);
-#define WISP_ATTN(GG, DD)                                                                         \
-    if (G == GG && d == DD) {                                                                     \
-        launch_attn<GG, DD>(q, kc, vc, kv_head_stride, pos, hk, tmax, scale, part, out, st);      \
-        return check_launch("k_attn");                                                            \
+    return attn_dispatch(q, kc, vc, kv_head_stride, pos, hq, hk, d, tmax, scale, ws, out, nullptr, stream);
+}
+
+// graphdec.py:163-174 in one pair of launches: dl_qk_rope's q/k head norm, rope and
+// K/V store at pos folded into the attention kernel (same bits as wisp_dl_qk_rope
+// followed by wisp_attn_decode on its qo).
+extern "C" int wisp_attn_decode_qk(const uint16_t* qkv, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                                   float eps, const uint16_t* cos, const uint16_t* sin, const int64_t* pos, int hq,
+                                   int hk, int d, uint16_t* kc, uint16_t* vc, int64_t kv_head_stride, int tmax,
+                                   float scale, void* ws, uint16_t* out, void* stream) {
+    clear_error();
+    if (!qkv || !q_norm_w || !k_norm_w || !cos || !sin || !pos || !kc || !vc || !ws || !out)
+        return fail_inval("null pointer");
+    if (hk < 1 || hq < hk || hq % hk) return fail_inval("hq must be a positive multiple of hk");
+    if (tmax < 1 || kv_head_stride < (int64_t)tmax * d) return fail_inval("kv_head_stride must be >= tmax*d");
+    if (!aligned(kc, 16) || !aligned(vc, 16) || (kv_head_stride * 2) % 16) {
+        set_error("kc, vc and the KV head stride must be 16-byte aligned");
+        return WISP_EALIGN;
     }
-    WISP_ATTN(8, 128)
-    WISP_ATTN(4, 128)
-    WISP_ATTN(2, 128)
-    WISP_ATTN(1, 128)
-    WISP_ATTN(16, 128)
-    WISP_ATTN(8, 64)
-    WISP_ATTN(4, 64)
-    WISP_ATTN(2, 64)
-    WISP_ATTN(1, 64)
-    WISP_ATTN(8, 256)
-    WISP_ATTN(4, 256)
-    WISP_ATTN(2, 256)
-    WISP_ATTN(1, 256)
-#undef WISP_ATTN
-    return fail_inval("supported: head dim 64/128/256 with 1, 2, 4, 8 (and 16 at d=128) query heads per KV head");
+    const QkPrep qp{qkv, q_norm_w, k_norm_w, cos, sin, kc, vc, eps, hq, hk};
+    return attn_dispatch(nullptr, kc, vc, kv_head_stride, pos, hq, hk, d, tmax, scale, ws, out, &qp, stream);
 }

@@ -49,8 +49,6 @@ struct GemvArgs {
     uint16_t* y;            // bf16 [O]
 };
 
-__device__ __forceinline__ float bf(uint32_t v16) { return __uint_as_float(v16 << 16); }
-__device__ __forceinline__ float rbf(float v) { return bf(f32_to_bf16(v)); }  // round to bf16, as float
 
 // 8 bf16 of a 16-byte chunk -> floats
 __device__ __forceinline__ void unpack8(const uint4 q, float* f) {
@@ -264,9 +262,6 @@ __global__ __launch_bounds__(64) void k_dl_qkrope(const uint16_t* __restrict__ q
                                                   const int64_t* __restrict__ pos_ptr, int Hq, int Hk,
                                                   uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
                                                   int64_t head_stride, uint16_t* __restrict__ qo) {
-#pragma clang fp contract(off)
-    constexpr int HALF = D / 2;
-    constexpr int NP = (HALF + 63) / 64;
     const int h = blockIdx.x, lane = threadIdx.x;
     const int64_t pos = *pos_ptr;
     const uint16_t* x = qkv + (int64_t)h * D;
@@ -276,34 +271,8 @@ __global__ __launch_bounds__(64) void k_dl_qkrope(const uint16_t* __restrict__ q
         return;
     }
     const bool isq = h < Hq;
-    const uint16_t* nw = isq ? qnw : knw;
-    float a[NP], b[NP];
-    float ss = 0.f;
-#pragma unroll
-    for (int t = 0; t < NP; ++t) {
-        const int i = lane + 64 * t;
-        a[t] = i < HALF ? bf(x[i]) : 0.f;
-        b[t] = i < HALF ? bf(x[i + HALF]) : 0.f;
-        ss += a[t] * a[t];
-        ss += b[t] * b[t];
-    }
-    ss = wave_sum(ss);
-    const float rs = rsqrtf(ss * (1.0f / (float)D) + eps);
     uint16_t* dst = isq ? qo + (int64_t)h * D : kc + (int64_t)(h - Hq) * head_stride + pos * D;
-    const uint16_t* cs = cos_t + pos * D;
-    const uint16_t* sn = sin_t + pos * D;
-#pragma unroll
-    for (int t = 0; t < NP; ++t) {
-        const int i = lane + 64 * t;
-        if (i < HALF) {
-            const float na = rbf(bf(nw[i]) * rbf(a[t] * rs));
-            const float nb = rbf(bf(nw[i + HALF]) * rbf(b[t] * rs));
-            const float lo = na * bf(cs[i]) + (-nb) * bf(sn[i]);
-            const float hi = nb * bf(cs[i + HALF]) + na * bf(sn[i + HALF]);
-            dst[i] = f32_to_bf16(lo);
-            dst[i + HALF] = f32_to_bf16(hi);
-        }
-    }
+    head_norm_rope<D>(x, isq ? qnw : knw, eps, cos_t + pos * D, sin_t + pos * D, dst, nullptr, lane);
 }
 
 // softmax (binary32) over E bf16 logits, top-k (descending; equal values: lower

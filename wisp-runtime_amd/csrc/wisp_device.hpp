@@ -423,6 +423,55 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+__device__ __forceinline__ float bf(uint32_t v16) { return __uint_as_float(v16 << 16); }
+__device__ __forceinline__ float rbf(float v) { return bf(f32_to_bf16(v)); }  // round to bf16, as float
+
+// One q or k head of the decoder on one wave (graphdec.py:163-170: q_norm / k_norm, the
+// Qwen3 RMSNorm module in bf16, then rope_decode at one position): lane t takes the
+// element pairs (i, i + D/2), i = t, t + 64, ...; the sum of squares adds a^2 + b^2 per
+// pair in that order, then the xor butterfly over the 64 lanes; x * rsqrt(mean + eps) and
+// the weight product are each rounded to bf16 as the module's bf16 tensors are; the
+// rotation runs in binary32 on those values and the cos/sin rows, rounded once. The
+// result goes to dst and, when non-null, to dst2 (bf16). Every lane of the wave calls it.
+template <int D>
+__device__ __forceinline__ void head_norm_rope(const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw,
+                                               float eps, const uint16_t* __restrict__ cs,
+                                               const uint16_t* __restrict__ sn, uint16_t* dst, uint16_t* dst2,
+                                               int lane) {
+#pragma clang fp contract(off)
+    constexpr int HALF = D / 2;
+    constexpr int NP = (HALF + 63) / 64;
+    float a[NP], b[NP];
+    float ss = 0.f;
+#pragma unroll
+    for (int t = 0; t < NP; ++t) {
+        const int i = lane + 64 * t;
+        a[t] = i < HALF ? bf(x[i]) : 0.f;
+        b[t] = i < HALF ? bf(x[i + HALF]) : 0.f;
+        ss += a[t] * a[t];
+        ss += b[t] * b[t];
+    }
+    ss = wave_sum(ss);
+    const float rs = rsqrtf(ss * (1.0f / (float)D) + eps);
+#pragma unroll
+    for (int t = 0; t < NP; ++t) {
+        const int i = lane + 64 * t;
+        if (i < HALF) {
+            const float na = rbf(bf(nw[i]) * rbf(a[t] * rs));
+            const float nb = rbf(bf(nw[i + HALF]) * rbf(b[t] * rs));
+            const float lo = na * bf(cs[i]) + (-nb) * bf(sn[i]);
+            const float hi = nb * bf(cs[i + HALF]) + na * bf(sn[i + HALF]);
+            const uint16_t l16 = f32_to_bf16(lo), h16 = f32_to_bf16(hi);
+            dst[i] = l16;
+            dst[i + HALF] = h16;
+            if (dst2) {
+                dst2[i] = l16;
+                dst2[i + HALF] = h16;
+            }
+        }
+    }
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
     // silu(g) * u = g * sigmoid(g) * u, as kernels.py:68 (fp32)
     return g * (1.0f / (1.0f + __expf(-g))) * u;

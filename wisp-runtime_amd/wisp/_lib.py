@@ -42,6 +42,8 @@ SIGNATURES = {
     "wisp_rope_decode": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "wisp_attn_ws_bytes": (_i64, [_i32, _i32, _i32]),
     "wisp_attn_decode": (_i32, [_vp, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, ctypes.c_float, _vp, _vp, _vp]),
+    "wisp_attn_decode_qk": (_i32, [_vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _i64, _i32,
+                                   ctypes.c_float, _vp, _vp, _vp]),
     "wisp_prefill_ws_bytes": (_i64, [_i64, _i64, _i64]),
     "wisp_moe_prefill": (_i32, [_vp, _i64, _i64, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _i64, _i64,
                                 _i32, _i64, _vp, _vp, _vp, _vp]),

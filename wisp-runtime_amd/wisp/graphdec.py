@@ -24,9 +24,10 @@ How this build lays it out:
   * Every tensor a segment reads or writes exists once (token/position in `ctl`, the
     residual streams, q/k/v, router logits, route row, meta), so the segments' kernel
     arguments never change and the graphs follow the device-side position and routing.
-  * A segment is nine launches per layer, all this package's gfx950 kernels: RMSNorm +
-    q/k/v GEMV, q/k head norm + rope + K/V store, attention over the static cache (two),
-    o_proj + residual, RMSNorm + router GEMV, route, and the two MoE decode kernels.
+  * A segment is eight launches per layer, all this package's gfx950 kernels: RMSNorm +
+    q/k/v GEMV, attention over the static cache with the q/k head norm + rope + K/V store
+    folded into its first launch (two), o_proj + residual, RMSNorm + router GEMV, route,
+    and the two MoE decode kernels.
   * Host step: the route kernel writes the row and bumps a sequence flag in pinned
     memory; one native call waits for the flag, runs the cache's LRU step, queues the
     page kernel for the misses and writes meta on the stream -- no stream sync per layer.
@@ -124,7 +125,6 @@ class GraphDecoder:
         self.hm = torch.zeros(1, 1, self.H, **bf)  # residual stream after attention
         self.xn = torch.zeros(1, 1, self.H, **bf)  # normed MoE input
         self.qkv = torch.zeros((self.Hq + 2 * self.Hk) * self.D, **bf)
-        self.qo = torch.zeros(self.Hq * self.D, **bf)
         self.rlogits = torch.zeros(self.E, **bf)
         self.logits = torch.zeros(1, s.cfg.vocab_size, **bf)
         self.prefetch = bool(rt is not None and getattr(rt, "prefetch", False))
@@ -229,9 +229,8 @@ class GraphDecoder:
         pos = self.ctl[1:2]
         kernels.dl_gemv(self.qkv, w["q"], a, w1=w["k"], w2=w["v"], a_row=a_row, b=b, norm_w=w["ln1"],
                         eps=w["eps1"], h_out=self.hbuf)
-        kernels.dl_qk_rope(self.qkv, w["qn"], w["kn"], w["epsq"], self.cos, self.sin, pos, Hq, Hk, D,
-                           self.kc[i], self.vc[i], self.qo)
-        attn = kernels.attn_decode(self.qo.view(Hq, D), self.kc[i], self.vc[i], pos, w["scale"])
+        attn = kernels.dl_qk_rope_attn(self.qkv, w["qn"], w["kn"], w["epsq"], self.cos, self.sin, pos, Hq, Hk, D,
+                                       self.kc[i], self.vc[i], w["scale"])
         kernels.dl_gemv(self.hm.view(H), w["o"], attn.view(Hq * D), res=self.hbuf)
         kernels.dl_gemv(self.rlogits, w["gate"], self.hm.view(H), norm_w=w["ln2"], eps=w["eps2"],
                         x_out=self.xn.view(H))

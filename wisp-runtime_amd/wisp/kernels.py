@@ -406,6 +406,32 @@ def dl_qk_rope(qkv, q_norm_w, k_norm_w, eps, cos, sin, pos, hq, hk, d, kc, vc, q
     return qo
 
 
+def dl_qk_rope_attn(qkv, q_norm_w, k_norm_w, eps, cos, sin, pos, hq, hk, d, kc, vc, scale):
+    """dl_qk_rope followed by attn_decode on its q heads, in one pair of launches (the q/k
+    head norm, rope and K/V store at pos run inside the attention workgroups; the same
+    bits as the two calls). Replaces graphdec.py:163-174 at batch 1. Returns
+    [1, hq, 1, d] bf16."""
+    for t, n in ((qkv, "qkv"), (q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w"), (cos, "cos"), (sin, "sin")):
+        _bf16_vec(t, n)
+    assert qkv.numel() == (hq + 2 * hk) * d
+    assert kc.shape == vc.shape and kc.shape[1] == hk and kc.shape[3] == d and kc.stride() == vc.stride()
+    assert kc.stride(-1) == 1 and kc.stride(-2) == d and cos.shape[-1] == d and sin.shape == cos.shape
+    assert kc.dtype == torch.bfloat16 and vc.dtype == torch.bfloat16
+    assert pos.dtype == torch.int64 and pos.numel() >= 1
+    dev = _lib.require_gpu(qkv, kc, vc, pos, what="dl_qk_rope_attn")
+    tmax = kc.shape[2]
+    L = _lib.lib()
+    ws = torch.empty(L.wisp_attn_ws_bytes(hq, d, tmax), dtype=torch.uint8, device=dev)
+    out = torch.empty((1, hq, 1, d), dtype=torch.bfloat16, device=dev)
+    _lib.check(
+        L.wisp_attn_decode_qk(_lib.ptr(qkv), _lib.ptr(q_norm_w), _lib.ptr(k_norm_w), float(eps), _lib.ptr(cos),
+                              _lib.ptr(sin), _lib.ptr(pos), hq, hk, d, _lib.ptr(kc), _lib.ptr(vc), kc.stride(1), tmax,
+                              float(scale), _lib.ptr(ws), _lib.ptr(out), _lib.stream(dev)),
+        "dl_qk_rope_attn",
+    )
+    return out
+
+
 def dl_route(logits, k, norm_topk, row, host_row=None, host_flag=None, seq=None):
     """route() of wisp/moe.py:41-47 at batch 1 on the device: softmax (float32) of the bf16
     router logits [E], top-k, renormalised if norm_topk, weights rounded to bf16;
