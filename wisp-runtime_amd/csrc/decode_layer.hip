@@ -95,9 +95,15 @@ __global__ __launch_bounds__(256) void k_dl_gemv(const GemvArgs g) {
     uint4 xv[CPL];
     const uint16_t* A = g.a + (g.a_row ? *g.a_row * (int64_t)K : 0);
     if (NORM) {
-        // h = a (+ b) in bf16; x = bf16(w * bf16(h * rsqrt(mean(h^2) + eps)))
+        // h = a (+ b) in bf16; x = bf16(w * bf16(h * rsqrt(mean(h^2) + eps))); the norm
+        // weights are requested with the inputs, before the reduction
         const uint4* a4 = reinterpret_cast<const uint4*>(A);
         const uint4* b4 = reinterpret_cast<const uint4*>(g.b);
+        const uint4* n4 = reinterpret_cast<const uint4*>(g.nw);
+        constexpr int PT = (CPL * 64 + 255) / 256;  // 16-byte chunks per thread
+        uint4 nv[PT];
+#pragma unroll
+        for (int t = 0; t < PT; ++t) nv[t] = n4[min((int)threadIdx.x + 256 * t, CPL * 64 - 1)];
         float ss = 0.f;
         for (int i = threadIdx.x; i < CPL * 64; i += 256) {
             float h[8];
@@ -112,17 +118,19 @@ __global__ __launch_bounds__(256) void k_dl_gemv(const GemvArgs g) {
             for (int e = 0; e < 8; ++e) ss += h[e] * h[e];
             xs[i] = pack8(h);
         }
-        ss = wave_sum(ss);
+        ss = wave_sum_dpp(ss);
         if (lane == 0) red[wv] = ss;
         __syncthreads();
         const float var = (red[0] + red[1] + red[2] + red[3]) * (1.0f / (float)K);
         const float rs = rsqrtf(var + g.eps);
-        const uint4* n4 = reinterpret_cast<const uint4*>(g.nw);
-        for (int i = threadIdx.x; i < CPL * 64; i += 256) {
+#pragma unroll
+        for (int t = 0; t < PT; ++t) {
+            const int i = threadIdx.x + 256 * t;
+            if (i >= CPL * 64) break;
             const uint4 hq = xs[i];
             float h[8], w[8], x[8];
             unpack8(hq, h);
-            unpack8(n4[i], w);
+            unpack8(nv[t], w);
 #pragma unroll
             for (int e = 0; e < 8; ++e) x[e] = w[e] * rbf(h[e] * rs);
             const uint4 xq = pack8(x);
