@@ -664,7 +664,7 @@ def run_c4(a) -> dict:
         def _expert_ids(self, i):
             return draws[self.pos - pos0][i]
 
-    dec = ZipfDecoder(model, rt, tmax=tmax)
+    dec = ZipfDecoder(model, rt, tmax=tmax, device_paging={"device": True, "host": False, "auto": "auto"}[a.c4_paging])
     with torch.no_grad():  # a filled context: random K/V up to pos0
         for i in range(Lr):
             dec.kc[i][:, :, :pos0].normal_()
@@ -675,8 +675,11 @@ def run_c4(a) -> dict:
             tok = dec.next(tok).argmax(-1)
             print(f"[bench] c4 warm-up token {w}", file=sys.stderr, flush=True)
         torch.cuda.synchronize()
-        st0 = dict(rt.cache.core.stats)
+        st0 = dict(rt.cache.core.stats)  # (device paging: the state copied back, paging off)
         b0 = rt.cache.bytes_h2d
+        if dec._dev:  # on again before the timed tokens
+            rt.cache.device_begin()
+            torch.cuda.synchronize()
         t1 = time.perf_counter()
         for _ in range(a.c4_tokens):
             tok = dec.next(tok).argmax(-1)
@@ -702,7 +705,9 @@ def run_c4(a) -> dict:
                                f"context {pos0}..{pos0 + a.c4_warmup + a.c4_tokens} of {tmax}, random-init weights",
                    "hit_rate": round(hits / max(1, hits + misses), 4),
                    "h2d_MB_per_token": round((rt.cache.bytes_h2d - b0) / a.c4_tokens / 1e6, 2),
-                   "store_GiB": round(store.total_gib, 2), "copy": rt.cache.copy},
+                   "store_GiB": round(store.total_gib, 2), "copy": rt.cache.copy,
+                   "paging": ("device: LRU step + page kernel inside the token's one graph" if dec._dev
+                              else "host: native LRU step between the layers' graphs")},
     }
 
 
@@ -935,6 +940,9 @@ def main():
     ap.add_argument("--c4-warmup", type=int, default=8)
     ap.add_argument("--c4-copy", default="auto", choices=["dma", "kernel", "auto"],
                     help="how expert misses cross PCIe (ExpertCache copy=)")
+    ap.add_argument("--c4-paging", default="auto", choices=["device", "host", "auto"],
+                    help="where each layer's LRU step runs: on the GPU inside the token's graph, or on the host "
+                         "between the layers' graphs (auto: the GPU when the cache allows it)")
     ap.add_argument("--summarize-c5", nargs="+", metavar="T:STATS_CSV:BENCH_LOG",
                     help="write profiles/moe_prefill_c5_q4_kernel_trace.md from per-T rocprofv3 --stats runs")
     ap.add_argument("--summarize-sq", nargs="+", metavar="T:PASS_A_CSV:PASS_B_CSV",

@@ -306,6 +306,42 @@ int wisp_cache_set_copy_mode(void* cache, int mode);
  * experts, releases the old pool, allocates the new one, re-copies. */
 int wisp_cache_resize(void* cache, int64_t nslots);
 
+/* Device paging: the graph decoder's per-layer paging point (graphdec.py:216-231:
+ * route row -> CacheCore.ensure -> copies of the misses -> meta) on the GPU, so
+ * a captured decode step needs no host decision between layers. The bookkeeping
+ * is cache_core.py:86-106 with the LRU policy (ticks per step, hits protected,
+ * free slots in ascending order, then the first-index argmin of `last` over the
+ * unprotected dynamic slots), kept in device memory while device paging is on.
+ * No reference counterpart as an interface (the reference decides on the host).
+ *
+ * begin: copy the core's LRU state to the device, ordered on `stream` after the
+ * copies already issued. Needs the LRU policy, copy mode 1, nslots - n_static <=
+ * 8192, nslots <= 2^20 and the free slots at the top of the pool (as the core
+ * hands them out); WISP_EINVAL otherwise. A no-op when device paging is on.
+ * While it is on, wisp_cache_issue / _ensure / _prepare_* / _resize return
+ * WISP_EINVAL (the host core is stale until _sync or _end). */
+int wisp_cache_device_begin(void* cache, void* stream);
+/* One layer on `stream`, capturable (no host sync, no allocation): keys =
+ * key_base + id_j, id_j = ids[j] (device int64 [k]) if ids, else row[j] (row:
+ * device float32 [ids (k) | weights (k)], e.g. wisp_dl_route's row; an id must
+ * be an integer in [0, n_ids)); meta (device float32 [2k]) = [slots | row's
+ * weights]; the misses are paged by a kernel reading the pinned store. A bad id
+ * or a miss with no evictable slot gets slot -1 (the MoE kernels then write NaN
+ * rows) and is reported by the next _sync / _end. 1 <= k <= 16; k = 0 launches
+ * both kernels without a step (a warm-up before capture). */
+int wisp_cache_device_step(void* cache, const float* row, const int64_t* ids, int64_t key_base, int64_t n_ids,
+                           int k, float* meta, void* stream);
+/* Synchronise `stream` and copy the device LRU state into the host core and the
+ * load counters; device paging stays on. WISP_EINVAL (once) if a step since
+ * the last sync met a bad id or had no evictable slot. The core's decayed
+ * frequencies (read only by the wsa policy and admission) are not advanced by
+ * device steps. */
+int wisp_cache_device_sync(void* cache, void* stream);
+/* wisp_cache_device_sync, then device paging off and its state freed. */
+int wisp_cache_device_end(void* cache, void* stream);
+/* 1 while device paging is on, else 0. */
+int wisp_cache_device_active(void* cache);
+
 /* ---------------------------------------------------------------------------
  * gpt-oss experts (wisp/gptoss.py). An expert is gate_up [H, 2I] (gate/up
  * interleaved on the output axis) and down [I, H], input-major, stored in the

@@ -159,7 +159,7 @@ def c4_setup():
     return store, rt, model, draws, kv0
 
 
-def _decode(c4_setup, use_graph):
+def _decode(c4_setup, use_graph, device_paging=False):
     """C4_TOKENS greedy decode tokens after a random context of C4_POS0 positions; returns the
     logits of each token, the decoder, and the sampled layers' (x, meta, slot rows, output)."""
     from wisp.cache import ExpertCache
@@ -184,7 +184,7 @@ def _decode(c4_setup, use_graph):
                                 self.rt.cache.gpu.index_select(0, slots).clone(), y.clone()))
             return y
 
-    dec = ZipfDecoder(model, rt, tmax=C4_TMAX, use_graph=use_graph)
+    dec = ZipfDecoder(model, rt, tmax=C4_TMAX, use_graph=use_graph, device_paging=device_paging)
     with torch.no_grad():
         dec.kv[:, :, :, :C4_POS0].copy_(kv0)
         dec.pos = C4_POS0
@@ -241,5 +241,20 @@ def test_c4_full_shape_graph_equals_eager_and_cache_matches_reference(c4_setup):
         err = float(np.linalg.norm(got - r) / np.linalg.norm(r))
         print(f"C4 pos {pos} layer {i}: MoE rel-L2 {err:.3e}")
         assert err <= 1e-3, (pos, i, err)
+
+    # the same decode with the paging points on the GPU: one graph per token, the same
+    # logits bit for bit and the same LRU bookkeeping
+    dgraph, ddec, _ = _decode(c4_setup, use_graph=True, device_paging=True)
+    assert ddec._dev and len(ddec.graphs) == 1
+    assert torch.equal(dgraph.view(torch.int16), eager.view(torch.int16)), "device paging differs from eager"
+    core = rt.cache.core
+    assert core.key2slot == ref.where
+    assert {n: core.stats[n] for n in ("hits", "misses", "evictions", "calls")} == {
+        n: ref.counts[n] for n in ("hits", "misses", "evictions", "calls")}
+    items = sorted(core.key2slot.items())
+    for c0 in range(0, len(items), 64):
+        keys = [kk for kk, _ in items[c0:c0 + 64]]
+        slots = torch.tensor([ss for _, ss in items[c0:c0 + 64]], device=DEV)
+        assert torch.equal(rt.cache.gpu.index_select(0, slots).cpu(), store.host[keys]), keys[:4]
     rt.cache.free()
     rt.cache = None

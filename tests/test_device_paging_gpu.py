@@ -1,0 +1,192 @@
+"""Device paging: the decode layer's LRU step (cache_core.py:86-106) and the paging of its
+misses run on the GPU (k_lru_step + k_page_list), checked step by step against the
+reference LRU (oracle/cache_core_ref.py) on the same key streams, including graph replays,
+repeated ids, a static region, bad ids and a request with no evictable slot."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from oracle.cache_core_ref import RefCore
+from wisp.cache import ExpertCache
+from wisp.store import ExpertStore
+
+pytestmark = pytest.mark.gpu
+H, I, G = 256, 128, 128
+N = H * I
+DEV = "cuda"
+
+
+def _store(L, E, seed=0):
+    rng = np.random.default_rng(seed)
+    st = ExpertStore(L, E, N, 4, G)
+    for key in range(L * E):
+        w = (rng.standard_normal(3 * N) * 0.02).astype(np.float32)
+        st.host[key].copy_(torch.from_numpy(O.quantize(w, 4, G)))
+    return st
+
+
+@pytest.fixture(scope="module")
+def store():
+    return _store(3, 24, seed=5)
+
+
+def _check_state(c, ref, st):
+    core = c.core  # ends device paging: the host core now holds the device state
+    assert core.key2slot == ref.where
+    assert core.stats == ref.counts
+    assert [int(v) for v in core.slot_key] == ref.owner
+    assert [float(v) for v in core.last] == ref.t_last
+    assert core.free == list(ref.stack)
+    assert core.tick == ref.now
+    for key, s in ref.where.items():  # every resident slot holds its store row
+        assert torch.equal(c.gpu[s].cpu(), st.host[key]), (key, s)
+
+
+def _row(ids, w):
+    return torch.tensor(list(map(float, ids)) + list(map(float, w)), dtype=torch.float32, device=DEV)
+
+
+@pytest.mark.parametrize("nslots,k,use_row", [(10, 4, False), (10, 8, True), (20, 16, False), (9, 1, True),
+                                             (64, 8, False)])
+def test_device_steps_match_reference_lru(store, nslots, k, use_row):
+    E = 24
+    c = ExpertCache(store, nslots, copy="kernel")
+    ref = RefCore(nslots, "lru")
+    rng = np.random.default_rng(nslots * 31 + k)
+    meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    c.device_begin()
+    assert c.device_paging
+    for it in range(60):
+        layer = int(rng.integers(0, 3))
+        ids = rng.choice(E, size=k, replace=False).astype(np.int64)
+        w = rng.random(k).astype(np.float32)
+        keys = [layer * E + int(v) for v in ids]
+        if use_row:
+            c.device_step(_row(ids, w), None, layer * E, E, k, meta)
+        else:
+            c.device_step(_row(np.zeros(k), w), torch.from_numpy(ids).to(DEV), layer * E, E, k, meta)
+        slots, _ = ref.ensure(keys)
+        m = meta.cpu()
+        assert [int(v) for v in m[:k]] == slots, it
+        assert torch.equal(m[k:], torch.from_numpy(w)), it
+        if it % 15 == 14:
+            c.device_sync()  # state copied back, device paging stays on
+            assert c.device_paging
+            assert c.core.stats == ref.counts  # (ends device paging)
+            c.device_begin()
+    _check_state(c, ref, store)
+    assert c.n_loads == ref.counts["misses"] and c.bytes_h2d == c.n_loads * store.nbytes
+    c.free()
+
+
+def test_repeated_ids_and_hits_in_one_step(store):
+    """Forced ids may repeat a key: the reference hands each occurrence of a missing key its
+    own slot and keeps the later one in key2slot; the device step does the same. (The pool is
+    large enough that no such orphaned slot is evicted: the reference raises when it evicts
+    a second slot of one key.)"""
+    E, nslots, k = 24, 40, 6
+    c = ExpertCache(store, nslots, copy="kernel")
+    ref = RefCore(nslots, "lru")
+    meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    row = _row(np.zeros(k), np.ones(k))
+    c.device_begin()
+    for ids in ([1, 1, 2, 3, 3, 3], [1, 2, 4, 5, 6, 7], [8, 9, 8, 10, 11, 1], [12, 13, 14, 15, 16, 17],
+                [2, 2, 2, 2, 2, 2], [18, 19, 20, 21, 22, 23]):
+        c.device_step(row, torch.tensor(ids, dtype=torch.int64, device=DEV), 0, E, k, meta)
+        slots, _ = ref.ensure(list(ids))
+        assert [int(v) for v in meta.cpu()[:k]] == slots, ids
+    _check_state(c, ref, store)
+    c.free()
+
+
+def test_static_region_and_host_steps_between(store):
+    """A cache with a preloaded static region (never evicted), device steps alternating with
+    host-side ensure calls (each ends device paging; the next begin uploads the state)."""
+    E, nslots, k, n_static = 24, 14, 4, 4
+    pre = [0, 5, 30, 47]
+    c = ExpertCache(store, nslots, n_static=n_static, preload_keys=pre, copy="kernel")
+    ref = RefCore(nslots, "lru", n_static=n_static)
+    ref.preload(pre)
+    rng = np.random.default_rng(9)
+    meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    for it in range(40):
+        layer = int(rng.integers(0, 3))
+        ids = rng.choice(E, size=k, replace=False).astype(np.int64)
+        keys = [layer * E + int(v) for v in ids]
+        if it % 3 == 2:
+            assert c.ensure(keys) == ref.ensure(keys)[0], it
+        else:
+            c.device_begin()
+            c.device_step(_row(ids, np.ones(k)), None, layer * E, E, k, meta)
+            assert [int(v) for v in meta.cpu()[:k]] == ref.ensure(keys)[0], it
+    _check_state(c, ref, store)
+    c.free()
+
+
+def test_graph_replays_of_device_steps(store):
+    """Three layers' paging points captured in one graph and replayed with new ids each time
+    (eager work and syncs between the replays); every replay matches the reference LRU."""
+    E, nslots, k = 24, 16, 8
+    c = ExpertCache(store, nslots, copy="kernel")
+    ref = RefCore(nslots, "lru")
+    ids = torch.zeros(3, k, dtype=torch.int64, device=DEV)
+    row = _row(np.zeros(k), np.linspace(0.1, 0.8, k))
+    metas = [torch.zeros(2 * k, dtype=torch.float32, device=DEV) for _ in range(3)]
+    c.device_begin()
+    c.device_step(row, None, 0, E, 0, metas[0])  # warm-up launch: changes nothing
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for layer in range(3):
+            c.device_step(row, ids[layer], layer * E, E, k, metas[layer])
+    rng = np.random.default_rng(11)
+    for rep in range(12):
+        draw = np.stack([rng.choice(E, size=k, replace=False) for _ in range(3)]).astype(np.int64)
+        ids.copy_(torch.from_numpy(draw))
+        g.replay()
+        x = torch.randn(512, 512, device=DEV)
+        (x @ x).sum().item()  # eager work and a sync between the replays
+        for layer in range(3):
+            slots, _ = ref.ensure([layer * E + int(v) for v in draw[layer]])
+            assert [int(v) for v in metas[layer].cpu()[:k]] == slots, (rep, layer)
+    _check_state(c, ref, store)
+    c.free()
+
+
+def test_bad_id_and_no_evictable_slot_are_reported(store):
+    E, k = 24, 4
+    c = ExpertCache(store, 6, copy="kernel")
+    meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    c.device_begin()
+    c.device_step(_row([1, 2, 99, 3], np.ones(k)), None, 0, E, k, meta)  # id 99 >= n_ids
+    m = meta.cpu()
+    assert int(m[2]) == -1 and all(int(v) >= 0 for v in m[[0, 1, 3]])
+    with pytest.raises(RuntimeError, match="outside"):
+        c.device_sync()
+    c.device_sync()  # reported once
+    c.device_end()
+    c2 = ExpertCache(store, 6, copy="kernel")
+    k = 8  # more keys than slots: the reference raises on the 7th miss
+    meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    c2.device_begin()
+    c2.device_step(_row(list(range(8)), np.ones(k)), None, 0, E, k, meta)
+    m = meta.cpu()
+    assert [int(v) for v in m[:6]] == list(range(6)) and [int(v) for v in m[6:8]] == [-1, -1]
+    with pytest.raises(RuntimeError, match="no evictable slot"):
+        c2.device_end()
+    assert not c2.device_paging
+    c.free()
+    c2.free()
+
+
+def test_device_paging_refusals(store):
+    c = ExpertCache(store, 8, copy="dma")
+    with pytest.raises(RuntimeError, match="page-kernel"):
+        c.device_begin()
+    c.free()
+    c = ExpertCache(store, 8, policy="wsa", copy="kernel")
+    with pytest.raises(RuntimeError, match="LRU"):
+        c.device_begin()
+    c.free()

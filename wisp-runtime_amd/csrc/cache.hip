@@ -1,7 +1,9 @@
 // Expert cache for batch-1 MoE decode: slot bookkeeping (CacheCore) and the
 // hipMalloc slot pool filled from a pinned host store by hipMemcpyAsync on a
-// side stream (ExpertCache). Host code only; no kernels of its own (the
-// decode-on-load mode reuses the dequant kernel).
+// side stream or by a page kernel that reads the pinned rows itself
+// (ExpertCache); optionally the LRU step on the GPU (device paging), so a
+// captured decode step needs no host decision between layers. The
+// decode-on-load mode reuses the dequant kernel.
 //
 // Reference semantics:
 //   CacheCore  wisp/cache_core.py:15-149 (LRU / WSA / static policies, ensure,
@@ -196,6 +198,20 @@ static void view_deleter(DLManagedTensor* m) {
     delete v;
 }
 
+// Device paging: the LRU state in device memory (one allocation) while it is on.
+constexpr int kDevMaxK = 16;        // keys per step
+constexpr int kDevMaxSlots = 8192;  // dynamic slots: their eviction keys are staged in LDS
+enum { kCtrTick, kCtrNextFree, kCtrHits, kCtrMisses, kCtrEvict, kCtrCalls, kCtrLoads, kCtrErr, kCtrN };
+enum { kDevErrSlot = 1, kDevErrKey = 2 };
+struct DevPaging {
+    int32_t* slot_key = nullptr;  // [nslots], -1 empty
+    int64_t* last = nullptr;      // [nslots], tick of the last use
+    int32_t* key2slot = nullptr;  // [nkeys], -1 not resident
+    int64_t* ctr = nullptr;       // [kCtrN]: tick, next free slot, hits, misses, evictions, calls, loads, error bits
+    int32_t* miss = nullptr;      // [1 + 2 kDevMaxK]: count, keys, slots of the last step's loads
+    int64_t nslots = 0, nkeys = 0, n_static = 0;
+};
+
 struct Cache {
     Core* core = nullptr;
     PoolBlock* pool = nullptr;
@@ -214,6 +230,9 @@ struct Cache {
     const uint8_t* host_dev = nullptr;   // the host store's device address (copy_mode 1)
     bool pending = false;
     int64_t bytes_h2d = 0, n_loads = 0;
+    void* dev_block = nullptr;  // device paging on when not null
+    DevPaging dev;
+    int64_t dev_loads_seen = 0;  // device loads already added to bytes_h2d / n_loads
 };
 
 static int hip_fail(hipError_t e, const char* what) {
@@ -256,13 +275,9 @@ struct PageMeta {
     int n;
 };
 typedef uint32_t pg_u32x4 __attribute__((ext_vector_type(4)));
-__global__ __launch_bounds__(256) void k_page_rows(const pg_u32x4* __restrict__ host, pg_u32x4* __restrict__ pool,
-                                                   const PagePairs p, int64_t row16, int64_t slot16, int64_t per,
-                                                   const PageMeta pm) {
-    const int r = blockIdx.y;
-    if (blockIdx.x == 0 && r == 0 && (int)threadIdx.x < pm.n) pm.dst[threadIdx.x] = pm.v[threadIdx.x];
-    const pg_u32x4* src = host + p.key[r] * row16;
-    pg_u32x4* dst = pool + p.slot[r] * slot16;
+// workgroup blockIdx.x's part [b0, b1) of one row (16-byte units), 4 loads in flight per thread
+__device__ __forceinline__ void page_part(const pg_u32x4* __restrict__ src, pg_u32x4* __restrict__ dst, int64_t row16,
+                                          int64_t per) {
     const int64_t b0 = (int64_t)blockIdx.x * per, b1 = min(row16, b0 + per);
     constexpr int U = 4;
     for (int64_t i = b0 + threadIdx.x; i < b1; i += 256 * U) {
@@ -277,6 +292,142 @@ __global__ __launch_bounds__(256) void k_page_rows(const pg_u32x4* __restrict__ 
             const int64_t ii = i + (int64_t)u * 256;
             if (ii < b1) dst[ii] = v[u];
         }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_page_rows(const pg_u32x4* __restrict__ host, pg_u32x4* __restrict__ pool,
+                                                   const PagePairs p, int64_t row16, int64_t slot16, int64_t per,
+                                                   const PageMeta pm) {
+    const int r = blockIdx.y;
+    if (blockIdx.x == 0 && r == 0 && (int)threadIdx.x < pm.n) pm.dst[threadIdx.x] = pm.v[threadIdx.x];
+    page_part(host + p.key[r] * row16, pool + p.slot[r] * slot16, row16, per);
+}
+
+// The rows of the miss list that k_lru_step left in device memory: grid
+// (kPageSplit, k), row blockIdx.y if it is below the list's count.
+__global__ __launch_bounds__(256) void k_page_list(const pg_u32x4* __restrict__ host, pg_u32x4* __restrict__ pool,
+                                                   const int32_t* __restrict__ miss, int64_t row16, int64_t slot16,
+                                                   int64_t per) {
+    const int r = blockIdx.y;
+    if (r >= miss[0]) return;
+    page_part(host + (int64_t)miss[1 + r] * row16, pool + (int64_t)miss[1 + kDevMaxK + r] * slot16, row16, per);
+}
+
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint32_t lo = __shfl_xor((unsigned)v, o, 64), hi = __shfl_xor((unsigned)(v >> 32), o, 64);
+        const uint64_t u = ((uint64_t)hi << 32) | lo;
+        v = u < v ? u : v;
+    }
+    return v;
+}
+
+// cache_core.py:86-106 (ensure) with the LRU policy, as one wave on the GPU, for
+// one layer: lane j < k takes key key_base + id_j (id_j = ids[j] if ids, else the
+// route row's id j, which must be an integer in [0, n_ids)). Hits are noted with
+// the step's tick; misses take free slots in ascending order, then the least
+// recently used unprotected slots. The reference picks each victim by a
+// first-index argmin of `last` over the unprotected dynamic slots, and every slot
+// it hands out becomes protected, so the i-th evicting miss (in key order) gets
+// the i-th smallest (last, slot) among the slots in [n_static, next free) that
+// are not hits of this step. meta = [slots (float) | the row's weights]; the
+// loads go to the miss list for k_page_list. A key that is not valid or a miss
+// without an evictable slot gets slot -1 in meta (the MoE kernels then write NaN
+// rows) and sets an error bit that the host reads when it syncs the state.
+// k <= 0: a warm-up launch that only clears the miss list.
+__global__ __launch_bounds__(64) void k_lru_step(const DevPaging d, const float* __restrict__ row,
+                                                 const int64_t* __restrict__ ids, int64_t key_base, int64_t n_ids,
+                                                 int k, float* __restrict__ meta) {
+    __shared__ uint64_t cand[kDevMaxSlots];
+    const int lane = threadIdx.x;
+    if (k <= 0) {
+        if (lane == 0) d.miss[0] = 0;
+        return;
+    }
+    const int64_t tick = d.ctr[kCtrTick] + 1;
+    const int64_t nf = d.ctr[kCtrNextFree];
+    const bool on = lane < k;
+    int key = -1;
+    float w = 0.f;
+    if (on) {
+        int64_t id = -1;
+        if (ids) {
+            id = ids[lane];
+        } else {
+            const float f = row[lane];
+            if (f >= 0.f && f < 16777216.f && (float)(int64_t)f == f) id = (int64_t)f;
+        }
+        if (id >= 0 && id < n_ids && key_base + id >= 0 && key_base + id < d.nkeys) key = (int)(key_base + id);
+        w = row[k + lane];
+    }
+    int slot = key >= 0 ? d.key2slot[key] : -1;
+    const bool hit = slot >= 0;
+    const uint64_t mm = __ballot(key >= 0 && !hit);
+    const uint64_t hm = __ballot(hit);
+    const uint64_t bad = __ballot(on && key < 0);
+    const bool miss = (mm >> lane) & 1ull;
+    const int nmiss = __popcll(mm);
+    const int rank = __popcll(mm & ((1ull << lane) - 1ull));
+    const int64_t nfree = d.nslots - nf;
+    const int from_free = (int)((int64_t)nmiss < nfree ? (int64_t)nmiss : nfree);
+    const int m = nmiss - from_free;  // misses that evict
+    if (miss && rank < from_free) slot = (int)(nf + rank);
+    int got = from_free;  // misses with a slot
+    int old_key = -1;     // the key this lane's victim held
+    if (m > 0) {
+        // eviction keys (last, slot) + 1 of the dynamic slots in use; this step's hits excluded
+        const int64_t nc = nf - d.n_static;
+        for (int64_t i = lane; i < nc; i += 64)
+            cand[i] = (((uint64_t)d.last[d.n_static + i] << 20) | (uint64_t)(d.n_static + i)) + 1ull;
+        __syncthreads();
+        if (hit && slot >= d.n_static) cand[slot - d.n_static] = ~0ull;
+        __syncthreads();
+        uint64_t prev = 0;
+        for (int r = 0; r < m; ++r) {
+            uint64_t best = ~0ull;
+            for (int64_t i = lane; i < nc; i += 64) {
+                const uint64_t v = cand[i];
+                if (v > prev && v < best) best = v;
+            }
+            best = wave_min_u64(best);
+            if (best == ~0ull) break;  // nothing evictable is left
+            prev = best;
+            if (miss && rank == from_free + r) slot = (int)((best - 1ull) & 0xFFFFFull);
+            ++got;
+        }
+        if (miss && rank >= from_free && slot >= 0) old_key = d.slot_key[slot];
+    }
+    // a key repeated later in the step: the later lane's slot is the one key2slot keeps
+    bool later = false;
+    for (int j = 0; j < k; ++j) {
+        const int kj = __shfl(key, j, 64);
+        later = later || (j > lane && kj == key);
+    }
+    const bool gets = miss && slot >= 0;
+    if (hit) d.last[slot] = tick;
+    if (gets) {
+        if (old_key >= 0) d.key2slot[old_key] = -1;
+        d.slot_key[slot] = key;
+        if (!later) d.key2slot[key] = slot;
+        d.last[slot] = tick;
+        d.miss[1 + rank] = key;
+        d.miss[1 + kDevMaxK + rank] = slot;
+    }
+    if (on) {
+        meta[lane] = (key >= 0 && slot >= 0) ? (float)slot : -1.f;
+        meta[k + lane] = w;
+    }
+    if (lane == 0) {
+        d.miss[0] = got;
+        d.ctr[kCtrTick] = tick;
+        d.ctr[kCtrNextFree] = nf + from_free;
+        d.ctr[kCtrHits] += __popcll(hm);
+        d.ctr[kCtrMisses] += got;
+        d.ctr[kCtrEvict] += got - from_free;
+        d.ctr[kCtrCalls] += 1;
+        d.ctr[kCtrLoads] += got;
+        d.ctr[kCtrErr] |= (got < nmiss ? kDevErrSlot : 0) | (bad ? kDevErrKey : 0);
     }
 }
 
@@ -424,6 +575,11 @@ static int core_ensure(Core& c, const int64_t* keys, int64_t n, int64_t* slots, 
 
 static Core* as_core(void* h) { return static_cast<Core*>(h); }
 static Cache* as_cache(void* h) { return static_cast<Cache*>(h); }
+
+// host-side bookkeeping while the device holds the LRU state would diverge from it
+static int dev_refuse(const Cache& c) {
+    return c.dev_block ? fail_inval("device paging is on: end it (wisp_cache_device_end) first") : WISP_OK;
+}
 
 }  // namespace wisp
 
@@ -660,6 +816,7 @@ extern "C" void wisp_cache_destroy(void* h) {
     (void)hipEventDestroy(c->order);
     (void)hipStreamDestroy(c->copy);
     if (c->staging) (void)hipFree(c->staging);
+    if (c->dev_block) (void)hipFree(c->dev_block);
     (void)hipSetDevice(cur);
     pool_release(c->pool);
     delete c->core;
@@ -713,6 +870,7 @@ extern "C" void wisp_cache_pool_dlpack_free(void* m) {
 
 extern "C" int wisp_cache_issue(void* h, const int64_t* keys, const int64_t* slots, int64_t n, void* compute) {
     clear_error();
+    if (dev_refuse(*as_cache(h))) return WISP_EINVAL;
     return issue(*as_cache(h), keys, slots, n, (hipStream_t)compute);
 }
 
@@ -724,6 +882,7 @@ extern "C" int wisp_cache_sync_compute(void* h, void* compute) {
 // cache.py:87-91: ensure residency, issue the misses' copies, order compute after them
 extern "C" int wisp_cache_ensure(void* h, const int64_t* keys, int64_t n, int64_t* slots, void* compute) {
     clear_error();
+    if (dev_refuse(*as_cache(h))) return WISP_EINVAL;
     Cache& c = *as_cache(h);
     std::vector<int64_t> lk, ls;
     int rc = core_ensure(*c.core, keys, n, slots, lk, ls);
@@ -793,6 +952,7 @@ extern "C" int wisp_cache_prepare_signaled(void* h, float* row_host, const volat
                                            int64_t key_base, int64_t n_ids, const int64_t* ids, float* meta_host,
                                            float* meta_dev, void* compute) {
     clear_error();
+    if (dev_refuse(*as_cache(h))) return WISP_EINVAL;
     if (k < 1 || k > 16 || !row_host || !flag || !meta_host || !meta_dev) return fail_inval("bad prepare_signaled args");
     const auto t0 = std::chrono::steady_clock::now();
     uint32_t f;
@@ -872,6 +1032,7 @@ extern "C" int wisp_cache_set_copy_mode(void* h, int mode) {
 // allocated, and the kept experts re-copied from the host store.
 extern "C" int wisp_cache_resize(void* h, int64_t nslots) {
     clear_error();
+    if (dev_refuse(*as_cache(h))) return WISP_EINVAL;
     Cache& c = *as_cache(h);
     if (c.decode_on_load) return fail_inval("resize is not supported with decode_on_load");
     if (nslots == c.nslots) return WISP_OK;
@@ -904,3 +1065,190 @@ extern "C" int wisp_cache_resize(void* h, int64_t nslots) {
     (void)hipSetDevice(cur);
     return rc;
 }
+
+// ------------------------------------------------------------------ device paging
+// The graph decoder's paging point on the GPU: wisp_cache_device_step queues
+// k_lru_step (the LRU ensure of one layer) and k_page_list (its misses, read from
+// the pinned store over PCIe) on a stream, with no host decision, so a whole decode
+// step can be one graph. While device paging is on, the LRU state lives in device
+// memory and the host core is stale: entry points that would read or change it are
+// refused until wisp_cache_device_sync / _end copy the state back.
+
+namespace wisp {
+
+static size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+// the device state -> the host core (and the cache's load counters)
+static int dev_download(Cache& c, hipStream_t st) {
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize (device paging)");
+    const DevPaging& d = c.dev;
+    std::vector<int32_t> sk(d.nslots), k2s(d.nkeys);
+    std::vector<int64_t> last(d.nslots), ctr(kCtrN);
+    e = hipMemcpy(sk.data(), d.slot_key, sizeof(int32_t) * d.nslots, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(last.data(), d.last, sizeof(int64_t) * d.nslots, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(k2s.data(), d.key2slot, sizeof(int32_t) * d.nkeys, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(ctr.data(), d.ctr, sizeof(int64_t) * kCtrN, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy (device paging state)");
+    Core& core = *c.core;
+    for (int64_t s = 0; s < d.nslots; ++s) {
+        core.slot_key[s] = sk[s];
+        core.last[s] = (double)last[s];
+    }
+    core.key2slot.clear();
+    for (int64_t key = 0; key < d.nkeys; ++key)
+        if (k2s[key] >= 0) core.key2slot[key] = k2s[key];
+    core.free.clear();
+    for (int64_t s = d.nslots - 1; s >= ctr[kCtrNextFree]; --s) core.free.push_back(s);
+    core.tick = ctr[kCtrTick];
+    core.hits = ctr[kCtrHits];
+    core.misses = ctr[kCtrMisses];
+    core.evictions = ctr[kCtrEvict];
+    core.calls = ctr[kCtrCalls];
+    const int64_t fresh = ctr[kCtrLoads] - c.dev_loads_seen;
+    c.bytes_h2d += fresh * c.row_bytes;
+    c.n_loads += fresh;
+    c.dev_loads_seen = ctr[kCtrLoads];
+    if (ctr[kCtrErr]) {
+        const int64_t zero = 0;
+        (void)hipMemcpy(d.ctr + kCtrErr, &zero, sizeof(int64_t), hipMemcpyHostToDevice);
+        set_error("device paging: %s%s", (ctr[kCtrErr] & kDevErrKey) ? "a routed id outside [0, n_ids) or the store; " : "",
+                  (ctr[kCtrErr] & kDevErrSlot) ? "no evictable slot for a miss (dynamic region smaller than k)" : "");
+        return WISP_EINVAL;
+    }
+    return WISP_OK;
+}
+
+}  // namespace wisp
+
+// Copy the host core's LRU state to the device and turn device paging on (a no-op
+// when it is on). Needs the LRU policy, the page-kernel copy mode, at most 8192
+// dynamic slots (2^20 in all) and the free slots at the top of the pool (the order
+// the core hands them out). Stream-ordered after the copies already issued.
+extern "C" int wisp_cache_device_begin(void* h, void* stream) {
+    clear_error();
+    Cache& c = *as_cache(h);
+    if (c.dev_block) return WISP_OK;
+    const Core& core = *c.core;
+    if (core.policy != kLRU) return fail_inval("device paging runs the LRU policy only");
+    if (c.copy_mode != 1 || !c.host_dev) return fail_inval("device paging needs the page-kernel copy mode");
+    if (!c.pool) return no_pool();
+    if (c.nslots > (1 << 20) || c.nslots - core.n_static > kDevMaxSlots)
+        return fail_inval("device paging: at most 8192 dynamic slots and 2^20 slots in all");
+    if (c.host_rows > INT32_MAX) return fail_inval("device paging: at most 2^31 - 1 store rows");
+    if (core.tick > (int64_t(1) << 42)) return fail_inval("device paging: tick beyond 2^42");
+    const int64_t nfree = (int64_t)core.free.size(), nf = c.nslots - nfree;
+    for (int64_t i = 0; i < nfree; ++i)
+        if (core.free[i] != c.nslots - 1 - i) return fail_inval("device paging needs the free slots at the top of the pool");
+    DevPaging d;
+    d.nslots = c.nslots;
+    d.nkeys = c.host_rows;
+    d.n_static = core.n_static;
+    std::vector<int32_t> sk(d.nslots), k2s(d.nkeys, -1);
+    std::vector<int64_t> last(d.nslots);
+    for (int64_t s = 0; s < d.nslots; ++s) {
+        sk[s] = (int32_t)core.slot_key[s];
+        last[s] = (int64_t)core.last[s];
+    }
+    for (const auto& kv : core.key2slot) {
+        if (kv.first < 0 || kv.first >= d.nkeys) return fail_inval("device paging: a resident key outside the store");
+        k2s[kv.first] = (int32_t)kv.second;
+    }
+    const int64_t ctr[kCtrN] = {core.tick, nf, core.hits, core.misses, core.evictions, core.calls, 0, 0};
+    const size_t b_sk = align256(sizeof(int32_t) * d.nslots), b_last = align256(sizeof(int64_t) * d.nslots),
+                 b_k2s = align256(sizeof(int32_t) * d.nkeys), b_ctr = align256(sizeof(int64_t) * kCtrN),
+                 b_miss = align256(sizeof(int32_t) * (1 + 2 * kDevMaxK));
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    (void)hipSetDevice(c.device);
+    hipStream_t st = (hipStream_t)stream;
+    void* block = nullptr;
+    hipError_t e = hipMalloc(&block, b_sk + b_last + b_k2s + b_ctr + b_miss);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipSetDevice(cur);
+        return hip_fail(e, "hipMalloc (device paging state)");
+    }
+    uint8_t* p = static_cast<uint8_t*>(block);
+    d.slot_key = reinterpret_cast<int32_t*>(p);
+    d.last = reinterpret_cast<int64_t*>(p + b_sk);
+    d.key2slot = reinterpret_cast<int32_t*>(p + b_sk + b_last);
+    d.ctr = reinterpret_cast<int64_t*>(p + b_sk + b_last + b_k2s);
+    d.miss = reinterpret_cast<int32_t*>(p + b_sk + b_last + b_k2s + b_ctr);
+    int rc = sync_compute(c, st);  // copies still pending on the side stream
+    if (!rc) {
+        e = hipMemcpyAsync(d.slot_key, sk.data(), sizeof(int32_t) * d.nslots, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(d.last, last.data(), sizeof(int64_t) * d.nslots, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(d.key2slot, k2s.data(), sizeof(int32_t) * d.nkeys, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(d.ctr, ctr, sizeof(int64_t) * kCtrN, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemsetAsync(d.miss, 0, sizeof(int32_t) * (1 + 2 * kDevMaxK), st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);  // the host vectors go out of scope
+        if (e != hipSuccess) rc = hip_fail(e, "uploading the device paging state");
+    }
+    (void)hipSetDevice(cur);
+    if (rc) {
+        (void)hipFree(block);
+        return rc;
+    }
+    c.dev = d;
+    c.dev_block = block;
+    c.dev_loads_seen = 0;
+    return WISP_OK;
+}
+
+// One layer's paging point on `stream` (capturable: no host sync, no allocation):
+// ensure the keys key_base + id (ids: device int64 [k], else the route row's ids,
+// row = device float32 [ids (k) | weights (k)]), meta (device float32 [2k]) =
+// [slots | weights], then the page kernel for the misses. k in [1, 16]; k = 0
+// launches both kernels without a step (a warm-up before graph capture).
+extern "C" int wisp_cache_device_step(void* h, const float* row, const int64_t* ids, int64_t key_base, int64_t n_ids,
+                                      int k, float* meta, void* stream) {
+    clear_error();
+    Cache& c = *as_cache(h);
+    if (!c.dev_block) return fail_inval("device paging is off (wisp_cache_device_begin)");
+    if (k < 0 || k > kDevMaxK) return fail_inval("device paging takes 0 <= k <= 16");
+    if (k > 0 && (!row || !meta || n_ids < 1)) return fail_inval("device paging step: null row / meta or n_ids < 1");
+    if (!c.pool) return no_pool();
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_lru_step, dim3(1), dim3(64), 0, st, c.dev, row, ids, key_base, n_ids, k, meta);
+    int rc = check_launch("k_lru_step");
+    if (rc) return rc;
+    const int64_t row16 = c.row_bytes / 16, slot16 = c.slot_bytes / 16;
+    const int64_t per = ((row16 + kPageSplit - 1) / kPageSplit + 1023) / 1024 * 1024;
+    hipLaunchKernelGGL(k_page_list, dim3(kPageSplit, k > 0 ? k : 1), dim3(256), 0, st,
+                       reinterpret_cast<const pg_u32x4*>(c.host_dev), reinterpret_cast<pg_u32x4*>(c.pool->ptr),
+                       c.dev.miss, row16, slot16, per);
+    return check_launch("k_page_list");
+}
+
+// Wait for `stream` and copy the device state into the host core (device paging
+// stays on). Reports (once) a step that met a bad id or had no evictable slot.
+extern "C" int wisp_cache_device_sync(void* h, void* stream) {
+    clear_error();
+    Cache& c = *as_cache(h);
+    if (!c.dev_block) return WISP_OK;
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    (void)hipSetDevice(c.device);
+    const int rc = dev_download(c, (hipStream_t)stream);
+    (void)hipSetDevice(cur);
+    return rc;
+}
+
+// wisp_cache_device_sync, then device paging off (its state freed).
+extern "C" int wisp_cache_device_end(void* h, void* stream) {
+    clear_error();
+    Cache& c = *as_cache(h);
+    if (!c.dev_block) return WISP_OK;
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    (void)hipSetDevice(c.device);
+    const int rc = dev_download(c, (hipStream_t)stream);
+    (void)hipFree(c.dev_block);
+    (void)hipSetDevice(cur);
+    c.dev_block = nullptr;
+    c.dev = DevPaging();
+    return rc;
+}
+
+extern "C" int wisp_cache_device_active(void* h) { return as_cache(h)->dev_block ? 1 : 0; }

@@ -87,6 +87,11 @@ SIGNATURES = {
                                            _vp]),
     "wisp_cache_set_copy_mode": (_i32, [_vp, _i32]),
     "wisp_cache_resize": (_i32, [_vp, _i64]),
+    "wisp_cache_device_begin": (_i32, [_vp, _vp]),
+    "wisp_cache_device_step": (_i32, [_vp, _vp, _vp, _i64, _i64, _i32, _vp, _vp]),
+    "wisp_cache_device_sync": (_i32, [_vp, _vp]),
+    "wisp_cache_device_end": (_i32, [_vp, _vp]),
+    "wisp_cache_device_active": (_i32, [_vp]),
     "wisp_set_tuning": (_i32, [_i32, _i32, _i32]),
     "wisp_act_read": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp]),
     "wisp_probe_empty": (_i32, [_vp]),

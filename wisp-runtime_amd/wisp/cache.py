@@ -29,6 +29,12 @@ def _p(a: np.ndarray) -> ctypes.c_void_p:
     return a.ctypes.data_as(ctypes.c_void_p)
 
 
+def _raise(rc: int) -> None:
+    """RuntimeError with the library's message, as the reference cache raises (cache_core.py:80)."""
+    if rc != 0:
+        raise RuntimeError(_lib.lib().wisp_last_error().decode(errors="replace"))
+
+
 _PyCapsule_New = ctypes.pythonapi.PyCapsule_New
 _PyCapsule_New.restype = ctypes.py_object
 _PyCapsule_New.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p]
@@ -109,17 +115,21 @@ class ExpertCache:
 
     @property
     def core(self) -> CacheCore:
-        """The bookkeeping core (owned by the native cache)."""
+        """The bookkeeping core (owned by the native cache); ends device paging first, so the
+        core holds the current state."""
+        self.device_end()
         return CacheCore._wrap(_lib.lib().wisp_cache_core(self._h), owned=False)
 
     @property
     def bytes_h2d(self) -> int:
+        self.device_sync()
         b, n = ctypes.c_int64(), ctypes.c_int64()
         _lib.lib().wisp_cache_counters(self._h, ctypes.byref(b), ctypes.byref(n))
         return b.value
 
     @property
     def n_loads(self) -> int:
+        self.device_sync()
         b, n = ctypes.c_int64(), ctypes.c_int64()
         _lib.lib().wisp_cache_counters(self._h, ctypes.byref(b), ctypes.byref(n))
         return n.value
@@ -127,11 +137,49 @@ class ExpertCache:
     def _stream(self):
         return ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
 
+    # ---- device paging ----------------------------------------------------
+    # The LRU step of a decode layer on the GPU (k_lru_step + the page kernel), so a
+    # captured decode step has no host decision per layer. While it is on, the LRU
+    # state lives in device memory; every host-side operation below ends it first.
+    @property
+    def device_paging(self) -> bool:
+        return bool(self._h) and bool(_lib.lib().wisp_cache_device_active(self._h))
+
+    def device_begin(self):
+        """Copy the core's LRU state to the device (LRU policy, copy="kernel", at most 8192
+        dynamic slots); RuntimeError if this cache cannot page on the device."""
+        _raise(_lib.lib().wisp_cache_device_begin(self._h, self._stream()))
+
+    def device_step(self, row: torch.Tensor, ids, key_base: int, n_ids: int, k: int, meta: torch.Tensor):
+        """Queue one layer's paging point on the current stream (capturable): keys = key_base +
+        id for the route row's ids (float32 row [ids | weights] on the device), or for `ids`
+        (int64 [k] on the device) if given; meta [2k] = [slots | weights]; misses paged.
+        k = 0: a warm-up launch of both kernels that changes nothing."""
+        assert row.dtype == torch.float32 and row.is_cuda and row.numel() >= 2 * k
+        assert meta.dtype == torch.float32 and meta.is_cuda and meta.numel() >= 2 * k
+        idp = None
+        if ids is not None:
+            assert ids.dtype == torch.int64 and ids.is_cuda and ids.is_contiguous() and ids.numel() >= k
+            idp = ctypes.c_void_p(ids.data_ptr())
+        _raise(_lib.lib().wisp_cache_device_step(self._h, ctypes.c_void_p(row.data_ptr()), idp, key_base, n_ids, k,
+                                                 ctypes.c_void_p(meta.data_ptr()), self._stream()))
+
+    def device_sync(self):
+        """Wait for the current stream and copy the device state into the core (stays on)."""
+        if self.device_paging:
+            _raise(_lib.lib().wisp_cache_device_sync(self._h, self._stream()))
+
+    def device_end(self):
+        """device_sync, then device paging off."""
+        if self.device_paging:
+            _raise(_lib.lib().wisp_cache_device_end(self._h, self._stream()))
+
     # ---- copies ---------------------------------------------------------
     def _issue(self, pairs):
         """Async host->GPU copies of [(key, slot)] on the side stream, ordered after queued compute."""
         if not pairs:
             return
+        self.device_end()
         k = _i64(p[0] for p in pairs)
         s = _i64(p[1] for p in pairs)
         _lib.check(_lib.lib().wisp_cache_issue(self._h, _p(k), _p(s), k.size, self._stream()), "ExpertCache._issue")
@@ -145,6 +193,7 @@ class ExpertCache:
 
     # ---- policies -------------------------------------------------------
     def ensure(self, keys):
+        self.device_end()
         k = _i64(keys)
         slots = np.empty(max(k.size, 1), np.int64)
         rc = _lib.lib().wisp_cache_ensure(self._h, _p(k), k.size, _p(slots), self._stream())
@@ -156,6 +205,7 @@ class ExpertCache:
         """One layer's host step of the graph decoder (graphdec.py:216-231) in one native call:
         ensure `keys`, write [slots | weights] into meta_host (pinned float32 [2k]) and copy it
         to meta_dev on the current stream. Returns the slots."""
+        self.device_end()
         k = _i64(keys)
         w = np.ascontiguousarray(np.asarray(weights, dtype=np.float32).reshape(-1))
         assert w.size == k.size and meta_host.numel() >= 2 * k.size and meta_dev.numel() >= 2 * k.size
@@ -175,6 +225,7 @@ class ExpertCache:
         keys = key_base + id (every id in [0, n_ids)), with `ids` (int64 numpy [k]) replacing
         the row's ids if given."""
         assert row_dev.dtype == torch.float32 and row_host.dtype == torch.float32 and row_host.numel() >= 2 * k
+        self.device_end()
         assert meta_host.numel() >= 2 * k and meta_dev.numel() >= 2 * k
         idp = None
         if ids is not None:
@@ -194,6 +245,7 @@ class ExpertCache:
         """prepare_row for a row the route kernel writes into the pinned row_host itself: wait
         until flag_host moves from flag_before, then ensure / copy / meta. Returns the flag."""
         assert row_host.is_pinned() and flag_host.is_pinned() and row_host.numel() >= 2 * k
+        self.device_end()
         idp = None
         if ids is not None:
             ids = np.ascontiguousarray(ids, dtype=np.int64)
@@ -267,6 +319,7 @@ class ExpertCache:
         assert not self.decode_on_load
         if nslots == self.nslots:
             return
+        self.device_end()
         torch.cuda.synchronize(self.device)
         self.gpu = None
         _lib.check(_lib.lib().wisp_cache_resize(self._h, nslots), "ExpertCache.resize")

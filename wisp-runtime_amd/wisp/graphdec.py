@@ -32,6 +32,12 @@ How this build lays it out:
     memory; one native call waits for the flag, runs the cache's LRU step, queues the
     page kernel for the misses and writes meta on the stream -- no stream sync per layer.
     With prefetch or a routing recorder the row is read back instead (one sync per layer).
+  * Device paging (the default where the cache allows it: LRU policy, page-kernel copies):
+    the paging point itself runs on the GPU (the cache's LRU step kernel, then its page
+    kernel for the misses, both reading the route row from device memory), so the L + 1
+    segments and the L paging points are captured as ONE graph per token and the host
+    only writes the token and position and replays it. The bookkeeping is the same LRU
+    step; the cache copies its state back to the host core when the host next needs it.
   * Prefill runs the model's own modules over chunks of tokens, attention in float32 over
     the static cache with the KV heads repeated for their query groups; K/V are written
     straight into the static buffers.
@@ -107,13 +113,19 @@ class DecodeShape:
 
 
 class GraphDecoder:
-    def __init__(self, model, rt=None, tmax=2048, use_graph=True):
+    def __init__(self, model, rt=None, tmax=2048, use_graph=True, device_paging="auto"):
+        """device_paging: "auto" = page on the GPU when the cache can (LRU policy, page-kernel
+        copies, no prefetch or routing recorder), True = require it, False = host steps."""
+        assert device_paging in ("auto", True, False), device_paging
         s = DecodeShape(model)
         self.shape, self.model, self.rt = s, model, rt
         self.L, self.H, self.Hq, self.Hk, self.D, self.G = s.L, s.H, s.Hq, s.Hk, s.D, s.G
         self.k, self.E, self.layers = s.k, s.E, s.layers
         self.dev, self.dt = s.dev, s.dt
         self.use_graph = use_graph
+        self.device_paging = device_paging
+        self._dev = False  # this capture pages on the GPU
+        self._ids_dev = self._ids_ring = None
         self.graphs, self._key = None, None
         self.pos = 0
         self.kv = None
@@ -234,8 +246,11 @@ class GraphDecoder:
         kernels.dl_gemv(self.hm.view(H), w["o"], attn.view(Hq * D), res=self.hbuf)
         kernels.dl_gemv(self.rlogits, w["gate"], self.hm.view(H), norm_w=w["ln2"], eps=w["eps2"],
                         x_out=self.xn.view(H))
-        kernels.dl_route(self.rlogits, self.k, w["norm_topk"], self.row.view(-1), self.row_host, self.flag_host,
-                         self.seq_dev)
+        if self._dev:  # the cache's LRU step reads the row on the device
+            kernels.dl_route(self.rlogits, self.k, w["norm_topk"], self.row.view(-1))
+        else:
+            kernels.dl_route(self.rlogits, self.k, w["norm_topk"], self.row.view(-1), self.row_host, self.flag_host,
+                             self.seq_dev)
         if self.prefetch:  # the next layer's router on this layer's input predicts its experts
             nxt = getattr(self.layers[i].mlp, "next_gate", None)
             guess = (torch.topk(nxt(self.xn.view(1, H)), self.k, dim=-1).indices.float() if nxt is not None
@@ -259,6 +274,43 @@ class GraphDecoder:
         else:
             kernels.dl_gemv(self.logits.view(-1), self.shape.w_head, a, a_row=a_row, b=b,
                             norm_w=self.shape.w_final, eps=self.shape.eps_final)
+
+    # ---------------------------------------------------------------- paging point on the GPU
+    def _forced_ids(self):
+        """True when a subclass replaces the router's expert ids (_expert_ids)."""
+        return type(self)._expert_ids is not GraphDecoder._expert_ids
+
+    def _device_ok(self):
+        """Whether this step pages on the GPU; starts device paging on the cache if so."""
+        rt = self.rt
+        if self.device_paging is False or rt is None or self.prefetch or rt.recorder is not None:
+            if self.device_paging is True:
+                raise RuntimeError("device paging needs a runtime without prefetch or a routing recorder")
+            return False
+        try:
+            rt.cache.device_begin()
+        except RuntimeError:
+            if self.device_paging is True:
+                raise
+            return False
+        return True
+
+    def _device_step(self, i):
+        """Layer i's paging point on the current stream: LRU step of the route row (or of the
+        forced ids), meta_dev written, misses paged."""
+        ids = self._ids_dev[i] if self._ids_dev is not None else None
+        self.rt.cache.device_step(self.row.view(-1), ids, i * self.E, self.E, self.k, self.meta_dev)
+
+    def _stage_ids(self):
+        """Forced expert ids of every layer for this token -> _ids_dev (pinned ring, so the
+        host can run ahead of the GPU by a few tokens)."""
+        buf, ev = self._ids_ring[self._ids_next]
+        ev.synchronize()  # the copy that last read this buffer has run
+        for i in range(self.L):
+            buf[i].copy_(torch.as_tensor(self._expert_ids(i), dtype=torch.int64))
+        self._ids_dev.copy_(buf, non_blocking=True)
+        ev.record()
+        self._ids_next = (self._ids_next + 1) % len(self._ids_ring)
 
     # ---------------------------------------------------------------- host step of one layer
     def _expert_ids(self, i):
@@ -287,7 +339,8 @@ class GraphDecoder:
     # ---------------------------------------------------------------- capture / replay
     def _cache_key(self):
         cache = self.rt.cache
-        return (id(cache), cache.gpu.data_ptr(), cache.store.bits, self.prefetch)
+        return (id(cache), cache.gpu.data_ptr(), cache.store.bits, self.prefetch, self.device_paging,
+                self.rt.recorder is not None)
 
     @torch.no_grad()
     def capture(self):
@@ -297,6 +350,14 @@ class GraphDecoder:
         if self.row.shape[1] != self._row_len():
             self.row = torch.zeros(1, self._row_len(), dtype=torch.float32, device=self.dev)
         self.graphs = None
+        self._dev = self._device_ok()
+        if self._dev and self._forced_ids():
+            self._ids_dev = torch.zeros(self.L, self.k, dtype=torch.int64, device=self.dev)
+            self._ids_ring = [(torch.zeros(self.L, self.k, dtype=torch.int64, pin_memory=True), torch.cuda.Event())
+                              for _ in range(4)]
+            self._ids_next = 0
+        else:
+            self._ids_dev = self._ids_ring = None
         k = self.k
         self.ctl[0] = 0
         self.ctl[1] = self.tmax  # scratch: never attended by a real position
@@ -309,15 +370,26 @@ class GraphDecoder:
             for _ in range(2):
                 for j in range(self.L + 1):
                     self._segment(j)
+            if self._dev:  # both paging kernels once, without a step
+                self.rt.cache.device_step(self.row.view(-1), None, 0, self.E, 0, self.meta_dev)
         torch.cuda.current_stream(self.dev).wait_stream(side)
         torch.cuda.synchronize(self.dev)
         pool = torch.cuda.graph_pool_handle()
         graphs = []
-        for j in range(self.L + 1):
+        if self._dev:  # one graph: segments and paging points
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, pool=pool):
-                self._segment(j)
+                for j in range(self.L + 1):
+                    self._segment(j)
+                    if j < self.L:
+                        self._device_step(j)
             graphs.append(g)
+        else:
+            for j in range(self.L + 1):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, pool=pool):
+                    self._segment(j)
+                graphs.append(g)
         self.graphs, self._key = graphs, self._cache_key()
         torch.cuda.synchronize(self.dev)
 
@@ -333,9 +405,32 @@ class GraphDecoder:
         assert self.pos < self.tmax, "context full"
         if self.use_graph and (self.graphs is None or self._key != self._cache_key()):
             self.capture()
+        if not self.use_graph:
+            self._dev = self._device_ok()
+            if self._dev and self._forced_ids() and self._ids_ring is None:
+                self._ids_dev = torch.zeros(self.L, self.k, dtype=torch.int64, device=self.dev)
+                self._ids_ring = [(torch.zeros(self.L, self.k, dtype=torch.int64, pin_memory=True),
+                                   torch.cuda.Event()) for _ in range(4)]
+                self._ids_next = 0
+        elif self._dev:
+            self.rt.cache.device_begin()  # again, if a host-side cache call ended it
         self.ctl[0:1].copy_(token.reshape(1))
         self.ctl[1].fill_(self.pos)
         rt = self.rt
+        if self._dev:  # the whole step on the GPU
+            if self._ids_dev is not None:
+                self._stage_ids()
+            if self.graphs is not None:
+                self.graphs[0].replay()
+            else:
+                for j in range(self.L + 1):
+                    self._segment(j)
+                    if j < self.L:
+                        self._device_step(j)
+            rt.stats["layer_calls"] += self.L
+            rt.stats["gpu_experts"] += self.L * self.k
+            self.pos += 1
+            return self.logits
         signalled = not self.prefetch and rt.recorder is None
         flag = int(self.flag_host[0])  # no route kernel is in flight here
         self._replay(0)
