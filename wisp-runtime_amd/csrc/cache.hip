@@ -323,6 +323,25 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
     return v;
 }
 
+// cand[i] = (last, slot) + 1 of dynamic slot n_static + i for i in [i0, min(n, i0 + 64 kLruBatch)):
+// all of a lane's loads issued before its LDS writes (one round trip; indexes past the end
+// re-read the last slot, n >= 1)
+constexpr int kLruBatch = 16;
+__device__ __forceinline__ void stage_eviction_keys(const DevPaging& d, int lane, int64_t i0, int64_t n,
+                                                    uint64_t* cand) {
+    int64_t v[kLruBatch];
+#pragma unroll
+    for (int u = 0; u < kLruBatch; ++u) {
+        const int64_t i = i0 + lane + 64 * u;
+        v[u] = d.last[d.n_static + (i < n ? i : n - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < kLruBatch; ++u) {
+        const int64_t i = i0 + lane + 64 * u;
+        if (i < n) cand[i] = (((uint64_t)v[u] << 20) | (uint64_t)(d.n_static + i)) + 1ull;
+    }
+}
+
 // cache_core.py:86-106 (ensure) with the LRU policy, as one wave on the GPU, for
 // one layer: lane j < k takes key key_base + id_j (id_j = ids[j] if ids, else the
 // route row's id j, which must be an integer in [0, n_ids)). Hits are noted with
@@ -347,6 +366,12 @@ __global__ __launch_bounds__(64) void k_lru_step(const DevPaging d, const float*
     }
     const int64_t tick = d.ctr[kCtrTick] + 1;
     const int64_t nf = d.ctr[kCtrNextFree];
+    // eviction keys (last, slot) + 1 of the dynamic slots, kLruBatch per lane per round of
+    // requests; a pool of at most 64 kLruBatch dynamic slots is requested here, with the
+    // counters and the row (the slots at or past the next free one are never candidates)
+    const int64_t nd = d.nslots - d.n_static;
+    const bool early = nd <= 64 * kLruBatch;
+    if (early && nd > 0) stage_eviction_keys(d, lane, 0, nd, cand);
     const bool on = lane < k;
     int key = -1;
     float w = 0.f;
@@ -376,10 +401,10 @@ __global__ __launch_bounds__(64) void k_lru_step(const DevPaging d, const float*
     int got = from_free;  // misses with a slot
     int old_key = -1;     // the key this lane's victim held
     if (m > 0) {
-        // eviction keys (last, slot) + 1 of the dynamic slots in use; this step's hits excluded
+        // candidates: the dynamic slots in use, this step's hits excluded
         const int64_t nc = nf - d.n_static;
-        for (int64_t i = lane; i < nc; i += 64)
-            cand[i] = (((uint64_t)d.last[d.n_static + i] << 20) | (uint64_t)(d.n_static + i)) + 1ull;
+        if (!early)
+            for (int64_t i0 = 0; i0 < nc; i0 += 64 * kLruBatch) stage_eviction_keys(d, lane, i0, nc, cand);
         __syncthreads();
         if (hit && slot >= d.n_static) cand[slot - d.n_static] = ~0ull;
         __syncthreads();
