@@ -337,7 +337,11 @@ int wisp_cache_device_step(void* cache, const float* row, const int64_t* ids, in
  * frequencies (read only by the wsa policy and admission) are not advanced by
  * device steps. */
 int wisp_cache_device_sync(void* cache, void* stream);
-/* wisp_cache_device_sync, then device paging off and its state freed. */
+/* wisp_cache_device_sync, then device paging off. The device state stays allocated
+ * at the same address (until the cache is destroyed or a begin finds a different
+ * slot count), so steps captured in a graph stay valid across end / begin; a
+ * captured step replayed while device paging is off does no step and writes
+ * slot -1 into meta. */
 int wisp_cache_device_end(void* cache, void* stream);
 /* 1 while device paging is on, else 0. */
 int wisp_cache_device_active(void* cache);

@@ -155,6 +155,40 @@ def test_graph_replays_of_device_steps(store):
     c.free()
 
 
+def test_captured_steps_stay_valid_across_end_and_begin(store):
+    """A graph of device steps captured once keeps working after device paging is ended (host
+    steps change the core) and begun again; replayed while it is off it does no step and
+    writes slot -1, and the state is unchanged."""
+    E, nslots, k = 24, 12, 4
+    c = ExpertCache(store, nslots, copy="kernel")
+    ref = RefCore(nslots, "lru")
+    ids = torch.zeros(k, dtype=torch.int64, device=DEV)
+    row = _row(np.zeros(k), np.ones(k))
+    meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    c.device_begin()
+    c.device_step(row, None, 0, E, 0, meta)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        c.device_step(row, ids, 24, E, k, meta)
+    rng = np.random.default_rng(13)
+    for rep in range(6):
+        draw = rng.choice(E, size=k, replace=False).astype(np.int64)
+        ids.copy_(torch.from_numpy(draw))
+        g.replay()
+        assert [int(v) for v in meta.cpu()[:k]] == ref.ensure([24 + int(v) for v in draw])[0], rep
+        host = [int(v) for v in rng.choice(E, size=k, replace=False)]
+        assert c.ensure(host) == ref.ensure(host)[0], rep  # ends device paging
+        assert not c.device_paging
+        if rep == 3:  # replayed while off: no step
+            g.replay()
+            assert [int(v) for v in meta.cpu()[:k]] == [-1] * k
+            assert c.core.stats == ref.counts
+        c.device_begin()
+    _check_state(c, ref, store)
+    c.free()
+
+
 def test_bad_id_and_no_evictable_slot_are_reported(store):
     E, k = 24, 4
     c = ExpertCache(store, 6, copy="kernel")

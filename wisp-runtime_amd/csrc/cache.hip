@@ -201,13 +201,14 @@ static void view_deleter(DLManagedTensor* m) {
 // Device paging: the LRU state in device memory (one allocation) while it is on.
 constexpr int kDevMaxK = 16;        // keys per step
 constexpr int kDevMaxSlots = 8192;  // dynamic slots: their eviction keys are staged in LDS
-enum { kCtrTick, kCtrNextFree, kCtrHits, kCtrMisses, kCtrEvict, kCtrCalls, kCtrLoads, kCtrErr, kCtrN };
+enum { kCtrTick, kCtrNextFree, kCtrHits, kCtrMisses, kCtrEvict, kCtrCalls, kCtrLoads, kCtrErr, kCtrOn, kCtrN };
 enum { kDevErrSlot = 1, kDevErrKey = 2 };
 struct DevPaging {
     int32_t* slot_key = nullptr;  // [nslots], -1 empty
     int64_t* last = nullptr;      // [nslots], tick of the last use
     int32_t* key2slot = nullptr;  // [nkeys], -1 not resident
-    int64_t* ctr = nullptr;       // [kCtrN]: tick, next free slot, hits, misses, evictions, calls, loads, error bits
+    int64_t* ctr = nullptr;       // [kCtrN]: tick, next free slot, hits, misses, evictions, calls, loads, error
+                                  // bits, on (1 while the device holds the state)
     int32_t* miss = nullptr;      // [1 + 2 kDevMaxK]: count, keys, slots of the last step's loads
     int64_t nslots = 0, nkeys = 0, n_static = 0;
 };
@@ -230,8 +231,12 @@ struct Cache {
     const uint8_t* host_dev = nullptr;   // the host store's device address (copy_mode 1)
     bool pending = false;
     int64_t bytes_h2d = 0, n_loads = 0;
-    void* dev_block = nullptr;  // device paging on when not null
+    // the device paging state: allocated by the first wisp_cache_device_begin and kept (at the
+    // same address, so captured steps stay valid) until the cache is destroyed or its slot
+    // count changes
+    void* dev_block = nullptr;
     DevPaging dev;
+    bool dev_on = false;
     int64_t dev_loads_seen = 0;  // device loads already added to bytes_h2d / n_loads
 };
 
@@ -354,13 +359,20 @@ __device__ __forceinline__ void stage_eviction_keys(const DevPaging& d, int lane
 // loads go to the miss list for k_page_list. A key that is not valid or a miss
 // without an evictable slot gets slot -1 in meta (the MoE kernels then write NaN
 // rows) and sets an error bit that the host reads when it syncs the state.
-// k <= 0: a warm-up launch that only clears the miss list.
+// k <= 0: a warm-up launch that only clears the miss list. A launch while device paging is
+// off (a captured step replayed after wisp_cache_device_end) does no step and writes slot -1
+// into meta.
 __global__ __launch_bounds__(64) void k_lru_step(const DevPaging d, const float* __restrict__ row,
                                                  const int64_t* __restrict__ ids, int64_t key_base, int64_t n_ids,
                                                  int k, float* __restrict__ meta) {
     __shared__ uint64_t cand[kDevMaxSlots];
     const int lane = threadIdx.x;
     if (k <= 0) {
+        if (lane == 0) d.miss[0] = 0;
+        return;
+    }
+    if (d.ctr[kCtrOn] == 0) {  // replayed while the host core holds the state: no step
+        if (lane < k) meta[lane] = -1.f;
         if (lane == 0) d.miss[0] = 0;
         return;
     }
@@ -603,7 +615,7 @@ static Cache* as_cache(void* h) { return static_cast<Cache*>(h); }
 
 // host-side bookkeeping while the device holds the LRU state would diverge from it
 static int dev_refuse(const Cache& c) {
-    return c.dev_block ? fail_inval("device paging is on: end it (wisp_cache_device_end) first") : WISP_OK;
+    return c.dev_on ? fail_inval("device paging is on: end it (wisp_cache_device_end) first") : WISP_OK;
 }
 
 }  // namespace wisp
@@ -1153,7 +1165,7 @@ static int dev_download(Cache& c, hipStream_t st) {
 extern "C" int wisp_cache_device_begin(void* h, void* stream) {
     clear_error();
     Cache& c = *as_cache(h);
-    if (c.dev_block) return WISP_OK;
+    if (c.dev_on) return WISP_OK;
     const Core& core = *c.core;
     if (core.policy != kLRU) return fail_inval("device paging runs the LRU policy only");
     if (c.copy_mode != 1 || !c.host_dev) return fail_inval("device paging needs the page-kernel copy mode");
@@ -1179,7 +1191,7 @@ extern "C" int wisp_cache_device_begin(void* h, void* stream) {
         if (kv.first < 0 || kv.first >= d.nkeys) return fail_inval("device paging: a resident key outside the store");
         k2s[kv.first] = (int32_t)kv.second;
     }
-    const int64_t ctr[kCtrN] = {core.tick, nf, core.hits, core.misses, core.evictions, core.calls, 0, 0};
+    const int64_t ctr[kCtrN] = {core.tick, nf, core.hits, core.misses, core.evictions, core.calls, 0, 0, 1};
     const size_t b_sk = align256(sizeof(int32_t) * d.nslots), b_last = align256(sizeof(int64_t) * d.nslots),
                  b_k2s = align256(sizeof(int32_t) * d.nkeys), b_ctr = align256(sizeof(int64_t) * kCtrN),
                  b_miss = align256(sizeof(int32_t) * (1 + 2 * kDevMaxK));
@@ -1187,12 +1199,24 @@ extern "C" int wisp_cache_device_begin(void* h, void* stream) {
     (void)hipGetDevice(&cur);
     (void)hipSetDevice(c.device);
     hipStream_t st = (hipStream_t)stream;
-    void* block = nullptr;
-    hipError_t e = hipMalloc(&block, b_sk + b_last + b_k2s + b_ctr + b_miss);
-    if (e != hipSuccess) {
-        (void)hipGetLastError();
-        (void)hipSetDevice(cur);
-        return hip_fail(e, "hipMalloc (device paging state)");
+    hipError_t e;
+    if (c.dev_block && (c.dev.nslots != d.nslots || c.dev.nkeys != d.nkeys)) {  // the slot count changed
+        e = hipDeviceSynchronize();
+        if (e != hipSuccess) {
+            (void)hipSetDevice(cur);
+            return hip_fail(e, "hipDeviceSynchronize (device paging state)");
+        }
+        (void)hipFree(c.dev_block);
+        c.dev_block = nullptr;
+    }
+    void* block = c.dev_block;
+    if (!block) {
+        e = hipMalloc(&block, b_sk + b_last + b_k2s + b_ctr + b_miss);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipSetDevice(cur);
+            return hip_fail(e, "hipMalloc (device paging state)");
+        }
     }
     uint8_t* p = static_cast<uint8_t*>(block);
     d.slot_key = reinterpret_cast<int32_t*>(p);
@@ -1211,12 +1235,10 @@ extern "C" int wisp_cache_device_begin(void* h, void* stream) {
         if (e != hipSuccess) rc = hip_fail(e, "uploading the device paging state");
     }
     (void)hipSetDevice(cur);
-    if (rc) {
-        (void)hipFree(block);
-        return rc;
-    }
     c.dev = d;
     c.dev_block = block;
+    if (rc) return rc;  // the block is kept (device paging stays off)
+    c.dev_on = true;
     c.dev_loads_seen = 0;
     return WISP_OK;
 }
@@ -1230,7 +1252,7 @@ extern "C" int wisp_cache_device_step(void* h, const float* row, const int64_t* 
                                       int k, float* meta, void* stream) {
     clear_error();
     Cache& c = *as_cache(h);
-    if (!c.dev_block) return fail_inval("device paging is off (wisp_cache_device_begin)");
+    if (!c.dev_on) return fail_inval("device paging is off (wisp_cache_device_begin)");
     if (k < 0 || k > kDevMaxK) return fail_inval("device paging takes 0 <= k <= 16");
     if (k > 0 && (!row || !meta || n_ids < 1)) return fail_inval("device paging step: null row / meta or n_ids < 1");
     if (!c.pool) return no_pool();
@@ -1251,7 +1273,7 @@ extern "C" int wisp_cache_device_step(void* h, const float* row, const int64_t* 
 extern "C" int wisp_cache_device_sync(void* h, void* stream) {
     clear_error();
     Cache& c = *as_cache(h);
-    if (!c.dev_block) return WISP_OK;
+    if (!c.dev_on) return WISP_OK;
     int cur = 0;
     (void)hipGetDevice(&cur);
     (void)hipSetDevice(c.device);
@@ -1260,20 +1282,22 @@ extern "C" int wisp_cache_device_sync(void* h, void* stream) {
     return rc;
 }
 
-// wisp_cache_device_sync, then device paging off (its state freed).
+// wisp_cache_device_sync, then device paging off. The state stays allocated at the same
+// address; a captured step replayed while it is off does nothing but write slot -1 into meta.
 extern "C" int wisp_cache_device_end(void* h, void* stream) {
     clear_error();
     Cache& c = *as_cache(h);
-    if (!c.dev_block) return WISP_OK;
+    if (!c.dev_on) return WISP_OK;
     int cur = 0;
     (void)hipGetDevice(&cur);
     (void)hipSetDevice(c.device);
-    const int rc = dev_download(c, (hipStream_t)stream);
-    (void)hipFree(c.dev_block);
+    int rc = dev_download(c, (hipStream_t)stream);
+    const int64_t off = 0;
+    const hipError_t e = hipMemcpy(c.dev.ctr + kCtrOn, &off, sizeof(int64_t), hipMemcpyHostToDevice);
+    if (e != hipSuccess && !rc) rc = hip_fail(e, "hipMemcpy (device paging off)");
     (void)hipSetDevice(cur);
-    c.dev_block = nullptr;
-    c.dev = DevPaging();
+    c.dev_on = false;
     return rc;
 }
 
-extern "C" int wisp_cache_device_active(void* h) { return as_cache(h)->dev_block ? 1 : 0; }
+extern "C" int wisp_cache_device_active(void* h) { return as_cache(h)->dev_on ? 1 : 0; }

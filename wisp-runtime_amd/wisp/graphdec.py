@@ -339,7 +339,7 @@ class GraphDecoder:
     # ---------------------------------------------------------------- capture / replay
     def _cache_key(self):
         cache = self.rt.cache
-        return (id(cache), cache.gpu.data_ptr(), cache.store.bits, self.prefetch, self.device_paging,
+        return (id(cache), cache.gpu.data_ptr(), cache.nslots, cache.store.bits, self.prefetch, self.device_paging,
                 self.rt.recorder is not None)
 
     @torch.no_grad()
