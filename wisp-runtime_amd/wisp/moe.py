@@ -80,6 +80,9 @@ def _expert_mlp(x, W3, I, H):
     return F.linear(F.silu(g) * u, W3[2].view(H, I))
 
 
+_mlp = _expert_mlp  # the reference's name (moe.py:42), imported by its callers (scripts/microbench.py:14)
+
+
 def _gate_linear(gate, H, E):
     """The router as a plain Linear [E, H] (transformers 5 wraps it in a top-k router module)."""
     if isinstance(gate, nn.Linear):
