@@ -331,6 +331,14 @@ int wisp_cache_device_begin(void* cache, void* stream);
  * both kernels without a step (a warm-up before capture). */
 int wisp_cache_device_step(void* cache, const float* row, const int64_t* ids, int64_t key_base, int64_t n_ids,
                            int k, float* meta, void* stream);
+/* wisp_dl_route (softmax of the bf16 logits [E], top-k, renormalised if norm_topk,
+ * bf16 weights; row = [ids | weights]) and wisp_cache_device_step on that choice
+ * (ids, if given, replace the chosen expert ids; the weights are the router's)
+ * in one launch, then the page kernel: the step's state reads overlap the
+ * router's softmax and top-k. E <= 1024; k as for wisp_cache_device_step
+ * (k = 0: warm-up launches). */
+int wisp_cache_device_route_step(void* cache, const uint16_t* logits, int E, int k, int norm_topk, float* row,
+                                 const int64_t* ids, int64_t key_base, int64_t n_ids, float* meta, void* stream);
 /* Synchronise `stream` and copy the device LRU state into the host core and the
  * load counters; device paging stays on. WISP_EINVAL (once) if a step since
  * the last sync met a bad id or had no evictable slot. The core's decayed

@@ -189,6 +189,41 @@ def test_captured_steps_stay_valid_across_end_and_begin(store):
     c.free()
 
 
+@pytest.mark.parametrize("E,k,norm", [(24, 8, True), (24, 4, False), (24, 1, True), (24, 16, True)])
+def test_route_step_equals_route_kernel_then_step(store, E, k, norm):
+    """The fused route + LRU kernel against wisp_dl_route followed by the LRU step: the same
+    row bits, the same meta, and the bookkeeping of the reference LRU, with the router's
+    choice and with forced ids."""
+    from wisp import kernels
+
+    nslots = 20
+    c = ExpertCache(store, nslots, copy="kernel")
+    ref = RefCore(nslots, "lru")
+    g = torch.Generator(device=DEV).manual_seed(E * 7 + k)
+    row_a = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    row_b = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    rng = np.random.default_rng(E + k)
+    c.device_begin()
+    c.device_route_step(torch.zeros(E, dtype=torch.bfloat16, device=DEV), 0, norm, row_b, None, 0, E, meta)
+    for it in range(30):
+        layer = it % 3
+        logits = torch.randn(E, generator=g, device=DEV).to(torch.bfloat16)
+        kernels.dl_route(logits, k, norm, row_a)
+        forced = None
+        if it % 4 == 3:
+            forced = torch.from_numpy(rng.choice(E, size=k, replace=False).astype(np.int64)).to(DEV)
+        c.device_route_step(logits, k, norm, row_b, forced, layer * E, E, meta)
+        assert torch.equal(row_a.view(torch.int32), row_b.view(torch.int32)), it
+        ids = forced.cpu().tolist() if forced is not None else [int(v) for v in row_a[:k].cpu()]
+        slots, _ = ref.ensure([layer * E + int(v) for v in ids])
+        m = meta.cpu()
+        assert [int(v) for v in m[:k]] == slots, it
+        assert torch.equal(m[k:], row_a[k:].cpu()), it
+    _check_state(c, ref, store)
+    c.free()
+
+
 def test_bad_id_and_no_evictable_slot_are_reported(store):
     E, k = 24, 4
     c = ExpertCache(store, 6, copy="kernel")

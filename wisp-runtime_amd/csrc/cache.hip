@@ -28,6 +28,7 @@
 #include <unordered_set>
 #include <vector>
 
+#include "route.hpp"
 #include "wisp_internal.hpp"
 
 namespace wisp {
@@ -347,9 +348,25 @@ __device__ __forceinline__ void stage_eviction_keys(const DevPaging& d, int lane
     }
 }
 
+// The step's state reads, requested before anything else the kernel does: the counters
+// and, for a pool of at most 64 kLruBatch dynamic slots, every eviction key.
+struct LruStart {
+    int64_t tick, nf;
+    bool on, early;
+};
+__device__ __forceinline__ LruStart lru_start(const DevPaging& d, int lane, uint64_t* cand) {
+    LruStart st;
+    st.on = d.ctr[kCtrOn] != 0;
+    st.tick = d.ctr[kCtrTick] + 1;
+    st.nf = d.ctr[kCtrNextFree];
+    const int64_t nd = d.nslots - d.n_static;
+    st.early = nd <= 64 * kLruBatch;
+    if (st.early && nd > 0) stage_eviction_keys(d, lane, 0, nd, cand);
+    return st;
+}
+
 // cache_core.py:86-106 (ensure) with the LRU policy, as one wave on the GPU, for
-// one layer: lane j < k takes key key_base + id_j (id_j = ids[j] if ids, else the
-// route row's id j, which must be an integer in [0, n_ids)). Hits are noted with
+// one layer: lane j < k holds key j (-1 if its id was not valid) and its weight w. Hits are noted with
 // the step's tick; misses take free slots in ascending order, then the least
 // recently used unprotected slots. The reference picks each victim by a
 // first-index argmin of `last` over the unprotected dynamic slots, and every slot
@@ -359,45 +376,17 @@ __device__ __forceinline__ void stage_eviction_keys(const DevPaging& d, int lane
 // loads go to the miss list for k_page_list. A key that is not valid or a miss
 // without an evictable slot gets slot -1 in meta (the MoE kernels then write NaN
 // rows) and sets an error bit that the host reads when it syncs the state.
-// k <= 0: a warm-up launch that only clears the miss list. A launch while device paging is
-// off (a captured step replayed after wisp_cache_device_end) does no step and writes slot -1
-// into meta.
-__global__ __launch_bounds__(64) void k_lru_step(const DevPaging d, const float* __restrict__ row,
-                                                 const int64_t* __restrict__ ids, int64_t key_base, int64_t n_ids,
-                                                 int k, float* __restrict__ meta) {
-    __shared__ uint64_t cand[kDevMaxSlots];
-    const int lane = threadIdx.x;
-    if (k <= 0) {
-        if (lane == 0) d.miss[0] = 0;
-        return;
-    }
-    if (d.ctr[kCtrOn] == 0) {  // replayed while the host core holds the state: no step
+// A launch while device paging is off (a captured step replayed after
+// wisp_cache_device_end) does no step and writes slot -1 into meta.
+__device__ __forceinline__ void lru_apply(const DevPaging& d, const LruStart& st, int lane, int k, int key, float w,
+                                          uint64_t* cand, float* __restrict__ meta) {
+    if (!st.on) {  // replayed while the host core holds the state: no step
         if (lane < k) meta[lane] = -1.f;
         if (lane == 0) d.miss[0] = 0;
         return;
     }
-    const int64_t tick = d.ctr[kCtrTick] + 1;
-    const int64_t nf = d.ctr[kCtrNextFree];
-    // eviction keys (last, slot) + 1 of the dynamic slots, kLruBatch per lane per round of
-    // requests; a pool of at most 64 kLruBatch dynamic slots is requested here, with the
-    // counters and the row (the slots at or past the next free one are never candidates)
-    const int64_t nd = d.nslots - d.n_static;
-    const bool early = nd <= 64 * kLruBatch;
-    if (early && nd > 0) stage_eviction_keys(d, lane, 0, nd, cand);
+    const int64_t tick = st.tick, nf = st.nf;
     const bool on = lane < k;
-    int key = -1;
-    float w = 0.f;
-    if (on) {
-        int64_t id = -1;
-        if (ids) {
-            id = ids[lane];
-        } else {
-            const float f = row[lane];
-            if (f >= 0.f && f < 16777216.f && (float)(int64_t)f == f) id = (int64_t)f;
-        }
-        if (id >= 0 && id < n_ids && key_base + id >= 0 && key_base + id < d.nkeys) key = (int)(key_base + id);
-        w = row[k + lane];
-    }
     int slot = key >= 0 ? d.key2slot[key] : -1;
     const bool hit = slot >= 0;
     const uint64_t mm = __ballot(key >= 0 && !hit);
@@ -415,7 +404,7 @@ __global__ __launch_bounds__(64) void k_lru_step(const DevPaging d, const float*
     if (m > 0) {
         // candidates: the dynamic slots in use, this step's hits excluded
         const int64_t nc = nf - d.n_static;
-        if (!early)
+        if (!st.early)
             for (int64_t i0 = 0; i0 < nc; i0 += 64 * kLruBatch) stage_eviction_keys(d, lane, i0, nc, cand);
         __syncthreads();
         if (hit && slot >= d.n_static) cand[slot - d.n_static] = ~0ull;
@@ -466,6 +455,64 @@ __global__ __launch_bounds__(64) void k_lru_step(const DevPaging d, const float*
         d.ctr[kCtrLoads] += got;
         d.ctr[kCtrErr] |= (got < nmiss ? kDevErrSlot : 0) | (bad ? kDevErrKey : 0);
     }
+}
+
+// key of lane j < k: key_base + id when id is in [0, n_ids) and the key in the store, else -1
+__device__ __forceinline__ int lru_key(const DevPaging& d, int64_t id, int64_t key_base, int64_t n_ids) {
+    return (id >= 0 && id < n_ids && key_base + id >= 0 && key_base + id < d.nkeys) ? (int)(key_base + id) : -1;
+}
+
+// The step for key_base + id_j, id_j = ids[j] if ids, else the route row's id j (an integer
+// in [0, n_ids)); weights from the row. k <= 0: a warm-up launch that only clears the miss list.
+__global__ __launch_bounds__(64) void k_lru_step(const DevPaging d, const float* __restrict__ row,
+                                                 const int64_t* __restrict__ ids, int64_t key_base, int64_t n_ids,
+                                                 int k, float* __restrict__ meta) {
+    __shared__ uint64_t cand[kDevMaxSlots];
+    const int lane = threadIdx.x;
+    if (k <= 0) {
+        if (lane == 0) d.miss[0] = 0;
+        return;
+    }
+    const LruStart st = lru_start(d, lane, cand);
+    int key = -1;
+    float w = 0.f;
+    if (lane < k) {
+        int64_t id = -1;
+        if (ids) {
+            id = ids[lane];
+        } else {
+            const float f = row[lane];
+            if (f >= 0.f && f < 16777216.f && (float)(int64_t)f == f) id = (int64_t)f;
+        }
+        key = lru_key(d, id, key_base, n_ids);
+        w = row[k + lane];
+    }
+    lru_apply(d, st, lane, k, key, w, cand, meta);
+}
+
+// The route kernel's choice (route.hpp: softmax, top-k, renormalised bf16 weights; row =
+// [ids | weights]) and the LRU step of those experts in one wave: the step's state reads
+// are in flight while the router's choice is computed. ids (optional) replace the chosen
+// expert ids; the weights are the router's.
+template <int EPL>
+__global__ __launch_bounds__(64) void k_route_lru(const DevPaging d, const uint16_t* __restrict__ logits, int E,
+                                                  int k, int norm, float* __restrict__ row,
+                                                  const int64_t* __restrict__ ids, int64_t key_base, int64_t n_ids,
+                                                  float* __restrict__ meta) {
+    __shared__ uint64_t cand[kDevMaxSlots];
+    const int lane = threadIdx.x;
+    if (k <= 0) {
+        if (lane == 0) d.miss[0] = 0;
+        return;
+    }
+    const LruStart st = lru_start(d, lane, cand);
+    const int64_t forced = ids ? ids[lane < k ? lane : 0] : -1;
+    const float val = route_select<EPL>(logits, E, k, norm);
+    if (lane < 2 * k) row[lane] = val;
+    const float w = __shfl(val, (k + lane) & 63, 64);
+    int key = -1;
+    if (lane < k) key = lru_key(d, ids ? forced : (int64_t)val, key_base, n_ids);
+    lru_apply(d, st, lane, k, key, w, cand, meta);
 }
 
 __global__ __launch_bounds__(64) void k_write_meta(const PageMeta pm) {
@@ -1259,6 +1306,38 @@ extern "C" int wisp_cache_device_step(void* h, const float* row, const int64_t* 
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(k_lru_step, dim3(1), dim3(64), 0, st, c.dev, row, ids, key_base, n_ids, k, meta);
     int rc = check_launch("k_lru_step");
+    if (rc) return rc;
+    const int64_t row16 = c.row_bytes / 16, slot16 = c.slot_bytes / 16;
+    const int64_t per = ((row16 + kPageSplit - 1) / kPageSplit + 1023) / 1024 * 1024;
+    hipLaunchKernelGGL(k_page_list, dim3(kPageSplit, k > 0 ? k : 1), dim3(256), 0, st,
+                       reinterpret_cast<const pg_u32x4*>(c.host_dev), reinterpret_cast<pg_u32x4*>(c.pool->ptr),
+                       c.dev.miss, row16, slot16, per);
+    return check_launch("k_page_list");
+}
+
+// wisp_dl_route (moe.py:41-47: softmax, top-k, renormalised bf16 weights into row) and
+// wisp_cache_device_step on its choice in one launch, then the page kernel.
+extern "C" int wisp_cache_device_route_step(void* h, const uint16_t* logits, int E, int k, int norm_topk, float* row,
+                                            const int64_t* ids, int64_t key_base, int64_t n_ids, float* meta,
+                                            void* stream) {
+    clear_error();
+    Cache& c = *as_cache(h);
+    if (!c.dev_on) return fail_inval("device paging is off (wisp_cache_device_begin)");
+    if (k < 0 || k > kDevMaxK) return fail_inval("device paging takes 0 <= k <= 16");
+    if (k > 0 && (!logits || !row || !meta || n_ids < 1 || E < k || E > 1024))
+        return fail_inval("device route step: null logits / row / meta, n_ids < 1 or E outside [k, 1024]");
+    if (!c.pool) return no_pool();
+    hipStream_t st = (hipStream_t)stream;
+    const int nt = norm_topk ? 1 : 0;
+#define WISP_RL(EPL) \
+    hipLaunchKernelGGL(k_route_lru<EPL>, dim3(1), dim3(64), 0, st, c.dev, logits, E, k, nt, row, ids, key_base, n_ids, meta)
+    if (E <= 64) WISP_RL(1);
+    else if (E <= 128) WISP_RL(2);
+    else if (E <= 256) WISP_RL(4);
+    else if (E <= 512) WISP_RL(8);
+    else WISP_RL(16);
+#undef WISP_RL
+    int rc = check_launch("k_route_lru");
     if (rc) return rc;
     const int64_t row16 = c.row_bytes / 16, slot16 = c.slot_bytes / 16;
     const int64_t per = ((row16 + kPageSplit - 1) / kPageSplit + 1023) / 1024 * 1024;

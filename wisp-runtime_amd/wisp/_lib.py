@@ -89,6 +89,7 @@ SIGNATURES = {
     "wisp_cache_resize": (_i32, [_vp, _i64]),
     "wisp_cache_device_begin": (_i32, [_vp, _vp]),
     "wisp_cache_device_step": (_i32, [_vp, _vp, _vp, _i64, _i64, _i32, _vp, _vp]),
+    "wisp_cache_device_route_step": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _i64, _i64, _vp, _vp]),
     "wisp_cache_device_sync": (_i32, [_vp, _vp]),
     "wisp_cache_device_end": (_i32, [_vp, _vp]),
     "wisp_cache_device_active": (_i32, [_vp]),

@@ -164,6 +164,23 @@ class ExpertCache:
         _raise(_lib.lib().wisp_cache_device_step(self._h, ctypes.c_void_p(row.data_ptr()), idp, key_base, n_ids, k,
                                                  ctypes.c_void_p(meta.data_ptr()), self._stream()))
 
+    def device_route_step(self, logits: torch.Tensor, k: int, norm_topk: bool, row: torch.Tensor, ids,
+                          key_base: int, n_ids: int, meta: torch.Tensor):
+        """The route kernel (softmax of the bf16 router logits [E], top-k, renormalised if
+        norm_topk, bf16 weights into row [ids | weights]) and device_step on its choice in
+        one launch, then the page kernel. ids (int64 [k] on the device) replace the chosen
+        expert ids if given."""
+        assert logits.dtype == torch.bfloat16 and logits.is_cuda and logits.is_contiguous()
+        assert row.dtype == torch.float32 and row.is_cuda and row.numel() >= 2 * k
+        assert meta.dtype == torch.float32 and meta.is_cuda and meta.numel() >= 2 * k
+        idp = None
+        if ids is not None:
+            assert ids.dtype == torch.int64 and ids.is_cuda and ids.is_contiguous() and ids.numel() >= k
+            idp = ctypes.c_void_p(ids.data_ptr())
+        _raise(_lib.lib().wisp_cache_device_route_step(
+            self._h, ctypes.c_void_p(logits.data_ptr()), logits.numel(), k, int(bool(norm_topk)),
+            ctypes.c_void_p(row.data_ptr()), idp, key_base, n_ids, ctypes.c_void_p(meta.data_ptr()), self._stream()))
+
     def device_sync(self):
         """Wait for the current stream and copy the device state into the core (stays on)."""
         if self.device_paging:

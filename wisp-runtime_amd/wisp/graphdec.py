@@ -33,8 +33,8 @@ How this build lays it out:
     page kernel for the misses and writes meta on the stream -- no stream sync per layer.
     With prefetch or a routing recorder the row is read back instead (one sync per layer).
   * Device paging (the default where the cache allows it: LRU policy, page-kernel copies):
-    the paging point itself runs on the GPU (the cache's LRU step kernel, then its page
-    kernel for the misses, both reading the route row from device memory), so the L + 1
+    the paging point itself runs on the GPU (one kernel takes the router's top-k and runs
+    the cache's LRU step on it, then the page kernel copies the misses), so the L + 1
     segments and the L paging points are captured as ONE graph per token and the host
     only writes the token and position and replays it. The bookkeeping is the same LRU
     step; the cache copies its state back to the host core when the host next needs it.
@@ -246,9 +246,7 @@ class GraphDecoder:
         kernels.dl_gemv(self.hm.view(H), w["o"], attn.view(Hq * D), res=self.hbuf)
         kernels.dl_gemv(self.rlogits, w["gate"], self.hm.view(H), norm_w=w["ln2"], eps=w["eps2"],
                         x_out=self.xn.view(H))
-        if self._dev:  # the cache's LRU step reads the row on the device
-            kernels.dl_route(self.rlogits, self.k, w["norm_topk"], self.row.view(-1))
-        else:
+        if not self._dev:  # (device paging: routed by the paging point's kernel, _device_step)
             kernels.dl_route(self.rlogits, self.k, w["norm_topk"], self.row.view(-1), self.row_host, self.flag_host,
                              self.seq_dev)
         if self.prefetch:  # the next layer's router on this layer's input predicts its experts
@@ -296,10 +294,12 @@ class GraphDecoder:
         return True
 
     def _device_step(self, i):
-        """Layer i's paging point on the current stream: LRU step of the route row (or of the
-        forced ids), meta_dev written, misses paged."""
+        """Layer i's routing and paging point on the current stream, one launch + the page
+        kernel: the router's top-k of rlogits into row, the LRU step of those experts (or of
+        the forced ids), meta_dev written, misses paged."""
         ids = self._ids_dev[i] if self._ids_dev is not None else None
-        self.rt.cache.device_step(self.row.view(-1), ids, i * self.E, self.E, self.k, self.meta_dev)
+        self.rt.cache.device_route_step(self.rlogits, self.k, self.shape.per_layer[i]["norm_topk"], self.row.view(-1),
+                                        ids, i * self.E, self.E, self.meta_dev)
 
     def _stage_ids(self):
         """Forced expert ids of every layer for this token -> _ids_dev (pinned ring, so the
@@ -370,8 +370,9 @@ class GraphDecoder:
             for _ in range(2):
                 for j in range(self.L + 1):
                     self._segment(j)
-            if self._dev:  # both paging kernels once, without a step
-                self.rt.cache.device_step(self.row.view(-1), None, 0, self.E, 0, self.meta_dev)
+            if self._dev:  # the paging point's kernels once, without a step
+                self.rt.cache.device_route_step(self.rlogits, 0, True, self.row.view(-1), None, 0, self.E,
+                                                self.meta_dev)
         torch.cuda.current_stream(self.dev).wait_stream(side)
         torch.cuda.synchronize(self.dev)
         pool = torch.cuda.graph_pool_handle()
