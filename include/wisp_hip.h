@@ -322,7 +322,7 @@ int wisp_cache_resize(void* cache, int64_t nslots);
  * WISP_EINVAL (the host core is stale until _sync or _end). */
 int wisp_cache_device_begin(void* cache, void* stream);
 /* One layer on `stream`, capturable (no host sync, no allocation): keys =
- * key_base + id_j, id_j = ids[j] (device int64 [k]) if ids, else row[j] (row:
+ * key_base + id_j, id_j = ids[j] (device int64 [k]) if ids and ids[j] >= 0, else row[j] (row:
  * device float32 [ids (k) | weights (k)], e.g. wisp_dl_route's row; an id must
  * be an integer in [0, n_ids)); meta (device float32 [2k]) = [slots | row's
  * weights]; the misses are paged by a kernel reading the pinned store. A bad id
@@ -333,7 +333,7 @@ int wisp_cache_device_step(void* cache, const float* row, const int64_t* ids, in
                            int k, float* meta, void* stream);
 /* wisp_dl_route (softmax of the bf16 logits [E], top-k, renormalised if norm_topk,
  * bf16 weights; row = [ids | weights]) and wisp_cache_device_step on that choice
- * (ids, if given, replace the chosen expert ids; the weights are the router's)
+ * (ids, if given, replace the chosen expert ids where >= 0; the weights are the router's)
  * in one launch, then the page kernel: the step's state reads overlap the
  * router's softmax and top-k. E <= 1024; k as for wisp_cache_device_step
  * (k = 0: warm-up launches). */

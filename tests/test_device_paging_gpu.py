@@ -211,11 +211,18 @@ def test_route_step_equals_route_kernel_then_step(store, E, k, norm):
         logits = torch.randn(E, generator=g, device=DEV).to(torch.bfloat16)
         kernels.dl_route(logits, k, norm, row_a)
         forced = None
+        chosen = [int(v) for v in row_a[:k].cpu()]
         if it % 4 == 3:
             forced = torch.from_numpy(rng.choice(E, size=k, replace=False).astype(np.int64)).to(DEV)
+        elif it % 4 == 1 and k < E:  # some lanes forced (ids outside the router's choice), the rest -1
+            other = [e for e in range(E) if e not in chosen]
+            f = [int(other[j]) if j % 2 == 0 and j < len(other) else -1 for j in range(k)]
+            forced = torch.tensor(f, dtype=torch.int64, device=DEV)
         c.device_route_step(logits, k, norm, row_b, forced, layer * E, E, meta)
         assert torch.equal(row_a.view(torch.int32), row_b.view(torch.int32)), it
-        ids = forced.cpu().tolist() if forced is not None else [int(v) for v in row_a[:k].cpu()]
+        ids = chosen
+        if forced is not None:
+            ids = [fv if fv >= 0 else cv for fv, cv in zip(forced.cpu().tolist(), chosen)]
         slots, _ = ref.ensure([layer * E + int(v) for v in ids])
         m = meta.cpu()
         assert [int(v) for v in m[:k]] == slots, it

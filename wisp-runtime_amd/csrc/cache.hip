@@ -462,8 +462,8 @@ __device__ __forceinline__ int lru_key(const DevPaging& d, int64_t id, int64_t k
     return (id >= 0 && id < n_ids && key_base + id >= 0 && key_base + id < d.nkeys) ? (int)(key_base + id) : -1;
 }
 
-// The step for key_base + id_j, id_j = ids[j] if ids, else the route row's id j (an integer
-// in [0, n_ids)); weights from the row. k <= 0: a warm-up launch that only clears the miss list.
+// The step for key_base + id_j, id_j = ids[j] if ids and ids[j] >= 0, else the route row's id
+// j (an integer in [0, n_ids)); weights from the row. k <= 0: a warm-up launch that only clears the miss list.
 __global__ __launch_bounds__(64) void k_lru_step(const DevPaging d, const float* __restrict__ row,
                                                  const int64_t* __restrict__ ids, int64_t key_base, int64_t n_ids,
                                                  int k, float* __restrict__ meta) {
@@ -477,12 +477,10 @@ __global__ __launch_bounds__(64) void k_lru_step(const DevPaging d, const float*
     int key = -1;
     float w = 0.f;
     if (lane < k) {
-        int64_t id = -1;
-        if (ids) {
-            id = ids[lane];
-        } else {
+        int64_t id = ids ? ids[lane] : -1;
+        if (id < 0) {  // the row's id
             const float f = row[lane];
-            if (f >= 0.f && f < 16777216.f && (float)(int64_t)f == f) id = (int64_t)f;
+            id = (f >= 0.f && f < 16777216.f && (float)(int64_t)f == f) ? (int64_t)f : -1;
         }
         key = lru_key(d, id, key_base, n_ids);
         w = row[k + lane];
@@ -493,7 +491,7 @@ __global__ __launch_bounds__(64) void k_lru_step(const DevPaging d, const float*
 // The route kernel's choice (route.hpp: softmax, top-k, renormalised bf16 weights; row =
 // [ids | weights]) and the LRU step of those experts in one wave: the step's state reads
 // are in flight while the router's choice is computed. ids (optional) replace the chosen
-// expert ids; the weights are the router's.
+// expert ids where they are >= 0; the weights are the router's.
 template <int EPL>
 __global__ __launch_bounds__(64) void k_route_lru(const DevPaging d, const uint16_t* __restrict__ logits, int E,
                                                   int k, int norm, float* __restrict__ row,
@@ -511,7 +509,7 @@ __global__ __launch_bounds__(64) void k_route_lru(const DevPaging d, const uint1
     if (lane < 2 * k) row[lane] = val;
     const float w = __shfl(val, (k + lane) & 63, 64);
     int key = -1;
-    if (lane < k) key = lru_key(d, ids ? forced : (int64_t)val, key_base, n_ids);
+    if (lane < k) key = lru_key(d, forced >= 0 ? forced : (int64_t)val, key_base, n_ids);
     lru_apply(d, st, lane, k, key, w, cand, meta);
 }
 

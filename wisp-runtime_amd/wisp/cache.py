@@ -153,7 +153,8 @@ class ExpertCache:
     def device_step(self, row: torch.Tensor, ids, key_base: int, n_ids: int, k: int, meta: torch.Tensor):
         """Queue one layer's paging point on the current stream (capturable): keys = key_base +
         id for the route row's ids (float32 row [ids | weights] on the device), or for `ids`
-        (int64 [k] on the device) if given; meta [2k] = [slots | weights]; misses paged.
+        (int64 [k] on the device; a negative entry keeps the row's id) if given; meta [2k] =
+        [slots | weights]; misses paged.
         k = 0: a warm-up launch of both kernels that changes nothing."""
         assert row.dtype == torch.float32 and row.is_cuda and row.numel() >= 2 * k
         assert meta.dtype == torch.float32 and meta.is_cuda and meta.numel() >= 2 * k
@@ -169,7 +170,7 @@ class ExpertCache:
         """The route kernel (softmax of the bf16 router logits [E], top-k, renormalised if
         norm_topk, bf16 weights into row [ids | weights]) and device_step on its choice in
         one launch, then the page kernel. ids (int64 [k] on the device) replace the chosen
-        expert ids if given."""
+        expert ids where they are >= 0."""
         assert logits.dtype == torch.bfloat16 and logits.is_cuda and logits.is_contiguous()
         assert row.dtype == torch.float32 and row.is_cuda and row.numel() >= 2 * k
         assert meta.dtype == torch.float32 and meta.is_cuda and meta.numel() >= 2 * k

@@ -303,11 +303,16 @@ class GraphDecoder:
 
     def _stage_ids(self):
         """Forced expert ids of every layer for this token -> _ids_dev (pinned ring, so the
-        host can run ahead of the GPU by a few tokens)."""
+        host can run ahead of the GPU by a few tokens); -1 (the router's choice) for a layer
+        whose _expert_ids is None."""
         buf, ev = self._ids_ring[self._ids_next]
         ev.synchronize()  # the copy that last read this buffer has run
         for i in range(self.L):
-            buf[i].copy_(torch.as_tensor(self._expert_ids(i), dtype=torch.int64))
+            ids = self._expert_ids(i)
+            if ids is None:
+                buf[i].fill_(-1)
+            else:
+                buf[i].copy_(torch.as_tensor(ids, dtype=torch.int64))
         self._ids_dev.copy_(buf, non_blocking=True)
         ev.record()
         self._ids_next = (self._ids_next + 1) % len(self._ids_ring)
