@@ -106,6 +106,40 @@ def test_graph_and_eager_decode_agree():
     rt.cache.free()
 
 
+def test_device_paging_with_partly_forced_routing_matches_host_steps():
+    """A decoder whose hook forces the experts of even layers only (None for the others: the
+    router's choice): the graph with the paging points on the GPU gives the host-step
+    decoder's logits bit for bit and the same cache bookkeeping."""
+    cfg, ref, gpu, rt = _models(seed=5)
+    ids = torch.randint(0, 128, (1, 4), generator=torch.Generator().manual_seed(6))
+    rng = np.random.default_rng(7)
+    draws = [[rng.choice(E, size=K, replace=False).astype(np.int64) for _ in range(L)] for _ in range(6)]
+
+    class Half(GraphDecoder):
+        def _expert_ids(self, i):
+            return draws[self.pos - 4][i] if i % 2 == 0 else None
+
+    outs, cores = [], []
+    for paging in (False, True):
+        rt.cache.free()
+        rt.cache = ExpertCache(rt.store, 10)
+        dec = Half(gpu, rt, tmax=64, device_paging=paging)
+        with torch.no_grad():
+            t = dec.prefill(ids[0].cuda()).argmax(-1)
+            seq = []
+            for _ in range(6):
+                lg = dec.next(t).clone()
+                seq.append(lg)
+                t = lg.argmax(-1)
+        assert dec._dev == paging and len(dec.graphs) == (1 if paging else L + 1)
+        outs.append(torch.stack(seq))
+        core = rt.cache.core
+        cores.append((dict(core.key2slot), dict(core.stats), list(core.free)))
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    assert cores[0] == cores[1]
+    rt.cache.free()
+
+
 def test_prefetch_and_recorder_paths_give_the_same_tokens():
     """The per-layer host step with prefetch of the next layer's predicted experts (and with a
     routing recorder) reads the row through the generic path; only slot placement may change,
