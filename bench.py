@@ -1067,9 +1067,10 @@ def main():
             "workload": f"C2: one Qwen3-30B-A3B MoE layer, decode batch 1, top-{K_TOP} of {E} experts, {bits}-bit "
                         f"group-{G}, H={H} I={I}, {a.layers} layer pools rotated",
             "weights": f"u{bits} group-{G} fp16 scale+min",
-            "accumulate": "fp32 (exact bf16 x code products, v_dot2 into fp32)",
-            "activation": "a = silu(g)*u kept between the kernels as a bf16 hi+lo pair (~17 significant bits; "
-                          "the reference keeps fp32); output bf16, rounded once",
+            "accumulate": "fp32 (kernel 1: exact bf16 x code products, v_dot2 into fp32; kernel 2: exact fp32 "
+                          "activation code products, v_fma_mix_f32 into fp32)",
+            "activation": "a = silu(g)*u kept between the kernels in fp32 (as the reference's a); output bf16, "
+                          "rounded once",
             "bytes_per_layer": layer_b,
             "path": "two kernel launches per layer (wisp_moe_decode / moe_decode_q4_fast)",
         },

@@ -89,11 +89,11 @@ int wisp_dequant(const uint8_t* rows, int64_t row_stride, const int64_t* row_ind
 
 /* Kernel 1 of a batch-1 MoE layer: for each of the k experts in meta and each
  * row r < I, a[j,r] = silu(Wg_j[r].x) * (Wu_j[r].x), fp32 accumulation,
- * written to the workspace `act` (wisp_act_bytes(k, I) bytes, internal
- * layout; wisp_act_read decodes it). x: H values of type x_dtype
- * (WISP_DT_BF16, WISP_DT_F16 or WISP_DT_F32; a non-bf16 x is used to ~17
- * significant bits: exact for fp16, within 2^-17 relative for fp32), 16-byte
- * aligned. bits in {4,3,2}; 1 <= k <= WISP_MAX_K.
+ * written to the workspace `act` (wisp_act_bytes(k, I) bytes: a as fp32 in
+ * the order a[j*I + r], the reference's fp32 `a`; wisp_act_read copies it
+ * out). x: H values of type x_dtype (WISP_DT_BF16, WISP_DT_F16 or
+ * WISP_DT_F32; every product of a code with x is exact), 16-byte aligned.
+ * bits in {4,3,2}; 1 <= k <= WISP_MAX_K.
  * Replaces wisp/kernels.py:20-69 (_gate_up_kernel, 4-bit) and 220-263
  * (_gate_up_kernel3, 3-bit); the 2-bit variant has no reference kernel. */
 int wisp_moe_gate_up(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
@@ -436,9 +436,10 @@ int wisp_dl_route(const void* logits, int E, int k, int norm_topk, float* row, f
  * kernels (wisp/kernels.py:115, 188, 310). */
 int wisp_set_tuning(int gu_rows, int gu_waves, int dn_iters);
 
-/* Decode the workspace written by wisp_moe_gate_up into fp32 a [k, I].
- * No reference counterpart (the reference's `a` is already fp32); used by
- * tests to check kernel 1 on its own. */
+/* Copy the workspace written by wisp_moe_gate_up (fp32 a [k, I]) into a.
+ * No reference counterpart (the reference's `a` is its own fp32 tensor);
+ * used by tests to check kernel 1 on its own. `bits` is checked (4, 3 or 2)
+ * but does not change the layout. */
 int wisp_act_read(const uint32_t* act, int k, int64_t I, int bits, float* a, void* stream);
 
 /* ------------------------------------------------------------------------

@@ -155,7 +155,9 @@ def test_gate_up_activation(bits, H, I, group):
                             torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(DEV), k, n, H, I, bits, group)
     err = _rel_l2(a.cpu().numpy().astype(np.float64), a_ref)
     print(f"gate_up bits={bits} H={H}: rel-L2 {err:.3e}")
-    assert err <= 2e-5, err
+    # the activation is fp32 between the kernels (the reference's `a`, kernels.py:133): the only error is the
+    # fp32 accumulation of the gate/up dot products and SiLU
+    assert err <= 2e-7, err
 
 
 @pytest.mark.parametrize("H,I,group,E,k", [(256, 128, 128, 6, 3), (2048, 768, 128, 10, 8)])

@@ -7,20 +7,20 @@
 // 72-112 (_down_kernel), 140-185 (_down_sum_kernel), 206-307 (3-bit twins).
 //
 // Work decomposition (MI355X: 256 CUs, wave64):
-//  * A lane owns one 32-code chunk of a row (16/12/8 bytes for 4/3/2-bit) and
-//    keeps the matching 32 operand values in registers as 16 bf16 pairs, so
+//  * A lane owns one 32-code chunk of a row (16/12/8 bytes for 4/3/2-bit), so
 //    the codes stream through 128/96/64-bit loads that are contiguous across
-//    the wave, and each chunk dot is 16 v_and_or_b32 + 16 v_dot2c_f32_bf16
-//    (+ window shifts). All loads of a wave are issued before any math.
+//    the wave. All loads of a wave are issued before any math.
 //  * Kernel 1: one wave = one expert x T*RPI rows (gate and up), RPI = rows
-//    per wave-wide load (1 when H = 2048). Per-lane partials are summed per
+//    per wave-wide load (1 when H = 2048). With a bf16 x a chunk dot is
+//    16 v_and_or_b32 + 16 v_dot2c_f32_bf16 against x in pair order (exact
+//    products); a fp16 or fp32 x is used as 32 fp32 values with one
+//    v_fma_mix_f32 per code (chunk_dot_f32). Per-lane partials are summed per
 //    row through LDS; SiLU(gate)*up is formed by the lane holding the row.
-//  * Kernel 2: one workgroup = k waves (wave j = expert j) over T*RPI output
-//    rows; per-lane partials are summed per row through LDS, then the k
-//    expert sums are combined in expert order and stored once as bf16.
-//  * The activation between the kernels is kept at ~17-bit precision as a
-//    bf16 hi/lo split (a = hi + lo), pre-arranged in the down kernel's pair
-//    order, so kernel 2 uses the same dot2 path (two dot2 per code pair).
+//  * The activation between the kernels is fp32 in natural order,
+//    act[j*I + r] (the reference's fp32 `a`, kernels.py:133, 197, 316).
+//  * Kernel 2: the activation chunk of a lane is 32 fp32 values staged in LDS;
+//    the codes enter v_fma_mix_f32 as fp16 subnormals (chunk_dot_f32), so every
+//    product q*a is exact and the sums are fp32, as the reference's are.
 #include <mutex>
 
 #include "wisp_device.hpp"
@@ -51,39 +51,34 @@ struct Layer {
     int odt;      // output dtype of the weighted sum: WISP_DT_BF16, WISP_DT_F16 or WISP_DT_F32
 };
 
-// The layer constants as the kernels use them: with C2 (the Qwen3-30B-A3B expert shape,
-// H = 2048, I = 768, G = 128) every shape-derived field is a compile-time constant, so the
-// kernels read no Layer field from kernel-argument memory before their weight loads (the
-// runtime fields come from the preloaded scalar arguments); otherwise the Layer as passed.
+// The layer constants of the Qwen3-30B-A3B expert shape (H = 2048, I = 768, G = 128) as compile-time
+// constants: the kernels specialised on it take no Layer argument (every field they need is a constant or one
+// of their preloaded scalar arguments), so nothing is read from kernel-argument memory before their weight
+// loads; other shapes take the Layer as passed.
 constexpr int kC2H = 2048, kC2I = 768, kC2G = 128;
 
-template <int BITS, bool C2>
-__device__ __forceinline__ Layer layer_of(const Layer& L, const uint8_t* pool, const float* meta, int64_t slot_bytes,
-                                          int nslots) {
-    if constexpr (C2) {
-        Layer c;
-        c.pool = pool;
-        c.meta = meta;
-        c.slot_bytes = slot_bytes;
-        c.nmb = (int64_t)kC2H * kC2I * BITS / 8;
-        c.nslots = nslots;
-        c.k = 0;  // taken from the kernel's own argument where needed
-        c.H = kC2H;
-        c.I = kC2I;
-        c.G = kC2G;
-        c.rowb_gu = kC2H * BITS / 8;
-        c.rowb_dn = kC2I * BITS / 8;
-        c.gpr_gu = kC2H / kC2G;
-        c.gpr_dn = kC2I / kC2G;
-        c.NGM = kC2H * kC2I / kC2G;
-        c.gsh = 2;  // log2(G / 32)
-        c.spr_gu = kC2H / 32;
-        c.spr_dn = kC2I / 32;
-        c.odt = L.odt;  // read only at the output store
-        return c;
-    } else {
-        return L;
-    }
+template <int BITS>
+__device__ __forceinline__ Layer layer_c2(const uint8_t* pool, const float* meta, int64_t slot_bytes, int nslots) {
+    Layer c;
+    c.pool = pool;
+    c.meta = meta;
+    c.slot_bytes = slot_bytes;
+    c.nmb = (int64_t)kC2H * kC2I * BITS / 8;
+    c.nslots = nslots;
+    c.k = 0;  // taken from the kernel's own argument where needed
+    c.H = kC2H;
+    c.I = kC2I;
+    c.G = kC2G;
+    c.rowb_gu = kC2H * BITS / 8;
+    c.rowb_dn = kC2I * BITS / 8;
+    c.gpr_gu = kC2H / kC2G;
+    c.gpr_dn = kC2I / kC2G;
+    c.NGM = kC2H * kC2I / kC2G;
+    c.gsh = 2;  // log2(G / 32)
+    c.spr_gu = kC2H / 32;
+    c.spr_dn = kC2I / 32;
+    c.odt = WISP_DT_BF16;  // kernels of this shape take the output dtype as a template argument
+    return c;
 }
 
 // out[h] = v rounded once (round to nearest even) to the caller's dtype
@@ -97,11 +92,10 @@ __device__ __forceinline__ void store_out(void* out, int odt, int h, float v) {
 }
 
 // ---------------------------------------------------------------------------
-// x in any of the three float types. XT: WISP_DT_BF16 (the native operand),
-// WISP_DT_F16 or WISP_DT_F32. A non-bf16 x is carried as a bf16 hi/lo split,
-// x = hi + lo (hi = bf16(x), lo = bf16(x - hi)): exact for fp16 x, within
-// 2^-17 relative for fp32 x, so the kernels' dot products see x to ~17 bits
-// as the reference's fp32 loads of x do (kernels.py:51-52).
+// x in any of the three float types. XT: WISP_DT_BF16 (the native operand of the
+// dot2 path), WISP_DT_F16 or WISP_DT_F32: those are converted to 32 fp32
+// values per chunk (exact) for the fma path, so every product with x is exact,
+// as the reference's fp32 loads of x (kernels.py:51-52) give.
 // ---------------------------------------------------------------------------
 template <int XT>
 struct XWords {
@@ -120,29 +114,23 @@ __device__ __forceinline__ void load_x_raw(const void* x, int c, uint32_t* w) {
     }
 }
 
-// raw dwords -> 16 bf16 hi dwords (+ 16 lo dwords for a non-bf16 x)
+// raw dwords -> 32 fp32 values in element order (exact for every XT)
 template <int XT>
-__device__ __forceinline__ void split_x(const uint32_t* w, uint32_t* hi, uint32_t* lo) {
-    if constexpr (XT == WISP_DT_BF16) {
+__device__ __forceinline__ void x_to_f32(const uint32_t* w, float* xf) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) hi[i] = w[i];
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float a, b;
-            if constexpr (XT == WISP_DT_F32) {
-                a = __uint_as_float(w[2 * i]);
-                b = __uint_as_float(w[2 * i + 1]);
-            } else {
-                a = half_lo_f(w[i]);
-                b = half_hi_f(w[i]);
-            }
-            hi[i] = pack_bf16x2(a, b);
-            lo[i] = pack_bf16x2(a - bf16_lo(hi[i]), b - bf16_hi(hi[i]));
+    for (int i = 0; i < 16; ++i) {
+        if constexpr (XT == WISP_DT_F32) {
+            xf[2 * i] = __uint_as_float(w[2 * i]);
+            xf[2 * i + 1] = __uint_as_float(w[2 * i + 1]);
+        } else if constexpr (XT == WISP_DT_F16) {
+            xf[2 * i] = half_lo_f(w[i]);
+            xf[2 * i + 1] = half_hi_f(w[i]);
+        } else {
+            xf[2 * i] = bf16_lo(w[i]);
+            xf[2 * i + 1] = bf16_hi(w[i]);
         }
     }
 }
-
 
 // slot id from the meta buffer: -1 unless an exact integer in [0, nslots)
 __device__ __forceinline__ int slot_from(float f, int nslots) {
@@ -157,58 +145,10 @@ __device__ __forceinline__ void wave_sync_lds() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Store a[j, r] into the activation workspace: segment r/32, pair slot of
-// r%32, as bf16 hi and lo parts of a * 2^-e.
-// Workspace layout: act[(j*(I/32) + s)*32 + P] = hi pair P, [+16+P] = lo pair P.
-template <int BITS>
-__device__ __forceinline__ void write_act(uint32_t* act, int j, int I, int r, float a) {
-    const int info = pair_slot<BITS>(r & 31);
-    const int P = info & 15, half = (info >> 4) & 1, e = info >> 5;
-    const float av = scale_pow2(a, e);
-    const uint16_t hi = f32_to_bf16(av);
-    const uint16_t lo = f32_to_bf16(av - bf16_to_f32(hi));
-    uint16_t* a16 = reinterpret_cast<uint16_t*>(act + ((int64_t)j * (I >> 5) + (r >> 5)) * 32);
-    a16[2 * P + half] = hi;
-    a16[2 * (16 + P) + half] = lo;
-}
+// a[j, r] into the fp32 activation workspace
+__device__ __forceinline__ void write_act(float* act, int j, int I, int r, float a) { act[(int64_t)j * I + r] = a; }
 
-// x operand of chunk c: hi (and lo) pairs, sum of stored values, sum of true values
-template <int BITS, int XT>
-__device__ __forceinline__ void load_x_operand(const void* x, int c, uint32_t* xp, uint32_t* xq, float& vsum,
-                                               float& xsum) {
-    uint32_t w[XWords<XT>::n], h[16], l[16];
-    load_x_raw<XT>(x, c, w);
-    split_x<XT>(w, h, l);
-    operand_pairs<BITS>(h, xp);
-    operand_sums<BITS>(xp, vsum, xsum);
-    if constexpr (XT != WISP_DT_BF16) {
-        float vl, tl;
-        operand_pairs<BITS>(l, xq);
-        operand_sums<BITS>(xq, vl, tl);
-        vsum += vl;
-        xsum += tl;
-    }
-}
-
-// activation operand of segment s of expert j: hi and lo pairs and their sums
-template <int BITS>
-__device__ __forceinline__ void load_act_operand(const uint32_t* act, int j, int I, int s, uint32_t* AH, uint32_t* AL,
-                                                 float& vsum, float& asum) {
-    const uint4* ap = reinterpret_cast<const uint4*>(act + ((int64_t)j * (I >> 5) + s) * 32);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint4 h = ap[i], l = ap[4 + i];
-        AH[4 * i] = h.x; AH[4 * i + 1] = h.y; AH[4 * i + 2] = h.z; AH[4 * i + 3] = h.w;
-        AL[4 * i] = l.x; AL[4 * i + 1] = l.y; AL[4 * i + 2] = l.z; AL[4 * i + 3] = l.w;
-    }
-    float vh, th, vl, tl;
-    operand_sums<BITS>(AH, vh, th);
-    operand_sums<BITS>(AL, vl, tl);
-    vsum = vh + vl;
-    asum = th + tl;
-}
-
-// dot of one chunk of codes against one operand, bias removed: sum q*v
+// dot of one chunk of codes against one bf16 operand in pair order, bias removed: sum q*v
 template <int BITS>
 __device__ __forceinline__ float chunk_dot(const uint32_t* codes, const uint32_t* opr, float bias, uint32_t B) {
     uint32_t p[16];
@@ -218,20 +158,6 @@ __device__ __forceinline__ float chunk_dot(const uint32_t* codes, const uint32_t
     for (int P = 0; P < 16; P += 2) {
         a0 = dot2(p[P], opr[P], a0);
         a1 = dot2(p[P + 1], opr[P + 1], a1);
-    }
-    return a0 + a1;
-}
-// same against a hi/lo split operand
-template <int BITS>
-__device__ __forceinline__ float chunk_dot_hl(const uint32_t* codes, const uint32_t* oh, const uint32_t* ol,
-                                              float bias, uint32_t B) {
-    uint32_t p[16];
-    code_pairs<BITS>(codes, p, B);
-    float a0 = bias, a1 = 0.f;
-#pragma unroll
-    for (int P = 0; P < 16; ++P) {
-        a0 = dot2(p[P], oh[P], a0);
-        a1 = dot2(p[P], ol[P], a1);
     }
     return a0 + a1;
 }
@@ -272,21 +198,25 @@ __device__ __forceinline__ int lanes_per_sum(int NQ) {
 // QSC: the 4 lanes of a quad share one (row, group) (G >= 128, H/32 % 4 == 0):
 //      each quad fetches its 4 fp16 values (gate s, gate m, up s, up m) with one
 //      16-bit load per lane and shares them with DPP broadcasts.
+// XF: x arrives as 32 fp32 values xf (fp16 / fp32 x, fma path); else as 16
+//     bf16 pair words xw (dot2 path).
+// FULL: H/32 == 64 and every row r0 .. r0 + T - 1 exists (the Qwen3 shape), so
+//     no lane is idle and no row index needs a clamp.
 // part: this wave's LDS scratch, T*2*64 floats.
 // ===========================================================================
-template <int BITS, int SPR_T, int T, bool QSC, bool HL>
-// The lanes' x words (xw, chunk `seg` of x; HL: x = xw + xl as bf16 hi/lo) are
-// loaded by the caller before the slot id is known; `ok` false (invalid slot
-// id) reads slot 0 and writes NaN rows.
+template <int BITS, int SPR_T, int T, bool QSC, bool XF, bool FULL = false>
+// The lanes' x (chunk `seg` of x) is loaded by the caller before the slot id is
+// known; `ok` false (invalid slot id) reads slot 0 and writes NaN rows.
 __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __restrict__ base, bool ok,
-                                             const uint32_t (&xw)[16], const uint32_t (&xl)[16],
-                                             uint32_t* __restrict__ act, int j, int r0, float* part) {
+                                             const uint32_t (&xw)[16], const float (&xf)[32],
+                                             float* __restrict__ act, int j, int r0, float* part) {
+    static_assert(!FULL || SPR_T == 64, "FULL needs one row per wave-wide load");
     const int SPR = SPR_T ? SPR_T : L.spr_gu;
     const int RPI = 64 / SPR;
     const int lane = threadIdx.x & 63;
-    int rr = lane / SPR;
+    int rr = FULL ? 0 : lane / SPR;
     const int seg = lane - rr * SPR;
-    const bool lane_on = rr < RPI;
+    const bool lane_on = FULL || rr < RPI;
     rr = lane_on ? rr : RPI - 1;  // idle lanes repeat an active lane's addresses
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb);
     const uint16_t* mn = sc + 3 * L.NGM;
@@ -297,7 +227,7 @@ __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __re
     uint32_t sv[T][QSC ? 1 : 4];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        const int r = min(r0 + t * RPI + rr, L.I - 1);
+        const int r = FULL ? r0 + t : min(r0 + t * RPI + rr, L.I - 1);
         const uint8_t* rp = base + (int64_t)r * L.rowb_gu + seg * (4 * BITS);
         load_chunk<BITS>(rp, cg[t]);
         load_chunk<BITS>(rp + L.nmb, cu[t]);
@@ -312,26 +242,24 @@ __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __re
             sv[t][3 % (QSC ? 1 : 4)] = mn[L.NGM + gidx];
         }
     }
-    uint32_t xp[16], xq[HL ? 16 : 1];
-    operand_pairs<BITS>(xw, xp);
-    float vs, xs;
-    operand_sums<BITS>(xp, vs, xs);
-    if constexpr (HL) {
-        float vl, tl;
-        operand_pairs<BITS>(xl, xq);
-        operand_sums<BITS>(xq, vl, tl);
-        vs += vl;
-        xs += tl;
+    uint32_t xp[16];
+    float xs, bias = 0.f;
+    if constexpr (XF) {
+        xs = chunk_sum_f32(xf);
+    } else {
+        float vs;
+        operand_pairs<BITS>(xw, xp);
+        operand_sums<BITS>(xp, vs, xs);
+        bias = -kBiasF * vs;
     }
-    const float bias = -kBiasF * vs;
     const uint32_t B = bias_vgpr();
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        const bool ok = lane_on && (r0 + t * RPI + rr < L.I);
+        const bool ok = FULL || (lane_on && (r0 + t * RPI + rr < L.I));
         float dg, du;
-        if constexpr (HL) {
-            dg = chunk_dot_hl<BITS>(cg[t], xp, xq, bias, B);
-            du = chunk_dot_hl<BITS>(cu[t], xp, xq, bias, B);
+        if constexpr (XF) {
+            dg = chunk_dot_f32<BITS>(cg[t], xf);
+            du = chunk_dot_f32<BITS>(cu[t], xf);
         } else {
             dg = chunk_dot<BITS>(cg[t], xp, bias, B);
             du = chunk_dot<BITS>(cu[t], xp, bias, B);
@@ -376,46 +304,83 @@ __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __re
         }
         if (q < NQ && sub == 0 && m == 0) {
             const int r = r0 + t * RPI + rq;
-            if (r < L.I) write_act<BITS>(act, j, L.I, r, ok ? silu_mul(v, u) : __builtin_nanf(""));
+            if (FULL || r < L.I) write_act(act, j, L.I, r, ok ? silu_mul(v, u) : __builtin_nanf(""));
         }
     }
 }
 
-// Kernel 1 (fast path), two-kernel form.
+// x of this lane's chunk: raw words (bf16) or 32 fp32 values (fp16 / fp32)
+template <int XT>
+__device__ __forceinline__ void x_operand(const uint32_t* xr, uint32_t (&xw)[16], float (&xf)[32]) {
+    if constexpr (XT == WISP_DT_BF16) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xw[i] = xr[i];
+    } else {
+        x_to_f32<XT>(xr, xf);
+    }
+}
+
+// Kernel 1 (fast path), two-kernel form, any shape with H/32 <= 64.
 // grid = (ceil(I / (NW*T*RPI)), k), block = 64*NW.
 // The leading scalar arguments are preloaded into SGPRs at dispatch (kernarg
 // preloading, built with -amdgpu-kernarg-preload-count): the slot-id read and
 // the x loads need no kernel-argument fetch first, so the only memory round
 // trip before the weight loads is the slot id itself.
-template <int BITS, int SPR_T, int T, int NW, bool QSC, int XT, bool C2>
+template <int BITS, int SPR_T, int T, int NW, bool QSC, int XT>
 __global__ __launch_bounds__(64 * NW) void k_gate_up(const float* __restrict__ meta,
                                                       const uint8_t* __restrict__ pool, int64_t slot_bytes,
                                                       int nslots, const void* __restrict__ x,
-                                                      uint32_t* __restrict__ act, const Layer L) {
+                                                      float* __restrict__ act, const Layer L) {
     __shared__ float part[NW][T * 2 * 64];
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = blockIdx.y;
-    // issue the slot-id read, the remaining kernel-argument reads and the x loads
-    // together; the scheduling barrier keeps every use (and so every wait) after them
+    // issue the slot-id read and the x loads together; the scheduling barrier keeps every use (and so every
+    // wait) after them
     const float f = meta[j];
-    const Layer Lc = layer_of<BITS, C2>(L, pool, meta, slot_bytes, nslots);
     uint32_t xr[XWords<XT>::n];
-    load_x_raw<XT>(x, (threadIdx.x & 63) % (SPR_T ? SPR_T : Lc.spr_gu), xr);
+    load_x_raw<XT>(x, (threadIdx.x & 63) % (SPR_T ? SPR_T : L.spr_gu), xr);
     __builtin_amdgcn_sched_barrier(0);
     const int slot = __builtin_amdgcn_readfirstlane(slot_from(f, nslots));
     const bool ok = slot >= 0;
     const uint8_t* base = pool + (int64_t)(ok ? slot : 0) * slot_bytes;
-    const int RPI = 64 / (SPR_T ? SPR_T : Lc.spr_gu);
+    const int RPI = 64 / (SPR_T ? SPR_T : L.spr_gu);
     const int r0 = (blockIdx.x * NW + wv) * (T * RPI);
-    uint32_t xw[16], xl[16];
-    split_x<XT>(xr, xw, xl);
-    gate_up_rows<BITS, SPR_T, T, QSC, XT != WISP_DT_BF16>(Lc, base, ok, xw, xl, act, j, r0, part[wv]);
+    uint32_t xw[16];
+    float xf[32];
+    x_operand<XT>(xr, xw, xf);
+    gate_up_rows<BITS, SPR_T, T, QSC, XT != WISP_DT_BF16>(L, base, ok, xw, xf, act, j, r0, part[wv]);
 }
 
-// Kernel 1 (generic): any H, G; one wave per (row, expert).
+// Kernel 1 at the Qwen3-30B-A3B shape: the same body with every shape field a compile-time constant and no
+// Layer argument.
+template <int BITS, int T, int NW, bool QSC, int XT>
+__global__ __launch_bounds__(64 * NW) void k_gate_up_c2(const float* __restrict__ meta,
+                                                         const uint8_t* __restrict__ pool, int64_t slot_bytes,
+                                                         int nslots, const void* __restrict__ x,
+                                                         float* __restrict__ act) {
+    static_assert(kC2I % (NW * T) == 0, "every row of the grid exists (gate_up_rows FULL)");
+    __shared__ float part[NW][T * 2 * 64];
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = blockIdx.y;
+    const float f = meta[j];
+    const Layer Lc = layer_c2<BITS>(pool, meta, slot_bytes, nslots);
+    uint32_t xr[XWords<XT>::n];
+    load_x_raw<XT>(x, threadIdx.x & 63, xr);
+    __builtin_amdgcn_sched_barrier(0);
+    const int slot = __builtin_amdgcn_readfirstlane(slot_from(f, nslots));
+    const bool ok = slot >= 0;
+    const uint8_t* base = pool + (int64_t)(ok ? slot : 0) * slot_bytes;
+    const int r0 = (blockIdx.x * NW + wv) * T;
+    uint32_t xw[16];
+    float xf[32];
+    x_operand<XT>(xr, xw, xf);
+    gate_up_rows<BITS, 64, T, QSC, XT != WISP_DT_BF16, true>(Lc, base, ok, xw, xf, act, j, r0, part[wv]);
+}
+
+// Kernel 1 (generic): any H, G; one wave per (row, expert); x as fp32 values (exact for every x dtype).
 template <int BITS, int XT>
 __global__ __launch_bounds__(64) void k_gate_up_generic(const Layer L, const void* __restrict__ x,
-                                                        uint32_t* __restrict__ act) {
+                                                        float* __restrict__ act) {
     const int lane = threadIdx.x;
     const int r = blockIdx.x, j = blockIdx.y;
     const int slot = __builtin_amdgcn_readfirstlane(slot_of(L.meta, j, L.nslots));
@@ -424,33 +389,25 @@ __global__ __launch_bounds__(64) void k_gate_up_generic(const Layer L, const voi
         const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
         const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb);
         const uint16_t* mn = sc + 3 * L.NGM;
-        const uint32_t B = bias_vgpr();
         for (int c = lane; c < L.spr_gu; c += 64) {
-            uint32_t cg[BITS], cu[BITS], xp[16], xq[16];
+            uint32_t cg[BITS], cu[BITS], xr[XWords<XT>::n];
+            float xf[32];
             const uint8_t* rp = base + (int64_t)r * L.rowb_gu + c * (4 * BITS);
             load_chunk<BITS>(rp, cg);
             load_chunk<BITS>(rp + L.nmb, cu);
-            float vs, xs;
-            load_x_operand<BITS, XT>(x, c, xp, xq, vs, xs);
-            const float bias = -kBiasF * vs;
+            load_x_raw<XT>(x, c, xr);
+            x_to_f32<XT>(xr, xf);
+            const float xs = chunk_sum_f32(xf);
             const int gidx = r * L.gpr_gu + (c * 32) / L.G;
-            float dg, du;
-            if constexpr (XT != WISP_DT_BF16) {
-                dg = chunk_dot_hl<BITS>(cg, xp, xq, bias, B);
-                du = chunk_dot_hl<BITS>(cu, xp, xq, bias, B);
-            } else {
-                dg = chunk_dot<BITS>(cg, xp, bias, B);
-                du = chunk_dot<BITS>(cu, xp, bias, B);
-            }
-            pg += h2f(sc[gidx]) * dg + h2f(mn[gidx]) * xs;
-            pu += h2f(sc[L.NGM + gidx]) * du + h2f(mn[L.NGM + gidx]) * xs;
+            pg += h2f(sc[gidx]) * chunk_dot_f32<BITS>(cg, xf) + h2f(mn[gidx]) * xs;
+            pu += h2f(sc[L.NGM + gidx]) * chunk_dot_f32<BITS>(cu, xf) + h2f(mn[L.NGM + gidx]) * xs;
         }
         pg = wave_sum(pg);
         pu = wave_sum(pu);
     } else {
         pg = pu = __builtin_nanf("");
     }
-    if (lane == 0) write_act<BITS>(act, j, L.I, r, silu_mul(pg, pu));
+    if (lane == 0) write_act(act, j, L.I, r, silu_mul(pg, pu));
 }
 
 // ===========================================================================
@@ -460,12 +417,12 @@ __global__ __launch_bounds__(64) void k_gate_up_generic(const Layer L, const voi
 // for I = 768), 0 = runtime.
 // QSC: quads share one (row, group) (G >= 128, I/32 % 4 == 0, T even): lane i
 //      of a quad loads one of (s, m) for rows t and t+1; DPP broadcasts share them.
-// Each wave stages its expert's activation (I dwords, segment stride 36 dwords
-// against bank conflicts) in LDS once, so a lane reads its 128-byte operand
-// from LDS instead of from L2.
+// Each wave stages its expert's fp32 activation (I values, 32-value segments
+// at a stride of 36 words against bank conflicts) in LDS once, so a lane reads
+// its 128-byte operand from LDS instead of from L2.
 // lds: (k*T*64 + k*T*RPI + k*I*36/32) floats.
-// WSUM: out[h] = bf16(sum_j w_j y_j[h]) (wave j scales its row sums by w_j,
-// loaded at the start); else y[j*H + h] = y_j[h].
+// WSUM: out[h] = sum_j w_j y_j[h] rounded once (wave j scales its row sums by
+// w_j, loaded at the start); else y[j*H + h] = y_j[h].
 // ===========================================================================
 template <int BITS, int SPR_T, int T, bool WSUM, bool QSC>
 // `meta`, `pool`, `slot_bytes`, `nslots`, `k` and `I` repeat fields of L as
@@ -474,7 +431,7 @@ template <int BITS, int SPR_T, int T, bool WSUM, bool QSC>
 // yields NaN partials.
 __device__ __forceinline__ void down_rows(const Layer& L, const float* meta,
                                           const uint8_t* __restrict__ pool, int64_t slot_bytes, int nslots, int k,
-                                          int I, const uint32_t* __restrict__ act, void* __restrict__ out,
+                                          int I, const float* __restrict__ act, void* __restrict__ out,
                                           float* __restrict__ y, int h0, float* lds) {
     static_assert(!QSC || T % 2 == 0, "quad-shared scales cover two rows per load");
     const int SPR = SPR_T ? SPR_T : L.spr_dn;
@@ -527,7 +484,7 @@ __device__ __forceinline__ void down_rows(const Layer& L, const float* meta,
                     sv[t] = (uint32_t)sc[h * L.gpr_dn + gi] | ((uint32_t)mn[h * L.gpr_dn + gi] << 16);
                 }
             }
-            // stage expert j's activation (hi/lo pairs) in LDS, segment stride 36 dwords
+            // stage expert j's activation in LDS, segment stride 36 words
 #pragma unroll
             for (int k2 = 0; k2 < APL; ++k2) {
                 const int i = min(lane + 64 * k2, na16 - 1);
@@ -537,24 +494,21 @@ __device__ __forceinline__ void down_rows(const Layer& L, const float* meta,
                 reinterpret_cast<uint4*>(stage)[i + (i >> 3)] = make_uint4(a.z, a.w, a.x, a.y);
             }
             wave_sync_lds();
-            uint32_t AH[16], AL[16];
+            float A[32];
             const uint4* ap = reinterpret_cast<const uint4*>(stage + seg * 36);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint4 hq = ap[i], lq = ap[4 + i];  // halves swapped in the stage
-                AH[4 * i] = hq.z; AH[4 * i + 1] = hq.w; AH[4 * i + 2] = hq.x; AH[4 * i + 3] = hq.y;
-                AL[4 * i] = lq.z; AL[4 * i + 1] = lq.w; AL[4 * i + 2] = lq.x; AL[4 * i + 3] = lq.y;
+            for (int i = 0; i < 8; ++i) {
+                const uint4 v = ap[i];  // halves swapped in the stage
+                A[4 * i] = __uint_as_float(v.z); A[4 * i + 1] = __uint_as_float(v.w);
+                A[4 * i + 2] = __uint_as_float(v.x); A[4 * i + 3] = __uint_as_float(v.y);
             }
-            float vh, th, vl, tl;
-            operand_sums<BITS>(AH, vh, th);
-            operand_sums<BITS>(AL, vl, tl);
-            const float as = th + tl;
-            const float bias = -kBiasF * (vh + vl);
-            const uint32_t B = bias_vgpr();
+            const float as = chunk_sum_f32(A);
+            // the sum uses the staged activation only: keep it ahead of every wait for the codes
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 const bool row_ok = lane_on && (h0 + t * RPI + rr < L.H);
-                const float d = chunk_dot_hl<BITS>(cd[t], AH, AL, bias, B);
+                const float d = chunk_dot_f32<BITS>(cd[t], A);
                 uint32_t s_, m_;
                 if (QSC) {
                     const uint32_t v2 = sv[t & ~1];
@@ -605,28 +559,32 @@ __device__ __forceinline__ void down_rows(const Layer& L, const float* meta,
 }
 
 // ===========================================================================
-// Kernel 2 for the Qwen3-30B-A3B shape (I = 768, k <= 8, launched for 4-bit
-// codes; 3- and 2-bit measure faster on k_down), weighted sum: one wave
-// computes RPW whole output rows over all k experts. Lane l takes the (expert,
-// chunk) pairs l, l + 64 and l + 128 of a row's k x 24 pairs, so all 64 lanes
-// work, each lane keeps its three activation chunks in registers for the wave's
-// rows, and a row total is one in-register reduction (DPP within 16-lane rows,
-// then the four rows) -- no exchange between waves, and every wave stores its
-// own rows as soon as they are done. Sum order: the three pairs of a lane, then
-// the lanes; the k expert weights are applied per pair.
-// The activations of all k experts are staged in LDS once per workgroup.
+// Kernel 2 for the Qwen3-30B-A3B shape (I = 768, k <= 8, 4-bit codes; 3- and
+// 2-bit use k_down), weighted sum: one wave computes RPW whole output rows over
+// all k experts. Lane l takes the (expert, chunk) pairs l, l + 64 and l + 128 of
+// a row's k x 24 pairs, so all 64 lanes work, each lane keeps its three
+// activation chunks (32 fp32 values each) in registers for the wave's rows, and
+// a row total is one in-register reduction (DPP within 16-lane rows, then the
+// four rows) -- no exchange between waves, and every wave stores its own rows
+// as soon as they are done. Sum order: the three pairs of a lane, then the
+// lanes; the k expert weights are applied per pair. The fp32 activations of all
+// k experts (24 KB) are staged in LDS once per workgroup. No Layer argument:
+// every argument arrives preloaded in SGPRs. The output dtype ODT is a template
+// argument: a branch on it between the rows would make the compiler wait for the
+// first row's store before the second row's arithmetic.
 // ===========================================================================
-template <int BITS, int RPW, int NWV>
+template <int RPW, int NWV, int ODT>
 __global__ __launch_bounds__(64 * NWV) void k_down_rows(const float* meta, const uint8_t* __restrict__ pool,
                                                         int64_t slot_bytes, int nslots, int k,
-                                                        const uint32_t* __restrict__ act, void* __restrict__ out,
-                                                        const Layer L0) {
+                                                        const float* __restrict__ act, void* __restrict__ out) {
+    constexpr int BITS = 4;
     constexpr int SEG = kC2I / 32, NC = 3, ROWB = kC2I * BITS / 8;
     constexpr int64_t NMB = (int64_t)kC2H * kC2I * BITS / 8;
     constexpr int NGM = kC2H * kC2I / kC2G, GPR = kC2I / kC2G;
     constexpr int ROWS_WG = RPW * NWV, NB = kC2H / ROWS_WG;
     constexpr bool QS = (RPW % 2) == 0;
-    __shared__ uint4 stage[8 * SEG * 9];  // per (expert, chunk): 8 uint4 of hi|lo pairs + 1 pad
+    constexpr int CW = 9;  // uint4 per (expert, chunk): 8 of values + 1 pad
+    __shared__ uint4 stage[8 * SEG * CW];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int rb = blockIdx.x;
@@ -693,34 +651,31 @@ __global__ __launch_bounds__(64 * NWV) void k_down_rows(const float* meta, const
         // compiler cannot fold the load and this store into a copy placed here
         const int idx = min((int)threadIdx.x + i * 64 * NWV, na - 1);
         const uint4 a = ap[i];
-        stage[(idx >> 3) * 9 + (idx & 7)] = make_uint4(a.z, a.w, a.x, a.y);
+        stage[(idx >> 3) * CW + (idx & 7)] = make_uint4(a.z, a.w, a.x, a.y);
     }
     __syncthreads();
-    uint32_t AH[NC][16], AL[NC][16];
-    float as[NC], bias[NC];
+    float A[NC][32];
+    float as[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const int e = on[c] ? ec[c] : 0;
-        const uint4* q = stage + (e * SEG + sg[c]) * 9;
+        const uint4* q = stage + (e * SEG + sg[c]) * CW;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint4 h = q[i], l = q[4 + i];  // halves swapped in the stage
-            AH[c][4 * i] = h.z; AH[c][4 * i + 1] = h.w; AH[c][4 * i + 2] = h.x; AH[c][4 * i + 3] = h.y;
-            AL[c][4 * i] = l.z; AL[c][4 * i + 1] = l.w; AL[c][4 * i + 2] = l.x; AL[c][4 * i + 3] = l.y;
+        for (int i = 0; i < 8; ++i) {
+            const uint4 v = q[i];  // halves swapped in the stage
+            A[c][4 * i] = __uint_as_float(v.z); A[c][4 * i + 1] = __uint_as_float(v.w);
+            A[c][4 * i + 2] = __uint_as_float(v.x); A[c][4 * i + 3] = __uint_as_float(v.y);
         }
-        float vh, th, vl, tl;
-        operand_sums<BITS>(AH[c], vh, th);
-        operand_sums<BITS>(AL[c], vl, tl);
-        as[c] = th + tl;
-        bias[c] = -kBiasF * (vh + vl);
+        as[c] = chunk_sum_f32(A[c]);
     }
-    const uint32_t B = bias_vgpr();
+    // everything above uses the staged activation only: keep it ahead of every wait for the codes
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < RPW; ++t) {
         float p = 0.f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            const float d = chunk_dot_hl<BITS>(cd[t][c], AH[c], AL[c], bias[c], B);
+            const float d = chunk_dot_f32<BITS>(cd[t][c], A[c]);
             uint32_t s_, m_;
             if constexpr (QS) {
                 const uint32_t v2 = sv[t / 2][c];
@@ -742,21 +697,20 @@ __global__ __launch_bounds__(64 * NWV) void k_down_rows(const float* meta, const
                           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 16)) +
                           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 32)) +
                           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 48));
-        if (lane == 0) store_out(out, L0.odt, h0 + t, tot);
+        if (lane == 0) store_out(out, ODT, h0 + t, tot);
     }
 }
 
 // Kernel 2 (fast path), two-kernel form.
 // grid = ceil(H / (T*RPI)), block = 64*k, dynamic LDS as for down_rows.
-template <int BITS, int SPR_T, int T, bool WSUM, bool QSC, bool C2>
+template <int BITS, int SPR_T, int T, bool WSUM, bool QSC>
 // The leading scalar arguments are preloaded into SGPRs at dispatch, as for
 // k_gate_up.
 __global__ __launch_bounds__(1024) void k_down(const float* meta, const uint8_t* __restrict__ pool,
                                                int64_t slot_bytes, int nslots, int k, int I,
-                                               const uint32_t* __restrict__ act, void* __restrict__ out,
-                                               float* __restrict__ y, const Layer L0) {
+                                               const float* __restrict__ act, void* __restrict__ out,
+                                               float* __restrict__ y, const Layer L) {
     extern __shared__ float lds[];
-    const Layer L = layer_of<BITS, C2>(L0, pool, meta, slot_bytes, nslots);
     const int RW = T * (64 / (SPR_T ? SPR_T : L.spr_dn));
     // XCD-aware row blocks: the dispatcher deals workgroups to the 8 XCDs in turn, so
     // workgroup b runs on XCD b % 8; give each XCD one contiguous range of row blocks,
@@ -768,11 +722,28 @@ __global__ __launch_bounds__(1024) void k_down(const float* meta, const uint8_t*
     down_rows<BITS, SPR_T, T, WSUM, QSC>(L, meta, pool, slot_bytes, nslots, k, I, act, out, y, rb * RW, lds);
 }
 
+// Kernel 2 at the Qwen3-30B-A3B shape (3- and 2-bit codes, per-expert y, k <= 16): k_down's body with the
+// shape fields compile-time constants and no Layer argument; odt is the output dtype of the weighted sum.
+template <int BITS, int T, bool WSUM, bool QSC>
+__global__ __launch_bounds__(1024) void k_down_c2(const float* meta, const uint8_t* __restrict__ pool,
+                                                  int64_t slot_bytes, int nslots, int k,
+                                                  const float* __restrict__ act, void* __restrict__ out,
+                                                  float* __restrict__ y, int odt) {
+    extern __shared__ float lds[];
+    Layer L = layer_c2<BITS>(pool, meta, slot_bytes, nslots);
+    L.odt = odt;
+    constexpr int RW = T * (64 / (kC2I / 32));
+    constexpr int NBLK = (kC2H + RW - 1) / RW;
+    int rb = blockIdx.x;
+    if ((NBLK & 7) == 0) rb = (rb & 7) * (NBLK >> 3) + (rb >> 3);
+    down_rows<BITS, kC2I / 32, T, WSUM, QSC>(L, meta, pool, slot_bytes, nslots, k, kC2I, act, out, y, rb * RW, lds);
+}
+
 // Kernel 2 (generic): any I, G and k; one workgroup of min(k, 16) waves per
 // output row, wave w takes experts w, w + 16, ...; the k expert sums meet in
 // LDS (dynamic, k floats) and are combined in expert order.
 template <int BITS, bool WSUM>
-__global__ __launch_bounds__(1024) void k_down_generic(const Layer L, const uint32_t* __restrict__ act,
+__global__ __launch_bounds__(1024) void k_down_generic(const Layer L, const float* __restrict__ act,
                                                        void* __restrict__ out, float* __restrict__ y) {
     extern __shared__ float rows[];
     const int lane = threadIdx.x & 63;
@@ -786,14 +757,18 @@ __global__ __launch_bounds__(1024) void k_down_generic(const Layer L, const uint
             const uint8_t* base = L.pool + (int64_t)slot * L.slot_bytes;
             const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + 3 * L.nmb) + 2 * L.NGM;
             const uint16_t* mn = sc + 3 * L.NGM;
-            const uint32_t B = bias_vgpr();
             for (int c = lane; c < L.spr_dn; c += 64) {
-                uint32_t cd[BITS], AH[16], AL[16];
+                uint32_t cd[BITS];
+                float A[32];
                 load_chunk<BITS>(base + 2 * L.nmb + (int64_t)h * L.rowb_dn + c * (4 * BITS), cd);
-                float vs, as;
-                load_act_operand<BITS>(act, j, L.I, c, AH, AL, vs, as);
+                const float4* ap = reinterpret_cast<const float4*>(act + (int64_t)j * L.I + c * 32);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float4 q = ap[i];
+                    A[4 * i] = q.x; A[4 * i + 1] = q.y; A[4 * i + 2] = q.z; A[4 * i + 3] = q.w;
+                }
                 const int gidx = h * L.gpr_dn + (c * 32) / L.G;
-                v += h2f(sc[gidx]) * chunk_dot_hl<BITS>(cd, AH, AL, -kBiasF * vs, B) + h2f(mn[gidx]) * as;
+                v += h2f(sc[gidx]) * chunk_dot_f32<BITS>(cd, A) + h2f(mn[gidx]) * chunk_sum_f32(A);
             }
             v = wave_sum(v);
         } else {
@@ -815,17 +790,10 @@ __global__ __launch_bounds__(1024) void k_down_generic(const Layer L, const uint
     }
 }
 
-// Workspace decode: a[j, r] = (hi + lo) * 2^e
-template <int BITS>
-__global__ void k_act_read(const uint32_t* __restrict__ act, int k, int I, float* __restrict__ a) {
+// Workspace decode: the fp32 activation, copied
+__global__ void k_act_read(const float* __restrict__ act, int64_t n, float* __restrict__ a) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)k * I) return;
-    const int j = (int)(i / I), r = (int)(i - (int64_t)j * I);
-    const int info = pair_slot<BITS>(r & 31);
-    const int P = info & 15, half = (info >> 4) & 1, e = info >> 5;
-    const uint16_t* a16 = reinterpret_cast<const uint16_t*>(act + ((int64_t)j * (I >> 5) + (r >> 5)) * 32);
-    const float v = bf16_to_f32(a16[2 * P + half]) + bf16_to_f32(a16[2 * (16 + P) + half]);
-    a[i] = v * (float)(1 << e);
+    if (i < n) a[i] = act[i];
 }
 
 // ---------------------------------------------------------------------------
@@ -876,20 +844,20 @@ static bool valid_dtype(int dt) { return dt == WISP_DT_BF16 || dt == WISP_DT_F16
 static bool is_c2(const Layer& L) { return L.H == kC2H && L.I == kC2I && L.G == kC2G; }
 
 template <int BITS, int SPR, int T, int NW, bool QSC, int XT>
-static void launch_gu(const Layer& L, const void* x, uint32_t* act, hipStream_t st) {
+static void launch_gu(const Layer& L, const void* x, float* act, hipStream_t st) {
     const int RPI = 64 / L.spr_gu;
     const int rows_wg = NW * T * RPI;
     const dim3 grid((L.I + rows_wg - 1) / rows_wg, L.k);
     if (SPR == 64 && is_c2(L))
-        hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW, QSC, XT, true>), grid, dim3(64 * NW), 0, st, L.meta, L.pool,
-                           L.slot_bytes, L.nslots, x, act, L);
+        hipLaunchKernelGGL((k_gate_up_c2<BITS, T, NW, QSC, XT>), grid, dim3(64 * NW), 0, st, L.meta, L.pool,
+                           L.slot_bytes, L.nslots, x, act);
     else
-        hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW, QSC, XT, false>), grid, dim3(64 * NW), 0, st, L.meta,
-                           L.pool, L.slot_bytes, L.nslots, x, act, L);
+        hipLaunchKernelGGL((k_gate_up<BITS, SPR, T, NW, QSC, XT>), grid, dim3(64 * NW), 0, st, L.meta, L.pool,
+                           L.slot_bytes, L.nslots, x, act, L);
 }
 
 template <int BITS, int XT>
-static int gate_up_bits(const Layer& L, const void* x, uint32_t* act, hipStream_t st) {
+static int gate_up_bits(const Layer& L, const void* x, float* act, hipStream_t st) {
     if (L.spr_gu > 64 || L.gsh < 0) {
         hipLaunchKernelGGL((k_gate_up_generic<BITS, XT>), dim3(L.I, L.k), dim3(64), 0, st, L, x, act);
         return check_launch("k_gate_up_generic");
@@ -929,22 +897,22 @@ static size_t dn_lds_bytes(const Layer& L, int T) {
 }
 
 template <int BITS, int SPR, int T, bool WSUM, bool QSC>
-static void launch_dn(const Layer& L, const uint32_t* act, void* out, float* y, hipStream_t st) {
+static void launch_dn(const Layer& L, const float* act, void* out, float* y, hipStream_t st) {
     const int RW = T * (64 / L.spr_dn);
     const size_t lds = dn_lds_bytes(L, T);
     const dim3 grid((L.H + RW - 1) / RW), block(64 * L.k);
     if (SPR == 24 && is_c2(L))
-        hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM, QSC, true>), grid, block, lds, st, L.meta, L.pool,
-                           L.slot_bytes, L.nslots, L.k, L.I, act, out, y, L);
+        hipLaunchKernelGGL((k_down_c2<BITS, T, WSUM, QSC>), grid, block, lds, st, L.meta, L.pool, L.slot_bytes,
+                           L.nslots, L.k, act, out, y, L.odt);
     else
-        hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM, QSC, false>), grid, block, lds, st, L.meta, L.pool,
-                           L.slot_bytes, L.nslots, L.k, L.I, act, out, y, L);
+        hipLaunchKernelGGL((k_down<BITS, SPR, T, WSUM, QSC>), grid, block, lds, st, L.meta, L.pool, L.slot_bytes,
+                           L.nslots, L.k, L.I, act, out, y, L);
 }
 
 template <int BITS, bool WSUM>
-static int down_bits(const Layer& L, const uint32_t* act, void* out, float* y, hipStream_t st) {
+static int down_bits(const Layer& L, const float* act, void* out, float* y, hipStream_t st) {
     // the fast path has one wave per expert (k <= 16) and stages k*I activation
-    // dwords in LDS: keep the whole LDS within 64 KB
+    // values in LDS: keep the whole LDS within 64 KB
     const bool tuned = L.spr_dn == 24 && L.gsh >= 2;
     if (L.k > 16 || L.spr_dn > 64 || L.gsh < 0 || dn_lds_bytes(L, tuned ? tuning().dn_iters : 4) > 65536) {
         const int nw = L.k < 16 ? L.k : 16;
@@ -963,8 +931,16 @@ static int down_bits(const Layer& L, const uint32_t* act, void* out, float* y, h
         if constexpr (BITS == 4) {  // 3- and 2-bit codes measure faster on the per-expert waves
             if (WSUM && is_c2(L) && L.k <= 8) {  // the default tuning of the C2 shape
                 constexpr int RPW = 2, NWV = 4;
-                hipLaunchKernelGGL((k_down_rows<BITS, RPW, NWV>), dim3(kC2H / (RPW * NWV)), dim3(64 * NWV), 0, st,
-                                   L.meta, L.pool, L.slot_bytes, L.nslots, L.k, act, out, L);
+                const dim3 grid(kC2H / (RPW * NWV)), block(64 * NWV);
+                if (L.odt == WISP_DT_F32)
+                    hipLaunchKernelGGL((k_down_rows<RPW, NWV, WISP_DT_F32>), grid, block, 0, st, L.meta, L.pool,
+                                       L.slot_bytes, L.nslots, L.k, act, out);
+                else if (L.odt == WISP_DT_F16)
+                    hipLaunchKernelGGL((k_down_rows<RPW, NWV, WISP_DT_F16>), grid, block, 0, st, L.meta, L.pool,
+                                       L.slot_bytes, L.nslots, L.k, act, out);
+                else
+                    hipLaunchKernelGGL((k_down_rows<RPW, NWV, WISP_DT_BF16>), grid, block, 0, st, L.meta, L.pool,
+                                       L.slot_bytes, L.nslots, L.k, act, out);
                 return check_launch("k_down_rows");
             }
         }
@@ -977,7 +953,7 @@ static int down_bits(const Layer& L, const uint32_t* act, void* out, float* y, h
 }
 
 template <int XT>
-static int gate_up_xt(const Layer& L, int bits, const void* x, uint32_t* act, hipStream_t st) {
+static int gate_up_xt(const Layer& L, int bits, const void* x, float* act, hipStream_t st) {
     switch (bits) {
     case 4: return gate_up_bits<4, XT>(L, x, act, st);
     case 3: return gate_up_bits<3, XT>(L, x, act, st);
@@ -986,7 +962,7 @@ static int gate_up_xt(const Layer& L, int bits, const void* x, uint32_t* act, hi
 }
 
 // kernel 1 of a validated layer
-static int gate_up_launch(const Layer& L, int bits, const void* x, int x_dtype, uint32_t* act, hipStream_t st) {
+static int gate_up_launch(const Layer& L, int bits, const void* x, int x_dtype, float* act, hipStream_t st) {
     switch (x_dtype) {
     case WISP_DT_F16: return gate_up_xt<WISP_DT_F16>(L, bits, x, act, st);
     case WISP_DT_F32: return gate_up_xt<WISP_DT_F32>(L, bits, x, act, st);
@@ -995,7 +971,7 @@ static int gate_up_launch(const Layer& L, int bits, const void* x, int x_dtype, 
 }
 
 // kernel 2 of a validated layer: weighted sum into out (L.odt) when out, else per-expert y
-static int down_launch(const Layer& L, int bits, const uint32_t* act, void* out, float* y, hipStream_t st) {
+static int down_launch(const Layer& L, int bits, const float* act, void* out, float* y, hipStream_t st) {
     if (out) {
         switch (bits) {
         case 4: return down_bits<4, true>(L, act, out, nullptr, st);
@@ -1093,7 +1069,7 @@ extern "C" int wisp_moe_gate_up(const uint8_t* pool, int64_t slot_bytes, int64_t
     if (!rc) rc = check_x(x, x_dtype);
     if (!rc) rc = check_act(act);
     if (rc) return rc;
-    return gate_up_launch(L, bits, x, x_dtype, act, (hipStream_t)stream);
+    return gate_up_launch(L, bits, x, x_dtype, reinterpret_cast<float*>(act), (hipStream_t)stream);
 }
 
 extern "C" int wisp_moe_down_sum(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
@@ -1107,7 +1083,7 @@ extern "C" int wisp_moe_down_sum(const uint8_t* pool, int64_t slot_bytes, int64_
     if (!out) return fail_inval("null out");
     if (!valid_dtype(out_dtype)) return fail_inval("out_dtype must be WISP_DT_BF16, WISP_DT_F16 or WISP_DT_F32");
     L.odt = out_dtype;
-    return down_launch(L, bits, act, out, nullptr, (hipStream_t)stream);
+    return down_launch(L, bits, reinterpret_cast<const float*>(act), out, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int wisp_moe_down(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
@@ -1119,7 +1095,7 @@ extern "C" int wisp_moe_down(const uint8_t* pool, int64_t slot_bytes, int64_t ns
     if (!rc) rc = check_act(act);
     if (rc) return rc;
     if (!y) return fail_inval("null y");
-    return down_launch(L, bits, act, nullptr, y, (hipStream_t)stream);
+    return down_launch(L, bits, reinterpret_cast<const float*>(act), nullptr, y, (hipStream_t)stream);
 }
 
 extern "C" int wisp_moe_decode(const uint8_t* pool, int64_t slot_bytes, int64_t nslots, const float* meta, int k,
@@ -1148,24 +1124,20 @@ extern "C" int wisp_moe_decode_noalloc(const uint8_t* pool, int64_t slot_bytes, 
     if (rc) return rc;
     // kernel 1 writes every activation value kernel 2 reads: nothing in the
     // scratch has to start at zero
-    rc = gate_up_launch(L, bits, x, x_dtype, act, st);
+    rc = gate_up_launch(L, bits, x, x_dtype, reinterpret_cast<float*>(act), st);
     if (rc) return rc;
     L.odt = out_dtype;
-    return down_launch(L, bits, act, out, nullptr, st);
+    return down_launch(L, bits, reinterpret_cast<const float*>(act), out, nullptr, st);
 }
 
 extern "C" int wisp_act_read(const uint32_t* act, int k, int64_t I, int bits, float* a, void* stream) {
     clear_error();
     if (!act || !a) return fail_inval("null pointer");
     if (k < 1 || I <= 0 || I % 32) return fail_inval("k >= 1 and I a positive multiple of 32");
+    if (!(bits == 4 || bits == 3 || bits == 2)) return fail_inval("bits must be 4, 3 or 2");
     const int64_t total = (int64_t)k * I;
     const dim3 grid((unsigned)((total + 255) / 256));
-    hipStream_t st = (hipStream_t)stream;
-    switch (bits) {
-    case 4: hipLaunchKernelGGL(k_act_read<4>, grid, dim3(256), 0, st, act, k, (int)I, a); break;
-    case 3: hipLaunchKernelGGL(k_act_read<3>, grid, dim3(256), 0, st, act, k, (int)I, a); break;
-    case 2: hipLaunchKernelGGL(k_act_read<2>, grid, dim3(256), 0, st, act, k, (int)I, a); break;
-    default: return fail_inval("bits must be 4, 3 or 2");
-    }
+    hipLaunchKernelGGL(k_act_read, grid, dim3(256), 0, (hipStream_t)stream, reinterpret_cast<const float*>(act), total,
+                       a);
     return check_launch("k_act_read");
 }

@@ -9,8 +9,13 @@
 // the constant 128*sum(v) is removed by starting the accumulator at
 // -128*sum(v). Products of a <=15-bit integer with a bf16 are exact in fp32.
 // Which two codes share a pair, and the exponent e of each, is fixed per bit
-// width by PairMap<BITS> below; the operand vector (x for gate/up, the
-// activation for down) is stored pre-arranged in the same pair order.
+// width by PairMap<BITS> below; the operand (a bf16 x for gate/up) is arranged
+// in the same pair order.
+//
+// Second trick (fp32 operands: the activation of the down projection, a fp16
+// or fp32 x): a code masked in place inside a 16-bit half reads as the fp16
+// subnormal q * 2^(p-24), so one v_fma_mix_f32 multiplies it by a fp32 value
+// exactly (chunk_dot_f32 below).
 //
 // A "chunk" is 32 consecutive codes of one matrix row (BITS*4 bytes); the 16
 // pairs of a chunk are numbered P = 0..15.
@@ -73,35 +78,40 @@ __device__ __forceinline__ uint32_t alignbit(uint32_t hi, uint32_t lo, uint32_t 
 template <int BITS>
 struct PairMap;
 
-// 4-bit: dword d holds codes 8d..8d+7 (nibble i at bits 4i). Window w>>4p puts
-// codes 8d+p and 8d+p+4 at bits 0-3 and 16-19.
+// 4-bit: dword d holds codes 8d..8d+7 (nibble i at bits 4i). Window w >> (4p - 3) puts
+// codes 8d+p and 8d+p+4 at bits 3-6 and 19-22: the pair reads as (128 + 8q, 128 + 8q'),
+// so the bias 128 is 16 times the code's top value instead of 128 (the accumulator
+// cancels 3 bits less), with the operand stored times 2^-3 (exact).
 template <>
 struct PairMap<4> {
     static constexpr int lo(int P) { return 8 * (P >> 2) + (P & 3); }
     static constexpr int hi(int P) { return lo(P) + 4; }
-    static constexpr int elo(int) { return 0; }
-    static constexpr int ehi(int) { return 0; }
+    static constexpr int elo(int) { return 3; }
+    static constexpr int ehi(int) { return 3; }
 };
 
 // 3-bit: 32 codes in 96 bits (code c at bit 3c). Pairs (c, c+5) for
-// c in 0..4 and 10..14 with the low code at window bit 1 (e=1) and the high
-// code at bit 16 (e=0); pairs (c, c+6) for c in 20..25 with the low code at
-// bit 0 (e=0) and the high code at bit 18 (e=2).
+// c in 0..4 and 10..14 with the low code at window bits 4-6 (e=4) and the high
+// code at bits 19-21 (e=3); pairs (c, c+6) for c in 20..25 with the low code at
+// bits 2-4 (e=2) and the high code at bits 20-22 (e=4). The codes sit as high
+// in the mantissa as their spacing allows, so the bias 128 stays small against
+// 2^e * q.
 template <>
 struct PairMap<3> {
     static constexpr int lo(int P) { return P < 5 ? P : (P < 10 ? 10 + (P - 5) : 20 + (P - 10)); }
     static constexpr int hi(int P) { return P < 5 ? P + 5 : (P < 10 ? 15 + (P - 5) : 26 + (P - 10)); }
-    static constexpr int elo(int P) { return P < 10 ? 1 : 0; }
-    static constexpr int ehi(int P) { return P < 10 ? 0 : 2; }
+    static constexpr int elo(int P) { return P < 10 ? 4 : 2; }
+    static constexpr int ehi(int P) { return P < 10 ? 3 : 4; }
 };
 
-// 2-bit: dword d holds codes 16d..16d+15 (code i at bits 2i). Windows w, w>>6,
-// w>>12 each give up to three pairs (i, i+8) at mantissa bits 0, 2 and 4.
+// 2-bit: dword d holds codes 16d..16d+15 (code i at bits 2i). Window w >> (4m - 3)
+// puts codes 2m, 2m+1 at bits 3-4 and 5-6 and codes 2m+8, 2m+9 at bits 19-20 and
+// 21-22: pairs (i, i+8) at e = 3 (i even) or 5 (i odd).
 template <>
 struct PairMap<2> {
     static constexpr int lo(int P) { return 16 * (P >> 3) + (P & 7); }
     static constexpr int hi(int P) { return lo(P) + 8; }
-    static constexpr int elo(int P) { return 2 * ((P & 7) % 3); }
+    static constexpr int elo(int P) { return (P & 1) ? 5 : 3; }
     static constexpr int ehi(int P) { return elo(P); }
 };
 
@@ -111,85 +121,59 @@ __device__ __forceinline__ void code_pairs(const uint32_t* d, uint32_t* p, uint3
 
 template <>
 __device__ __forceinline__ void code_pairs<4>(const uint32_t* d, uint32_t* p, uint32_t B) {
-    constexpr uint32_t M = 0x000F000Fu;
+    constexpr uint32_t M = 0x00780078u;  // bits 3-6 of each half
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t w = d[i];
-        p[4 * i + 0] = ao(w, M, B);
-        p[4 * i + 1] = ao(w >> 4, M, B);
-        p[4 * i + 2] = ao(w >> 8, M, B);
-        p[4 * i + 3] = ao(w >> 12, M, B);
+        p[4 * i + 0] = ao(w << 3, M, B);
+        p[4 * i + 1] = ao(w >> 1, M, B);
+        p[4 * i + 2] = ao(w >> 5, M, B);
+        p[4 * i + 3] = ao(w >> 9, M, B);
     }
 }
 
 template <>
 __device__ __forceinline__ void code_pairs<3>(const uint32_t* d, uint32_t* p, uint32_t B) {
-    constexpr uint32_t MA = 0x0007000Eu;  // low code at bits 1-3, high code at bits 16-18
-    constexpr uint32_t MC = 0x001C0007u;  // low code at bits 0-2, high code at bits 18-20
+    constexpr uint32_t MA = 0x00380070u;  // low code at bits 4-6, high code at bits 19-21
+    constexpr uint32_t MC = 0x0070001Cu;  // low code at bits 2-4, high code at bits 20-22
     const uint32_t d0 = d[0], d1 = d[1], d2 = d[2];
-    // window start 3c-1 for c = 0..4
-    p[0] = ao(d0 << 1, MA, B);
-    p[1] = ao(alignbit(d1, d0, 2), MA, B);
-    p[2] = ao(alignbit(d1, d0, 5), MA, B);
-    p[3] = ao(alignbit(d1, d0, 8), MA, B);
-    p[4] = ao(alignbit(d1, d0, 11), MA, B);
-    // window start 3c-1 for c = 10..14
-    p[5] = ao(alignbit(d1, d0, 29), MA, B);
-    p[6] = ao(d1, MA, B);
-    p[7] = ao(alignbit(d2, d1, 3), MA, B);
-    p[8] = ao(alignbit(d2, d1, 6), MA, B);
-    p[9] = ao(alignbit(d2, d1, 9), MA, B);
-    // window start 3c for c = 20..25
-    p[10] = ao(alignbit(d2, d1, 28), MC, B);
-    p[11] = ao(alignbit(d2, d1, 31), MC, B);
-    p[12] = ao(d2 >> 2, MC, B);
-    p[13] = ao(d2 >> 5, MC, B);
-    p[14] = ao(d2 >> 8, MC, B);
-    p[15] = ao(d2 >> 11, MC, B);
+    // window start 3c-4 for c = 0..4
+    p[0] = ao(d0 << 4, MA, B);
+    p[1] = ao(d0 << 1, MA, B);
+    p[2] = ao(alignbit(d1, d0, 2), MA, B);
+    p[3] = ao(alignbit(d1, d0, 5), MA, B);
+    p[4] = ao(alignbit(d1, d0, 8), MA, B);
+    // window start 3c-4 for c = 10..14
+    p[5] = ao(alignbit(d1, d0, 26), MA, B);
+    p[6] = ao(alignbit(d1, d0, 29), MA, B);
+    p[7] = ao(d1, MA, B);
+    p[8] = ao(alignbit(d2, d1, 3), MA, B);
+    p[9] = ao(alignbit(d2, d1, 6), MA, B);
+    // window start 3c-2 for c = 20..25
+    p[10] = ao(alignbit(d2, d1, 26), MC, B);
+    p[11] = ao(alignbit(d2, d1, 29), MC, B);
+    p[12] = ao(d2, MC, B);
+    p[13] = ao(d2 >> 3, MC, B);
+    p[14] = ao(d2 >> 6, MC, B);
+    p[15] = ao(d2 >> 9, MC, B);
 }
 
 template <>
 __device__ __forceinline__ void code_pairs<2>(const uint32_t* d, uint32_t* p, uint32_t B) {
-    constexpr uint32_t M0 = 0x00030003u, M2 = 0x000C000Cu, M4 = 0x00300030u;
+    constexpr uint32_t M3 = 0x00180018u, M5 = 0x00600060u;  // bits 3-4 / 5-6 of each half
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const uint32_t w0 = d[i], w6 = d[i] >> 6, w12 = d[i] >> 12;
-        p[8 * i + 0] = ao(w0, M0, B);
-        p[8 * i + 1] = ao(w0, M2, B);
-        p[8 * i + 2] = ao(w0, M4, B);
-        p[8 * i + 3] = ao(w6, M0, B);
-        p[8 * i + 4] = ao(w6, M2, B);
-        p[8 * i + 5] = ao(w6, M4, B);
-        p[8 * i + 6] = ao(w12, M0, B);
-        p[8 * i + 7] = ao(w12, M2, B);
+        const uint32_t w = d[i];
+        const uint32_t w0 = w << 3, w1 = w >> 1, w2 = w >> 5, w3 = w >> 9;
+        p[8 * i + 0] = ao(w0, M3, B);
+        p[8 * i + 1] = ao(w0, M5, B);
+        p[8 * i + 2] = ao(w1, M3, B);
+        p[8 * i + 3] = ao(w1, M5, B);
+        p[8 * i + 4] = ao(w2, M3, B);
+        p[8 * i + 5] = ao(w2, M5, B);
+        p[8 * i + 6] = ao(w3, M3, B);
+        p[8 * i + 7] = ao(w3, M5, B);
     }
-}
-
-// Chunk-relative code index c (0..31) -> pair slot: P | half<<4 | e<<5
-// (closed forms of the inverse of PairMap<BITS>).
-template <int BITS>
-__device__ __forceinline__ int pair_slot(int c);
-template <>
-__device__ __forceinline__ int pair_slot<4>(int c) {
-    return (((c >> 3) << 2) | (c & 3)) | (((c >> 2) & 1) << 4);
-}
-template <>
-__device__ __forceinline__ int pair_slot<2>(int c) {
-    const int i = c & 7;
-    const int e = 2 * (i - 3 * ((i * 11) >> 5));  // 2*(i % 3) for i < 8
-    return ((c >> 4) << 3 | i) | (((c >> 3) & 1) << 4) | (e << 5);
-}
-template <>
-__device__ __forceinline__ int pair_slot<3>(int c) {
-    // c: 0-4 -> (c,lo,1) 5-9 -> (c-5,hi,0) 10-14 -> (c-5,lo,1) 15-19 -> (c-10,hi,0)
-    //    20-25 -> (c-10,lo,0) 26-31 -> (c-16,hi,2)
-    if (c < 20) {
-        const int blk = c / 5;  // 0..3
-        const int P = c - 5 * ((blk + 1) >> 1);
-        const int half = blk & 1;
-        return P | (half << 4) | ((half ? 0 : 1) << 5);
-    }
-    return c < 26 ? (c - 10) : ((c - 16) | (1 << 4) | (2 << 5));
 }
 
 // exact multiplication by 2^-e for the small e used here
@@ -302,6 +286,102 @@ __device__ __forceinline__ void dequant32_f32(const uint32_t* d, uint32_t sm, fl
     }
 }
 
+// Sum of q_i * a_i over one 32-code chunk (BITS dwords d, element i at bit BITS*i) against 32 fp32 values a[i]
+// in element order: exact products, fp32 accumulation (the fp32 q*a of the reference's down kernels,
+// kernels.py:107-111, 166-184). Each code is masked in place inside a 16-bit half, where it reads as the fp16
+// subnormal q * 2^(p-24) for its bit offset p in the half (p + BITS <= 10, so the exponent field stays zero),
+// and one v_fma_mix_f32 multiplies that half by a[i] exactly and adds in fp32. Codes at the same offset share
+// accumulators, which are scaled back by 2^(24-p) (exact) at the end. 13 VALU instructions per 8 codes at 4 bits.
+template <int BITS>
+__device__ __forceinline__ float chunk_dot_f32(const uint32_t* d, const float* a);
+
+template <>
+__device__ __forceinline__ float chunk_dot_f32<4>(const uint32_t* d, const float* a) {
+    // dword w: nibbles 0/4 at p = 0 of the two halves, 1/5 at p = 4; after >> 8: 2/6 at p = 0, 3/7 at p = 4
+    float s0a = 0.f, s0b = 0.f, s4a = 0.f, s4b = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t x = d[w], y = x >> 8;
+        const uint32_t c0 = x & 0x000F000Fu, c1 = x & 0x00F000F0u, c2 = y & 0x000F000Fu, c3 = y & 0x00F000F0u;
+        const float* v = a + 8 * w;
+        s0a = __builtin_fmaf(half_lo_f(c0), v[0], s0a);
+        s0b = __builtin_fmaf(half_hi_f(c0), v[4], s0b);
+        s4a = __builtin_fmaf(half_lo_f(c1), v[1], s4a);
+        s4b = __builtin_fmaf(half_hi_f(c1), v[5], s4b);
+        s0a = __builtin_fmaf(half_lo_f(c2), v[2], s0a);
+        s0b = __builtin_fmaf(half_hi_f(c2), v[6], s0b);
+        s4a = __builtin_fmaf(half_lo_f(c3), v[3], s4a);
+        s4b = __builtin_fmaf(half_hi_f(c3), v[7], s4b);
+    }
+    return (s0a + s0b) * 0x1p24f + (s4a + s4b) * 0x1p20f;
+}
+
+template <>
+__device__ __forceinline__ float chunk_dot_f32<2>(const uint32_t* d, const float* a) {
+    // dword w holds codes 16w .. 16w + 15; mask 3 << 2k takes code k (low half) and 8 + k (high half) of x, and
+    // codes 4 + k and 12 + k of x >> 8, all at p = 2k
+    float s[4][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        const uint32_t x = d[w], y = x >> 8;
+        const float* v = a + 16 * w;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t M = 0x00030003u << (2 * k);
+            const uint32_t cx = x & M, cy = y & M;
+            s[k][0] = __builtin_fmaf(half_lo_f(cx), v[k], s[k][0]);
+            s[k][1] = __builtin_fmaf(half_hi_f(cx), v[8 + k], s[k][1]);
+            s[k][0] = __builtin_fmaf(half_lo_f(cy), v[4 + k], s[k][0]);
+            s[k][1] = __builtin_fmaf(half_hi_f(cy), v[12 + k], s[k][1]);
+        }
+    }
+    return ((s[0][0] + s[0][1]) * 0x1p24f + (s[1][0] + s[1][1]) * 0x1p22f) +
+           ((s[2][0] + s[2][1]) * 0x1p20f + (s[3][0] + s[3][1]) * 0x1p18f);
+}
+
+template <>
+__device__ __forceinline__ float chunk_dot_f32<3>(const uint32_t* d, const float* a) {
+    // 24-bit windows, masked without the bias: window P holds code PairMap<3>::lo(P) in the low half and code
+    // PairMap<3>::hi(P) in the high half at the offsets below (0, 1 or 2; fp16 subnormals need p + 3 <= 10)
+    constexpr uint32_t MA = 0x0007000Eu, MC = 0x001C0007u;  // (c, c+5): p = 1 / 0; (c, c+6): p = 0 / 2
+    const uint32_t d0 = d[0], d1 = d[1], d2 = d[2];
+    const uint32_t w[16] = {(d0 << 1) & MA,
+                            alignbit(d1, d0, 2) & MA,
+                            alignbit(d1, d0, 5) & MA,
+                            alignbit(d1, d0, 8) & MA,
+                            alignbit(d1, d0, 11) & MA,
+                            alignbit(d1, d0, 29) & MA,
+                            d1 & MA,
+                            alignbit(d2, d1, 3) & MA,
+                            alignbit(d2, d1, 6) & MA,
+                            alignbit(d2, d1, 9) & MA,
+                            alignbit(d2, d1, 28) & MC,
+                            alignbit(d2, d1, 31) & MC,
+                            (d2 >> 2) & MC,
+                            (d2 >> 5) & MC,
+                            (d2 >> 8) & MC,
+                            (d2 >> 11) & MC};
+    float s[3][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};  // by offset p, two chains each
+#pragma unroll
+    for (int P = 0; P < 16; ++P) {
+        const int pl = P < 10 ? 1 : 0, ph = P < 10 ? 0 : 2;
+        s[pl][P & 1] = __builtin_fmaf(half_lo_f(w[P]), a[PairMap<3>::lo(P)], s[pl][P & 1]);
+        s[ph][(P + 1) & 1] = __builtin_fmaf(half_hi_f(w[P]), a[PairMap<3>::hi(P)], s[ph][(P + 1) & 1]);
+    }
+    return ((s[0][0] + s[0][1]) * 0x1p24f + (s[1][0] + s[1][1]) * 0x1p23f) + (s[2][0] + s[2][1]) * 0x1p22f;
+}
+
+// Sum of the 32 fp32 values of one chunk, two chains (pairs of elements) then combined.
+__device__ __forceinline__ float chunk_sum_f32(const float* a) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) {
+        s0 += a[i];
+        s1 += a[i + 1];
+    }
+    return s0 + s1;
+}
+
 // dequant32_f32 rounded to bf16 (RTNE), as 16 pairs in element order.
 template <int BITS>
 __device__ __forceinline__ void dequant32(const uint32_t* d, uint32_t sm, uint32_t* out) {
@@ -352,7 +432,7 @@ __device__ __forceinline__ void operand_sums(const uint32_t* pr, float& vsum, fl
     }
     vsum = a0 + a1;
     if (BITS == 4) {
-        tsum = vsum;
+        tsum = vsum * 8.0f;  // every 4-bit operand is stored times 2^-3 (exact scalings)
     } else {
         float b0 = 0.f, b1 = 0.f;
 #pragma unroll
