@@ -559,25 +559,25 @@ __device__ __forceinline__ void down_rows(const Layer& L, const float* meta,
 }
 
 // ===========================================================================
-// Kernel 2 for the Qwen3-30B-A3B shape (I = 768, k <= 8, 4-bit codes; 3- and
-// 2-bit use k_down), weighted sum: one wave computes RPW whole output rows over
-// all k experts. Lane l takes the (expert, chunk) pairs l, l + 64 and l + 128 of
-// a row's k x 24 pairs, so all 64 lanes work, each lane keeps its three
-// activation chunks (32 fp32 values each) in registers for the wave's rows, and
-// a row total is one in-register reduction (DPP within 16-lane rows, then the
-// four rows) -- no exchange between waves, and every wave stores its own rows
-// as soon as they are done. Sum order: the three pairs of a lane, then the
-// lanes; the k expert weights are applied per pair. The fp32 activations of all
-// k experts (24 KB) are staged in LDS once per workgroup. No Layer argument:
+// Kernel 2 for the Qwen3-30B-A3B shape (I = 768, k <= 8, 4/3/2-bit codes),
+// weighted sum: one wave computes RPW whole output rows over all k experts.
+// Lane l takes the (expert, chunk) pairs l, l + 64 and l + 128 of a row's
+// k x 24 pairs, so all 64 lanes work, each lane keeps its three activation
+// chunks (32 fp32 values each) in registers for the wave's rows, and a row
+// total is one in-register reduction (DPP within 16-lane rows, then the four
+// rows) -- no exchange between waves, and every wave stores its own rows as
+// soon as they are done. Sum order: the three pairs of a lane, then the lanes;
+// the k expert weights are applied per pair. The fp32 activations of all k
+// experts (24 KB) are staged in LDS once per workgroup. No Layer argument:
 // every argument arrives preloaded in SGPRs. The output dtype ODT is a template
 // argument: a branch on it between the rows would make the compiler wait for the
-// first row's store before the second row's arithmetic.
+// first row's store before the second row's arithmetic. Default launch: one row
+// per wave, 4 waves per workgroup, 512 workgroups (two waves per SIMD).
 // ===========================================================================
-template <int RPW, int NWV, int ODT>
+template <int BITS, int RPW, int NWV, int ODT>
 __global__ __launch_bounds__(64 * NWV) void k_down_rows(const float* meta, const uint8_t* __restrict__ pool,
                                                         int64_t slot_bytes, int nslots, int k,
                                                         const float* __restrict__ act, void* __restrict__ out) {
-    constexpr int BITS = 4;
     constexpr int SEG = kC2I / 32, NC = 3, ROWB = kC2I * BITS / 8;
     constexpr int64_t NMB = (int64_t)kC2H * kC2I * BITS / 8;
     constexpr int NGM = kC2H * kC2I / kC2G, GPR = kC2I / kC2G;
@@ -928,21 +928,19 @@ static int down_bits(const Layer& L, const float* act, void* out, float* y, hipS
     case 1: launch_dn<BITS, 24, 1, WSUM, false>(L, act, out, y, st); break;
     case 2: launch_dn<BITS, 24, 2, WSUM, (bool)WISP_QSC>(L, act, out, y, st); break;
     case 4:
-        if constexpr (BITS == 4) {  // 3- and 2-bit codes measure faster on the per-expert waves
-            if (WSUM && is_c2(L) && L.k <= 8) {  // the default tuning of the C2 shape
-                constexpr int RPW = 2, NWV = 4;
-                const dim3 grid(kC2H / (RPW * NWV)), block(64 * NWV);
-                if (L.odt == WISP_DT_F32)
-                    hipLaunchKernelGGL((k_down_rows<RPW, NWV, WISP_DT_F32>), grid, block, 0, st, L.meta, L.pool,
-                                       L.slot_bytes, L.nslots, L.k, act, out);
-                else if (L.odt == WISP_DT_F16)
-                    hipLaunchKernelGGL((k_down_rows<RPW, NWV, WISP_DT_F16>), grid, block, 0, st, L.meta, L.pool,
-                                       L.slot_bytes, L.nslots, L.k, act, out);
-                else
-                    hipLaunchKernelGGL((k_down_rows<RPW, NWV, WISP_DT_BF16>), grid, block, 0, st, L.meta, L.pool,
-                                       L.slot_bytes, L.nslots, L.k, act, out);
-                return check_launch("k_down_rows");
-            }
+        if (WSUM && is_c2(L) && L.k <= 8) {  // the default tuning of the C2 shape: the row kernel
+            constexpr int RPW = 1, NWV = 4;
+            const dim3 grid(kC2H / (RPW * NWV)), block(64 * NWV);
+            if (L.odt == WISP_DT_F32)
+                hipLaunchKernelGGL((k_down_rows<BITS, RPW, NWV, WISP_DT_F32>), grid, block, 0, st, L.meta, L.pool,
+                                   L.slot_bytes, L.nslots, L.k, act, out);
+            else if (L.odt == WISP_DT_F16)
+                hipLaunchKernelGGL((k_down_rows<BITS, RPW, NWV, WISP_DT_F16>), grid, block, 0, st, L.meta, L.pool,
+                                   L.slot_bytes, L.nslots, L.k, act, out);
+            else
+                hipLaunchKernelGGL((k_down_rows<BITS, RPW, NWV, WISP_DT_BF16>), grid, block, 0, st, L.meta, L.pool,
+                                   L.slot_bytes, L.nslots, L.k, act, out);
+            return check_launch("k_down_rows");
         }
         launch_dn<BITS, 24, 4, WSUM, (bool)WISP_QSC>(L, act, out, y, st);
         break;
