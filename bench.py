@@ -83,6 +83,8 @@ class Layers:
         self.act = torch.empty((layers, K_TOP, I), dtype=torch.int32, device=dev)
         self.out = torch.empty((layers, H), dtype=torch.bfloat16, device=dev)
         self.stream = torch.cuda.Stream(dev)
+        self.stamps = torch.zeros(8, dtype=torch.int64, device=dev)
+        self.clock_hz = 1.0e8  # calibrated by setup_pass
         torch.cuda.synchronize()
         print(f"[bench] slot pool {self.pool.numel() / 2**30:.2f} GiB ({layers} layers x {E} experts)",
               file=sys.stderr, flush=True)
@@ -129,62 +131,108 @@ def upload_graph(g, stream) -> None:
         raise RuntimeError(f"hipGraphUpload failed ({rc})")
 
 
-def capture_steps(stream, body, first: int, count: int):
-    """Graphs that run steps first .. first+count-1 of `body` (each step's launches on the
-    graph's stream): [(graph, replays)], a CHUNK-step graph replayed count // CHUNK times and
-    a graph of the remainder, so exactly `count` steps run. Each graph is uploaded to the
-    device once captured."""
-    out = []
-    full, rest = divmod(count, CHUNK) if count > CHUNK else (0, count)
-    for n, reps in ((CHUNK, full), (rest, 1)):
-        if reps == 0 or n == 0:
-            continue
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(stream):
-            with torch.cuda.graph(g, stream=stream):
-                st = _lib.stream(stream.device)
-                for i in range(first, first + n):
-                    body(i, st)
-        if os.environ.get("WISP_BENCH_UPLOAD", "1") == "1":
-            upload_graph(g, stream)
-        out.append((g, reps))
+def _stamp(W, slot: int, st) -> None:
+    """Capture/launch the GPU clock stamp kernel writing W.stamps[slot] on stream st."""
+    _lib.check(_lib.lib().wisp_probe_stamp(_lib.ptr(W.stamps[slot]), st), "probe_stamp")
+
+
+def _capture(stream, fn):
+    """One graph of whatever fn(st) enqueues on the graph's stream, uploaded once captured."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            fn(_lib.stream(stream.device))
+    if os.environ.get("WISP_BENCH_UPLOAD", "1") == "1":
+        upload_graph(g, stream)
+    return g
+
+
+def stamped_run(W, body, warmup: int, steps: int):
+    """Seconds per step over exactly `steps` steps of `body` after `warmup` untimed ones.
+
+    The timed steps are bracketed by two GPU clock stamps (k_probe_stamp: s_memrealtime) captured in the same
+    graph as the warm-up steps that precede them, so the interval holds exactly the timed steps and none of a
+    graph launch's own latency (about 8 us per replay on MI355X, which HIP events around a replay include).
+    Runs longer than CHUNK steps continue in further graphs (each graph boundary inside the interval adds that
+    latency once per CHUNK steps). Also returns the HIP-event time of the whole replayed sequence."""
+    warm_chunks = [(i, min(CHUNK, warmup - i)) for i in range(0, max(warmup - 1, 0) // CHUNK * CHUNK, CHUNK)]
+    w_tail0 = sum(n for _, n in warm_chunks)
+    graphs = []
+    for i0, n in warm_chunks:
+        graphs.append(_capture(W.stream, lambda st, i0=i0, n=n: [body(i, st) for i in range(i0, i0 + n)]))
+    t0 = min(steps, CHUNK)
+
+    def first(st):
+        for i in range(w_tail0, warmup):
+            body(i, st)
+        _stamp(W, 0, st)
+        for i in range(warmup, warmup + t0):
+            body(i, st)
+        if t0 == steps:
+            _stamp(W, 1, st)
+
+    graphs.append(_capture(W.stream, first))
+    i = warmup + t0
+    while i < warmup + steps:
+        n = min(CHUNK, warmup + steps - i)
+        last = i + n == warmup + steps
+
+        def more(st, i0=i, n=n, last=last):
+            for k in range(i0, i0 + n):
+                body(k, st)
+            if last:
+                _stamp(W, 1, st)
+
+        graphs.append(_capture(W.stream, more))
+        i += n
     torch.cuda.synchronize()
-    return out
-
-
-def timed_steps(stream, warm, timed, steps: int):
-    """Seconds per step: the warm-up graphs, then HIP events on the replay stream around
-    exactly `steps` steps. A GPU sleep between the two keeps the host's submission of the
-    timed graphs out of the timed interval (the events bracket GPU work only)."""
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(W.stream):
+        torch.cuda._sleep(200_000)  # the host submits every replay before the GPU reaches them
+        e0.record(W.stream)
+        for g in graphs:
+            g.replay()
+        e1.record(W.stream)
     torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        for g, reps in warm:
-            for _ in range(reps):
-                g.replay()
-        torch.cuda._sleep(200_000)
-        e0.record(stream)
-        for g, reps in timed:
-            for _ in range(reps):
-                g.replay()
-        e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e-3 / steps
+    st = W.stamps.cpu()
+    ticks = int(st[1]) - int(st[0])
+    del graphs
+    return ticks / W.clock_hz / steps, e0.elapsed_time(e1) * 1e-3
 
 
 def setup_pass(W: Layers):
     """Set-up, not a step: one layer for every (pool, routing round) of the rotation, replayed
     from a graph, so module loading, the first graph launch of the process and the first
     touch of every expert page the steps will read happen before the warm-up steps -- the
-    state of a decoder that has been running."""
+    state of a decoder that has been running. The same graph, bracketed by GPU clock stamps
+    and HIP events, calibrates the stamps' clock rate (ticks per second)."""
     with torch.cuda.stream(W.stream):  # one eager layer loads the code, the rest runs as a graph replay
         W.layer(0, _lib.stream(W.dev))
     torch.cuda.synchronize()
-    for g, reps in capture_steps(W.stream, W.layer, 0, ROUNDS * W.layers):
+    n = ROUNDS * W.layers
+
+    def body(st):
+        _stamp(W, 0, st)
+        for i in range(n):
+            W.layer(i, st)
+        _stamp(W, 1, st)
+
+    g = _capture(W.stream, body)
+    torch.cuda.synchronize()
+    rates = []
+    for _ in range(2):  # the second replay calibrates (the first may carry first-launch costs)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(W.stream):
-            for _ in range(reps):
-                g.replay()
+            e0.record(W.stream)
+            g.replay()
+            e1.record(W.stream)
+        torch.cuda.synchronize()
+        st = W.stamps.cpu()
+        rates.append((int(st[1]) - int(st[0])) / (e0.elapsed_time(e1) * 1e-3))
+    W.clock_hz = rates[-1]
+    del g
     torch.cuda.synchronize()
 
 
@@ -204,20 +252,24 @@ def replay_seconds(stream, g, reps: int) -> float:
 
 def measure(W: Layers, steps: int, warmup: int):
     """Seconds per layer (both kernels) and per kernel alone over exactly `steps` steps after
-    `warmup` untimed ones: graph replays, HIP events on the replay stream."""
+    `warmup` untimed ones (stamped_run), plus kernel 1's time per launch from HIP events around a
+    graph of max(steps, CHUNK) kernel-1 launches (the roofline's time base)."""
     setup_pass(W)
-    res = dict(steps=steps, warmup=warmup)
+    res = dict(steps=steps, warmup=warmup, clock_hz=W.clock_hz)
     for name, body in (("layer", W.layer), ("gu", W.gate_up), ("dn", W.down)):
-        warm = capture_steps(W.stream, body, 0, warmup) if warmup else []
-        timed = capture_steps(W.stream, body, warmup, steps)
-        res[name] = timed_steps(W.stream, warm, timed, steps)
-        del warm, timed
+        res[name], res[name + "_events_s"] = stamped_run(W, body, warmup, steps)
+    n = max(steps, CHUNK)
+    g = _capture(W.stream, lambda st: [W.gate_up(i, st) for i in range(n)])
+    replay_seconds(W.stream, g, 1)  # untimed replay
+    res["gu_events"] = replay_seconds(W.stream, g, 1) / n
+    res["gu_events_launches"] = n
+    del g
     return res
 
 
 def run_floor(a) -> dict:
     """The floors of the C2 layer, measured the way the layer is (graph replays over the same
-    48-pool rotation, HIP events, exactly --steps launches per probe): an empty kernel; a
+    48-pool rotation, GPU clock stamps, exactly --steps launches per probe): an empty kernel; a
     plain streaming read of kernel 1's and of kernel 2's algorithmic bytes from the pool of
     step i; the same reads with the start address taken from a slot id in device memory
     (the dependent round trip the decode kernels pay first); and the C2 layer itself."""
@@ -259,13 +311,10 @@ def run_floor(a) -> dict:
             for i in range(4):
                 body(i, st)
         torch.cuda.synchronize()
-        warm = capture_steps(W.stream, body, 0, a.warmup) if a.warmup else []
-        timed = capture_steps(W.stream, body, a.warmup, a.steps)
-        t = timed_steps(W.stream, warm, timed, a.steps)
+        t, _ = stamped_run(W, body, a.warmup, a.steps)
         rows[name] = {"us_per_launch": round(t * 1e6, 3), "bytes": nbytes,
                       "GB_per_s": round(nbytes / t / 1e9, 1) if nbytes else None}
         print(f"[bench] floor {name}: {t * 1e6:.3f} us", file=sys.stderr, flush=True)
-        del warm, timed
     lay = rows["c2_layer"]["us_per_launch"] * 1e-6
     return {
         "metric": f"\u00b5s per launch of the C2 layer's floors ({a.bits}-bit), in-graph",
@@ -380,6 +429,20 @@ def trace_profile_name(bits: int) -> str:
     return os.path.join(PROFILES, f"moe_decode_c2_q{bits}_kernel_trace.md")
 
 
+def rocprof_from_profile(bits: int):
+    """(gate_up, down) average kernel durations in ns from the committed rocprofv3 kernel-trace summary of
+    this bit width, or (None, None)."""
+    path = trace_profile_name(bits)
+    out = {"gate_up": None, "down": None}
+    if os.path.exists(path):
+        with open(path) as f:
+            for line in f:
+                for k in out:
+                    if line.startswith(f"rocprof_avg_ns_{k}:"):
+                        out[k] = float(line.split(":")[1])
+    return out["gate_up"], out["down"]
+
+
 def summarize_trace(trace_csv: str, stats_csv: str, bits: int, cmd: str, bench_line: str) -> str:
     """Markdown summary of a rocprofv3 --kernel-trace --stats run of bench.py: the stats
     rows of the two decode kernels, and from the trace the start-to-start interval of
@@ -417,6 +480,10 @@ def summarize_trace(trace_csv: str, stats_csv: str, bits: int, cmd: str, bench_l
         avg = float(r["AverageNs"])
         lines.append(f"| `{r['Name']}` | {r['Calls']} | {avg:.0f} | {r['MinNs']} | {r['MaxNs']} | "
                      f"{float(r['StdDev']):.0f} | {alg} | {alg / avg:.0f} |")
+    lines.append("")
+    for r in stats:
+        k = short(r["Name"])
+        lines.append(f"rocprof_avg_ns_{'gate_up' if k == 'k_gate_up' else 'down'}: {float(r['AverageNs']):.0f}")
     lines.append("")
     lines.append("Start-to-start interval of consecutive launches of the same kernel (the single-kernel graph "
                  "replays, under the profiler):")
@@ -1081,21 +1148,34 @@ def main():
             "down_sum_us": round(m["dn"] * 1e6, 3),
             "gate_up_bytes": gu_b,
             "down_bytes": dn_b,
-            "timing": "HIP events on the replay stream around graph replays of exactly `steps` layer steps "
-                      "(pool i % 48, routing round i // 48 % 8) after `warmup` untimed ones and one set-up "
-                      "layer per pool and routing round; per-launch averages include the in-graph launch gaps",
+            "timing": "exactly `steps` steps (pool i % 48, routing round i // 48 % 8) after `warmup` untimed "
+                      "ones and one set-up layer per pool and routing round, all in graph replays on one stream; "
+                      "the timed steps are bracketed by two GPU clock stamps (s_memrealtime, clock rate "
+                      "calibrated against HIP events over the set-up graph) captured in the same graph as the "
+                      "warm-up steps, so the interval excludes a graph launch's own latency; per-launch times "
+                      "include the in-graph gap between consecutive kernels",
+            "clock_hz": round(m["clock_hz"]),
+            "hip_event_ms_whole_replay": round(m["layer_events_s"] * 1e3, 4),
         },
         "roofline": {
             "bound": "hbm",
             "kernel": "k_gate_up (kernel 1: gate_up + SiLU, 2/3 of the layer's bytes)",
-            "achieved": round(gu_b / m["gu"] / 1e9, 1),
+            "achieved": round(gu_b / m["gu_events"] / 1e9, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
-            "frac": round(gu_b / m["gu"] / 1e9 / PEAK_HBM_GBS, 4),
+            "frac": round(gu_b / m["gu_events"] / 1e9 / PEAK_HBM_GBS, 4),
             "traffic": traffic_from_profile(bits),
+            "time_basis": f"HIP events on the replay stream around one graph replay of {m['gu_events_launches']} "
+                          f"consecutive kernel-1 launches: {m['gu_events'] * 1e6:.3f} us per launch, in-graph "
+                          "(the launch gap between kernels included)",
         },
         "cpu_baseline": None,
     }
+    rp_gu, rp_dn = rocprof_from_profile(bits)
+    if rp_gu:
+        res["roofline"]["rocprof_avg_us"] = round(rp_gu / 1e3, 3)
+        res["roofline"]["frac_rocprof"] = round(gu_b / rp_gu / PEAK_HBM_GBS, 4)
+        res["roofline"]["rocprof_profile"] = os.path.relpath(trace_profile_name(bits), ROOT)
 
     if not a.no_cpu_baseline:
         sys.path.insert(0, ROOT)

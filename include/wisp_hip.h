@@ -451,6 +451,12 @@ int wisp_act_read(const uint32_t* act, int k, int64_t I, int bits, float* a, voi
 /* An empty kernel (one wave): the cost of one launch inside a graph. */
 int wisp_probe_empty(void* stream);
 
+/* The GPU's constant-rate real-time counter (s_memrealtime) written to *dst
+ * (device uint64, 8-byte aligned) by one lane when the kernel runs: two of
+ * them captured in a graph around a run of steps time exactly those steps on
+ * the GPU's clock (bench.py). */
+int wisp_probe_stamp(uint64_t* dst, void* stream);
+
 /* A plain streaming read of `bytes` (a multiple of 16) from base with 16-byte
  * non-temporal loads over `workgroups` workgroups of 256 threads; nothing is
  * written to `sink` (a device buffer of `workgroups` uint32, kept so the loads

@@ -11,12 +11,24 @@
 //    base + s * stride, s = slot[0] (a float slot id, 0 unless an integer in
 //    [0, nslots)) read from device memory first: the dependent round trip
 //    (slot id -> data) the decode kernels pay before their weight loads.
+//  * k_probe_stamp: one lane reads the GPU's constant-rate real-time counter
+//    (s_memrealtime) and writes it to dst with a vector store. Two stamps
+//    captured in a graph around a run of steps time those steps on the GPU's
+//    own clock, without the graph's launch latency.
 #include "wisp_device.hpp"
 #include "wisp_internal.hpp"
 
 namespace wisp {
 
 __global__ void k_probe_empty() {}
+
+__global__ __launch_bounds__(64) void k_probe_stamp(uint64_t* __restrict__ dst) {
+    const uint64_t t = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) {
+        volatile uint64_t* d = dst;  // an ordinary (vector) global store
+        *d = t;
+    }
+}
 
 constexpr int kProbeThreads = 256;
 constexpr int kProbeUnroll = 4;  // 16-byte loads in flight per thread and step
@@ -55,6 +67,13 @@ extern "C" int wisp_probe_empty(void* stream) {
     clear_error();
     hipLaunchKernelGGL(k_probe_empty, dim3(1), dim3(64), 0, (hipStream_t)stream);
     return check_launch("k_probe_empty");
+}
+
+extern "C" int wisp_probe_stamp(uint64_t* dst, void* stream) {
+    clear_error();
+    if (!dst || !aligned(dst, 8)) return fail_inval("probe_stamp: dst must be an 8-byte aligned device pointer");
+    hipLaunchKernelGGL(k_probe_stamp, dim3(1), dim3(64), 0, (hipStream_t)stream, dst);
+    return check_launch("k_probe_stamp");
 }
 
 extern "C" int wisp_probe_read(const uint8_t* base, const float* slot, int64_t stride, int64_t nslots, int64_t bytes,

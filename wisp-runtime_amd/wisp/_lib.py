@@ -96,6 +96,7 @@ SIGNATURES = {
     "wisp_set_tuning": (_i32, [_i32, _i32, _i32]),
     "wisp_act_read": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp]),
     "wisp_probe_empty": (_i32, [_vp]),
+    "wisp_probe_stamp": (_i32, [_vp, _vp]),
     "wisp_probe_read": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp]),
 }
 
