@@ -371,11 +371,14 @@ def _attn_case(Hq, Hk, D, T, seed):
 
 
 @pytest.mark.parametrize("Hq,Hk,D,T", [(32, 4, 128, 256), (8, 8, 64, 130), (4, 1, 256, 70), (32, 2, 128, 64),
-                                       (16, 4, 128, 4096), (8, 2, 128, 6000)])
+                                       (16, 4, 128, 4096), (8, 2, 128, 6000), (32, 4, 128, 4096)])
 def test_attn_decode_matches_oracle(Hq, Hk, D, T):
+    """(32, 4, 128, 4096) is the C4 decoder's shape (8 query heads per KV head, 64 chunks of 64 positions,
+    several merge batches); positions cover the first chunk, a chunk boundary, the middle of a chunk in the
+    middle of the cache and the last position."""
     q, k, v, tq, tk, tv = _attn_case(Hq, Hk, D, T, seed=Hq + D + T)
     scale = D ** -0.5
-    for pos in sorted({0, 1, 63, 64, min(100, T - 1), T - 1}):
+    for pos in sorted({0, 1, 63, 64, min(100, T - 1), T // 2 + 33, T - 1}):
         if pos >= T:
             continue
         p = torch.tensor([pos], dtype=torch.int64, device=DEV)
