@@ -140,6 +140,100 @@ def test_device_paging_with_partly_forced_routing_matches_host_steps():
     rt.cache.free()
 
 
+class _DenseMoE(torch.nn.Module):
+    """Dense reference MoE block with the attributes the decoder reads (gate, top_k,
+    norm_topk, E, I, next_gate), as the reference's test stand-in (test_graphdec.py:12-35)."""
+
+    def __init__(self, h, i, e, k):
+        super().__init__()
+        self.gate = torch.nn.Linear(h, e, bias=False)
+        self.w1, self.w3, self.w2 = (torch.nn.Parameter(torch.randn(e, i, h) * 0.1),
+                                     torch.nn.Parameter(torch.randn(e, i, h) * 0.1),
+                                     torch.nn.Parameter(torch.randn(e, h, i) * 0.1))
+        self.top_k, self.norm_topk, self.E, self.I, self.next_gate = k, True, e, i, None
+        self.forced = None  # expert ids replacing the top-k of a one-token forward
+        self.agreed = []  # per forced forward: were they this router's own top-k?
+
+    def mix(self, x, sel, rw):
+        y = torch.zeros_like(x)
+        for e, w in zip(sel, rw, strict=True):
+            y = y + w * (torch.nn.functional.silu(x @ self.w1[e].T) * (x @ self.w3[e].T)) @ self.w2[e].T
+        return y
+
+    def forward(self, h):
+        x = h.reshape(-1, h.shape[-1])
+        rw = torch.softmax(self.gate(x), dim=1, dtype=torch.float32)
+        if self.forced is not None:
+            sel = torch.tensor(self.forced).view(1, -1)
+            self.agreed.append(set(self.forced) == set(torch.topk(rw, self.top_k, -1).indices[0].tolist()))
+            rw = rw.gather(1, sel)
+        else:
+            rw, sel = torch.topk(rw, self.top_k, -1)
+        rw = (rw / rw.sum(-1, keepdim=True)).to(x.dtype)
+        return torch.stack([self.mix(x[t : t + 1], sel[t], rw[t])[0] for t in range(x.shape[0])]).view_as(h)
+
+
+def test_prepare_and_moe_overrides_own_the_expert_step():
+    """The reference's decoder test (test_graphdec.py:39-78): a subclass overrides the host
+    step `_prepare(i, row)` (it receives the route row [expert ids | weights] of every layer)
+    and `_moe(i)` (a dense MoE of those experts), with no runtime at all; decoding then
+    matches transformers on the same model. Here the model is decoded in bf16 by this
+    package's attention/router kernels against a float32 host run of the same bf16-exact
+    weights (head_dim 64: the decode attention kernel takes head dims 64, 128 and 256).
+    The host run takes each layer's experts from the row the decoder's _prepare received
+    (its weights from its own router), so a near-tie that bf16 and float32 break apart
+    cannot flip an expert between the two; nearly every choice must still be the host
+    router's own top-k."""
+    torch.manual_seed(0)
+    cfg = Qwen3MoeConfig(vocab_size=100, hidden_size=64, intermediate_size=64, moe_intermediate_size=32,
+                         num_hidden_layers=3, num_attention_heads=4, num_key_value_heads=2, head_dim=64,
+                         num_experts=8, num_experts_per_tok=2, norm_topk_prob=True, max_position_embeddings=256,
+                         decoder_sparse_step=1, mlp_only_layers=[])
+    ref = Qwen3MoeForCausalLM(cfg).eval()
+    for lay in ref.model.layers:
+        lay.mlp = _DenseMoE(64, 32, 8, 2)
+    with torch.no_grad():
+        for p in ref.parameters():
+            p.copy_(p.to(torch.bfloat16).float())
+    gpu = copy.deepcopy(ref).to("cuda", torch.bfloat16)
+    _fresh_rotary(gpu, cfg, "cuda")
+    rows = []
+
+    class DenseDecoder(GraphDecoder):
+        def _prepare(self, i, row):
+            k = self.k
+            rows.append((i, row))
+            self.sel, self.w = [int(v) for v in row[:k]], row[k : 2 * k]
+
+        def _moe(self, i):
+            w = [torch.tensor(v, device=self.dev, dtype=self.dt) for v in self.w]
+            return self.layers[i].mlp.mix(self.xn.view(1, -1), self.sel, w).view(1, 1, -1)
+
+    ids = torch.randint(0, 100, (1, 7), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        out = ref(input_ids=ids, use_cache=True)
+        pk, t = out.past_key_values, out.logits[:, -1].argmax(-1)
+        dec = DenseDecoder(gpu, None, tmax=64, use_graph=False)
+        dec.load_kv(pk, 7)
+        for step in range(6):
+            got = dec.next(t.cuda())
+            for i, row in rows[-3:]:
+                ref.model.layers[i].mlp.forced = [int(v) for v in row[:2]]
+            r = ref(input_ids=t[:, None], past_key_values=pk, use_cache=True)
+            for lay in ref.model.layers:
+                lay.mlp.forced = None
+            pk = r.past_key_values
+            err, ok = _close(got, r.logits[:, -1], 2e-2)
+            print(f"step {step} rel-L2 {err:.3e}")
+            assert ok, (step, err)
+            t = r.logits[:, -1].argmax(-1)
+    assert not dec._dev and [i for i, _ in rows] == list(range(3)) * 6
+    agreed = [a for lay in ref.model.layers for a in lay.mlp.agreed]
+    assert len(agreed) == 18 and sum(agreed) >= 16, agreed  # the host router's own top-k (nearly) always
+    for _, row in rows:  # [expert ids | normalised weights]
+        assert len(row) == 4 and all(0 <= v < 8 and v == int(v) for v in row[:2]) and abs(sum(row[2:]) - 1) < 1e-2
+
+
 def test_prefetch_and_recorder_paths_give_the_same_tokens():
     """The per-layer host step with prefetch of the next layer's predicted experts (and with a
     routing recorder) reads the row through the generic path; only slot placement may change,

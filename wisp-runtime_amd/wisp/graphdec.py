@@ -256,7 +256,9 @@ class GraphDecoder:
             self.row[:, 2 * self.k :].copy_(guess)
 
     def _moe(self, i):
-        """The MoE output [H] of layer i on xn with the routing in meta_dev."""
+        """The MoE output [H] of layer i on xn with the routing in meta_dev. Overridable, as
+        the reference's (graphdec.py:189-197): an override returns any contiguous tensor of
+        H values of the model's dtype."""
         cache = self.rt.cache
         st = cache.store
         return kernels.moe_decode_fast(cache.gpu, self.meta_dev, self.xn.view(self.H), self.k, st.n, self.H,
@@ -281,10 +283,15 @@ class GraphDecoder:
     def _device_ok(self):
         """Whether this step pages on the GPU; starts device paging on the cache if so."""
         rt = self.rt
-        if self.device_paging is False or rt is None or self.prefetch or rt.recorder is not None:
+        if (self.device_paging is False or rt is None or self.prefetch or rt.recorder is not None
+                or self._custom_prepare()):
             if self.device_paging is True:
-                raise RuntimeError("device paging needs a runtime without prefetch or a routing recorder")
+                raise RuntimeError("device paging needs a runtime without prefetch, a routing recorder or a "
+                                   "_prepare override")
             return False
+        dyn = rt.cache.nslots - getattr(rt.cache, "n_static", 0)
+        if dyn < self.k:  # the host steps' core refuses it as well, on the first miss
+            raise RuntimeError(f"the cache has {dyn} dynamic slots, fewer than top-k = {self.k}: no evictable slot")
         try:
             rt.cache.device_begin()
         except RuntimeError:
@@ -323,10 +330,18 @@ class GraphDecoder:
         router's own. A hook for synthetic routing; the weights stay the router's."""
         return None
 
-    def _host_step_read_back(self, i):
-        """The host step through a read-back of the route row (prefetch or a recorder)."""
+    def _custom_prepare(self):
+        """True when a subclass replaces the host step (_prepare)."""
+        return type(self)._prepare is not GraphDecoder._prepare
+
+    def _prepare(self, i, row):
+        """Host step of layer i from the route row read back to the host (row: the list
+        [expert ids | weights (| predicted next ids)] of floats): page the experts (or the
+        _expert_ids hook's), write meta_dev, prefetch the predicted ones, count the step.
+        The reference's overridable host step (graphdec.py:216-234): a subclass that
+        overrides it owns the whole step; the decoder then reads the row back every layer
+        (one sync per layer) and pages nothing itself, as with prefetch or a recorder."""
         rt, cache, k = self.rt, self.rt.cache, self.k
-        row = self.row.cpu()[0].tolist()  # the one sync of this layer
         ex = [int(v) for v in row[:k]]
         forced = self._expert_ids(i)
         if forced is not None:
@@ -340,9 +355,13 @@ class GraphDecoder:
         if self.prefetch and i + 1 < self.L:
             nxt = (i + 1) * self.E
             rt.stats["prefetched"] += cache.prefetch([nxt + int(e) for e in set(row[2 * k : 3 * k])], list(slots))
+        rt.stats["layer_calls"] += 1
+        rt.stats["gpu_experts"] += k
 
     # ---------------------------------------------------------------- capture / replay
     def _cache_key(self):
+        if self.rt is None:  # (a _prepare / _moe override owns the experts)
+            return (None, self.prefetch, self.device_paging)
         cache = self.rt.cache
         return (id(cache), cache.gpu.data_ptr(), cache.nslots, cache.store.bits, self.prefetch, self.device_paging,
                 self.rt.recorder is not None)
@@ -437,17 +456,20 @@ class GraphDecoder:
             rt.stats["gpu_experts"] += self.L * self.k
             self.pos += 1
             return self.logits
-        signalled = not self.prefetch and rt.recorder is None
+        custom = self._custom_prepare()
+        if rt is None and not custom:
+            raise RuntimeError("a decoder without a runtime needs _prepare and _moe overrides")
+        signalled = not (custom or self.prefetch or rt.recorder is not None)
         flag = int(self.flag_host[0])  # no route kernel is in flight here
         self._replay(0)
         for i in range(self.L):
             if signalled:  # wait for the route kernel's row in host memory; page; write meta
                 flag = rt.cache.prepare_signaled(self.row_host, self.flag_host, flag, i * self.E, self.k, self.E,
                                                  self._expert_ids(i), self.meta_host, self.meta_dev)
+                rt.stats["layer_calls"] += 1
+                rt.stats["gpu_experts"] += self.k
             else:
-                self._host_step_read_back(i)
-            rt.stats["layer_calls"] += 1
-            rt.stats["gpu_experts"] += self.k
+                self._prepare(i, self.row.cpu()[0].tolist())  # the one sync of this layer
             self._replay(i + 1)
         self.pos += 1
         return self.logits
