@@ -81,6 +81,57 @@ def test_device_steps_match_reference_lru(store, nslots, k, use_row):
     c.free()
 
 
+@pytest.mark.parametrize("nslots,n_static", [(1500, 0), (6144, 0), (2100, 40)])
+def test_device_steps_past_1024_dynamic_slots(nslots, n_static):
+    """Pools of more than 1024 dynamic slots stage the eviction keys in batches of 1024
+    slots while the step runs (the other staging path of k_lru_step). k = 16 steps fill the
+    pool to 8 free slots, then one step of 16 new keys takes the 8 free slots and evicts 8,
+    then random steps over 8192 keys mix hits with evicting misses; every step's meta, the
+    counters at every sync and the final state match the reference LRU."""
+    L, E, n, k = 64, 128, 1024, 16  # 8192 keys of 1632-byte rows
+    st = ExpertStore(L, E, n, 4, 128)
+    gen = torch.Generator().manual_seed(nslots)
+    st.host.copy_(torch.randint(0, 256, tuple(st.host.shape), dtype=torch.uint8, generator=gen))
+    pre = list(range(8000, 8000 + n_static))
+    c = ExpertCache(st, nslots, n_static=n_static, preload_keys=pre or None, copy="kernel")
+    ref = RefCore(nslots, "lru", n_static=n_static)
+    if pre:
+        ref.preload(pre)
+    meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    rng = np.random.default_rng(nslots + n_static)
+    c.device_begin()
+
+    def step(keys, it):
+        keys = [int(v) for v in keys]
+        layer = keys[0] // E
+        ids = np.array([v - layer * E for v in keys], dtype=np.int64)
+        assert all(0 <= v < E for v in ids)
+        w = rng.random(len(keys)).astype(np.float32)
+        c.device_step(_row(ids, w), None, layer * E, E, len(keys), meta)
+        m = meta.cpu()
+        assert [int(v) for v in m[: len(keys)]] == ref.ensure(keys)[0], it
+
+    fill = nslots - n_static - 8
+    for it, k0 in enumerate(range(0, fill, k)):  # keys 0 .. fill-1, at most k of one layer per step
+        layer = k0 // E
+        hi = min(k0 + k, fill, (layer + 1) * E)
+        step(range(k0, hi), it)
+    assert ref.counts["evictions"] == 0 and len(ref.stack) == 8
+    base = (fill // E + 1) * E  # 16 keys of a layer not used yet: 8 take the free slots, 8 evict
+    step(range(base, base + k), "mixed")
+    assert ref.counts["evictions"] == 8 and not ref.stack
+    for it in range(300):
+        layer = int(rng.integers(0, L))
+        step(layer * E + rng.choice(E, size=k, replace=False), it)
+        if it % 100 == 99:
+            c.device_sync()
+            assert c.core.stats == ref.counts, it  # (ends device paging)
+            c.device_begin()
+    assert ref.counts["evictions"] > 600
+    _check_state(c, ref, st)
+    c.free()
+
+
 def test_repeated_ids_and_hits_in_one_step(store):
     """Forced ids may repeat a key: the reference hands each occurrence of a missing key its
     own slot and keeps the later one in key2slot; the device step does the same. (The pool is
@@ -244,15 +295,18 @@ def test_bad_id_and_no_evictable_slot_are_reported(store):
     c.device_sync()  # reported once
     c.device_end()
     c2 = ExpertCache(store, 6, copy="kernel")
-    k = 8  # more keys than slots: the reference raises on the 7th miss
+    k = 8  # more keys than slots: the reference raises on the 7th miss; here the step is refused on the host
     meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
     c2.device_begin()
-    c2.device_step(_row(list(range(8)), np.ones(k)), None, 0, E, k, meta)
-    m = meta.cpu()
-    assert [int(v) for v in m[:6]] == list(range(6)) and [int(v) for v in m[6:8]] == [-1, -1]
     with pytest.raises(RuntimeError, match="no evictable slot"):
-        c2.device_end()
-    assert not c2.device_paging
+        c2.device_step(_row(list(range(8)), np.ones(k)), None, 0, E, k, meta)
+    logits = torch.zeros(E, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="no evictable slot"):
+        c2.device_route_step(logits, k, True, torch.zeros(2 * k, device=DEV), None, 0, E, meta)
+    c2.device_step(_row(list(range(6)), np.ones(6)), None, 0, E, 6, meta)  # k = the dynamic slots: placed
+    assert sorted(int(v) for v in meta[:6].cpu()) == list(range(6))
+    c2.device_end()
+    assert not c2.device_paging and c2.core.stats["misses"] == 6
     c.free()
     c2.free()
 

@@ -1288,6 +1288,18 @@ extern "C" int wisp_cache_device_begin(void* h, void* stream) {
     return WISP_OK;
 }
 
+// k distinct keys can always be placed when k <= the dynamic slots: the step's hits
+// are protected, and the misses take the other dynamic slots. With fewer dynamic
+// slots than k a miss can find no evictable slot (the reference's CacheCore.acquire
+// raises on it, cache_core.py:64-84), so the step is refused on the host before any
+// launch rather than left to the device report that only the next sync reads.
+static int no_slot_for_k(const Cache& c, int k) {
+    char msg[160];
+    std::snprintf(msg, sizeof msg, "device paging: top-k %d exceeds the %lld dynamic slots (no evictable slot)", k,
+                  (long long)(c.nslots - c.dev.n_static));
+    return fail_inval(msg);
+}
+
 // One layer's paging point on `stream` (capturable: no host sync, no allocation):
 // ensure the keys key_base + id (ids: device int64 [k], else the route row's ids,
 // row = device float32 [ids (k) | weights (k)]), meta (device float32 [2k]) =
@@ -1300,6 +1312,7 @@ extern "C" int wisp_cache_device_step(void* h, const float* row, const int64_t* 
     if (!c.dev_on) return fail_inval("device paging is off (wisp_cache_device_begin)");
     if (k < 0 || k > kDevMaxK) return fail_inval("device paging takes 0 <= k <= 16");
     if (k > 0 && (!row || !meta || n_ids < 1)) return fail_inval("device paging step: null row / meta or n_ids < 1");
+    if (k > c.nslots - c.dev.n_static) return no_slot_for_k(c, k);
     if (!c.pool) return no_pool();
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(k_lru_step, dim3(1), dim3(64), 0, st, c.dev, row, ids, key_base, n_ids, k, meta);
@@ -1324,6 +1337,7 @@ extern "C" int wisp_cache_device_route_step(void* h, const uint16_t* logits, int
     if (k < 0 || k > kDevMaxK) return fail_inval("device paging takes 0 <= k <= 16");
     if (k > 0 && (!logits || !row || !meta || n_ids < 1 || E < k || E > 1024))
         return fail_inval("device route step: null logits / row / meta, n_ids < 1 or E outside [k, 1024]");
+    if (k > c.nslots - c.dev.n_static) return no_slot_for_k(c, k);
     if (!c.pool) return no_pool();
     hipStream_t st = (hipStream_t)stream;
     const int nt = norm_topk ? 1 : 0;

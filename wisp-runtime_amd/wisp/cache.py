@@ -69,7 +69,7 @@ class ExpertCache:
         # kept as bf16 (cache.py:25-27)
         self.decode_on_load = bool(decode_on_load) and store.bits < 16
         self.cpu_store = cpu_store
-        self.nslots = nslots
+        self.nslots, self.n_static = nslots, n_static
         self.slot_bytes = 3 * store.n * 2 if self.decode_on_load else store.nbytes
         host = store.host
         assert host.dtype == torch.uint8 and host.dim() == 2 and host.is_contiguous() and not host.is_cuda
