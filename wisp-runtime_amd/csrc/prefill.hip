@@ -537,18 +537,19 @@ __device__ __forceinline__ void wait_lgkm0() {
 }
 
 // 64 lanes x 16 (dma16s) or 4 (dma4s) bytes from sbase + each lane's 32-bit offset to
-// LDS [lds, lds + 64*size): the base in an SGPR pair, no 64-bit address arithmetic per lane
+// LDS [lds, lds + 64*size): the base in an SGPR pair, no 64-bit address arithmetic per lane.
+// M0 carries the LDS address and is declared clobbered.
 __device__ __forceinline__ void dma16s(uint32_t lds, const void* sbase, uint32_t voff) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                  :
                  : "s"(lds), "v"(voff), "s"(sbase)
-                 : "memory");
+                 : "memory", "m0");
 }
 __device__ __forceinline__ void dma4s(uint32_t lds, const void* sbase, uint32_t voff) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
                  :
                  : "s"(lds), "v"(voff), "s"(sbase)
-                 : "memory");
+                 : "memory", "m0");
 }
 __device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
     const uint64_t v = (uint64_t)(uintptr_t)p;
