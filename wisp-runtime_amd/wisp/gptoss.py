@@ -20,11 +20,16 @@ PagedGptOssBlock.forward:
     (token, expert) pair exactly once, grouped per expert by one stable sort of the routing;
     experts are paged rt.chunk at a time and run as bf16 GEMMs on their bit-exactly
     dequantized weights.
-Reading gpt-oss checkpoints (their MXFP4 safetensors) is outside this build's scope; the
-MXFP4 decode itself is a HIP kernel (kernels.mxfp4_to_bf16).
+Checkpoints: build_store quantizes the experts of a gpt-oss safetensors checkpoint (MXFP4
+blocks and scales, decoded by the HIP kernel kernels.mxfp4_to_bf16, or plain bf16) into an
+ExpertStore (gptoss.py:67-90), and load_skeleton_gptoss builds the model with paged blocks
+and loads its non-expert tensors and the expert biases (gptoss.py:146-176).
 """
 
 from __future__ import annotations
+
+import os
+import time
 
 import torch
 import torch.nn as nn
@@ -47,6 +52,76 @@ def expert_w3(gate_up, down):
     half = gate_up.numel() // 2
     flat = gate_up.reshape(-1)
     return torch.stack([flat[:half], flat[half:], down.reshape(-1)])
+
+
+def _layer_experts(ck, l, device):
+    """gate_up [E, H, 2I] and down [E, I, H] (bf16, on `device`) of layer l of checkpoint ck
+    (a SafetensorsDir): MXFP4 blocks [E, out, K/32, 16] + scales [E, out, K/32] decoded and
+    transposed to [E, K, out], or the plain tensors (gptoss.py:38-49)."""
+    p = f"model.layers.{l}.mlp.experts."
+    if p + "gate_up_proj_blocks" in ck:
+        gu = mxfp4_to_bf16(ck.get(p + "gate_up_proj_blocks").to(device), ck.get(p + "gate_up_proj_scales").to(device))
+        dn = mxfp4_to_bf16(ck.get(p + "down_proj_blocks").to(device), ck.get(p + "down_proj_scales").to(device))
+        return gu.transpose(1, 2).contiguous(), dn.transpose(1, 2).contiguous()
+    return ck.get(p + "gate_up_proj").to(device), ck.get(p + "down_proj").to(device)
+
+
+def build_store(model_dir, cfg, bits, group=128, device="cuda", cache_dir=None, pin=True):
+    """The experts of a gpt-oss checkpoint quantized into a new ExpertStore of [3, H*I] rows
+    (gptoss.py:67-90; gpt-oss has I == H). With cache_dir (and bits < 16) the rows are read
+    from, or else written to, a cache file of this shape."""
+    from .store import ExpertStore, SafetensorsDir
+
+    L, E, H, I = cfg.num_hidden_layers, cfg.num_local_experts, cfg.hidden_size, cfg.intermediate_size
+    if H != I:
+        raise ValueError(f"the [3, n] expert rows need intermediate_size == hidden_size (gpt-oss): {I} != {H}")
+    st = ExpertStore(L, E, H * I, bits, group, pin)
+    path = None
+    if cache_dir and bits < 16:
+        os.makedirs(cache_dir, exist_ok=True)
+        path = os.path.join(cache_dir, f"store_gptoss_b{bits}_g{group}_{L}x{E}x{H * I}.u8")
+        if os.path.exists(path) and os.path.getsize(path) == st.host.numel():
+            st.load(path)
+            return st
+    ck = SafetensorsDir(model_dir)
+    for l in range(L):
+        gu, dn = _layer_experts(ck, l, device)
+        st.fill(((st.key(l, e), expert_w3(gu[e], dn[e])) for e in range(E)), device)
+        del gu, dn
+    if path:
+        st.save(path)
+    return st
+
+
+@torch.no_grad()
+def load_skeleton_gptoss(model_dir, rt, device="cuda"):
+    """gpt-oss built on the meta device with every MLP replaced by a PagedGptOssBlock on rt,
+    the non-expert tensors and the experts' biases loaded to `device` (gptoss.py:146-176).
+    Returns (model, cfg)."""
+    from transformers import AutoConfig, AutoModelForCausalLM
+
+    from .model import _fresh_rotary, _load_non_experts, nbytes_of
+    from .store import SafetensorsDir
+
+    cfg = AutoConfig.from_pretrained(model_dir)
+    t0 = time.time()
+    with torch.device("meta"):
+        model = AutoModelForCausalLM.from_config(cfg, dtype=torch.bfloat16)
+    blocks = []
+    for i, layer in enumerate(model.model.layers):
+        layer.mlp = PagedGptOssBlock(layer.mlp.router, i, rt, cfg, device)
+        blocks.append(layer.mlp)
+    ck = SafetensorsDir(model_dir)
+    _load_non_experts(model, ck, device)
+    for l, blk in enumerate(blocks):
+        p = f"model.layers.{l}.mlp.experts."
+        blk.gub.copy_(ck.get(p + "gate_up_proj_bias"))
+        blk.db.copy_(ck.get(p + "down_proj_bias"))
+    _fresh_rotary(model, cfg, device)
+    model.eval()
+    print(f"[model] gpt-oss non-expert weights on {device}: {nbytes_of(model) / 2**30:.2f} GiB "
+          f"({time.time() - t0:.0f}s)", flush=True)
+    return model, cfg
 
 
 def clamped_swiglu(gu, alpha: float, limit: float):

@@ -1,12 +1,13 @@
 """Qwen3-MoE model skeletons whose experts live in an ExpertStore: only the non-expert
-weights are on the GPU. Runtime set-up entry points as the reference's wisp/model.py
-(make_runtime, configure: model.py:58-95) and a random-initialised skeleton of any
-Qwen3-MoE config for the synthetic workloads. Loading a checkpoint (the reference's
-load_skeleton, model.py:20-55) is outside this build's scope: no checkpoint reaches this
-path, and the synthetic skeletons carry the same module structure.
+weights are on the GPU. Entry points as the reference's wisp/model.py: load_skeleton
+(model.py:20-55: a checkpoint's non-expert tensors), make_runtime and configure
+(model.py:58-95); and a random-initialised skeleton of any Qwen3-MoE config for the
+synthetic workloads, with the same module structure.
 """
 
 from __future__ import annotations
+
+import time
 
 import torch
 import torch.nn as nn
@@ -37,6 +38,47 @@ def _fresh_rotary(model, cfg, device):
 def _gates_with_storage(model, cfg, device, dtype):
     for layer in model.model.layers:  # real storage, so attach() keeps a real router module
         layer.mlp.gate = nn.Linear(cfg.hidden_size, cfg.num_experts, bias=False, device=device, dtype=dtype)
+
+
+def _load_non_experts(model, ck, device):
+    """Every tensor of checkpoint `ck` (a SafetensorsDir) outside the experts, assigned to
+    the model's parameters on `device`; the output head is tied to the embedding when the
+    config ties them and the checkpoint has none."""
+    sd = ck.load([k for k in ck.names() if ".mlp.experts." not in k], device)
+    res = model.load_state_dict(sd, strict=False, assign=True)
+    missing = [k for k in res.missing_keys if "rotary" not in k]
+    if missing == ["lm_head.weight"] and getattr(model.config, "tie_word_embeddings", False):
+        model.lm_head.weight = model.model.embed_tokens.weight
+        missing = []
+    if missing:
+        raise KeyError(f"the checkpoint lacks {missing[:5]}")
+
+
+@torch.no_grad()
+def load_skeleton(model_dir, rt, device="cuda"):
+    """The model of `model_dir` (config.json + safetensors) built on the meta device, paged
+    MoE blocks attached to rt, every non-expert tensor loaded straight to `device`
+    (model.py:20-55); gpt-oss checkpoints go to gptoss.load_skeleton_gptoss. The experts
+    come from rt's store (ExpertStore.from_safetensors). Returns (model, cfg)."""
+    from transformers import AutoConfig
+
+    from .store import SafetensorsDir
+
+    cfg = AutoConfig.from_pretrained(model_dir)
+    if cfg.model_type == "gpt_oss":
+        from .gptoss import load_skeleton_gptoss
+
+        return load_skeleton_gptoss(model_dir, rt, device)
+    t0 = time.time()
+    model = _meta_model(cfg, torch.bfloat16)
+    _gates_with_storage(model, cfg, device, torch.bfloat16)
+    attach(model, rt)
+    _load_non_experts(model, SafetensorsDir(model_dir), device)
+    _fresh_rotary(model, cfg, device)
+    model.eval()
+    print(f"[model] non-expert weights on {device}: {nbytes_of(model) / 2**30:.2f} GiB ({time.time() - t0:.0f}s)",
+          flush=True)
+    return model, cfg
 
 
 @torch.no_grad()

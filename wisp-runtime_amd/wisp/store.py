@@ -1,6 +1,7 @@
 """The quantized experts of every layer, in pinned host memory: the source the expert cache
 pages from. Reference interface: wisp/store.py:12-110 (ExpertStore: L, E, n, bits, group,
-nbytes, host, pinned, total_gib, key, put, from_experts, _save, _load); same row format.
+nbytes, host, pinned, total_gib, key, put, from_experts, from_safetensors, _save, _load);
+same row format.
 
 Layout. One row of `nbytes = expert_nbytes(n, bits, group)` bytes per (layer, expert) at
 row `key = layer * E + expert`, all rows in ONE page-locked allocation, so a cache miss is
@@ -12,6 +13,10 @@ ring of device staging rows and copies each finished row to its pinned row on a 
 stream, so the PCIe transfer of one expert overlaps the quantization of the next ones;
 the host never waits per expert.
 
+Checkpoints. `from_safetensors` quantizes the experts of a Qwen3-MoE safetensors checkpoint
+through `fill` (per-expert tensors as published, or per-layer fused ones as newer
+transformers write them); `SafetensorsDir` reads a checkpoint directory by tensor name.
+
 Persistence. A `.u8` file is the rows back to back with no header (its size identifies the
 shape: L * E * nbytes). `save` writes through a temporary file renamed into place; both
 directions stream 64 MiB at a time, so a 15 GB store never needs a second copy in memory.
@@ -19,6 +24,7 @@ directions stream 64 MiB at a time, so a 15 GB store never needs a second copy i
 
 from __future__ import annotations
 
+import json
 import os
 import time
 from typing import Iterable
@@ -40,6 +46,55 @@ def _host_rows(nrows: int, nbytes: int, pin: bool):
         except RuntimeError as err:
             print(f"[store] page-locked allocation refused ({err}); the store is pageable", flush=True)
     return torch.empty((nrows, nbytes), dtype=torch.uint8), False
+
+
+class SafetensorsDir:
+    """The tensors of a safetensors checkpoint directory by name: the weight map of
+    model.safetensors.index.json (a sharded checkpoint) or the names in the one
+    model.safetensors. Each file is opened once; `get` reads one tensor to the CPU,
+    `load` many straight to a device (the reference's _reader, gptoss.py:52-64, and the
+    loops of model.py:37-43)."""
+
+    def __init__(self, model_dir):
+        from safetensors import safe_open
+
+        self.dir, self._open = model_dir, {}
+        index = os.path.join(model_dir, "model.safetensors.index.json")
+        if os.path.exists(index):
+            with open(index) as f:
+                self.files = dict(json.load(f)["weight_map"])
+        else:
+            with safe_open(os.path.join(model_dir, "model.safetensors"), framework="pt") as h:
+                self.files = {name: "model.safetensors" for name in h.keys()}
+
+    def __contains__(self, name) -> bool:
+        return name in self.files
+
+    def names(self):
+        return list(self.files)
+
+    def get(self, name) -> torch.Tensor:
+        from safetensors import safe_open
+
+        f = self.files[name]
+        h = self._open.get(f)
+        if h is None:
+            h = self._open[f] = safe_open(os.path.join(self.dir, f), framework="pt", device="cpu")
+        return h.get_tensor(name)
+
+    def load(self, names, device="cpu") -> dict:
+        """{name: tensor on `device`} for `names`, one pass over each file that holds some."""
+        from safetensors import safe_open
+
+        by_file = {}
+        for name in names:
+            by_file.setdefault(self.files[name], []).append(name)
+        out = {}
+        for f, group in sorted(by_file.items()):
+            with safe_open(os.path.join(self.dir, f), framework="pt", device=str(device)) as h:
+                for name in group:
+                    out[name] = h.get_tensor(name)
+        return out
 
 
 class ExpertStore:
@@ -113,6 +168,46 @@ class ExpertStore:
         st = cls(len(layers), len(layers[0]), n, bits, group, pin)
         st.fill(((st.key(l, e), torch.stack([g.reshape(-1), u.reshape(-1), d.reshape(-1)]))
                  for l, exps in enumerate(layers) for e, (g, u, d) in enumerate(exps)), device)
+        return st
+
+    @classmethod
+    def from_safetensors(cls, model_dir, cfg, bits, group=128, device="cuda", cache_dir=None, pin=True):
+        """The experts of a Qwen3-MoE checkpoint quantized into a new store (store.py:54-93).
+        Expert tensors per expert (model.layers.{l}.mlp.experts.{e}.gate_proj / up_proj /
+        down_proj .weight, as published) or fused per layer (experts.gate_up_proj [E, 2I, H],
+        gate rows first, and experts.down_proj [E, H, I]). With cache_dir (and bits < 16) the
+        rows are read from, or else written to, the reference's cache file of this shape."""
+        L, E = cfg.num_hidden_layers, cfg.num_experts
+        H, I = cfg.hidden_size, cfg.moe_intermediate_size
+        st = cls(L, E, H * I, bits, group, pin)
+        path = None
+        if cache_dir and bits < 16:
+            os.makedirs(cache_dir, exist_ok=True)
+            path = cls.cache_file(cache_dir, bits, group, L, E, H * I)
+            if os.path.exists(path) and os.path.getsize(path) == st.host.numel():
+                st.load(path)
+                return st
+        ck = SafetensorsDir(model_dir)
+
+        def experts():
+            for l in range(L):
+                p = f"model.layers.{l}.mlp.experts."
+                if p + "gate_up_proj" in ck:
+                    gu, dn = ck.get(p + "gate_up_proj"), ck.get(p + "down_proj")
+                    assert gu.shape == (E, 2 * I, H) and dn.shape == (E, H, I), (gu.shape, dn.shape)
+                    for e in range(E):
+                        yield st.key(l, e), torch.stack([gu[e, :I].reshape(-1), gu[e, I:].reshape(-1),
+                                                         dn[e].reshape(-1)])
+                else:
+                    for e in range(E):
+                        q = f"{p}{e}."
+                        yield st.key(l, e), torch.stack([ck.get(q + "gate_proj.weight").reshape(-1),
+                                                         ck.get(q + "up_proj.weight").reshape(-1),
+                                                         ck.get(q + "down_proj.weight").reshape(-1)])
+
+        st.fill(experts(), device)
+        if path:
+            st.save(path)
         return st
 
     # ---------------------------------------------------------------- persistence
