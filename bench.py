@@ -272,7 +272,9 @@ def run_floor(a) -> dict:
     48-pool rotation, GPU clock stamps, exactly --steps launches per probe): an empty kernel; a
     plain streaming read of kernel 1's and of kernel 2's algorithmic bytes from the pool of
     step i; the same reads with the start address taken from a slot id in device memory
-    (the dependent round trip the decode kernels pay first); and the C2 layer itself."""
+    (the dependent round trip the decode kernels pay first); the layer's skeleton (every data
+    movement of the two kernels, no arithmetic) as two launches and as one launch with a grid
+    barrier; and the C2 layer itself."""
     dev = torch.device("cuda:0")
     W = Layers(dev, a.bits, a.layers)
     gu_b, dn_b = alg_bytes(a.bits)
@@ -298,10 +300,28 @@ def run_floor(a) -> dict:
         return body
 
     W.slot_ids = torch.arange(W.layers, dtype=torch.float32, device=dev).view(-1, 1).contiguous()
+    skel_act = torch.zeros(W.layers, 8 * 768, dtype=torch.float32, device=dev)
+    skel_out = torch.zeros(W.layers, 2048, dtype=torch.int16, device=dev)
+    skel_sync = torch.zeros(L.wisp_probe_skeleton_sync_bytes() // 4 + 64, dtype=torch.int32, device=dev)
+    sync_off = (-skel_sync.data_ptr()) % 256 // 4  # a 256-byte aligned start
+    sync = skel_sync[sync_off:]
+
+    def skeleton(one_launch):
+        gu16, dn16 = gu_b // 16 * 16, dn_b // 16 * 16
+
+        def body(i, st):
+            l = i % W.layers
+            _lib.check(L.wisp_probe_skeleton(_lib.ptr(W.pool), _lib.ptr(W.slot_ids[l]), pool_stride, W.layers, gu16,
+                                             dn16, _lib.ptr(skel_act[l]), _lib.ptr(skel_out[l]), _lib.ptr(sync),
+                                             int(one_launch), st), "probe_skeleton")
+        return body
+
     probes = [("empty_kernel", empty, 0), ("read_gate_up_bytes", reader(gu_b, False), gu_b),
               ("read_down_bytes", reader(dn_b, False), dn_b),
               ("read_gate_up_bytes_after_slot_read", reader(gu_b, True), gu_b),
               ("read_down_bytes_after_slot_read", reader(dn_b, True), dn_b),
+              ("layer_skeleton_two_launches", skeleton(False), gu_b + dn_b),
+              ("layer_skeleton_one_launch", skeleton(True), gu_b + dn_b),
               ("c2_layer", W.layer, gu_b + dn_b), ("c2_gate_up", W.gate_up, gu_b), ("c2_down", W.down, dn_b)]
     rows = {}
     setup_pass(W)
@@ -315,6 +335,9 @@ def run_floor(a) -> dict:
         rows[name] = {"us_per_launch": round(t * 1e6, 3), "bytes": nbytes,
                       "GB_per_s": round(nbytes / t / 1e9, 1) if nbytes else None}
         print(f"[bench] floor {name}: {t * 1e6:.3f} us", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    if int(sync[L.wisp_probe_skeleton_sync_bytes() // 4 - 64].item()):  # the error word
+        raise RuntimeError("layer_skeleton_one_launch: a bounded grid-barrier wait gave up (not all resident)")
     lay = rows["c2_layer"]["us_per_launch"] * 1e-6
     return {
         "metric": f"\u00b5s per launch of the C2 layer's floors ({a.bits}-bit), in-graph",
@@ -521,7 +544,9 @@ def summarize_stats(stats_csv: str, title: str, cmd: str, bench_line: str, top: 
 
 
 FLOOR_PROBES = ("empty_kernel", "read_gate_up_bytes", "read_down_bytes", "read_gate_up_bytes_after_slot_read",
-                "read_down_bytes_after_slot_read", "c2_layer", "c2_gate_up", "c2_down")
+                "read_down_bytes_after_slot_read", "layer_skeleton_two_launches", "layer_skeleton_one_launch",
+                "c2_layer", "c2_gate_up", "c2_down")
+FLOOR_ALTERNATING = ("layer_skeleton_two_launches", "c2_layer")  # two kernels per step: no single-kernel run
 
 
 def summarize_floor(trace_csv: str, log: str, cmd: str) -> str:
@@ -535,8 +560,11 @@ def summarize_floor(trace_csv: str, log: str, cmd: str) -> str:
     rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Dispatch_Id"]))
 
     def kind(n):
-        return ("probe_empty" if "k_probe_empty" in n else "probe_read" if "k_probe_read" in n else
-                "k_gate_up" if "k_gate_up" in n else "k_down" if "k_down" in n else None)
+        for key in ("k_probe_empty", "k_probe_read", "k_probe_skel_a", "k_probe_skel_b", "k_probe_skel_one",
+                    "k_gate_up", "k_down"):
+            if key in n:
+                return key[2:] if key.startswith("k_probe") else key
+        return None
 
     runs = []  # consecutive dispatches of one kernel, split at any other kernel (e.g. the sleep before timing)
     sep = True
@@ -565,11 +593,11 @@ def summarize_floor(trace_csv: str, log: str, cmd: str) -> str:
              "| probe | kernel | bytes | dispatches | median ns | mean ns | min ns | GB/s at mean |",
              "|---|---|---|---|---|---|---|---|"]
     names = [p for p in FLOOR_PROBES]
-    # the c2_layer probe alternates k_gate_up / k_down dispatches: one run of each per replay
+    # the alternating probes dispatch two kernels per step: runs of one dispatch, skipped below
     i = 0
     for name in names:
         nbytes = res["floors"][name]["bytes"]
-        if name == "c2_layer":
+        if name in FLOOR_ALTERNATING:
             continue
         while i < len(runs) and len(runs[i][1]) < steps:
             i += 1

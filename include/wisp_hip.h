@@ -466,6 +466,22 @@ int wisp_probe_stamp(uint64_t* dst, void* stream);
 int wisp_probe_read(const uint8_t* base, const float* slot, int64_t stride, int64_t nslots, int64_t bytes,
                     int workgroups, uint32_t* sink, void* stream);
 
+/* The C2 layer's skeleton: every data movement of the two decode kernels
+ * without their arithmetic. Reads gu_bytes from the (slot-selected, as in
+ * wisp_probe_read) base over 768 workgroups and writes act (device float
+ * [6144]); then reads the next dn_bytes over 512 workgroups, stages all of
+ * act in LDS and writes out (device uint16 [2048]). one_launch = 0: as two
+ * launches (the layer's structure); 1: as one launch whose 512 consuming
+ * workgroups wait at a grid barrier, with `sync` a zeroed, 256-byte aligned
+ * device buffer of wisp_probe_skeleton_sync_bytes() bytes kept between
+ * calls; a nonzero uint32 at its last 256-byte line (byte offset
+ * wisp_probe_skeleton_sync_bytes() - 256) means a bounded wait gave up.
+ * EINVAL when the 768 workgroups cannot all be resident. gu_bytes <=
+ * 25,165,824 and dn_bytes <= 8,388,608, multiples of 16. */
+int wisp_probe_skeleton(const uint8_t* base, const float* slot, int64_t stride, int64_t nslots, int64_t gu_bytes,
+                        int64_t dn_bytes, float* act, uint16_t* out, void* sync, int one_launch, void* stream);
+int64_t wisp_probe_skeleton_sync_bytes(void);
+
 #ifdef __cplusplus
 }
 #endif

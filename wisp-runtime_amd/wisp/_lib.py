@@ -98,6 +98,8 @@ SIGNATURES = {
     "wisp_probe_empty": (_i32, [_vp]),
     "wisp_probe_stamp": (_i32, [_vp, _vp]),
     "wisp_probe_read": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp]),
+    "wisp_probe_skeleton": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _vp]),
+    "wisp_probe_skeleton_sync_bytes": (_i64, []),
 }
 
 _lib: ctypes.CDLL | None = None
