@@ -513,21 +513,43 @@ __device__ __forceinline__ float rbf(float v) { return bf(f32_to_bf16(v)); }  //
 // the weight product are each rounded to bf16 as the module's bf16 tensors are; the
 // rotation runs in binary32 on those values and the cos/sin rows, rounded once. The
 // result goes to dst and, when non-null, to dst2 (bf16). Every lane of the wave calls it.
+// In two steps: hnr_load reads the lane's inputs into registers (a caller issues these
+// loads ahead of others whose data it needs later), hnr_finish does the arithmetic.
 template <int D>
-__device__ __forceinline__ void head_norm_rope(const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw,
-                                               float eps, const uint16_t* __restrict__ cs,
-                                               const uint16_t* __restrict__ sn, uint16_t* dst, uint16_t* dst2,
-                                               int lane) {
+struct HnrIn {
+    static constexpr int NP = (D / 2 + 63) / 64;
+    uint16_t a[NP], b[NP], wa[NP], wb[NP], ca[NP], cb[NP], sa[NP], sb[NP];
+};
+template <int D>
+__device__ __forceinline__ void hnr_load(const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw,
+                                         const uint16_t* __restrict__ cs, const uint16_t* __restrict__ sn, int lane,
+                                         HnrIn<D>& in) {
+    constexpr int HALF = D / 2;
+#pragma unroll
+    for (int t = 0; t < HnrIn<D>::NP; ++t) {
+        const int i = min(lane + 64 * t, HALF - 1);  // lanes past the head repeat its last pair (unused)
+        in.a[t] = x[i];
+        in.b[t] = x[i + HALF];
+        in.wa[t] = nw[i];
+        in.wb[t] = nw[i + HALF];
+        in.ca[t] = cs[i];
+        in.cb[t] = cs[i + HALF];
+        in.sa[t] = sn[i];
+        in.sb[t] = sn[i + HALF];
+    }
+}
+template <int D>
+__device__ __forceinline__ void hnr_finish(const HnrIn<D>& in, float eps, uint16_t* dst, uint16_t* dst2, int lane) {
 #pragma clang fp contract(off)
     constexpr int HALF = D / 2;
-    constexpr int NP = (HALF + 63) / 64;
+    constexpr int NP = HnrIn<D>::NP;
     float a[NP], b[NP];
     float ss = 0.f;
 #pragma unroll
     for (int t = 0; t < NP; ++t) {
         const int i = lane + 64 * t;
-        a[t] = i < HALF ? bf(x[i]) : 0.f;
-        b[t] = i < HALF ? bf(x[i + HALF]) : 0.f;
+        a[t] = i < HALF ? bf(in.a[t]) : 0.f;
+        b[t] = i < HALF ? bf(in.b[t]) : 0.f;
         ss += a[t] * a[t];
         ss += b[t] * b[t];
     }
@@ -537,10 +559,10 @@ __device__ __forceinline__ void head_norm_rope(const uint16_t* __restrict__ x, c
     for (int t = 0; t < NP; ++t) {
         const int i = lane + 64 * t;
         if (i < HALF) {
-            const float na = rbf(bf(nw[i]) * rbf(a[t] * rs));
-            const float nb = rbf(bf(nw[i + HALF]) * rbf(b[t] * rs));
-            const float lo = na * bf(cs[i]) + (-nb) * bf(sn[i]);
-            const float hi = nb * bf(cs[i + HALF]) + na * bf(sn[i + HALF]);
+            const float na = rbf(bf(in.wa[t]) * rbf(a[t] * rs));
+            const float nb = rbf(bf(in.wb[t]) * rbf(b[t] * rs));
+            const float lo = na * bf(in.ca[t]) + (-nb) * bf(in.sa[t]);
+            const float hi = nb * bf(in.cb[t]) + na * bf(in.sb[t]);
             const uint16_t l16 = f32_to_bf16(lo), h16 = f32_to_bf16(hi);
             dst[i] = l16;
             dst[i + HALF] = h16;
@@ -550,6 +572,15 @@ __device__ __forceinline__ void head_norm_rope(const uint16_t* __restrict__ x, c
             }
         }
     }
+}
+template <int D>
+__device__ __forceinline__ void head_norm_rope(const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw,
+                                               float eps, const uint16_t* __restrict__ cs,
+                                               const uint16_t* __restrict__ sn, uint16_t* dst, uint16_t* dst2,
+                                               int lane) {
+    HnrIn<D> in;
+    hnr_load<D>(x, nw, cs, sn, lane, in);
+    hnr_finish<D>(in, eps, dst, dst2, lane);
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
