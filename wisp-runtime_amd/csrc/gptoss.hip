@@ -12,7 +12,7 @@
 // Kernels:
 //   k_mxfp4      MXFP4 blocks + power-of-two scales -> bf16 (gptoss.py:22-29)
 //   k_go_gate_up partial gate_up GEMV: per expert, column block and block of
-//                kGoRows input rows, fp32 partial sums of x . W_gu (bf16 weights)
+//                16 * go_pairs_gu(bits) input rows, fp32 partial sums of x . W_gu (bf16 weights)
 //   k_go_down    sums the gate_up partials of its kGoRows activation rows, adds the
 //                bias and applies the clamped SwiGLU with the reference's bf16
 //                rounding steps, then the partial down GEMV over those rows
@@ -82,15 +82,22 @@ __global__ __launch_bounds__(256) void k_mxfp4(const uint8_t* __restrict__ block
 // Decode layer.
 
 constexpr int kGoWaves = 4;         // waves per workgroup
-constexpr int kGoRows = 64;         // input rows per workgroup (4 waves x 16)
 constexpr int kGoCols = 1024;       // output columns per workgroup (32 lanes x 32)
-constexpr int kGoPairs = 4;         // row pairs per half-wave (16 rows per wave)
 constexpr int kGoRedStride = 1056;  // LDS floats per partial vector (32 x 33: conflict-free transpose)
+// Row pairs per half-wave: input rows per workgroup = 16 x pairs. Gate_up takes 80 rows, so its
+// grid at the gpt-oss-20b shape (6 x 36 x 4 = 864 workgroups) is resident at once at four
+// workgroups per CU; with 64 rows it was 1,080, whose last 56 ran as a second round. Down keeps
+// 64 rows (its prologue pairs two threads with each gate_up column of its rows).
+// 64 rows for 3-bit codes, whose decode needs more registers (80 rows spilled there).
+constexpr int go_pairs_gu(int bits) { return bits == 3 ? 4 : 5; }
+constexpr int kGoPairsDN = 4, kGoRows = 16 * kGoPairsDN;
+constexpr int kGoMaxPart = 32;      // gate_up partials a down-prologue thread requests together
 
 struct GoLayer {
     const uint8_t* pool;
     int64_t slot_bytes;
     int nslots, k, H, I, G, E;
+    int gsh;            // log2(G) when G is a power of two, else -1
     int64_t n;          // H * I
     int64_t scale_off;  // byte offset of the fp16 scales in an expert (3n*bits/8)
     int64_t NG;         // groups per expert (3n/G); the mins follow the scales
@@ -118,18 +125,19 @@ __device__ __forceinline__ int go_expert(const GoLayer& L, int j) {
     return (f >= 0.f && f < (float)L.E && (float)e == f) ? e : -1;
 }
 
-// The workgroup's column GEMV over rows [r0, r0 + kGoRows) of a [R, C] input-major
+// The workgroup's column GEMV over rows [r0, r0 + 16*PAIRS) of a [R, C] input-major
 // matrix whose element (r, c) is flat element e0 + r*C + c of the expert.
 // Lane l of wave w owns columns col0 + 32*(l%32) .. +31 and, with half
-// h = l/32, the row pairs r0 + 16w + 8h + 2p (p < 4). xpair(r) returns the bf16
+// h = l/32, the row pairs r0 + 4*PAIRS*w + 2*PAIRS*h + 2p (p < PAIRS). xpair(r) returns the bf16
 // pair (x[r], x[r+1]) of the operand. Rows past R and columns past C read
 // clamped (in-bounds) weights and contribute nothing (zero operand / no
 // store). pre() runs after the weight loads are issued and before the first
 // xpair() (the down kernel forms its operand there). The partial sums of the 2*kGoWaves
 // half-waves are reduced through LDS in a fixed order and stored as
 // dst[c - col0] for c < C.
-template <int BITS, typename XPair, typename Pre>
-__device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int64_t e0, int R, int C, int G,
+// POW2G: G = 2^gsh, so a chunk's quant group is its element index shifted (else a division).
+template <int BITS, int PAIRS, bool POW2G, typename XPair, typename Pre>
+__device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int64_t e0, int R, int C, int G, int gsh,
                                            int64_t scale_off, int64_t NG, int r0, int col0, XPair xpair, Pre pre,
                                            float* red, float* __restrict__ dst, bool poison) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, h = lane >> 5, cl = lane & 31;
@@ -138,34 +146,35 @@ __device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int
     const int cc = col_on ? c : C - 32;
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(base + scale_off);
     const uint16_t* mn = sc + NG;
-    uint32_t cd[kGoPairs][2][BITS];
-    uint32_t sv[kGoPairs][2][2];
-    uint32_t xp[kGoPairs];
+    uint32_t cd[PAIRS][2][BITS];
+    uint32_t sv[PAIRS][2][2];
+    uint32_t xp[PAIRS];
 #pragma unroll
-    for (int p = 0; p < kGoPairs; ++p) {
-        const int r = r0 + 16 * wv + 8 * h + 2 * p;
+    for (int p = 0; p < PAIRS; ++p) {
+        const int r = r0 + 4 * PAIRS * wv + 2 * PAIRS * h + 2 * p;
         const bool row_on = r < R;  // R is even: the pair is whole or absent
         const int rr = row_on ? r : R - 2;
+        const int64_t eb = e0 + (int64_t)rr * C + cc;  // element of the pair's first row
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            const int64_t e = e0 + (int64_t)(rr + t) * C + cc;
+            const int64_t e = eb + (t ? C : 0);
             load_chunk<BITS>(base + e * BITS / 8, cd[p][t]);
-            const int64_t g = e / G;
+            const int64_t g = POW2G ? e >> gsh : e / G;  // e is a multiple of 32: the chunk is in one group
             sv[p][t][0] = sc[g];
             sv[p][t][1] = mn[g];
         }
     }
     pre();  // runs while the weight loads are in flight
 #pragma unroll
-    for (int p = 0; p < kGoPairs; ++p) {
-        const int r = r0 + 16 * wv + 8 * h + 2 * p;
+    for (int p = 0; p < PAIRS; ++p) {
+        const int r = r0 + 4 * PAIRS * wv + 2 * PAIRS * h + 2 * p;
         xp[p] = r < R ? xpair(r) : 0u;
     }
     float acc[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) acc[i] = 0.f;
 #pragma unroll
-    for (int p = 0; p < kGoPairs; ++p) {
+    for (int p = 0; p < PAIRS; ++p) {
         // the two rows' bf16 weights (RTNE of fp32(q*s) + m, q*s exact), one dot2
         float w0[32], w1[32];
         if constexpr (BITS == 3) {
@@ -200,21 +209,23 @@ __device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int
     }
 }
 
-// grid (ceil(2I / kGoCols), S1 = ceil(H / kGoRows), k)
-template <int BITS>
+// grid (ceil(2I / kGoCols), S1 = ceil(H / (16 * go_pairs_gu(BITS))), k)
+template <int BITS, bool POW2G>
 __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_gate_up(const GoLayer L) {
     __shared__ float red[2 * kGoWaves * kGoRedStride];
     const int j = blockIdx.z;
     const int slot = go_slot(L, j);
     const uint8_t* base = L.pool + (int64_t)(slot >= 0 ? slot : 0) * L.slot_bytes;
-    const int C = 2 * L.I, col0 = blockIdx.x * kGoCols, r0 = blockIdx.y * kGoRows;
+    constexpr int PAIRS = go_pairs_gu(BITS);
+    const int C = 2 * L.I, col0 = blockIdx.x * kGoCols, r0 = blockIdx.y * 16 * PAIRS;
     const uint32_t* xw = reinterpret_cast<const uint32_t*>(L.x);
-    go_colgemv<BITS>(base, 0, L.H, C, L.G, L.scale_off, L.NG, r0, col0, [&](int r) { return xw[r >> 1]; },
+    go_colgemv<BITS, PAIRS, POW2G>(base, 0, L.H, C, L.G, L.gsh, L.scale_off, L.NG, r0, col0,
+                                   [&](int r) { return xw[r >> 1]; },
                      [] {}, red, L.p1 + ((int64_t)j * L.S1 + blockIdx.y) * C + col0, slot < 0);
 }
 
 // grid (ceil(H / kGoCols), S2 = ceil(I / kGoRows), k)
-template <int BITS>
+template <int BITS, bool POW2G>
 __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
     __shared__ float red[2 * kGoWaves * kGoRedStride];
     __shared__ float gu[2 * kGoRows];
@@ -226,19 +237,20 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
     const int I2 = 2 * L.I, i0 = blockIdx.y * kGoRows;
     auto prologue = [&] {
         // gate_up outputs of activation rows i0 .. i0+kGoRows-1: gu = bf16(bf16(x . W) + bias). The S1
-        // partial sums of a column are split between two threads, each requesting 8 at a time.
+        // partial sums of a column are split between two threads, each requesting up to kGoMaxPart
+        // at once (all of them at the gpt-oss shapes) and adding them in order.
         const int t = threadIdx.x & (2 * kGoRows - 1), hf = threadIdx.x / (2 * kGoRows);
         const int c = 2 * i0 + t;
         const int per = (L.S1 + 1) / 2, s0 = hf * per, s1 = min(L.S1, s0 + per);
         float v = 0.f;
-        if (c < I2) {
+        if (c < I2 && s0 < s1) {
             const float* p = L.p1 + (int64_t)j * L.S1 * I2 + c;
-            for (int sb = s0; sb < s1; sb += 8) {
-                float u8[8];
+            for (int sb = s0; sb < s1; sb += kGoMaxPart) {
+                float u8[kGoMaxPart];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) u8[u] = p[(int64_t)min(sb + u, s1 - 1) * I2];
+                for (int u = 0; u < kGoMaxPart; ++u) u8[u] = p[(int64_t)min(sb + u, s1 - 1) * I2];
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
+                for (int u = 0; u < kGoMaxPart; ++u)
                     if (sb + u < s1) v += u8[u];
             }
         }
@@ -281,7 +293,8 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
         __syncthreads();
     };
     const uint8_t* base = L.pool + (int64_t)(slot >= 0 ? slot : 0) * L.slot_bytes;
-    go_colgemv<BITS>(base, 2 * L.n, L.I, L.H, L.G, L.scale_off, L.NG, i0, blockIdx.x * kGoCols,
+    go_colgemv<BITS, kGoPairsDN, POW2G>(base, 2 * L.n, L.I, L.H, L.G, L.gsh, L.scale_off, L.NG, i0,
+                                        blockIdx.x * kGoCols,
                      [&](int r) { return actp[(r - i0) >> 1]; }, prologue, red,
                      L.p2 + ((int64_t)j * L.S2 + blockIdx.y) * L.H + blockIdx.x * kGoCols, slot < 0);
 }
@@ -338,13 +351,13 @@ __global__ __launch_bounds__(kGoOutCols * kGoOutSlices) void k_go_out(const GoLa
     if (sl == 0 && h < L.H) L.out[h] = f32_to_bf16(y);
 }
 
-template <int BITS>
+template <int BITS, bool POW2G>
 static void launch_go(const GoLayer& L, hipStream_t st) {
     const int C1 = 2 * L.I;
-    hipLaunchKernelGGL(k_go_gate_up<BITS>, dim3((C1 + kGoCols - 1) / kGoCols, L.S1, L.k), dim3(64 * kGoWaves), 0,
-                       st, L);
-    hipLaunchKernelGGL(k_go_down<BITS>, dim3((L.H + kGoCols - 1) / kGoCols, L.S2, L.k), dim3(64 * kGoWaves), 0, st,
-                       L);
+    hipLaunchKernelGGL((k_go_gate_up<BITS, POW2G>), dim3((C1 + kGoCols - 1) / kGoCols, L.S1, L.k),
+                       dim3(64 * kGoWaves), 0, st, L);
+    hipLaunchKernelGGL((k_go_down<BITS, POW2G>), dim3((L.H + kGoCols - 1) / kGoCols, L.S2, L.k),
+                       dim3(64 * kGoWaves), 0, st, L);
     hipLaunchKernelGGL(k_go_out, dim3((L.H + kGoOutCols - 1) / kGoOutCols), dim3(kGoOutCols * kGoOutSlices), 0, st, L);
 }
 
@@ -370,7 +383,7 @@ extern "C" int wisp_mxfp4_to_bf16(const uint8_t* blocks, const uint8_t* scales, 
 
 extern "C" int64_t wisp_gptoss_ws_bytes(int k, int64_t H, int64_t I) {
     if (k < 1 || H < 1 || I < 1) return -1;
-    const int64_t S1 = (H + kGoRows - 1) / kGoRows, S2 = (I + kGoRows - 1) / kGoRows;
+    const int64_t S1 = (H + 63) / 64, S2 = (I + kGoRows - 1) / kGoRows;  // S1: the most gate_up row blocks
     return 4 * ((int64_t)k * S1 * 2 * I + (int64_t)k * S2 * H);
 }
 
@@ -414,16 +427,19 @@ extern "C" int wisp_gptoss_decode(const uint8_t* pool, int64_t slot_bytes, int64
     L.db = down_bias;
     L.alpha = alpha;
     L.limit = limit;
-    L.S1 = (int)((H + kGoRows - 1) / kGoRows);
+    const int rows_gu = 16 * go_pairs_gu(bits);
+    L.S1 = (int)((H + rows_gu - 1) / rows_gu);
     L.S2 = (int)((I + kGoRows - 1) / kGoRows);
     L.p1 = static_cast<float*>(ws);
     L.p2 = L.p1 + (int64_t)k * L.S1 * 2 * I;
     L.out = out;
     hipStream_t st = (hipStream_t)stream;
+    L.gsh = (group & (group - 1)) == 0 ? __builtin_ctzll((unsigned long long)group) : -1;
+    const bool p2 = L.gsh >= 0;
     switch (bits) {
-    case 4: launch_go<4>(L, st); break;
-    case 3: launch_go<3>(L, st); break;
-    default: launch_go<2>(L, st); break;
+    case 4: p2 ? launch_go<4, true>(L, st) : launch_go<4, false>(L, st); break;
+    case 3: p2 ? launch_go<3, true>(L, st) : launch_go<3, false>(L, st); break;
+    default: p2 ? launch_go<2, true>(L, st) : launch_go<2, false>(L, st); break;
     }
     return check_launch("k_go");
 }
