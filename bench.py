@@ -995,15 +995,29 @@ def run_gptoss(a) -> dict:
 
 
 def _cpu_model() -> str:
-    """The host CPU's model name (the baseline depends on it)."""
+    """The host CPU as /proc/cpuinfo and sysfs describe it (the baseline depends on it): model
+    name, family/model/stepping, logical CPUs online and the L3 size of cpu0's cache."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key in ("model name", "cpu family", "model", "stepping") and key not in info:
+                    info[key] = val.strip()
     except OSError:
         pass
-    return platform.processor() or platform.machine()
+    name = info.get("model name") or platform.processor() or platform.machine()
+    parts = [name]
+    if "cpu family" in info:
+        parts.append(f"family {info['cpu family']} model {info.get('model', '?')} stepping {info.get('stepping', '?')}")
+    parts.append(f"{os.cpu_count()} logical CPUs")
+    try:
+        with open("/sys/devices/system/cpu/cpu0/cache/index3/size") as f:
+            parts.append(f"L3 {f.read().strip()} (cpu0's)")
+    except OSError:
+        pass
+    return ", ".join(parts)
 
 
 def main():
@@ -1209,17 +1223,20 @@ def main():
         sys.path.insert(0, ROOT)
         from oracle import cpu_baseline as CB  # the baseline side only
 
-        # bounded sample: 96 distinct experts from one layer pool on the host, 8 routed per layer
-        rows = W.pool[:96].cpu()
-        lg = torch.randn((64, 96), generator=torch.Generator().manual_seed(5))
+        # bounded sample: NX distinct experts (the first layer pools) on the host, 8 routed per layer;
+        # NX * nbytes (1.2 GB at 4 bits) is larger than any EPYC's L3, so the weights come from DRAM
+        NX = min(480, W.pool.shape[0])
+        rows = W.pool[:NX].cpu()
+        lg = torch.randn((64, NX), generator=torch.Generator().manual_seed(5))
         s_cpu, w_cpu = route(lg, K_TOP)
         routes = [(s_cpu[i].tolist(), w_cpu[i].float().tolist()) for i in range(64)]
         xcpu = [W.xs[i % W.layers].cpu() for i in range(8)]
-        med, cnt, thr = CB.time_layers(rows, routes, xcpu, H, I, bits, G, budget_s=a.cpu_budget)
+        med, cnt, thr = CB.time_layers(rows, routes, xcpu, H, I, bits, G, budget_s=a.cpu_budget, warm=5)
         # the same layer on one thread, and C1 (one expert at weight 1), on smaller samples
-        med1, cnt1, _ = CB.time_layers(rows, routes, xcpu, H, I, bits, G, budget_s=a.cpu_budget / 3, warm=1, threads=1)
-        one = [([r], [1.0]) for r in range(96)]
-        medc1, cntc1, _ = CB.time_layers(rows, one, xcpu, H, I, bits, G, budget_s=a.cpu_budget / 5, threads=thr)
+        med1, cnt1, _ = CB.time_layers(rows, routes, xcpu, H, I, bits, G, budget_s=a.cpu_budget / 3, warm=2, threads=1)
+        one = [([r], [1.0]) for r in range(NX)]
+        medc1, cntc1, _ = CB.time_layers(rows, one, xcpu, H, I, bits, G, budget_s=a.cpu_budget / 5, warm=5,
+                                         threads=thr)
         # the same layer on both paths: step 47 (the last layer pool, slot offsets past 15 GB)
         i_chk = W.layers - 1
         with torch.cuda.stream(W.stream):
@@ -1238,8 +1255,9 @@ def main():
             "unit": "GB/s",
             "cores": thr,
             "kind": "port",
-            "sample": f"{cnt} MoE layers (8 of 96 distinct experts each, rotated), median; torch dequant->bf16 "
-                      f"F.linear on {thr} threads; {round(med * 1e6, 1)} us/layer; cpu={cpu}",
+            "sample": f"{cnt} MoE layers after 5 warm-up ones (8 of {NX} distinct experts each, "
+                      f"{NX * W.nb / 1e9:.2f} GB of weights, rotated), median; torch dequant->bf16 F.linear on "
+                      f"{thr} threads; {round(med * 1e6, 1)} us/layer; cpu={cpu}",
             "us_per_layer": round(med * 1e6, 1),
             "rel_l2_gpu_vs_cpu_one_layer": round(rel, 6),
             "rel_l2_note": "bf16 dequant->F.linear rounds weights and intermediates to bf16 (expected ~3-5e-3); "

@@ -57,8 +57,9 @@ def moe_layer_cpu(rows: torch.Tensor, slots, weights, x: torch.Tensor, H: int, I
 
 
 def time_layers(rows: torch.Tensor, routes, xs, H: int, I: int, bits: int, group: int = 128, budget_s: float = 15.0,
-                warm: int = 2, threads: int | None = None):
-    """Median seconds per layer over a bounded sample (stops after ~budget_s seconds).
+                warm: int = 5, threads: int | None = None):
+    """Median seconds per layer over a bounded sample (stops after ~budget_s seconds), after
+    `warm` untimed layers.
     `rows` are host expert buffers; `routes` is a list of (slots, weights); distinct
     experts are rotated so reads come from DRAM (microbench.py:78)."""
     threads = threads or os.cpu_count() or 1
