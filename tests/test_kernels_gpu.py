@@ -160,6 +160,30 @@ def test_gate_up_activation(bits, H, I, group):
     assert err <= 2e-7, err
 
 
+@pytest.mark.parametrize("bits", [4, 3, 2])
+@pytest.mark.parametrize("xdt", [np.float32, np.float16])
+@pytest.mark.parametrize("H,I,group", [(2048, 768, 128), (256, 128, 128)])
+def test_gate_up_activation_float_x(bits, xdt, H, I, group):
+    """A float32 (or float16) x, not representable in bf16, against the binary64 layer on the same
+    values: the reference widens any float x exactly (kernels.py:50-51), and so does kernel 1 (every
+    code x x product exact in fp32); what is left is the fp32 accumulation, as in the reference. A
+    product of a code with a bf16 or fp16 x has at most 12 / 15 significant bits, so fp32 sums of
+    them round rarely (<= 2e-7 measured); with a float32 x every product has 24+ bits and every
+    addition rounds (3-6e-7 measured), hence 1e-6 for float32, 1000x below the layer's 1e-3 bar."""
+    rng = np.random.default_rng(bits * 7 + H)
+    n, E, k = H * I, 4, 3
+    pool = _pool(E, H, I, bits, group, seed=bits * 5 + I)
+    sel, rw = _route(rng, E, k)
+    x = (rng.standard_normal(H) * (1.0 + 1e-3 * rng.standard_normal(H))).astype(xdt)
+    a_ref, _, _ = O.moe_layer_f64(pool, sel, rw, x, H, I, bits, group)
+    meta = torch.from_numpy(O.meta(sel, rw)).to(DEV)
+    a = kernels.gate_up_act(torch.from_numpy(pool).to(DEV), meta, torch.from_numpy(x).to(DEV), k, n, H, I, bits,
+                            group)
+    err = _rel_l2(a.cpu().numpy().astype(np.float64), a_ref)
+    print(f"gate_up float x {np.dtype(xdt).name} bits={bits} H={H}: rel-L2 {err:.3e}")
+    assert err <= (1e-6 if xdt == np.float32 else 2e-7), err
+
+
 @pytest.mark.parametrize("H,I,group,E,k", [(256, 128, 128, 6, 3), (2048, 768, 128, 10, 8)])
 def test_moe_decode_q4_per_expert_path(H, I, group, E, k):
     """kernels.py:115-137: slots int64 + weight tensor, per-expert y then torch weighted sum."""
