@@ -91,7 +91,7 @@ constexpr int kGoRedStride = 1056;  // LDS floats per partial vector (32 x 33: c
 // 64 rows for 3-bit codes, whose decode needs more registers (80 rows spilled there).
 constexpr int go_pairs_gu(int bits) { return bits == 3 ? 4 : 5; }
 constexpr int kGoPairsDN = 4, kGoRows = 16 * kGoPairsDN;
-constexpr int kGoMaxPart = 32;      // gate_up partials a down-prologue thread requests together
+constexpr int kGoMaxPart = 20;      // gate_up partials a down-prologue thread requests together (18 at H = 2880)
 
 struct GoLayer {
     const uint8_t* pool;
@@ -235,23 +235,34 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
     const int j = blockIdx.z;
     const int slot = go_slot(L, j), ex = go_expert(L, j);
     const int I2 = 2 * L.I, i0 = blockIdx.y * kGoRows;
-    auto prologue = [&] {
-        // gate_up outputs of activation rows i0 .. i0+kGoRows-1: gu = bf16(bf16(x . W) + bias). The S1
-        // partial sums of a column are split between two threads, each requesting up to kGoMaxPart
-        // at once (all of them at the gpt-oss shapes) and adding them in order.
-        const int t = threadIdx.x & (2 * kGoRows - 1), hf = threadIdx.x / (2 * kGoRows);
-        const int c = 2 * i0 + t;
-        const int per = (L.S1 + 1) / 2, s0 = hf * per, s1 = min(L.S1, s0 + per);
-        float v = 0.f;
-        if (c < I2 && s0 < s1) {
-            const float* p = L.p1 + (int64_t)j * L.S1 * I2 + c;
-            for (int sb = s0; sb < s1; sb += kGoMaxPart) {
-                float u8[kGoMaxPart];
+    // gate_up outputs of activation rows i0 .. i0+kGoRows-1: gu = bf16(bf16(x . W) + bias). The S1 partial
+    // sums of a column are split between two threads. The first kGoMaxPart of a thread's partials (all of
+    // them at the gpt-oss shapes) and the column's bias are requested before the weight rows: vector loads
+    // retire in issue order, so requested after them they would wait for the whole weight stream, and the
+    // prologue below would start only once the weights were in. Indices are clamped so every load is
+    // unconditional; only the sums are predicated.
+    const int t = threadIdx.x & (2 * kGoRows - 1), hf = threadIdx.x / (2 * kGoRows);
+    const int c = 2 * i0 + t, cl = min(c, I2 - 1);
+    const int per = (L.S1 + 1) / 2, s0 = hf * per, s1 = min(L.S1, s0 + per);
+    const float* pcol = L.p1 + (int64_t)j * L.S1 * I2 + cl;
+    float u8[kGoMaxPart];
 #pragma unroll
-                for (int u = 0; u < kGoMaxPart; ++u) u8[u] = p[(int64_t)min(sb + u, s1 - 1) * I2];
+    for (int u = 0; u < kGoMaxPart; ++u) u8[u] = pcol[(int64_t)min(s0 + u, L.S1 - 1) * I2];
+    const uint16_t bias = L.gub[(int64_t)(ex >= 0 ? ex : 0) * I2 + cl];
+    __builtin_amdgcn_sched_barrier(0);
+    auto prologue = [&] {
+        float v = 0.f;
+        if (c < I2) {
+#pragma unroll
+            for (int u = 0; u < kGoMaxPart; ++u)
+                if (s0 + u < s1) v += u8[u];
+            for (int sb = s0 + kGoMaxPart; sb < s1; sb += kGoMaxPart) {  // more than 2 kGoMaxPart row blocks
+                float w8[kGoMaxPart];
+#pragma unroll
+                for (int u = 0; u < kGoMaxPart; ++u) w8[u] = pcol[(int64_t)min(sb + u, s1 - 1) * I2];
 #pragma unroll
                 for (int u = 0; u < kGoMaxPart; ++u)
-                    if (sb + u < s1) v += u8[u];
+                    if (sb + u < s1) v += w8[u];
             }
         }
         half_sum[hf][t] = v;
@@ -260,7 +271,7 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
             float g = 0.f;
             if (c < I2) {
                 g = half_sum[0][t] + half_sum[1][t];
-                g = ex >= 0 ? bf16r(bf16r(g) + bf16_to_f32(L.gub[(int64_t)ex * I2 + c])) : __builtin_nanf("");
+                g = ex >= 0 ? bf16r(bf16r(g) + bf16_to_f32(bias)) : __builtin_nanf("");
             }
             gu[t] = g;
         }
