@@ -136,7 +136,10 @@ __device__ __forceinline__ int go_expert(const GoLayer& L, int j) {
 // half-waves are reduced through LDS in a fixed order and stored as
 // dst[c - col0] for c < C.
 // POW2G: G = 2^gsh, so a chunk's quant group is its element index shifted (else a division).
-template <int BITS, int PAIRS, bool POW2G, typename XPair, typename Pre>
+// XFIRST: xpair reads global memory and needs nothing from pre(), so the operand pairs are
+// requested before the weight rows (loads retire in issue order: requested after them, the
+// first dot product would wait for the wave's whole weight stream).
+template <int BITS, int PAIRS, bool POW2G, bool XFIRST, typename XPair, typename Pre>
 __device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int64_t e0, int R, int C, int G, int gsh,
                                            int64_t scale_off, int64_t NG, int r0, int col0, XPair xpair, Pre pre,
                                            float* red, float* __restrict__ dst, bool poison) {
@@ -149,6 +152,13 @@ __device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int
     uint32_t cd[PAIRS][2][BITS];
     uint32_t sv[PAIRS][2][2];
     uint32_t xp[PAIRS];
+    if constexpr (XFIRST) {
+#pragma unroll
+        for (int p = 0; p < PAIRS; ++p) {
+            const int r = r0 + 4 * PAIRS * wv + 2 * PAIRS * h + 2 * p;
+            xp[p] = xpair(min(r, R - 2));
+        }
+    }
 #pragma unroll
     for (int p = 0; p < PAIRS; ++p) {
         const int r = r0 + 4 * PAIRS * wv + 2 * PAIRS * h + 2 * p;
@@ -168,7 +178,8 @@ __device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int
 #pragma unroll
     for (int p = 0; p < PAIRS; ++p) {
         const int r = r0 + 4 * PAIRS * wv + 2 * PAIRS * h + 2 * p;
-        xp[p] = r < R ? xpair(r) : 0u;
+        if constexpr (!XFIRST) xp[p] = r < R ? xpair(r) : 0u;
+        else if (r >= R) xp[p] = 0u;  // (the row pair is absent: its loads read a clamped, real pair)
     }
     float acc[32];
 #pragma unroll
@@ -219,7 +230,8 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_gate_up(const GoLayer L
     constexpr int PAIRS = go_pairs_gu(BITS);
     const int C = 2 * L.I, col0 = blockIdx.x * kGoCols, r0 = blockIdx.y * 16 * PAIRS;
     const uint32_t* xw = reinterpret_cast<const uint32_t*>(L.x);
-    go_colgemv<BITS, PAIRS, POW2G>(base, 0, L.H, C, L.G, L.gsh, L.scale_off, L.NG, r0, col0,
+    // (3-bit codes keep the operand loads after the weights: requested first they spilled there)
+    go_colgemv<BITS, PAIRS, POW2G, BITS != 3>(base, 0, L.H, C, L.G, L.gsh, L.scale_off, L.NG, r0, col0,
                                    [&](int r) { return xw[r >> 1]; },
                      [] {}, red, L.p1 + ((int64_t)j * L.S1 + blockIdx.y) * C + col0, slot < 0);
 }
@@ -304,7 +316,7 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
         __syncthreads();
     };
     const uint8_t* base = L.pool + (int64_t)(slot >= 0 ? slot : 0) * L.slot_bytes;
-    go_colgemv<BITS, kGoPairsDN, POW2G>(base, 2 * L.n, L.I, L.H, L.G, L.gsh, L.scale_off, L.NG, i0,
+    go_colgemv<BITS, kGoPairsDN, POW2G, false>(base, 2 * L.n, L.I, L.H, L.G, L.gsh, L.scale_off, L.NG, i0,
                                         blockIdx.x * kGoCols,
                      [&](int r) { return actp[(r - i0) >> 1]; }, prologue, red,
                      L.p2 + ((int64_t)j * L.S2 + blockIdx.y) * L.H + blockIdx.x * kGoCols, slot < 0);
