@@ -65,8 +65,9 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 
 // Workgroup of 4 waves; wave w owns rows (blockIdx.x*4 + w)*R .. +R-1. A lane
 // owns the 16-byte chunks lane, lane+64, ... (CPL = K/512 of them) of every
-// row, so each load instruction of a wave reads 1 KB contiguous. All weight
-// loads are issued before the input is formed.
+// row, so each load instruction of a wave reads 1 KB contiguous. The input's
+// loads are issued first, then every weight load; the input is formed while the
+// weights stream.
 template <int CPL, int R, bool NORM>
 __global__ __launch_bounds__(256) void k_dl_gemv(const GemvArgs g) {
 #pragma clang fp contract(off)
@@ -76,6 +77,30 @@ __global__ __launch_bounds__(256) void k_dl_gemv(const GemvArgs g) {
     const int wv = threadIdx.x >> 6;
     const int K = CPL * 512;
     const int row0 = (blockIdx.x * 4 + wv) * R;
+
+    // The operand's inputs (and the residual) are requested before the weight rows: vector loads
+    // retire in issue order, so requested after them the RMSNorm below would start only once the
+    // wave's whole weight stream had arrived.
+    const uint16_t* A = g.a + (g.a_row ? *g.a_row * (int64_t)K : 0);
+    const uint4* a4 = reinterpret_cast<const uint4*>(A);
+    constexpr int PT = (CPL * 64 + 255) / 256;  // 16-byte chunks per thread (NORM)
+    uint4 av[NORM ? PT : 1], bv[NORM ? PT : 1], nv[NORM ? PT : 1];
+    uint4 xv[CPL];
+    if constexpr (NORM) {
+        const uint4* b4 = reinterpret_cast<const uint4*>(g.b);
+        const uint4* n4 = reinterpret_cast<const uint4*>(g.nw);
+#pragma unroll
+        for (int t = 0; t < PT; ++t) {
+            const int i = min((int)threadIdx.x + 256 * t, CPL * 64 - 1);
+            av[t] = a4[i];
+            if (g.b) bv[t] = b4[i];
+            nv[t] = n4[i];
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) xv[c] = a4[c * 64 + lane];
+    }
+    const uint16_t resv = g.res && lane < R ? g.res[min(row0 + lane, g.O - 1)] : (uint16_t)0;
 
     uint4 wr[R][CPL];
 #pragma unroll
@@ -92,26 +117,20 @@ __global__ __launch_bounds__(256) void k_dl_gemv(const GemvArgs g) {
             wr[r][c] = make_uint4(v.x, v.y, v.z, v.w);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);  // the prologue's arithmetic stays behind every load
 
-    uint4 xv[CPL];
-    const uint16_t* A = g.a + (g.a_row ? *g.a_row * (int64_t)K : 0);
-    if (NORM) {
-        // h = a (+ b) in bf16; x = bf16(w * bf16(h * rsqrt(mean(h^2) + eps))); the norm
-        // weights are requested with the inputs, before the reduction
-        const uint4* a4 = reinterpret_cast<const uint4*>(A);
-        const uint4* b4 = reinterpret_cast<const uint4*>(g.b);
-        const uint4* n4 = reinterpret_cast<const uint4*>(g.nw);
-        constexpr int PT = (CPL * 64 + 255) / 256;  // 16-byte chunks per thread
-        uint4 nv[PT];
-#pragma unroll
-        for (int t = 0; t < PT; ++t) nv[t] = n4[min((int)threadIdx.x + 256 * t, CPL * 64 - 1)];
+    if constexpr (NORM) {
+        // h = a (+ b) in bf16; x = bf16(w * bf16(h * rsqrt(mean(h^2) + eps)))
         float ss = 0.f;
-        for (int i = threadIdx.x; i < CPL * 64; i += 256) {
+#pragma unroll
+        for (int t = 0; t < PT; ++t) {
+            const int i = threadIdx.x + 256 * t;
+            if (i >= CPL * 64) break;
             float h[8];
-            unpack8(a4[i], h);
+            unpack8(av[t], h);
             if (g.b) {
                 float bb[8];
-                unpack8(b4[i], bb);
+                unpack8(bv[t], bb);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) h[e] = rbf(h[e] + bb[e]);
             }
@@ -144,10 +163,6 @@ __global__ __launch_bounds__(256) void k_dl_gemv(const GemvArgs g) {
         __syncthreads();
 #pragma unroll
         for (int c = 0; c < CPL; ++c) xv[c] = xs[c * 64 + lane];
-    } else {
-        const uint4* a4 = reinterpret_cast<const uint4*>(A);
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) xv[c] = a4[c * 64 + lane];
     }
 
     float acc[R];
@@ -171,7 +186,7 @@ __global__ __launch_bounds__(256) void k_dl_gemv(const GemvArgs g) {
         const int o = row0 + lane;
         if (o < g.O) {
             float yv = rbf(v);
-            if (g.res) yv = rbf(bf(g.res[o]) + yv);
+            if (g.res) yv = rbf(bf(resv) + yv);
             g.y[o] = f32_to_bf16(yv);
         }
     }
