@@ -340,6 +340,13 @@ __global__ __launch_bounds__(kGoOutCols * kGoOutSlices) void k_go_out(const GoLa
         float v[kGoOutBatch];
 #pragma unroll
         for (int jj = 0; jj < kGoOutBatch; ++jj) v[jj] = 0.f;
+        // The batch's routing weights, expert ids and down biases are requested right after the first
+        // partials: not before them (the expert ids are a round trip that would hold up the partials'
+        // issue) and not after the sums (a round trip of its own at the end). Indices are clamped, so
+        // every load is unconditional.
+        float wj[kGoOutBatch];
+        int exj[kGoOutBatch];
+        uint16_t dbv[kGoOutBatch];
         for (int sb = s0; sb < s1; sb += kGoOutUnroll) {
             float t[kGoOutBatch][kGoOutUnroll];
 #pragma unroll
@@ -349,6 +356,16 @@ __global__ __launch_bounds__(kGoOutCols * kGoOutSlices) void k_go_out(const GoLa
                     const int j = min(j0 + jj, L.k - 1), s = min(sb + u, s1 - 1);
                     t[jj][u] = L.p2[((int64_t)j * L.S2 + s) * L.H + hh];
                 }
+            if (sb == s0) {
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int jj = 0; jj < kGoOutBatch; ++jj) {
+                    const int j = min(j0 + jj, L.k - 1);
+                    exj[jj] = go_expert(L, j);
+                    wj[jj] = L.meta[L.k + j];
+                    dbv[jj] = L.db[(int64_t)(exj[jj] >= 0 ? exj[jj] : 0) * L.H + hh];
+                }
+            }
 #pragma unroll
             for (int jj = 0; jj < kGoOutBatch; ++jj)
 #pragma unroll
@@ -359,13 +376,14 @@ __global__ __launch_bounds__(kGoOutCols * kGoOutSlices) void k_go_out(const GoLa
         for (int jj = 0; jj < kGoOutBatch; ++jj) part[sl][jj][c] = v[jj];
         __syncthreads();
         if (sl == 0) {
-            for (int jj = 0; jj < kGoOutBatch && j0 + jj < L.k; ++jj) {
-                const int j = j0 + jj, ex = go_expert(L, j);
+#pragma unroll
+            for (int jj = 0; jj < kGoOutBatch; ++jj) {
+                if (j0 + jj >= L.k) break;
                 float sum = part[0][jj][c];
 #pragma unroll
                 for (int q = 1; q < kGoOutSlices; ++q) sum += part[q][jj][c];
-                const float w = bf16r(L.meta[L.k + j]);
-                const float o = ex >= 0 ? bf16r(bf16r(sum) + bf16_to_f32(L.db[(int64_t)ex * L.H + hh])) : __builtin_nanf("");
+                const float w = bf16r(wj[jj]);
+                const float o = exj[jj] >= 0 ? bf16r(bf16r(sum) + bf16_to_f32(dbv[jj])) : __builtin_nanf("");
                 y += bf16r(o * w);
             }
         }
