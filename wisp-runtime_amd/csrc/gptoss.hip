@@ -347,6 +347,12 @@ __global__ __launch_bounds__(kGoOutCols * kGoOutSlices) void k_go_out(const GoLa
         float wj[kGoOutBatch];
         int exj[kGoOutBatch];
         uint16_t dbv[kGoOutBatch];
+#pragma unroll
+        for (int jj = 0; jj < kGoOutBatch; ++jj) {  // (set below in the slice's first step; slice 0 has one)
+            wj[jj] = 0.f;
+            exj[jj] = -1;
+            dbv[jj] = 0;
+        }
         for (int sb = s0; sb < s1; sb += kGoOutUnroll) {
             float t[kGoOutBatch][kGoOutUnroll];
 #pragma unroll
