@@ -69,8 +69,6 @@ __device__ __forceinline__ f32x4_t mfma_k16(uint2 a, uint2 b, f32x4_t c) {
 //    them into its own operands for that row (its loads of row pos read the old cache).
 //    The inputs of that arithmetic are loaded before the K/V rows: loads retire in
 //    issue order, so the head norms run while the K/V data is still arriving.
-//  * A workgroup whose chunk lies past pos reads nothing and writes an empty record
-//    (m = -inf, l = 0): the merge then needs no position of its own.
 // ---------------------------------------------------------------------------
 struct QkPrep {
     const uint16_t* qkv;  // [q (Hq heads) | k (Hk) | v (Hk)] of D
@@ -100,14 +98,7 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
     const int split = blockIdx.x, hk = blockIdx.y;
     const int64_t pos = *pos_ptr;
     const int p0 = split * kChunk;
-    float* rec = part + ((int64_t)hk * nsplit + split) * G * (2 + D);
-    if ((int64_t)p0 > pos) {  // the whole workgroup: chunks past pos are never read
-        if (threadIdx.x < G) {
-            rec[threadIdx.x * (2 + D)] = -INFINITY;
-            rec[threadIdx.x * (2 + D) + 1] = 0.f;
-        }
-        return;
-    }
+    if ((int64_t)p0 > pos) return;  // the whole workgroup: chunks past pos are never read
     const int plast = (int)min<int64_t>(min<int64_t>(pos, (int64_t)p0 + kChunk - 1), (int64_t)tmax - 1);
     const int pw = p0 + 16 * wv;
     const uint16_t* kh = kc + hk * head_stride;
@@ -252,6 +243,7 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
     }
     __syncthreads();
 
+    float* rec = part + ((int64_t)hk * nsplit + split) * G * (2 + D);
     for (int e = threadIdx.x; e < HQ * D; e += 256) {
         const int hq = e / D, d = e - hq * D;
         const f32x4_t v = (red_o[0][hq][d] + red_o[1][hq][d]) + (red_o[2][hq][d] + red_o[3][hq][d]);
@@ -286,17 +278,18 @@ __device__ __forceinline__ float row0_max(float v) {
 // batches of 16 with a running maximum. Lane b < 16 reads the m and l of the batch's
 // chunk b and computes its weight (one exponential per chunk); the weights reach the
 // o sums of every lane through readlane. The four waves' sums are rescaled to the
-// common maximum in LDS. Every chunk has a record; those past pos are empty (m =
-// -inf, l = 0, o never written), weigh 0 and are skipped, so no position is read.
+// common maximum in LDS. Only the chunks up to pos have records (pos read from device
+// memory, so graphs follow it).
 template <int D>
-__global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ part, int G, int nsplit,
-                                                    uint16_t* __restrict__ out) {
+__global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ part, const int64_t* __restrict__ pos_ptr,
+                                                    int G, int nsplit, uint16_t* __restrict__ out) {
     constexpr int DPL = D / 64, B = 16;
     __shared__ float red_m[4], red_l[4];
     __shared__ float red_o[4][D];
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // chunk indices in SGPRs
     const int h = blockIdx.x, hk = h / G, g = h - hk * G;
-    const int nv = nsplit;
+    const int64_t pos = *pos_ptr;
+    const int nv = (int)min<int64_t>(nsplit, pos / kChunk + 1);
     const float* base = part + ((int64_t)hk * nsplit * G + g) * (2 + D);
     const int64_t stride = (int64_t)G * (2 + D);
     float M = -INFINITY, L = 0.f, O[DPL];
@@ -311,23 +304,21 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ pa
             for (int t = 0; t < DPL; ++t) ov[b][t] = base[c * stride + 2 + lane * DPL + t];
         }
         const int cl = c0 + wv + 4 * (lane & 15);
+        const bool have = lane < 16 && cl < nv;
         const int cc = min(cl, nv - 1);
-        const float mc = lane < 16 && cl < nv ? base[cc * stride] : -INFINITY;
+        const float mc = have ? base[cc * stride] : -INFINITY;
         const float lc = base[cc * stride + 1];
-        const bool have = mc != -INFINITY;  // a chunk at or before pos
         const float Mn = fmaxf(M, row0_max(mc));
         const float f = M == -INFINITY ? 0.f : expf(M - Mn);  // rescale of the sums so far
         const float w = have ? expf(mc - Mn) : 0.f;
-        L = L * f + row0_sum(have ? w * lc : 0.f);
+        L = L * f + row0_sum(w * lc);
 #pragma unroll
         for (int t = 0; t < DPL; ++t) O[t] *= f;
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const float wb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), b));
-            if (wb != 0.f) {  // uniform: empty records' o are never read into the sums
 #pragma unroll
-                for (int t = 0; t < DPL; ++t) O[t] += wb * ov[b][t];
-            }
+            for (int t = 0; t < DPL; ++t) O[t] += wb * ov[b][t];
         }
         M = Mn;
     }
@@ -362,7 +353,7 @@ static void launch_attn(const uint16_t* q, const uint16_t* kc, const uint16_t* v
     else
         hipLaunchKernelGGL((k_attn_mfma<G, D, false>), dim3(nsplit, hk), dim3(256), 0, st, q, kc, vc, hs, pos, tmax,
                            scale, part, nsplit, QkPrep{});
-    hipLaunchKernelGGL((k_attn_merge<D>), dim3(hk * G), dim3(256), 0, st, part, G, nsplit, out);
+    hipLaunchKernelGGL((k_attn_merge<D>), dim3(hk * G), dim3(256), 0, st, part, pos, G, nsplit, out);
 }
 
 static int attn_dispatch(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, int64_t kv_head_stride,
