@@ -316,7 +316,8 @@ int wisp_cache_resize(void* cache, int64_t nslots);
  *
  * begin: copy the core's LRU state to the device, ordered on `stream` after the
  * copies already issued. Needs the LRU policy, copy mode 1, nslots - n_static <=
- * 8192, nslots <= 2^20 and the free slots at the top of the pool (as the core
+ * 26880 (the step holds every dynamic slot's eviction key in registers: one wave
+ * up to 1024 slots, else up to 15 waves of 28 keys per thread), nslots <= 2^20 and the free slots at the top of the pool (as the core
  * hands them out); WISP_EINVAL otherwise. A no-op when device paging is on.
  * While it is on, wisp_cache_issue / _ensure / _prepare_* / _resize return
  * WISP_EINVAL (the host core is stale until _sync or _end). */

@@ -83,10 +83,10 @@ def test_device_steps_match_reference_lru(store, nslots, k, use_row):
 
 @pytest.mark.parametrize("nslots,n_static", [(1500, 0), (6144, 0), (2100, 40)])
 def test_device_steps_past_1024_dynamic_slots(nslots, n_static):
-    """Pools of more than 1024 dynamic slots stage the eviction keys in batches of 1024
-    slots while the step runs (the other staging path of k_lru_step). k = 16 steps fill the
-    pool to 8 free slots, then one step of 16 new keys takes the 8 free slots and evicts 8,
-    then random steps over 8192 keys mix hits with evicting misses; every step's meta, the
+    """Pools of more than 1024 dynamic slots hold the eviction keys in the registers of the
+    waves beside the one that routes (the multi-wave form of k_lru_step). k = 16 steps fill
+    the pool to 8 free slots, then one step of 16 new keys takes the 8 free slots and evicts
+    8, then random steps over 8192 keys mix hits with evicting misses; every step's meta, the
     counters at every sync and the final state match the reference LRU."""
     L, E, n, k = 64, 128, 1024, 16  # 8192 keys of 1632-byte rows
     st = ExpertStore(L, E, n, 4, 128)
@@ -128,6 +128,99 @@ def test_device_steps_past_1024_dynamic_slots(nslots, n_static):
             assert c.core.stats == ref.counts, it  # (ends device paging)
             c.device_begin()
     assert ref.counts["evictions"] > 600
+    _check_state(c, ref, st)
+    c.free()
+
+
+@pytest.mark.parametrize("nslots,n_static", [(12000, 0), (20000, 300), (26880, 0)])
+def test_device_steps_in_large_pools(nslots, n_static):
+    """Pools up to the device step's limit of 26,880 dynamic slots (15 waves of 28 eviction
+    keys per thread): filled to 8 free slots, a mixed free/evicting step, then random steps
+    over 32,768 keys taken three ways in turn -- the LRU step on the row's ids, the route +
+    LRU kernel with forced ids, and a captured graph of the LRU step replayed with new ids --
+    each step's meta and the final state equal to the reference LRU's."""
+    L, E, n, k = 256, 128, 1024, 16  # 32768 keys of 1632-byte rows
+    st = ExpertStore(L, E, n, 4, 128)
+    gen = torch.Generator().manual_seed(nslots)
+    st.host.copy_(torch.randint(0, 256, tuple(st.host.shape), dtype=torch.uint8, generator=gen))
+    pre = list(range(32000, 32000 + n_static))
+    c = ExpertCache(st, nslots, n_static=n_static, preload_keys=pre or None, copy="kernel")
+    ref = RefCore(nslots, "lru", n_static=n_static)
+    if pre:
+        ref.preload(pre)
+    meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    ids = torch.zeros(k, dtype=torch.int64, device=DEV)
+    row = _row(np.zeros(k), np.linspace(0.05, 0.8, k))
+    # 48 router logits: the route kernel requests the key -> slot entries of ids below 64, so
+    # forced ids of 64 .. 127 take its other path (a read of the entry)
+    logits = torch.randn(48, device=DEV).to(torch.bfloat16)
+    rng = np.random.default_rng(nslots + n_static)
+    c.device_begin()
+    c.device_step(row, None, 0, E, 0, meta)  # warm-up launch before capture: changes nothing
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    gbase = 7 * E  # the captured step's layer
+    with torch.cuda.graph(g):
+        c.device_step(row, ids, gbase, E, k, meta)
+
+    def step(keys, it, how):
+        keys = [int(v) for v in keys]
+        n_k = len(keys)
+        layer = keys[0] // E
+        local = np.array([v - layer * E for v in keys], dtype=np.int64)
+        assert all(0 <= v < E for v in local)
+        if how == "graph":  # the captured step: k keys of layer gbase / E
+            assert layer == gbase // E and n_k == k
+            ids.copy_(torch.from_numpy(local))
+            g.replay()
+        elif how == "route":  # every lane's id forced: the router's own choice is replaced
+            assert n_k == k
+            ids.copy_(torch.from_numpy(local))
+            c.device_route_step(logits, k, True, torch.zeros(2 * k, device=DEV), ids, layer * E, E, meta)
+        else:
+            c.device_step(_row(local, np.ones(n_k)), None, layer * E, E, n_k, meta)
+        assert [int(v) for v in meta[:n_k].cpu()] == ref.ensure(keys)[0], (it, how)
+
+    fill = nslots - n_static - 8
+    for it, k0 in enumerate(range(0, fill, k)):  # keys 0 .. fill-1, at most k of one layer per step
+        layer = k0 // E
+        hi = min(k0 + k, fill, (layer + 1) * E)
+        step(range(k0, hi), it, "route" if hi - k0 == k and it % 2 else "row")
+    assert ref.counts["evictions"] == 0 and len(ref.stack) == 8
+    base = (fill // E + 1) * E
+    step(range(base, base + k), "mixed", "route")
+    assert ref.counts["evictions"] == 8 and not ref.stack
+    for it in range(150):
+        how = ("row", "route", "graph")[it % 3]
+        layer = gbase // E if how == "graph" else int(rng.integers(0, L))
+        step(layer * E + rng.choice(E, size=k, replace=False), it, how)
+    assert ref.counts["evictions"] > 200
+    _check_state(c, ref, st)
+    c.free()
+
+
+def test_route_step_forced_ids_past_the_routers_experts():
+    """The route + LRU kernel (one wave, 64 slots) with 32 router logits and forced ids over a
+    layer of 160 experts: ids below 64 find their residency among the entries the kernel
+    requests at its start, the others read it; every step equals the reference LRU."""
+    L, E, n, k, nslots = 2, 160, 1024, 8, 64
+    st = ExpertStore(L, E, n, 4, 128)
+    gen = torch.Generator().manual_seed(3)
+    st.host.copy_(torch.randint(0, 256, tuple(st.host.shape), dtype=torch.uint8, generator=gen))
+    c = ExpertCache(st, nslots, copy="kernel")
+    ref = RefCore(nslots, "lru")
+    meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    row = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    logits = torch.randn(32, device=DEV).to(torch.bfloat16)
+    rng = np.random.default_rng(21)
+    c.device_begin()
+    for it in range(80):
+        layer = it % L
+        draw = rng.choice(E, size=k, replace=False).astype(np.int64)
+        c.device_route_step(logits, k, True, row, torch.from_numpy(draw).to(DEV), layer * E, E, meta)
+        slots, _ = ref.ensure([layer * E + int(v) for v in draw])
+        assert [int(v) for v in meta[:k].cpu()] == slots, it
+    assert ref.counts["evictions"] > 200
     _check_state(c, ref, st)
     c.free()
 
@@ -314,6 +407,11 @@ def test_bad_id_and_no_evictable_slot_are_reported(store):
 def test_device_paging_refusals(store):
     c = ExpertCache(store, 8, copy="dma")
     with pytest.raises(RuntimeError, match="page-kernel"):
+        c.device_begin()
+    c.free()
+    small = ExpertStore(1, 8, 1024, 4, 128)  # more dynamic slots than the device step holds keys for
+    c = ExpertCache(small, 26881, copy="kernel")
+    with pytest.raises(RuntimeError, match="26880 dynamic slots"):
         c.device_begin()
     c.free()
     c = ExpertCache(store, 8, policy="wsa", copy="kernel")

@@ -200,8 +200,12 @@ static void view_deleter(DLManagedTensor* m) {
 }
 
 // Device paging: the LRU state in device memory (one allocation) while it is on.
-constexpr int kDevMaxK = 16;        // keys per step
-constexpr int kDevMaxSlots = 8192;  // dynamic slots: their eviction keys are staged in LDS
+constexpr int kDevMaxK = 16;  // keys per step
+// The LRU step holds every dynamic slot's eviction key in registers for the whole step:
+// kLruSmall keys per lane of one wave for pools of at most 64 kLruSmall dynamic slots, else
+// kLruBig keys per thread of up to 15 waves beside the wave that routes (16 in all).
+constexpr int kLruSmall = 16, kLruBig = 28;
+constexpr int kDevMaxSlots = 15 * 64 * kLruBig;  // 26880 dynamic slots
 enum { kCtrTick, kCtrNextFree, kCtrHits, kCtrMisses, kCtrEvict, kCtrCalls, kCtrLoads, kCtrErr, kCtrOn, kCtrN };
 enum { kDevErrSlot = 1, kDevErrKey = 2 };
 struct DevPaging {
@@ -319,110 +323,217 @@ __global__ __launch_bounds__(256) void k_page_list(const pg_u32x4* __restrict__ 
     page_part(host + (int64_t)miss[1 + r] * row16, pool + (int64_t)miss[1 + kDevMaxK + r] * slot16, row16, per);
 }
 
+// Wave-wide minimum of a 64-bit value (every lane active; the result is wave-uniform):
+// DPP inside each 16-lane row (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), then
+// the four row minima through readlane.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, true);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, true);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t min_u64(uint64_t a, uint64_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+    v = min_u64(v, dpp_u64<0xB1>(v));
+    v = min_u64(v, dpp_u64<0x4E>(v));
+    v = min_u64(v, dpp_u64<0x141>(v));
+    v = min_u64(v, dpp_u64<0x140>(v));
+    return min_u64(min_u64(readlane_u64(v, 0), readlane_u64(v, 16)), min_u64(readlane_u64(v, 32), readlane_u64(v, 48)));
+}
+
+// The step's counters (wave 0).
+struct LruCtr {
+    int64_t tick, nf;
+    bool on;
+};
+__device__ __forceinline__ LruCtr lru_counters(const DevPaging& d) {
+    LruCtr st;
+    st.on = d.ctr[kCtrOn] != 0;
+    st.tick = d.ctr[kCtrTick] + 1;
+    st.nf = d.ctr[kCtrNextFree];
+    return st;
+}
+
+// Which threads hold eviction keys: every lane of the one wave (R = kLruSmall), else the
+// threads past wave 0 (wave 0 routes and classifies, and its registers stay free for that).
+// Key holder t of nt holds dynamic slot i = t + nt u (u < R).
+template <int R>
+__device__ __forceinline__ int lru_holder() {
+    return R == kLruSmall ? (int)threadIdx.x : (int)threadIdx.x - 64;
+}
+template <int R>
+__device__ __forceinline__ int lru_holders() {
+    return R == kLruSmall ? (int)blockDim.x : (int)blockDim.x - 64;
+}
+
+// Eviction keys in registers: dynamic slot i as (last, slot) + 1, or ~0 past the pool (a key is
+// never 0, so 0 is below every key). One request per key, all before any use; 32-bit slot
+// indexes (nd <= kDevMaxSlots), so each request needs one offset register. The one-wave form
+// also holds each slot's key (owner) in `own`, so the victims' old keys need no dependent read.
+template <int R>
+__device__ __forceinline__ void lru_stage(const DevPaging& d, int nd, uint64_t (&key)[R], int32_t (&own)[R]) {
+    const int t = lru_holder<R>(), nt = lru_holders<R>();
+    const int64_t* __restrict__ lp = d.last + d.n_static;
+    const int32_t* __restrict__ op = d.slot_key + d.n_static;
+    int64_t v[R];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const uint32_t lo = __shfl_xor((unsigned)v, o, 64), hi = __shfl_xor((unsigned)(v >> 32), o, 64);
-        const uint64_t u = ((uint64_t)hi << 32) | lo;
-        v = u < v ? u : v;
+    for (int u = 0; u < R; ++u) {
+        v[u] = lp[min(t + nt * u, nd - 1)];
+        if constexpr (R == kLruSmall) own[u] = op[min(t + nt * u, nd - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int i = t + nt * u;
+        key[u] = i < nd ? (((uint64_t)v[u] << 20) | (uint64_t)(d.n_static + i)) + 1ull : ~0ull;
+    }
+}
+
+// The one-wave form's owner of dynamic slot i (0 <= i < 64 kLruSmall), held by lane i % 64
+// in own[i / 64]; every lane of the wave active (the lane reads go through ds_bpermute).
+__device__ __forceinline__ int lru_owner_of(const int32_t (&own)[kLruSmall], int i) {
+    const int src = i & 63, reg = i >> 6;
+    int v = -1;
+#pragma unroll
+    for (int u = 0; u < kLruSmall; ++u) {
+        const int o = __shfl(own[u], src, 64);
+        v = reg == u ? o : v;
     }
     return v;
 }
 
-// cand[i] = (last, slot) + 1 of dynamic slot n_static + i for i in [i0, min(n, i0 + 64 kLruBatch)):
-// all of a lane's loads issued before its LDS writes (one round trip; indexes past the end
-// re-read the last slot, n >= 1)
-constexpr int kLruBatch = 16;
-__device__ __forceinline__ void stage_eviction_keys(const DevPaging& d, int lane, int64_t i0, int64_t n,
-                                                    uint64_t* cand) {
-    int64_t v[kLruBatch];
-#pragma unroll
-    for (int u = 0; u < kLruBatch; ++u) {
-        const int64_t i = i0 + lane + 64 * u;
-        v[u] = d.last[d.n_static + (i < n ? i : n - 1)];
-    }
-#pragma unroll
-    for (int u = 0; u < kLruBatch; ++u) {
-        const int64_t i = i0 + lane + 64 * u;
-        if (i < n) cand[i] = (((uint64_t)v[u] << 20) | (uint64_t)(d.n_static + i)) + 1ull;
-    }
-}
-
-// The step's state reads, requested before anything else the kernel does: the counters
-// and, for a pool of at most 64 kLruBatch dynamic slots, every eviction key.
-struct LruStart {
-    int64_t tick, nf;
-    bool on, early;
+// What wave 0 tells the other waves of the step (through LDS, before the eviction rounds).
+struct LruShared {
+    uint64_t wmin[2][16];     // per-wave round minima, two buffers (rounds alternate)
+    int32_t hits[kDevMaxK];   // this step's hit slots
+    int32_t nhit, m;          // hits, misses that evict
+    int64_t nc;               // dynamic slots in use at the step's start
 };
-__device__ __forceinline__ LruStart lru_start(const DevPaging& d, int lane, uint64_t* cand) {
-    LruStart st;
-    st.on = d.ctr[kCtrOn] != 0;
-    st.tick = d.ctr[kCtrTick] + 1;
-    st.nf = d.ctr[kCtrNextFree];
-    const int64_t nd = d.nslots - d.n_static;
-    st.early = nd <= 64 * kLruBatch;
-    if (st.early && nd > 0) stage_eviction_keys(d, lane, 0, nd, cand);
-    return st;
+
+// Wave 0's per-lane view of the step.
+struct LruLane {
+    int key, slot, rank, from_free, nmiss;
+    float w;
+    bool miss, hit, on;
+    uint64_t hm, bad;
+};
+
+// cache_core.py:86-106 (ensure) with the LRU policy on the GPU, for one layer, in three
+// parts: lru_classify (wave 0: lane j < k holds key j, -1 if its id was not valid, and its
+// weight w), lru_evict (every wave of the workgroup) and lru_commit (wave 0). Hits are
+// noted with the step's tick; misses take free slots in ascending order, then the least
+// recently used unprotected slots. The reference picks each victim by a first-index argmin
+// of `last` over the unprotected dynamic slots, and every slot it hands out becomes
+// protected, so the i-th evicting miss (in key order) gets the i-th smallest (last, slot)
+// among the slots in [n_static, next free) that are not hits of this step. meta = [slots
+// (float) | the row's weights]; the loads go to the miss list for k_page_list. A key that is
+// not valid or a miss without an evictable slot gets slot -1 in meta (the MoE kernels then
+// write NaN rows) and sets an error bit that the host reads when it syncs the state. A
+// launch while device paging is off (a captured step replayed after wisp_cache_device_end)
+// does no step and writes slot -1 into meta.
+// `resident` is key2slot[key] (-1 for key < 0), looked up by the caller.
+__device__ __forceinline__ LruLane lru_classify(const DevPaging& d, const LruCtr& st, int lane, int k, int key,
+                                                int resident, float w, LruShared& sh) {
+    LruLane ln{};
+    ln.key = key;
+    ln.w = w;
+    ln.on = st.on;
+    if (!st.on) {  // replayed while the host core holds the state: no step
+        if (lane == 0) {
+            sh.m = 0;
+            sh.nhit = 0;
+            sh.nc = 0;
+        }
+        return ln;
+    }
+    const int64_t nf = st.nf;
+    int slot = key >= 0 ? resident : -1;
+    ln.hit = slot >= 0;
+    const uint64_t mm = __ballot(key >= 0 && !ln.hit);
+    ln.hm = __ballot(ln.hit);
+    ln.bad = __ballot(lane < k && key < 0);
+    ln.miss = (mm >> lane) & 1ull;
+    ln.nmiss = __popcll(mm);
+    ln.rank = __popcll(mm & ((1ull << lane) - 1ull));
+    const int64_t nfree = d.nslots - nf;
+    ln.from_free = (int)((int64_t)ln.nmiss < nfree ? (int64_t)ln.nmiss : nfree);
+    if (ln.miss && ln.rank < ln.from_free) slot = (int)(nf + ln.rank);
+    ln.slot = slot;
+    if (ln.hit) sh.hits[__popcll(ln.hm & ((1ull << lane) - 1ull))] = slot;
+    if (lane == 0) {
+        sh.m = ln.nmiss - ln.from_free;  // misses that evict
+        sh.nhit = __popcll(ln.hm);
+        sh.nc = nf - d.n_static;
+    }
+    return ln;
 }
 
-// cache_core.py:86-106 (ensure) with the LRU policy, as one wave on the GPU, for
-// one layer: lane j < k holds key j (-1 if its id was not valid) and its weight w. Hits are noted with
-// the step's tick; misses take free slots in ascending order, then the least
-// recently used unprotected slots. The reference picks each victim by a
-// first-index argmin of `last` over the unprotected dynamic slots, and every slot
-// it hands out becomes protected, so the i-th evicting miss (in key order) gets
-// the i-th smallest (last, slot) among the slots in [n_static, next free) that
-// are not hits of this step. meta = [slots (float) | the row's weights]; the
-// loads go to the miss list for k_page_list. A key that is not valid or a miss
-// without an evictable slot gets slot -1 in meta (the MoE kernels then write NaN
-// rows) and sets an error bit that the host reads when it syncs the state.
-// A launch while device paging is off (a captured step replayed after
-// wisp_cache_device_end) does no step and writes slot -1 into meta.
-__device__ __forceinline__ void lru_apply(const DevPaging& d, const LruStart& st, int lane, int k, int key, float w,
-                                          uint64_t* cand, float* __restrict__ meta) {
-    if (!st.on) {  // replayed while the host core holds the state: no step
+// The eviction rounds, run by every wave of the workgroup after the barrier that publishes
+// `sh`: round r takes the smallest key above the last round's among the keys of the slots in
+// use (each thread's R registers, then the wave's minimum by DPP, then the waves' minima
+// through LDS), so every wave sees the same winner and runs the same number of rounds and
+// barriers. A winner that is a hit of this step is protected: it is passed over (at most
+// one round per hit). Returns the victims found; wave 0's evicting miss of rank
+// from_free + i gets victim i in ln.slot.
+template <int R>
+__device__ __forceinline__ int lru_evict(LruShared& sh, uint64_t (&key)[R], LruLane& ln, bool wave0) {
+    const int m = sh.m;
+    if (m <= 0) return 0;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int nc = (int)sh.nc, t = lru_holder<R>(), nt = lru_holders<R>();
+#pragma unroll
+    for (int u = 0; u < R; ++u)
+        if (t + nt * u >= nc) key[u] = ~0ull;  // free slots are not candidates (wave 0 of R = kLruBig holds none)
+    const int nhit = sh.nhit;
+    const int hs = lane < nhit ? sh.hits[lane] : -1;
+    uint64_t prev = 0;
+    int found = 0, buf = 0;
+    while (found < m) {
+        uint64_t best = ~0ull;
+#pragma unroll
+        for (int u = 0; u < R; ++u) best = (key[u] > prev && key[u] < best) ? key[u] : best;
+        best = wave_min_u64(best);
+        if (nw > 1) {
+            if (lane == 0) sh.wmin[buf][wv] = best;
+            __syncthreads();
+            best = ~0ull;
+            for (int w = 0; w < nw; ++w) best = min_u64(best, sh.wmin[buf][w]);
+            buf ^= 1;
+        }
+        if (best == ~0ull) break;  // nothing evictable is left
+        prev = best;
+        const int s = (int)((best - 1ull) & 0xFFFFFull);
+        if (__ballot(hs == s)) continue;  // a hit of this step
+        if (wave0 && ln.miss && ln.rank == ln.from_free + found) ln.slot = s;
+        ++found;
+    }
+    return found;
+}
+
+// Wave 0: the step's writes (slot table, LRU ticks, the miss list, meta and counters).
+template <int R>
+__device__ __forceinline__ void lru_commit(const DevPaging& d, const LruCtr& st, int lane, int k, const LruLane& ln,
+                                           int evicted, const int32_t (&own)[R], float* __restrict__ meta) {
+    if (!ln.on) {
         if (lane < k) meta[lane] = -1.f;
         if (lane == 0) d.miss[0] = 0;
         return;
     }
     const int64_t tick = st.tick, nf = st.nf;
-    const bool on = lane < k;
-    int slot = key >= 0 ? d.key2slot[key] : -1;
-    const bool hit = slot >= 0;
-    const uint64_t mm = __ballot(key >= 0 && !hit);
-    const uint64_t hm = __ballot(hit);
-    const uint64_t bad = __ballot(on && key < 0);
-    const bool miss = (mm >> lane) & 1ull;
-    const int nmiss = __popcll(mm);
-    const int rank = __popcll(mm & ((1ull << lane) - 1ull));
-    const int64_t nfree = d.nslots - nf;
-    const int from_free = (int)((int64_t)nmiss < nfree ? (int64_t)nmiss : nfree);
-    const int m = nmiss - from_free;  // misses that evict
-    if (miss && rank < from_free) slot = (int)(nf + rank);
-    int got = from_free;  // misses with a slot
-    int old_key = -1;     // the key this lane's victim held
-    if (m > 0) {
-        // candidates: the dynamic slots in use, this step's hits excluded
-        const int64_t nc = nf - d.n_static;
-        if (!st.early)
-            for (int64_t i0 = 0; i0 < nc; i0 += 64 * kLruBatch) stage_eviction_keys(d, lane, i0, nc, cand);
-        __syncthreads();
-        if (hit && slot >= d.n_static) cand[slot - d.n_static] = ~0ull;
-        __syncthreads();
-        uint64_t prev = 0;
-        for (int r = 0; r < m; ++r) {
-            uint64_t best = ~0ull;
-            for (int64_t i = lane; i < nc; i += 64) {
-                const uint64_t v = cand[i];
-                if (v > prev && v < best) best = v;
-            }
-            best = wave_min_u64(best);
-            if (best == ~0ull) break;  // nothing evictable is left
-            prev = best;
-            if (miss && rank == from_free + r) slot = (int)((best - 1ull) & 0xFFFFFull);
-            ++got;
-        }
-        if (miss && rank >= from_free && slot >= 0) old_key = d.slot_key[slot];
+    const int key = ln.key, slot = ln.slot;
+    const int got = ln.from_free + evicted;  // misses with a slot
+    // the key this lane's victim held: from the staged owners (one wave), else read
+    const bool evicts = ln.miss && ln.rank >= ln.from_free && slot >= 0;
+    int old_key = -1;
+    if constexpr (R == kLruSmall) {
+        const int o = lru_owner_of(own, evicts ? slot - (int)d.n_static : 0);
+        old_key = evicts ? o : -1;
+    } else {
+        old_key = evicts ? d.slot_key[slot] : -1;
     }
     // a key repeated later in the step: the later lane's slot is the one key2slot keeps
     bool later = false;
@@ -430,30 +541,30 @@ __device__ __forceinline__ void lru_apply(const DevPaging& d, const LruStart& st
         const int kj = __shfl(key, j, 64);
         later = later || (j > lane && kj == key);
     }
-    const bool gets = miss && slot >= 0;
-    if (hit) d.last[slot] = tick;
+    const bool gets = ln.miss && slot >= 0;
+    if (ln.hit) d.last[slot] = tick;
     if (gets) {
         if (old_key >= 0) d.key2slot[old_key] = -1;
         d.slot_key[slot] = key;
         if (!later) d.key2slot[key] = slot;
         d.last[slot] = tick;
-        d.miss[1 + rank] = key;
-        d.miss[1 + kDevMaxK + rank] = slot;
+        d.miss[1 + ln.rank] = key;
+        d.miss[1 + kDevMaxK + ln.rank] = slot;
     }
-    if (on) {
+    if (lane < k) {
         meta[lane] = (key >= 0 && slot >= 0) ? (float)slot : -1.f;
-        meta[k + lane] = w;
+        meta[k + lane] = ln.w;
     }
     if (lane == 0) {
         d.miss[0] = got;
         d.ctr[kCtrTick] = tick;
-        d.ctr[kCtrNextFree] = nf + from_free;
-        d.ctr[kCtrHits] += __popcll(hm);
+        d.ctr[kCtrNextFree] = nf + ln.from_free;
+        d.ctr[kCtrHits] += __popcll(ln.hm);
         d.ctr[kCtrMisses] += got;
-        d.ctr[kCtrEvict] += got - from_free;
+        d.ctr[kCtrEvict] += evicted;
         d.ctr[kCtrCalls] += 1;
         d.ctr[kCtrLoads] += got;
-        d.ctr[kCtrErr] |= (got < nmiss ? kDevErrSlot : 0) | (bad ? kDevErrKey : 0);
+        d.ctr[kCtrErr] |= (got < ln.nmiss ? kDevErrSlot : 0) | (ln.bad ? kDevErrKey : 0);
     }
 }
 
@@ -462,55 +573,130 @@ __device__ __forceinline__ int lru_key(const DevPaging& d, int64_t id, int64_t k
     return (id >= 0 && id < n_ids && key_base + id >= 0 && key_base + id < d.nkeys) ? (int)(key_base + id) : -1;
 }
 
+// Launch shape of the step kernels for nd >= 1 dynamic slots: one wave of kLruSmall keys per
+// lane, or wave 0 plus waves of kLruBig keys per thread (at most 16 in all).
+static inline int lru_threads(int64_t nd) {
+    return nd <= 64 * kLruSmall ? 64 : (int)(64 * (1 + (nd + 64 * kLruBig - 1) / (64 * kLruBig)));
+}
+
+// Wave 0's part of a step before the eviction rounds, `classify` (route / read the keys and
+// classify them), and the key holders' staging: one wave requests its keys first, then does
+// the rest; with kLruBig keys the other waves stage while wave 0 works, in disjoint branches
+// (so wave 0's registers never hold keys and the keys' registers never hold its state).
+template <int R, typename Classify>
+__device__ __forceinline__ LruLane lru_begin(const DevPaging& d, uint64_t (&key)[R], int32_t (&own)[R],
+                                             Classify classify) {
+    const int nd = (int)(d.nslots - d.n_static);  // in [1, kDevMaxSlots] (device_begin)
+    LruLane ln{};
+    if constexpr (R == kLruSmall) {
+        lru_stage<R>(d, nd, key, own);
+        ln = classify();
+    } else if (threadIdx.x < 64) {
+        ln = classify();
+#pragma unroll
+        for (int u = 0; u < R; ++u) key[u] = ~0ull;
+    } else {
+        lru_stage<R>(d, nd, key, own);
+    }
+    return ln;
+}
+
 // The step for key_base + id_j, id_j = ids[j] if ids and ids[j] >= 0, else the route row's id
-// j (an integer in [0, n_ids)); weights from the row. k <= 0: a warm-up launch that only clears the miss list.
-__global__ __launch_bounds__(64) void k_lru_step(const DevPaging d, const float* __restrict__ row,
-                                                 const int64_t* __restrict__ ids, int64_t key_base, int64_t n_ids,
-                                                 int k, float* __restrict__ meta) {
-    __shared__ uint64_t cand[kDevMaxSlots];
-    const int lane = threadIdx.x;
+// j (an integer in [0, n_ids)); weights from the row. k <= 0: a warm-up launch that only
+// clears the miss list. R keys per key holder, blockDim.x = lru_threads(dynamic slots).
+template <int R>
+__global__ __launch_bounds__(R == kLruSmall ? 64 : 1024) void k_lru_step(const DevPaging d,
+                                                                          const float* __restrict__ row,
+                                                                          const int64_t* __restrict__ ids,
+                                                                          int64_t key_base, int64_t n_ids, int k,
+                                                                          float* __restrict__ meta) {
+    __shared__ LruShared sh;
+    const int lane = threadIdx.x & 63;
+    const bool wave0 = threadIdx.x < 64;
     if (k <= 0) {
-        if (lane == 0) d.miss[0] = 0;
+        if (threadIdx.x == 0) d.miss[0] = 0;
         return;
     }
-    const LruStart st = lru_start(d, lane, cand);
-    int key = -1;
-    float w = 0.f;
-    if (lane < k) {
-        int64_t id = ids ? ids[lane] : -1;
-        if (id < 0) {  // the row's id
-            const float f = row[lane];
-            id = (f >= 0.f && f < 16777216.f && (float)(int64_t)f == f) ? (int64_t)f : -1;
+    LruCtr st{};
+    if (wave0) st = lru_counters(d);
+    uint64_t key[R];
+    int32_t own[R];
+    LruLane ln = lru_begin<R>(d, key, own, [&] {
+        int kk = -1;
+        float w = 0.f;
+        if (lane < k) {
+            int64_t id = ids ? ids[lane] : -1;
+            if (id < 0) {  // the row's id
+                const float f = row[lane];
+                id = (f >= 0.f && f < 16777216.f && (float)(int64_t)f == f) ? (int64_t)f : -1;
+            }
+            kk = lru_key(d, id, key_base, n_ids);
+            w = row[k + lane];
         }
-        key = lru_key(d, id, key_base, n_ids);
-        w = row[k + lane];
-    }
-    lru_apply(d, st, lane, k, key, w, cand, meta);
+        return lru_classify(d, st, lane, k, kk, kk >= 0 ? d.key2slot[kk] : -1, w, sh);
+    });
+    __syncthreads();
+    const int evicted = lru_evict<R>(sh, key, ln, wave0);
+    if (wave0) lru_commit<R>(d, st, lane, k, ln, evicted, own, meta);
 }
 
 // The route kernel's choice (route.hpp: softmax, top-k, renormalised bf16 weights; row =
-// [ids | weights]) and the LRU step of those experts in one wave: the step's state reads
-// are in flight while the router's choice is computed. ids (optional) replace the chosen
-// expert ids where they are >= 0; the weights are the router's.
-template <int EPL>
-__global__ __launch_bounds__(64) void k_route_lru(const DevPaging d, const uint16_t* __restrict__ logits, int E,
-                                                  int k, int norm, float* __restrict__ row,
-                                                  const int64_t* __restrict__ ids, int64_t key_base, int64_t n_ids,
-                                                  float* __restrict__ meta) {
-    __shared__ uint64_t cand[kDevMaxSlots];
-    const int lane = threadIdx.x;
+// [ids | weights]) and the LRU step of those experts in one launch: wave 0 routes while the
+// eviction keys are in flight. ids (optional) replace the chosen expert ids where they are
+// >= 0; the weights are the router's. The key -> slot entries of ids 0 .. 64 EPL - 1 (every
+// expert the router can pick) are requested at the start with the rest, so the chosen keys'
+// residency needs no dependent read (a forced id past them is read). Launch shape as for
+// k_lru_step.
+template <int EPL, int R>
+__global__ __launch_bounds__(R == kLruSmall ? 64 : 1024) void k_route_lru(const DevPaging d,
+                                                                           const uint16_t* __restrict__ logits, int E,
+                                                                           int k, int norm, float* __restrict__ row,
+                                                                           const int64_t* __restrict__ ids,
+                                                                           int64_t key_base, int64_t n_ids,
+                                                                           float* __restrict__ meta) {
+    __shared__ LruShared sh;
+    const int lane = threadIdx.x & 63;
+    const bool wave0 = threadIdx.x < 64;
     if (k <= 0) {
-        if (lane == 0) d.miss[0] = 0;
+        if (threadIdx.x == 0) d.miss[0] = 0;
         return;
     }
-    const LruStart st = lru_start(d, lane, cand);
-    const int64_t forced = ids ? ids[lane < k ? lane : 0] : -1;
-    const float val = route_select<EPL>(logits, E, k, norm);
-    if (lane < 2 * k) row[lane] = val;
-    const float w = __shfl(val, (k + lane) & 63, 64);
-    int key = -1;
-    if (lane < k) key = lru_key(d, forced >= 0 ? forced : (int64_t)val, key_base, n_ids);
-    lru_apply(d, st, lane, k, key, w, cand, meta);
+    LruCtr st{};
+    int64_t forced = -1;
+    int32_t pre[EPL];  // key2slot[key_base + lane + 64 t], clamped into the table
+    if (wave0) {
+        st = lru_counters(d);
+        forced = ids ? ids[lane < k ? lane : 0] : -1;
+#pragma unroll
+        for (int t = 0; t < EPL; ++t) {
+            const int64_t kq = key_base + lane + 64 * t;
+            pre[t] = d.key2slot[kq < 0 ? 0 : (kq < d.nkeys ? kq : d.nkeys - 1)];
+        }
+    }
+    uint64_t key[R];
+    int32_t own[R];
+    LruLane ln = lru_begin<R>(d, key, own, [&] {
+        const float val = route_select<EPL>(logits, E, k, norm);
+        if (lane < 2 * k) row[lane] = val;
+        const float w = __shfl(val, (k + lane) & 63, 64);
+        int kk = -1;
+        if (lane < k) kk = lru_key(d, forced >= 0 ? forced : (int64_t)val, key_base, n_ids);
+        // residency of key_base + id from the requested entries (every lane takes part in the
+        // lane reads), or read for an id past them
+        const int64_t id = kk >= 0 ? (int64_t)kk - key_base : 0;
+        const int src = (int)(id & 63), reg = (int)(id >> 6);
+        int res = -1;
+#pragma unroll
+        for (int t = 0; t < EPL; ++t) {
+            const int o = __shfl(pre[t], src, 64);
+            res = reg == t ? o : res;
+        }
+        if (kk >= 0 && id >= 64 * EPL) res = d.key2slot[kk];
+        return lru_classify(d, st, lane, k, kk, kk >= 0 ? res : -1, w, sh);
+    });
+    __syncthreads();
+    const int evicted = lru_evict<R>(sh, key, ln, wave0);
+    if (wave0) lru_commit<R>(d, st, lane, k, ln, evicted, own, meta);
 }
 
 __global__ __launch_bounds__(64) void k_write_meta(const PageMeta pm) {
@@ -1204,7 +1390,7 @@ static int dev_download(Cache& c, hipStream_t st) {
 }  // namespace wisp
 
 // Copy the host core's LRU state to the device and turn device paging on (a no-op
-// when it is on). Needs the LRU policy, the page-kernel copy mode, at most 8192
+// when it is on). Needs the LRU policy, the page-kernel copy mode, at most 26880
 // dynamic slots (2^20 in all) and the free slots at the top of the pool (the order
 // the core hands them out). Stream-ordered after the copies already issued.
 extern "C" int wisp_cache_device_begin(void* h, void* stream) {
@@ -1216,7 +1402,7 @@ extern "C" int wisp_cache_device_begin(void* h, void* stream) {
     if (c.copy_mode != 1 || !c.host_dev) return fail_inval("device paging needs the page-kernel copy mode");
     if (!c.pool) return no_pool();
     if (c.nslots > (1 << 20) || c.nslots - core.n_static > kDevMaxSlots)
-        return fail_inval("device paging: at most 8192 dynamic slots and 2^20 slots in all");
+        return fail_inval("device paging: at most 26880 dynamic slots and 2^20 slots in all");
     if (c.host_rows > INT32_MAX) return fail_inval("device paging: at most 2^31 - 1 store rows");
     if (core.tick > (int64_t(1) << 42)) return fail_inval("device paging: tick beyond 2^42");
     const int64_t nfree = (int64_t)core.free.size(), nf = c.nslots - nfree;
@@ -1315,7 +1501,12 @@ extern "C" int wisp_cache_device_step(void* h, const float* row, const int64_t* 
     if (k > c.nslots - c.dev.n_static) return no_slot_for_k(c, k);
     if (!c.pool) return no_pool();
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_lru_step, dim3(1), dim3(64), 0, st, c.dev, row, ids, key_base, n_ids, k, meta);
+    const int64_t nd = c.nslots - c.dev.n_static;
+    if (nd <= 64 * kLruSmall)
+        hipLaunchKernelGGL(k_lru_step<kLruSmall>, dim3(1), dim3(64), 0, st, c.dev, row, ids, key_base, n_ids, k, meta);
+    else
+        hipLaunchKernelGGL(k_lru_step<kLruBig>, dim3(1), dim3(lru_threads(nd)), 0, st, c.dev, row, ids, key_base,
+                           n_ids, k, meta);
     int rc = check_launch("k_lru_step");
     if (rc) return rc;
     const int64_t row16 = c.row_bytes / 16, slot16 = c.slot_bytes / 16;
@@ -1341,13 +1532,25 @@ extern "C" int wisp_cache_device_route_step(void* h, const uint16_t* logits, int
     if (!c.pool) return no_pool();
     hipStream_t st = (hipStream_t)stream;
     const int nt = norm_topk ? 1 : 0;
-#define WISP_RL(EPL) \
-    hipLaunchKernelGGL(k_route_lru<EPL>, dim3(1), dim3(64), 0, st, c.dev, logits, E, k, nt, row, ids, key_base, n_ids, meta)
-    if (E <= 64) WISP_RL(1);
-    else if (E <= 128) WISP_RL(2);
-    else if (E <= 256) WISP_RL(4);
-    else if (E <= 512) WISP_RL(8);
-    else WISP_RL(16);
+    const int64_t nd = c.nslots - c.dev.n_static;
+#define WISP_RL(EPL)                                                                                               \
+    if (nd <= 64 * kLruSmall)                                                                                      \
+        hipLaunchKernelGGL((k_route_lru<EPL, kLruSmall>), dim3(1), dim3(64), 0, st, c.dev, logits, E, k, nt, row, \
+                           ids, key_base, n_ids, meta);                                                            \
+    else                                                                                                           \
+        hipLaunchKernelGGL((k_route_lru<EPL, kLruBig>), dim3(1), dim3(lru_threads(nd)), 0, st, c.dev, logits, E,  \
+                           k, nt, row, ids, key_base, n_ids, meta)
+    if (E <= 64) {
+        WISP_RL(1);
+    } else if (E <= 128) {
+        WISP_RL(2);
+    } else if (E <= 256) {
+        WISP_RL(4);
+    } else if (E <= 512) {
+        WISP_RL(8);
+    } else {
+        WISP_RL(16);
+    }
 #undef WISP_RL
     int rc = check_launch("k_route_lru");
     if (rc) return rc;

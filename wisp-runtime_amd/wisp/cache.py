@@ -146,7 +146,7 @@ class ExpertCache:
         return bool(self._h) and bool(_lib.lib().wisp_cache_device_active(self._h))
 
     def device_begin(self):
-        """Copy the core's LRU state to the device (LRU policy, copy="kernel", at most 8192
+        """Copy the core's LRU state to the device (LRU policy, copy="kernel", at most 26880
         dynamic slots); RuntimeError if this cache cannot page on the device."""
         _raise(_lib.lib().wisp_cache_device_begin(self._h, self._stream()))
 
