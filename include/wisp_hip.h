@@ -309,16 +309,20 @@ int wisp_cache_resize(void* cache, int64_t nslots);
 /* Device paging: the graph decoder's per-layer paging point (graphdec.py:216-231:
  * route row -> CacheCore.ensure -> copies of the misses -> meta) on the GPU, so
  * a captured decode step needs no host decision between layers. The bookkeeping
- * is cache_core.py:86-106 with the LRU policy (ticks per step, hits protected,
- * free slots in ascending order, then the first-index argmin of `last` over the
- * unprotected dynamic slots), kept in device memory while device paging is on.
- * No reference counterpart as an interface (the reference decides on the host).
+ * is cache_core.py:30-106 with any policy (the clock and its 1e100
+ * renormalisation, decayed frequencies and scores, ticks per step, hits
+ * protected, free slots in ascending order, then the first-index argmin of
+ * `last` (lru) or `score` (wsa, static) over the unprotected dynamic slots),
+ * kept in device memory while device paging is on. No reference counterpart as
+ * an interface (the reference decides on the host).
  *
- * begin: copy the core's LRU state to the device, ordered on `stream` after the
- * copies already issued. Needs the LRU policy, copy mode 1, nslots - n_static <=
- * 26880 (the step holds every dynamic slot's eviction key in registers: one wave
- * up to 1024 slots, else up to 15 waves of 28 keys per thread), nslots <= 2^20 and the free slots at the top of the pool (as the core
- * hands them out); WISP_EINVAL otherwise. A no-op when device paging is on.
+ * begin: copy the core's state to the device, ordered on `stream` after the
+ * copies already issued. Needs copy mode 1, nslots - n_static <= 26880 (the
+ * step holds every dynamic slot's eviction key in registers: one wave up to
+ * 1024 slots, else up to 15 waves of 28 keys per thread), nslots <= 2^20, the
+ * free slots at the top of the pool (as the core hands them out) and every
+ * resident or noted key in the store; WISP_EINVAL otherwise. A no-op when
+ * device paging is on.
  * While it is on, wisp_cache_issue / _ensure / _prepare_* / _resize return
  * WISP_EINVAL (the host core is stale until _sync or _end). */
 int wisp_cache_device_begin(void* cache, void* stream);
@@ -340,11 +344,10 @@ int wisp_cache_device_step(void* cache, const float* row, const int64_t* ids, in
  * (k = 0: warm-up launches). */
 int wisp_cache_device_route_step(void* cache, const uint16_t* logits, int E, int k, int norm_topk, float* row,
                                  const int64_t* ids, int64_t key_base, int64_t n_ids, float* meta, void* stream);
-/* Synchronise `stream` and copy the device LRU state into the host core and the
- * load counters; device paging stays on. WISP_EINVAL (once) if a step since
- * the last sync met a bad id or had no evictable slot. The core's decayed
- * frequencies (read only by the wsa policy and admission) are not advanced by
- * device steps. */
+/* Synchronise `stream` and copy the device state into the host core (keys first
+ * noted on the device join its frequency table in the order of their first
+ * notes) and the load counters; device paging stays on. WISP_EINVAL (once) if a
+ * step since the last sync met a bad id or had no evictable slot. */
 int wisp_cache_device_sync(void* cache, void* stream);
 /* wisp_cache_device_sync, then device paging off. The device state stays allocated
  * at the same address (until the cache is destroyed or a begin finds a different

@@ -1,7 +1,9 @@
-"""Device paging: the decode layer's LRU step (cache_core.py:86-106) and the paging of its
-misses run on the GPU (k_lru_step + k_page_list), checked step by step against the
-reference LRU (oracle/cache_core_ref.py) on the same key streams, including graph replays,
-repeated ids, a static region, bad ids and a request with no evictable slot."""
+"""Device paging: the decode layer's cache step (cache_core.py:30-106: clock, notes, ensure)
+and the paging of its misses run on the GPU (k_lru_step / k_route_lru + k_page_list),
+checked step by step against the reference core (oracle/cache_core_ref.py) on the same key
+streams -- LRU, WSA and static policies, the whole state (owners, ticks, scores, the
+frequency table in insertion order, inc) -- including graph replays, repeated ids, a static
+region, the 1e100 renormalisation, bad ids and a request with no evictable slot."""
 
 import numpy as np
 import pytest
@@ -38,6 +40,9 @@ def _check_state(c, ref, st):
     assert core.stats == ref.counts
     assert [int(v) for v in core.slot_key] == ref.owner
     assert [float(v) for v in core.last] == ref.t_last
+    assert [float(v) for v in core.score] == ref.f_score
+    assert list(core.freq.items()) == list(ref.acc.items())  # values and insertion order
+    assert core.inc == ref.unit
     assert core.free == list(ref.stack)
     assert core.tick == ref.now
     for key, s in ref.where.items():  # every resident slot holds its store row
@@ -48,12 +53,14 @@ def _row(ids, w):
     return torch.tensor(list(map(float, ids)) + list(map(float, w)), dtype=torch.float32, device=DEV)
 
 
-@pytest.mark.parametrize("nslots,k,use_row", [(10, 4, False), (10, 8, True), (20, 16, False), (9, 1, True),
-                                             (64, 8, False)])
-def test_device_steps_match_reference_lru(store, nslots, k, use_row):
+@pytest.mark.parametrize("nslots,k,use_row,policy", [(10, 4, False, "lru"), (10, 8, True, "lru"),
+                                                    (20, 16, False, "lru"), (9, 1, True, "lru"),
+                                                    (64, 8, False, "lru"), (10, 4, False, "wsa"),
+                                                    (20, 8, True, "wsa"), (12, 6, False, "static")])
+def test_device_steps_match_reference_lru(store, nslots, k, use_row, policy):
     E = 24
-    c = ExpertCache(store, nslots, copy="kernel")
-    ref = RefCore(nslots, "lru")
+    c = ExpertCache(store, nslots, policy=policy, copy="kernel")
+    ref = RefCore(nslots, policy)
     rng = np.random.default_rng(nslots * 31 + k)
     meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
     c.device_begin()
@@ -78,6 +85,37 @@ def test_device_steps_match_reference_lru(store, nslots, k, use_row):
             c.device_begin()
     _check_state(c, ref, store)
     assert c.n_loads == ref.counts["misses"] and c.bytes_h2d == c.n_loads * store.nbytes
+    c.free()
+
+
+@pytest.mark.parametrize("policy,nslots", [("wsa", 16), ("lru", 16), ("wsa", 1300)])
+def test_device_steps_through_the_renormalisation(store, policy, nslots):
+    """decay 0.25: inc grows fourfold a step and passes 1e100 at step 167, where every
+    frequency, every score and inc are divided by 1e100 (cache_core.py:34-38); steps on both
+    sides, with host steps before device paging begins, equal the reference core's, scores
+    and the frequency table included. 1,300 slots: the multi-wave form over 72 keys (no
+    evictions: the dynamic region never fills)."""
+    E, k = 24, 6
+    c = ExpertCache(store, nslots, policy=policy, decay=0.25, copy="kernel")
+    ref = RefCore(nslots, policy, decay=0.25)
+    rng = np.random.default_rng(17)
+    meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
+    for it in range(5):  # host steps first: keys already in the table when device paging begins
+        keys = [int(v) for v in rng.choice(3 * E, size=k, replace=False)]
+        assert c.ensure(keys) == ref.ensure(keys)[0], it
+    c.device_begin()
+    for it in range(220):
+        layer = int(rng.integers(0, 3))
+        ids = rng.choice(E, size=k, replace=False).astype(np.int64)
+        c.device_step(_row(ids, np.ones(k)), None, layer * E, E, k, meta)
+        slots, _ = ref.ensure([layer * E + int(v) for v in ids])
+        assert [int(v) for v in meta[:k].cpu()] == slots, it
+        if it in (150, 175):
+            c.device_sync()
+            assert c.core.inc == ref.unit, it  # (ends device paging)
+            c.device_begin()
+    assert ref.unit < 1e100 and ref.now == 225
+    _check_state(c, ref, store)
     c.free()
 
 
@@ -132,8 +170,9 @@ def test_device_steps_past_1024_dynamic_slots(nslots, n_static):
     c.free()
 
 
-@pytest.mark.parametrize("nslots,n_static", [(12000, 0), (20000, 300), (26880, 0)])
-def test_device_steps_in_large_pools(nslots, n_static):
+@pytest.mark.parametrize("nslots,n_static,policy", [(12000, 0, "lru"), (20000, 300, "lru"), (26880, 0, "lru"),
+                                                    (14000, 200, "wsa")])
+def test_device_steps_in_large_pools(nslots, n_static, policy):
     """Pools up to the device step's limit of 26,880 dynamic slots (15 waves of 28 eviction
     keys per thread): filled to 8 free slots, a mixed free/evicting step, then random steps
     over 32,768 keys taken three ways in turn -- the LRU step on the row's ids, the route +
@@ -144,8 +183,8 @@ def test_device_steps_in_large_pools(nslots, n_static):
     gen = torch.Generator().manual_seed(nslots)
     st.host.copy_(torch.randint(0, 256, tuple(st.host.shape), dtype=torch.uint8, generator=gen))
     pre = list(range(32000, 32000 + n_static))
-    c = ExpertCache(st, nslots, n_static=n_static, preload_keys=pre or None, copy="kernel")
-    ref = RefCore(nslots, "lru", n_static=n_static)
+    c = ExpertCache(st, nslots, policy=policy, n_static=n_static, preload_keys=pre or None, copy="kernel")
+    ref = RefCore(nslots, policy, n_static=n_static)
     if pre:
         ref.preload(pre)
     meta = torch.zeros(2 * k, dtype=torch.float32, device=DEV)
@@ -414,7 +453,4 @@ def test_device_paging_refusals(store):
     with pytest.raises(RuntimeError, match="26880 dynamic slots"):
         c.device_begin()
     c.free()
-    c = ExpertCache(store, 8, policy="wsa", copy="kernel")
-    with pytest.raises(RuntimeError, match="LRU"):
-        c.device_begin()
-    c.free()
+

@@ -199,22 +199,28 @@ static void view_deleter(DLManagedTensor* m) {
     delete v;
 }
 
-// Device paging: the LRU state in device memory (one allocation) while it is on.
+// Device paging: the core's state in device memory (one allocation) while it is on.
 constexpr int kDevMaxK = 16;  // keys per step
-// The LRU step holds every dynamic slot's eviction key in registers for the whole step:
+// The step holds every dynamic slot's eviction key in registers for the whole step:
 // kLruSmall keys per lane of one wave for pools of at most 64 kLruSmall dynamic slots, else
 // kLruBig keys per thread of up to 15 waves beside the wave that routes (16 in all).
 constexpr int kLruSmall = 16, kLruBig = 28;
 constexpr int kDevMaxSlots = 15 * 64 * kLruBig;  // 26880 dynamic slots
-enum { kCtrTick, kCtrNextFree, kCtrHits, kCtrMisses, kCtrEvict, kCtrCalls, kCtrLoads, kCtrErr, kCtrOn, kCtrN };
+enum { kCtrTick, kCtrNextFree, kCtrHits, kCtrMisses, kCtrEvict, kCtrCalls, kCtrLoads, kCtrErr, kCtrOn, kCtrInc, kCtrN };
 enum { kDevErrSlot = 1, kDevErrKey = 2 };
+constexpr int64_t kFirstBefore = -2, kFirstNever = -1;  // DevPaging::first, besides a device stamp
 struct DevPaging {
     int32_t* slot_key = nullptr;  // [nslots], -1 empty
     int64_t* last = nullptr;      // [nslots], tick of the last use
+    double* score = nullptr;      // [nslots], the decayed frequency of the slot's key at its last note
     int32_t* key2slot = nullptr;  // [nkeys], -1 not resident
+    double* freq = nullptr;       // [nkeys], decayed access frequency (0 for keys never noted)
+    int64_t* first = nullptr;     // [nkeys], kFirstBefore: in the core's table before device paging began;
+                                  // kFirstNever; else 64 tick + position of the key's first note on the device
     int64_t* ctr = nullptr;       // [kCtrN]: tick, next free slot, hits, misses, evictions, calls, loads, error
-                                  // bits, on (1 while the device holds the state)
+                                  // bits, on (1 while the device holds the state), the bits of inc (binary64)
     int32_t* miss = nullptr;      // [1 + 2 kDevMaxK]: count, keys, slots of the last step's loads
+    double decay = 1.0;
     int64_t nslots = 0, nkeys = 0, n_static = 0;
 };
 
@@ -242,6 +248,7 @@ struct Cache {
     void* dev_block = nullptr;
     DevPaging dev;
     bool dev_on = false;
+    bool dev_score = false;      // the core's policy evicts by score (WSA, static), not by last use
     int64_t dev_loads_seen = 0;  // device loads already added to bytes_h2d / n_loads
 };
 
@@ -346,16 +353,23 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
     return min_u64(min_u64(readlane_u64(v, 0), readlane_u64(v, 16)), min_u64(readlane_u64(v, 32), readlane_u64(v, 48)));
 }
 
-// The step's counters (wave 0).
+// The step's counters and its clock (cache_core.py:30-38, step): tick + 1, inc / decay, and
+// when that passes 1e100 every frequency, every score and inc itself divided by 1e100 (the
+// renormalisation, applied by lru_commit). Uniform scalar reads, taken by every wave.
 struct LruCtr {
     int64_t tick, nf;
-    bool on;
+    double inc;
+    bool on, renorm;
 };
 __device__ __forceinline__ LruCtr lru_counters(const DevPaging& d) {
     LruCtr st;
     st.on = d.ctr[kCtrOn] != 0;
     st.tick = d.ctr[kCtrTick] + 1;
     st.nf = d.ctr[kCtrNextFree];
+    double inc = __longlong_as_double((long long)d.ctr[kCtrInc]) / d.decay;
+    st.renorm = inc > 1e100;
+    if (st.renorm) inc = inc / 1e100;
+    st.inc = inc;
     return st;
 }
 
@@ -371,25 +385,38 @@ __device__ __forceinline__ int lru_holders() {
     return R == kLruSmall ? (int)blockDim.x : (int)blockDim.x - 64;
 }
 
-// Eviction keys in registers: dynamic slot i as (last, slot) + 1, or ~0 past the pool (a key is
-// never 0, so 0 is below every key). One request per key, all before any use; 32-bit slot
-// indexes (nd <= kDevMaxSlots), so each request needs one offset register. The one-wave form
-// also holds each slot's key (owner) in `own`, so the victims' old keys need no dependent read.
-template <int R>
-__device__ __forceinline__ void lru_stage(const DevPaging& d, int nd, uint64_t (&key)[R], int32_t (&own)[R]) {
+// Eviction keys in registers, dynamic slot i (slot n_static + i) of holder t in key[u],
+// i = t + nt u, ~0 past the pool. LRU (SC false): (last, slot) + 1 as one integer (never 0,
+// so 0 is below every key). Score policies (SC true): the bits of the slot's score (a
+// non-negative binary64, so its bits order as its value; divided by 1e100 first when this step
+// renormalises), the slot implied by the position. One request per key, all before any use;
+// 32-bit slot indexes (nd <= kDevMaxSlots), so each request needs one offset register. The
+// one-wave form also holds each slot's key (owner) in `own`, so the victims' old keys need no
+// dependent read.
+template <int R, bool SC>
+__device__ __forceinline__ void lru_stage(const DevPaging& d, int nd, bool renorm, uint64_t (&key)[R],
+                                          int32_t (&own)[R]) {
     const int t = lru_holder<R>(), nt = lru_holders<R>();
     const int64_t* __restrict__ lp = d.last + d.n_static;
+    const double* __restrict__ sp = d.score + d.n_static;
     const int32_t* __restrict__ op = d.slot_key + d.n_static;
-    int64_t v[R];
+    uint64_t v[R];
 #pragma unroll
     for (int u = 0; u < R; ++u) {
-        v[u] = lp[min(t + nt * u, nd - 1)];
-        if constexpr (R == kLruSmall) own[u] = op[min(t + nt * u, nd - 1)];
+        const int i = min(t + nt * u, nd - 1);
+        v[u] = SC ? (uint64_t)__double_as_longlong(sp[i]) : (uint64_t)lp[i];
+        if constexpr (R == kLruSmall) own[u] = op[i];
     }
 #pragma unroll
     for (int u = 0; u < R; ++u) {
         const int i = t + nt * u;
-        key[u] = i < nd ? (((uint64_t)v[u] << 20) | (uint64_t)(d.n_static + i)) + 1ull : ~0ull;
+        uint64_t kv;
+        if constexpr (SC) {
+            kv = renorm ? (uint64_t)__double_as_longlong(__longlong_as_double((long long)v[u]) / 1e100) : v[u];
+        } else {
+            kv = ((v[u] << 20) | (uint64_t)(d.n_static + i)) + 1ull;
+        }
+        key[u] = i < nd ? kv : ~0ull;
     }
 }
 
@@ -409,6 +436,7 @@ __device__ __forceinline__ int lru_owner_of(const int32_t (&own)[kLruSmall], int
 // What wave 0 tells the other waves of the step (through LDS, before the eviction rounds).
 struct LruShared {
     uint64_t wmin[2][16];     // per-wave round minima, two buffers (rounds alternate)
+    int32_t wslot[2][16];     // their slots (score policies)
     int32_t hits[kDevMaxK];   // this step's hit slots
     int32_t nhit, m;          // hits, misses that evict
     int64_t nc;               // dynamic slots in use at the step's start
@@ -417,24 +445,30 @@ struct LruShared {
 // Wave 0's per-lane view of the step.
 struct LruLane {
     int key, slot, rank, from_free, nmiss;
+    int lead, mult;  // the first lane holding this lane's key; on that lane, how many lanes hold it
     float w;
     bool miss, hit, on;
     uint64_t hm, bad;
+    double fq;       // freq[key] at the step's start (lead lanes)
+    int64_t fst;     // first[key] (lead lanes)
 };
 
-// cache_core.py:86-106 (ensure) with the LRU policy on the GPU, for one layer, in three
-// parts: lru_classify (wave 0: lane j < k holds key j, -1 if its id was not valid, and its
-// weight w), lru_evict (every wave of the workgroup) and lru_commit (wave 0). Hits are
-// noted with the step's tick; misses take free slots in ascending order, then the least
-// recently used unprotected slots. The reference picks each victim by a first-index argmin
-// of `last` over the unprotected dynamic slots, and every slot it hands out becomes
-// protected, so the i-th evicting miss (in key order) gets the i-th smallest (last, slot)
-// among the slots in [n_static, next free) that are not hits of this step. meta = [slots
-// (float) | the row's weights]; the loads go to the miss list for k_page_list. A key that is
-// not valid or a miss without an evictable slot gets slot -1 in meta (the MoE kernels then
-// write NaN rows) and sets an error bit that the host reads when it syncs the state. A
-// launch while device paging is off (a captured step replayed after wisp_cache_device_end)
-// does no step and writes slot -1 into meta.
+// cache_core.py:86-106 (ensure) on the GPU, for one layer, in three parts: lru_classify
+// (wave 0: lane j < k holds key j, -1 if its id was not valid, and its weight w), lru_evict
+// (every wave of the workgroup) and lru_commit (wave 0). The step's clock and notes
+// (cache_core.py:30-51: inc, every key's decayed frequency with one addition of inc per
+// occurrence in key order, a resident key's tick and score) are kept for every policy, as
+// the reference keeps them. Misses take free slots in ascending order, then the unprotected
+// slot with the smallest eviction key: `last` (LRU) or `score` (WSA, static). The reference
+// picks each victim by a first-index argmin over the unprotected dynamic slots, and every slot
+// it hands out becomes protected, so the i-th evicting miss (in key order) gets the i-th
+// smallest (key, slot) among the slots in [n_static, next free) that are not hits of this
+// step (a score policy's notes change only hits' scores before the victims are chosen).
+// meta = [slots (float) | the row's weights]; the loads go to the miss list for k_page_list.
+// A key that is not valid or a miss without an evictable slot gets slot -1 in meta (the MoE
+// kernels then write NaN rows) and sets an error bit that the host reads when it syncs the
+// state. A launch while device paging is off (a captured step replayed after
+// wisp_cache_device_end) does no step and writes slot -1 into meta.
 // `resident` is key2slot[key] (-1 for key < 0), looked up by the caller.
 __device__ __forceinline__ LruLane lru_classify(const DevPaging& d, const LruCtr& st, int lane, int k, int key,
                                                 int resident, float w, LruShared& sh) {
@@ -449,6 +483,19 @@ __device__ __forceinline__ LruLane lru_classify(const DevPaging& d, const LruCtr
             sh.nc = 0;
         }
         return ln;
+    }
+    // the notes: the first lane of each key adds inc once per lane holding it (in lru_commit);
+    // its frequency and first-note stamp are requested here and used after the rounds
+    ln.lead = lane;
+    ln.mult = 0;
+    for (int j = 0; j < k; ++j) {
+        const int kj = __shfl(key, j, 64);
+        if (kj == key && j < ln.lead) ln.lead = j;
+        ln.mult += kj == key ? 1 : 0;
+    }
+    if (key >= 0 && ln.lead == lane) {
+        ln.fq = d.freq[key];
+        ln.fst = d.first[key];
     }
     const int64_t nf = st.nf;
     int slot = key >= 0 ? resident : -1;
@@ -479,8 +526,42 @@ __device__ __forceinline__ LruLane lru_classify(const DevPaging& d, const LruCtr
 // barriers. A winner that is a hit of this step is protected: it is passed over (at most
 // one round per hit). Returns the victims found; wave 0's evicting miss of rank
 // from_free + i gets victim i in ln.slot.
-template <int R>
-__device__ __forceinline__ int lru_evict(LruShared& sh, uint64_t (&key)[R], LruLane& ln, bool wave0) {
+// (value, slot) order of the score policies: value first, then the lower slot.
+__device__ __forceinline__ bool pair_lt(uint64_t a, int sa, uint64_t b, int sb) {
+    return a < b || (a == b && sa < sb);
+}
+template <int CTRL>
+__device__ __forceinline__ void pair_min_dpp(uint64_t& v, int& s) {
+    const uint64_t ov = dpp_u64<CTRL>(v);
+    const int os = __builtin_amdgcn_update_dpp(0, s, CTRL, 0xF, 0xF, true);
+    if (pair_lt(ov, os, v, s)) {
+        v = ov;
+        s = os;
+    }
+}
+// wave-wide (value, slot) minimum, as wave_min_u64 (every lane active; wave-uniform result)
+__device__ __forceinline__ void wave_min_pair(uint64_t& v, int& s) {
+    pair_min_dpp<0xB1>(v, s);
+    pair_min_dpp<0x4E>(v, s);
+    pair_min_dpp<0x141>(v, s);
+    pair_min_dpp<0x140>(v, s);
+    uint64_t bv = readlane_u64(v, 0);
+    int bs = __builtin_amdgcn_readlane(s, 0);
+#pragma unroll
+    for (int r = 16; r < 64; r += 16) {
+        const uint64_t rv = readlane_u64(v, r);
+        const int rs = __builtin_amdgcn_readlane(s, r);
+        if (pair_lt(rv, rs, bv, bs)) {
+            bv = rv;
+            bs = rs;
+        }
+    }
+    v = bv;
+    s = bs;
+}
+
+template <int R, bool SC>
+__device__ __forceinline__ int lru_evict(LruShared& sh, uint64_t (&key)[R], LruLane& ln, bool wave0, int n_static) {
     const int m = sh.m;
     if (m <= 0) return 0;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -490,31 +571,71 @@ __device__ __forceinline__ int lru_evict(LruShared& sh, uint64_t (&key)[R], LruL
         if (t + nt * u >= nc) key[u] = ~0ull;  // free slots are not candidates (wave 0 of R = kLruBig holds none)
     const int nhit = sh.nhit;
     const int hs = lane < nhit ? sh.hits[lane] : -1;
-    uint64_t prev = 0;
     int found = 0, buf = 0;
-    while (found < m) {
-        uint64_t best = ~0ull;
+    if constexpr (!SC) {
+        uint64_t prev = 0;
+        while (found < m) {
+            uint64_t best = ~0ull;
 #pragma unroll
-        for (int u = 0; u < R; ++u) best = (key[u] > prev && key[u] < best) ? key[u] : best;
-        best = wave_min_u64(best);
-        if (nw > 1) {
-            if (lane == 0) sh.wmin[buf][wv] = best;
-            __syncthreads();
-            best = ~0ull;
-            for (int w = 0; w < nw; ++w) best = min_u64(best, sh.wmin[buf][w]);
-            buf ^= 1;
+            for (int u = 0; u < R; ++u) best = (key[u] > prev && key[u] < best) ? key[u] : best;
+            best = wave_min_u64(best);
+            if (nw > 1) {
+                if (lane == 0) sh.wmin[buf][wv] = best;
+                __syncthreads();
+                best = ~0ull;
+                for (int w = 0; w < nw; ++w) best = min_u64(best, sh.wmin[buf][w]);
+                buf ^= 1;
+            }
+            if (best == ~0ull) break;  // nothing evictable is left
+            prev = best;
+            const int s = (int)((best - 1ull) & 0xFFFFFull);
+            if (__ballot(hs == s)) continue;  // a hit of this step
+            if (wave0 && ln.miss && ln.rank == ln.from_free + found) ln.slot = s;
+            ++found;
         }
-        if (best == ~0ull) break;  // nothing evictable is left
-        prev = best;
-        const int s = (int)((best - 1ull) & 0xFFFFFull);
-        if (__ballot(hs == s)) continue;  // a hit of this step
-        if (wave0 && ln.miss && ln.rank == ln.from_free + found) ln.slot = s;
-        ++found;
+    } else {
+        uint64_t pv = 0;  // the last round's (score bits, slot); slot -1 is below every slot
+        int ps = -1;
+        while (found < m) {
+            uint64_t bv = ~0ull;
+            int bs = 0x7FFFFFFF;
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                const int s = n_static + t + nt * u;
+                if (key[u] != ~0ull && pair_lt(pv, ps, key[u], s) && pair_lt(key[u], s, bv, bs)) {
+                    bv = key[u];
+                    bs = s;
+                }
+            }
+            wave_min_pair(bv, bs);
+            if (nw > 1) {
+                if (lane == 0) {
+                    sh.wmin[buf][wv] = bv;
+                    sh.wslot[buf][wv] = bs;
+                }
+                __syncthreads();
+                bv = ~0ull;
+                bs = 0x7FFFFFFF;
+                for (int w = 0; w < nw; ++w)
+                    if (pair_lt(sh.wmin[buf][w], sh.wslot[buf][w], bv, bs)) {
+                        bv = sh.wmin[buf][w];
+                        bs = sh.wslot[buf][w];
+                    }
+                buf ^= 1;
+            }
+            if (bv == ~0ull) break;  // nothing evictable is left
+            pv = bv;
+            ps = bs;
+            if (__ballot(hs == bs)) continue;  // a hit of this step
+            if (wave0 && ln.miss && ln.rank == ln.from_free + found) ln.slot = bs;
+            ++found;
+        }
     }
     return found;
 }
 
-// Wave 0: the step's writes (slot table, LRU ticks, the miss list, meta and counters).
+// Wave 0: the step's writes (the clock and notes, slot table, ticks and scores, the miss
+// list, meta and counters).
 template <int R>
 __device__ __forceinline__ void lru_commit(const DevPaging& d, const LruCtr& st, int lane, int k, const LruLane& ln,
                                            int evicted, const int32_t (&own)[R], float* __restrict__ meta) {
@@ -526,6 +647,27 @@ __device__ __forceinline__ void lru_commit(const DevPaging& d, const LruCtr& st,
     const int64_t tick = st.tick, nf = st.nf;
     const int key = ln.key, slot = ln.slot;
     const int got = ln.from_free + evicted;  // misses with a slot
+    // the renormalisation (every frequency and score / 1e100), before this step's own writes
+    // of the same entries, which follow in this wave's program order
+    if (st.renorm) {
+        for (int64_t i = lane; i < d.nkeys; i += 64) d.freq[i] = d.freq[i] / 1e100;
+        for (int64_t i = lane; i < d.nslots; i += 64) d.score[i] = d.score[i] / 1e100;
+    }
+    // the notes: a key's lead lane adds inc once per lane holding the key, one addition at a
+    // time as the reference's loop does; a key first noted here gets its order stamp
+    double f = 0.0;
+    if (key >= 0 && ln.lead == lane) {
+        f = st.renorm ? ln.fq / 1e100 : ln.fq;
+        for (int j = 0; j < ln.mult; ++j) f = f + st.inc;
+        d.freq[key] = f;
+        if (ln.fst == kFirstNever) d.first[key] = tick * 64 + lane;
+    }
+    // every lane of a key takes the lead's frequency: the score of its slot if it is resident
+    // or loaded now (cache_core.py:46 and :82)
+    const long long fb = __double_as_longlong(f);
+    const uint32_t flo = (uint32_t)__shfl((int)(uint32_t)fb, ln.lead, 64);
+    const uint32_t fhi = (uint32_t)__shfl((int)(uint32_t)((uint64_t)fb >> 32), ln.lead, 64);
+    const double fk = __longlong_as_double((long long)(((uint64_t)fhi << 32) | flo));
     // the key this lane's victim held: from the staged owners (one wave), else read
     const bool evicts = ln.miss && ln.rank >= ln.from_free && slot >= 0;
     int old_key = -1;
@@ -542,12 +684,16 @@ __device__ __forceinline__ void lru_commit(const DevPaging& d, const LruCtr& st,
         later = later || (j > lane && kj == key);
     }
     const bool gets = ln.miss && slot >= 0;
-    if (ln.hit) d.last[slot] = tick;
+    if (ln.hit) {
+        d.last[slot] = tick;
+        d.score[slot] = fk;
+    }
     if (gets) {
         if (old_key >= 0) d.key2slot[old_key] = -1;
         d.slot_key[slot] = key;
         if (!later) d.key2slot[key] = slot;
         d.last[slot] = tick;
+        d.score[slot] = fk;
         d.miss[1 + ln.rank] = key;
         d.miss[1 + kDevMaxK + ln.rank] = slot;
     }
@@ -558,6 +704,7 @@ __device__ __forceinline__ void lru_commit(const DevPaging& d, const LruCtr& st,
     if (lane == 0) {
         d.miss[0] = got;
         d.ctr[kCtrTick] = tick;
+        d.ctr[kCtrInc] = (int64_t)__double_as_longlong(st.inc);
         d.ctr[kCtrNextFree] = nf + ln.from_free;
         d.ctr[kCtrHits] += __popcll(ln.hm);
         d.ctr[kCtrMisses] += got;
@@ -583,28 +730,29 @@ static inline int lru_threads(int64_t nd) {
 // classify them), and the key holders' staging: one wave requests its keys first, then does
 // the rest; with kLruBig keys the other waves stage while wave 0 works, in disjoint branches
 // (so wave 0's registers never hold keys and the keys' registers never hold its state).
-template <int R, typename Classify>
-__device__ __forceinline__ LruLane lru_begin(const DevPaging& d, uint64_t (&key)[R], int32_t (&own)[R],
+template <int R, bool SC, typename Classify>
+__device__ __forceinline__ LruLane lru_begin(const DevPaging& d, bool renorm, uint64_t (&key)[R], int32_t (&own)[R],
                                              Classify classify) {
     const int nd = (int)(d.nslots - d.n_static);  // in [1, kDevMaxSlots] (device_begin)
     LruLane ln{};
     if constexpr (R == kLruSmall) {
-        lru_stage<R>(d, nd, key, own);
+        lru_stage<R, SC>(d, nd, renorm, key, own);
         ln = classify();
     } else if (threadIdx.x < 64) {
         ln = classify();
 #pragma unroll
         for (int u = 0; u < R; ++u) key[u] = ~0ull;
     } else {
-        lru_stage<R>(d, nd, key, own);
+        lru_stage<R, SC>(d, nd, renorm, key, own);
     }
     return ln;
 }
 
 // The step for key_base + id_j, id_j = ids[j] if ids and ids[j] >= 0, else the route row's id
 // j (an integer in [0, n_ids)); weights from the row. k <= 0: a warm-up launch that only
-// clears the miss list. R keys per key holder, blockDim.x = lru_threads(dynamic slots).
-template <int R>
+// clears the miss list. R keys per key holder, blockDim.x = lru_threads(dynamic slots); SC:
+// a score policy (WSA, static) rather than LRU.
+template <int R, bool SC>
 __global__ __launch_bounds__(R == kLruSmall ? 64 : 1024) void k_lru_step(const DevPaging d,
                                                                           const float* __restrict__ row,
                                                                           const int64_t* __restrict__ ids,
@@ -617,11 +765,10 @@ __global__ __launch_bounds__(R == kLruSmall ? 64 : 1024) void k_lru_step(const D
         if (threadIdx.x == 0) d.miss[0] = 0;
         return;
     }
-    LruCtr st{};
-    if (wave0) st = lru_counters(d);
+    const LruCtr st = lru_counters(d);
     uint64_t key[R];
     int32_t own[R];
-    LruLane ln = lru_begin<R>(d, key, own, [&] {
+    LruLane ln = lru_begin<R, SC>(d, st.renorm, key, own, [&] {
         int kk = -1;
         float w = 0.f;
         if (lane < k) {
@@ -636,7 +783,7 @@ __global__ __launch_bounds__(R == kLruSmall ? 64 : 1024) void k_lru_step(const D
         return lru_classify(d, st, lane, k, kk, kk >= 0 ? d.key2slot[kk] : -1, w, sh);
     });
     __syncthreads();
-    const int evicted = lru_evict<R>(sh, key, ln, wave0);
+    const int evicted = lru_evict<R, SC>(sh, key, ln, wave0, (int)d.n_static);
     if (wave0) lru_commit<R>(d, st, lane, k, ln, evicted, own, meta);
 }
 
@@ -645,9 +792,9 @@ __global__ __launch_bounds__(R == kLruSmall ? 64 : 1024) void k_lru_step(const D
 // eviction keys are in flight. ids (optional) replace the chosen expert ids where they are
 // >= 0; the weights are the router's. The key -> slot entries of ids 0 .. 64 EPL - 1 (every
 // expert the router can pick) are requested at the start with the rest, so the chosen keys'
-// residency needs no dependent read (a forced id past them is read). Launch shape as for
-// k_lru_step.
-template <int EPL, int R>
+// residency needs no dependent read (a forced id past them is read). Launch shape and SC as
+// for k_lru_step.
+template <int EPL, int R, bool SC>
 __global__ __launch_bounds__(R == kLruSmall ? 64 : 1024) void k_route_lru(const DevPaging d,
                                                                            const uint16_t* __restrict__ logits, int E,
                                                                            int k, int norm, float* __restrict__ row,
@@ -661,11 +808,10 @@ __global__ __launch_bounds__(R == kLruSmall ? 64 : 1024) void k_route_lru(const 
         if (threadIdx.x == 0) d.miss[0] = 0;
         return;
     }
-    LruCtr st{};
+    const LruCtr st = lru_counters(d);
     int64_t forced = -1;
     int32_t pre[EPL];  // key2slot[key_base + lane + 64 t], clamped into the table
     if (wave0) {
-        st = lru_counters(d);
         forced = ids ? ids[lane < k ? lane : 0] : -1;
 #pragma unroll
         for (int t = 0; t < EPL; ++t) {
@@ -675,7 +821,7 @@ __global__ __launch_bounds__(R == kLruSmall ? 64 : 1024) void k_route_lru(const 
     }
     uint64_t key[R];
     int32_t own[R];
-    LruLane ln = lru_begin<R>(d, key, own, [&] {
+    LruLane ln = lru_begin<R, SC>(d, st.renorm, key, own, [&] {
         const float val = route_select<EPL>(logits, E, k, norm);
         if (lane < 2 * k) row[lane] = val;
         const float w = __shfl(val, (k + lane) & 63, 64);
@@ -695,7 +841,7 @@ __global__ __launch_bounds__(R == kLruSmall ? 64 : 1024) void k_route_lru(const 
         return lru_classify(d, st, lane, k, kk, kk >= 0 ? res : -1, w, sh);
     });
     __syncthreads();
-    const int evicted = lru_evict<R>(sh, key, ln, wave0);
+    const int evicted = lru_evict<R, SC>(sh, key, ln, wave0, (int)d.n_static);
     if (wave0) lru_commit<R>(d, st, lane, k, ln, evicted, own, meta);
 }
 
@@ -1352,20 +1498,35 @@ static int dev_download(Cache& c, hipStream_t st) {
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize (device paging)");
     const DevPaging& d = c.dev;
     std::vector<int32_t> sk(d.nslots), k2s(d.nkeys);
-    std::vector<int64_t> last(d.nslots), ctr(kCtrN);
+    std::vector<int64_t> last(d.nslots), ctr(kCtrN), first(d.nkeys);
+    std::vector<double> score(d.nslots), freq(d.nkeys);
     e = hipMemcpy(sk.data(), d.slot_key, sizeof(int32_t) * d.nslots, hipMemcpyDeviceToHost);
     if (e == hipSuccess) e = hipMemcpy(last.data(), d.last, sizeof(int64_t) * d.nslots, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(score.data(), d.score, sizeof(double) * d.nslots, hipMemcpyDeviceToHost);
     if (e == hipSuccess) e = hipMemcpy(k2s.data(), d.key2slot, sizeof(int32_t) * d.nkeys, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(freq.data(), d.freq, sizeof(double) * d.nkeys, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(first.data(), d.first, sizeof(int64_t) * d.nkeys, hipMemcpyDeviceToHost);
     if (e == hipSuccess) e = hipMemcpy(ctr.data(), d.ctr, sizeof(int64_t) * kCtrN, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpy (device paging state)");
     Core& core = *c.core;
     for (int64_t s = 0; s < d.nslots; ++s) {
         core.slot_key[s] = sk[s];
         core.last[s] = (double)last[s];
+        core.score[s] = score[s];
     }
     core.key2slot.clear();
     for (int64_t key = 0; key < d.nkeys; ++key)
         if (k2s[key] >= 0) core.key2slot[key] = k2s[key];
+    // the frequency table: keys noted before device paging began keep their place; keys first
+    // noted on the device join it in the order of their first notes (step, then position)
+    std::vector<std::pair<int64_t, int64_t>> fresh_keys;
+    for (int64_t key = 0; key < d.nkeys; ++key) {
+        if (first[key] == kFirstBefore) core.freq[key] = freq[key];
+        else if (first[key] >= 0) fresh_keys.emplace_back(first[key], key);
+    }
+    std::sort(fresh_keys.begin(), fresh_keys.end());
+    for (const auto& fk : fresh_keys) core.freq_at(fk.second) = freq[fk.second];
+    core.inc = __builtin_bit_cast(double, ctr[kCtrInc]);
     core.free.clear();
     for (int64_t s = d.nslots - 1; s >= ctr[kCtrNextFree]; --s) core.free.push_back(s);
     core.tick = ctr[kCtrTick];
@@ -1389,16 +1550,16 @@ static int dev_download(Cache& c, hipStream_t st) {
 
 }  // namespace wisp
 
-// Copy the host core's LRU state to the device and turn device paging on (a no-op
-// when it is on). Needs the LRU policy, the page-kernel copy mode, at most 26880
-// dynamic slots (2^20 in all) and the free slots at the top of the pool (the order
-// the core hands them out). Stream-ordered after the copies already issued.
+// Copy the host core's state to the device and turn device paging on (a no-op when it
+// is on). Any policy (LRU evicts by last use, WSA and static by score); needs the
+// page-kernel copy mode, at most 26880 dynamic slots (2^20 in all), the free slots at
+// the top of the pool (the order the core hands them out) and every noted key in the
+// store. Stream-ordered after the copies already issued.
 extern "C" int wisp_cache_device_begin(void* h, void* stream) {
     clear_error();
     Cache& c = *as_cache(h);
     if (c.dev_on) return WISP_OK;
     const Core& core = *c.core;
-    if (core.policy != kLRU) return fail_inval("device paging runs the LRU policy only");
     if (c.copy_mode != 1 || !c.host_dev) return fail_inval("device paging needs the page-kernel copy mode");
     if (!c.pool) return no_pool();
     if (c.nslots > (1 << 20) || c.nslots - core.n_static > kDevMaxSlots)
@@ -1412,8 +1573,10 @@ extern "C" int wisp_cache_device_begin(void* h, void* stream) {
     d.nslots = c.nslots;
     d.nkeys = c.host_rows;
     d.n_static = core.n_static;
+    d.decay = core.decay;
     std::vector<int32_t> sk(d.nslots), k2s(d.nkeys, -1);
-    std::vector<int64_t> last(d.nslots);
+    std::vector<int64_t> last(d.nslots), first(d.nkeys, kFirstNever);
+    std::vector<double> freq(d.nkeys, 0.0);
     for (int64_t s = 0; s < d.nslots; ++s) {
         sk[s] = (int32_t)core.slot_key[s];
         last[s] = (int64_t)core.last[s];
@@ -1422,10 +1585,17 @@ extern "C" int wisp_cache_device_begin(void* h, void* stream) {
         if (kv.first < 0 || kv.first >= d.nkeys) return fail_inval("device paging: a resident key outside the store");
         k2s[kv.first] = (int32_t)kv.second;
     }
-    const int64_t ctr[kCtrN] = {core.tick, nf, core.hits, core.misses, core.evictions, core.calls, 0, 0, 1};
+    for (const auto& kv : core.freq) {
+        if (kv.first < 0 || kv.first >= d.nkeys) return fail_inval("device paging: a noted key outside the store");
+        freq[kv.first] = kv.second;
+        first[kv.first] = kFirstBefore;
+    }
+    const int64_t ctr[kCtrN] = {core.tick, nf, core.hits, core.misses, core.evictions, core.calls, 0, 0, 1,
+                                __builtin_bit_cast(int64_t, core.inc)};
     const size_t b_sk = align256(sizeof(int32_t) * d.nslots), b_last = align256(sizeof(int64_t) * d.nslots),
-                 b_k2s = align256(sizeof(int32_t) * d.nkeys), b_ctr = align256(sizeof(int64_t) * kCtrN),
-                 b_miss = align256(sizeof(int32_t) * (1 + 2 * kDevMaxK));
+                 b_score = align256(sizeof(double) * d.nslots), b_k2s = align256(sizeof(int32_t) * d.nkeys),
+                 b_freq = align256(sizeof(double) * d.nkeys), b_first = align256(sizeof(int64_t) * d.nkeys),
+                 b_ctr = align256(sizeof(int64_t) * kCtrN), b_miss = align256(sizeof(int32_t) * (1 + 2 * kDevMaxK));
     int cur = 0;
     (void)hipGetDevice(&cur);
     (void)hipSetDevice(c.device);
@@ -1442,7 +1612,7 @@ extern "C" int wisp_cache_device_begin(void* h, void* stream) {
     }
     void* block = c.dev_block;
     if (!block) {
-        e = hipMalloc(&block, b_sk + b_last + b_k2s + b_ctr + b_miss);
+        e = hipMalloc(&block, b_sk + b_last + b_score + b_k2s + b_freq + b_first + b_ctr + b_miss);
         if (e != hipSuccess) {
             (void)hipGetLastError();
             (void)hipSetDevice(cur);
@@ -1451,15 +1621,29 @@ extern "C" int wisp_cache_device_begin(void* h, void* stream) {
     }
     uint8_t* p = static_cast<uint8_t*>(block);
     d.slot_key = reinterpret_cast<int32_t*>(p);
-    d.last = reinterpret_cast<int64_t*>(p + b_sk);
-    d.key2slot = reinterpret_cast<int32_t*>(p + b_sk + b_last);
-    d.ctr = reinterpret_cast<int64_t*>(p + b_sk + b_last + b_k2s);
-    d.miss = reinterpret_cast<int32_t*>(p + b_sk + b_last + b_k2s + b_ctr);
+    p += b_sk;
+    d.last = reinterpret_cast<int64_t*>(p);
+    p += b_last;
+    d.score = reinterpret_cast<double*>(p);
+    p += b_score;
+    d.key2slot = reinterpret_cast<int32_t*>(p);
+    p += b_k2s;
+    d.freq = reinterpret_cast<double*>(p);
+    p += b_freq;
+    d.first = reinterpret_cast<int64_t*>(p);
+    p += b_first;
+    d.ctr = reinterpret_cast<int64_t*>(p);
+    p += b_ctr;
+    d.miss = reinterpret_cast<int32_t*>(p);
     int rc = sync_compute(c, st);  // copies still pending on the side stream
     if (!rc) {
         e = hipMemcpyAsync(d.slot_key, sk.data(), sizeof(int32_t) * d.nslots, hipMemcpyHostToDevice, st);
         if (e == hipSuccess) e = hipMemcpyAsync(d.last, last.data(), sizeof(int64_t) * d.nslots, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(d.score, core.score.data(), sizeof(double) * d.nslots, hipMemcpyHostToDevice, st);
         if (e == hipSuccess) e = hipMemcpyAsync(d.key2slot, k2s.data(), sizeof(int32_t) * d.nkeys, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(d.freq, freq.data(), sizeof(double) * d.nkeys, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(d.first, first.data(), sizeof(int64_t) * d.nkeys, hipMemcpyHostToDevice, st);
         if (e == hipSuccess) e = hipMemcpyAsync(d.ctr, ctr, sizeof(int64_t) * kCtrN, hipMemcpyHostToDevice, st);
         if (e == hipSuccess) e = hipMemsetAsync(d.miss, 0, sizeof(int32_t) * (1 + 2 * kDevMaxK), st);
         if (e == hipSuccess) e = hipStreamSynchronize(st);  // the host vectors go out of scope
@@ -1470,6 +1654,7 @@ extern "C" int wisp_cache_device_begin(void* h, void* stream) {
     c.dev_block = block;
     if (rc) return rc;  // the block is kept (device paging stays off)
     c.dev_on = true;
+    c.dev_score = core.policy != kLRU;
     c.dev_loads_seen = 0;
     return WISP_OK;
 }
@@ -1484,6 +1669,28 @@ static int no_slot_for_k(const Cache& c, int k) {
     std::snprintf(msg, sizeof msg, "device paging: top-k %d exceeds the %lld dynamic slots (no evictable slot)", k,
                   (long long)(c.nslots - c.dev.n_static));
     return fail_inval(msg);
+}
+
+// the step kernels' launch for nd dynamic slots (one wave up to 64 kLruSmall, else lru_threads)
+template <bool SC>
+static void launch_lru_step(const Cache& c, int64_t nd, hipStream_t st, const float* row, const int64_t* ids,
+                            int64_t key_base, int64_t n_ids, int k, float* meta) {
+    if (nd <= 64 * kLruSmall)
+        hipLaunchKernelGGL((k_lru_step<kLruSmall, SC>), dim3(1), dim3(64), 0, st, c.dev, row, ids, key_base, n_ids, k,
+                           meta);
+    else
+        hipLaunchKernelGGL((k_lru_step<kLruBig, SC>), dim3(1), dim3(lru_threads(nd)), 0, st, c.dev, row, ids,
+                           key_base, n_ids, k, meta);
+}
+template <int EPL, bool SC>
+static void launch_route_lru(const Cache& c, int64_t nd, hipStream_t st, const uint16_t* logits, int E, int k, int nt,
+                             float* row, const int64_t* ids, int64_t key_base, int64_t n_ids, float* meta) {
+    if (nd <= 64 * kLruSmall)
+        hipLaunchKernelGGL((k_route_lru<EPL, kLruSmall, SC>), dim3(1), dim3(64), 0, st, c.dev, logits, E, k, nt, row,
+                           ids, key_base, n_ids, meta);
+    else
+        hipLaunchKernelGGL((k_route_lru<EPL, kLruBig, SC>), dim3(1), dim3(lru_threads(nd)), 0, st, c.dev, logits, E,
+                           k, nt, row, ids, key_base, n_ids, meta);
 }
 
 // One layer's paging point on `stream` (capturable: no host sync, no allocation):
@@ -1502,11 +1709,10 @@ extern "C" int wisp_cache_device_step(void* h, const float* row, const int64_t* 
     if (!c.pool) return no_pool();
     hipStream_t st = (hipStream_t)stream;
     const int64_t nd = c.nslots - c.dev.n_static;
-    if (nd <= 64 * kLruSmall)
-        hipLaunchKernelGGL(k_lru_step<kLruSmall>, dim3(1), dim3(64), 0, st, c.dev, row, ids, key_base, n_ids, k, meta);
+    if (c.dev_score)
+        launch_lru_step<true>(c, nd, st, row, ids, key_base, n_ids, k, meta);
     else
-        hipLaunchKernelGGL(k_lru_step<kLruBig>, dim3(1), dim3(lru_threads(nd)), 0, st, c.dev, row, ids, key_base,
-                           n_ids, k, meta);
+        launch_lru_step<false>(c, nd, st, row, ids, key_base, n_ids, k, meta);
     int rc = check_launch("k_lru_step");
     if (rc) return rc;
     const int64_t row16 = c.row_bytes / 16, slot16 = c.slot_bytes / 16;
@@ -1533,13 +1739,11 @@ extern "C" int wisp_cache_device_route_step(void* h, const uint16_t* logits, int
     hipStream_t st = (hipStream_t)stream;
     const int nt = norm_topk ? 1 : 0;
     const int64_t nd = c.nslots - c.dev.n_static;
-#define WISP_RL(EPL)                                                                                               \
-    if (nd <= 64 * kLruSmall)                                                                                      \
-        hipLaunchKernelGGL((k_route_lru<EPL, kLruSmall>), dim3(1), dim3(64), 0, st, c.dev, logits, E, k, nt, row, \
-                           ids, key_base, n_ids, meta);                                                            \
-    else                                                                                                           \
-        hipLaunchKernelGGL((k_route_lru<EPL, kLruBig>), dim3(1), dim3(lru_threads(nd)), 0, st, c.dev, logits, E,  \
-                           k, nt, row, ids, key_base, n_ids, meta)
+#define WISP_RL(EPL)                                                                                   \
+    if (c.dev_score)                                                                                   \
+        launch_route_lru<EPL, true>(c, nd, st, logits, E, k, nt, row, ids, key_base, n_ids, meta);     \
+    else                                                                                               \
+        launch_route_lru<EPL, false>(c, nd, st, logits, E, k, nt, row, ids, key_base, n_ids, meta)
     if (E <= 64) {
         WISP_RL(1);
     } else if (E <= 128) {

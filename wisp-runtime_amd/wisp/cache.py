@@ -138,15 +138,15 @@ class ExpertCache:
         return ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
 
     # ---- device paging ----------------------------------------------------
-    # The LRU step of a decode layer on the GPU (k_lru_step + the page kernel), so a
-    # captured decode step has no host decision per layer. While it is on, the LRU
-    # state lives in device memory; every host-side operation below ends it first.
+    # The cache step of a decode layer on the GPU (k_lru_step + the page kernel; any
+    # policy), so a captured decode step has no host decision per layer. While it is on,
+    # the core's state lives in device memory; every host-side operation below ends it first.
     @property
     def device_paging(self) -> bool:
         return bool(self._h) and bool(_lib.lib().wisp_cache_device_active(self._h))
 
     def device_begin(self):
-        """Copy the core's LRU state to the device (LRU policy, copy="kernel", at most 26880
+        """Copy the core's state to the device (any policy, copy="kernel", at most 26880
         dynamic slots); RuntimeError if this cache cannot page on the device."""
         _raise(_lib.lib().wisp_cache_device_begin(self._h, self._stream()))
 
