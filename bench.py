@@ -389,6 +389,88 @@ def pmc_pass(bits: int) -> None:
     print("[bench] pmc pass done", file=sys.stderr, flush=True)
 
 
+def calib_copies(dev) -> None:
+    """Three plain device copies of CALIB_BYTES: the reference dispatches a counter pass
+    scales FETCH_SIZE / WRITE_SIZE by (the last three copy dispatches of the run)."""
+    src = torch.empty(CALIB_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("[bench] calibration copies done", file=sys.stderr, flush=True)
+
+
+SQ_PASS_A = ("SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_ACTIVE_INST_VMEM "
+             "SQ_WAIT_INST_LDS SQ_VALU_MFMA_BUSY_CYCLES SQ_WAIT_ANY")
+SQ_PASS_B = ("SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT SQ_INSTS_VMEM_RD SQ_INSTS_SALU "
+             "SQ_WAIT_INST_ANY SQ_LDS_DATA_FIFO_FULL")
+
+
+def summarize_kernel_pmc(title: str, cmd: str, fetch_csv: str, write_csv: str, sq_a_csv: str, sq_b_csv: str,
+                         specs) -> str:
+    """Markdown summary of four rocprofv3 --pmc passes over one workload (FETCH_SIZE, WRITE_SIZE,
+    then the two SQ passes) for the kernels named in specs = [(name substring, algorithmic bytes
+    per dispatch)]: HBM traffic scaled by the run's own calibration copies, and the issue and
+    wait shares (1,024 SIMDs at 2.4 GHz, 4 cycles per wave64 VALU instruction; durations include
+    the profiler's per-dispatch overhead)."""
+    import csv as _csv
+    import collections
+
+    fetch = _pmc_rows(fetch_csv, "FETCH_SIZE")
+    write = _pmc_rows(write_csv, "WRITE_SIZE")
+
+    def mean_of(rows, pred):
+        v = [x for n, x in rows if pred(n)]
+        return (sum(v) / len(v), len(v)) if v else (float("nan"), 0)
+
+    cf, ncf = mean_of(fetch, lambda n: n == "CALIBRATION")
+    cw, ncw = mean_of(write, lambda n: n == "CALIBRATION")
+    f_scale = cf * 1024 / CALIB_BYTES
+    w_scale = cw * 1024 / CALIB_BYTES
+    sq = collections.defaultdict(lambda: collections.defaultdict(list))
+    for path in (sq_a_csv, sq_b_csv):
+        with open(path) as f:
+            for r in _csv.DictReader(f):
+                for pat, _ in specs:
+                    if pat in r["Kernel_Name"]:
+                        sq[pat][r["Counter_Name"]].append(float(r["Counter_Value"]))
+                        if path == sq_a_csv and r["Counter_Name"] == "SQ_WAVE_CYCLES":
+                            sq[pat]["_ns"].append(float(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    lines = [f"# {title} (rocprofv3 --pmc)", "", "Commands (from the repository root on the GPU box, one pass each):",
+             "", "```", cmd, "```", "",
+             f"Calibration copy: {CALIB_BYTES} B device-to-device in the same runs; FETCH_SIZE {cf:.0f} KiB (n={ncf}), "
+             f"WRITE_SIZE {cw:.0f} KiB (n={ncw}); scale fetch {f_scale:.4f}, write {w_scale:.4f} (counter bytes / "
+             "true bytes).", "",
+             "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | fetched B (scaled) | written B (scaled) | "
+             "algorithmic B (read + written) | fetched / algorithmic | traffic / algorithmic |",
+             "|---|---|---|---|---|---|---|---|---|"]
+    for pat, alg in specs:
+        fk, nf = mean_of(fetch, lambda n, p=pat: p in n)
+        wk, nw = mean_of(write, lambda n, p=pat: p in n)
+        fb, wb = fk * 1024 / f_scale, wk * 1024 / w_scale
+        lines.append(f"| `{pat}` | {nf}/{nw} | {fk:.1f} | {wk:.1f} | {fb:.0f} | {wb:.0f} | {alg} | {fb / alg:.3f} | "
+                     f"{(fb + wb) / alg:.3f} |")
+    lines += ["", "SQ counters, averages per dispatch (VALU share = SQ_INSTS_VALU x 4 / (1,024 x cycles), cycles = "
+              "dispatch duration x 2.4 GHz; MFMA share = SQ_VALU_MFMA_BUSY_CYCLES / (1,024 x cycles); SQ_INSTS_VALU "
+              "counts the MFMA instructions too):", "",
+              "| kernel | us | VALU insts | MFMA insts | LDS insts | VMEM reads | LDS bank-conflict cycles | VALU share "
+              "| MFMA share | wait / wave cycles |",
+              "|---|---|---|---|---|---|---|---|---|---|"]
+    for pat, _ in specs:
+        c = sq[pat]
+        if not c.get("_ns"):
+            lines.append(f"| `{pat}` | (no dispatches) |||||||||")
+            continue
+        av = {n: sum(v) / len(v) for n, v in c.items()}
+        cyc = 1024 * av["_ns"] * 2.4
+        lines.append(f"| `{pat}` | {av['_ns'] / 1e3:.1f} | {av['SQ_INSTS_VALU'] / 1e6:.3f} M | "
+                     f"{av['SQ_INSTS_MFMA'] / 1e6:.3f} M | {av['SQ_INSTS_LDS'] / 1e6:.3f} M | "
+                     f"{av['SQ_INSTS_VMEM_RD'] / 1e6:.3f} M | {av['SQ_LDS_BANK_CONFLICT'] / 1e6:.3f} M | "
+                     f"{av['SQ_INSTS_VALU'] * 4 / cyc:.1%} | {av['SQ_VALU_MFMA_BUSY_CYCLES'] / cyc:.1%} | "
+                     f"{av['SQ_WAIT_ANY'] / av['SQ_WAVE_CYCLES']:.0%} |")
+    return "\n".join(lines) + "\n"
+
+
 def _pmc_rows(csv_path: str, counter: str):
     """(kernel name, value) per dispatch for `counter` from a rocprofv3 counter_collection.csv."""
     import csv
@@ -994,6 +1076,106 @@ def run_gptoss(a) -> dict:
     }
 
 
+def run_attn(a) -> dict:
+    """Decode attention at the C4 shape (Qwen3-30B-A3B: 32 q heads, 4 KV heads, head dim 128,
+    KV cache of 4,096 positions), as the graph decoder runs it (graphdec.py:163-174): the q/k
+    head norm, rope and K/V store at the position folded into the attention workgroups, then the
+    chunk merge (wisp_attn_decode_qk, two launches). --attn-layers layer caches (8 MB each at
+    4,096 positions, past the Infinity Cache) are rotated, one call per layer per replay, all
+    layers' calls ten times over in one graph, timed with HIP events around --attn-reps replays
+    after 2. The position
+    is --attn-pos (every call attends over positions 0 .. pos)."""
+    dev = torch.device("cuda:0")
+    HQ, HK, D, TM = 32, 4, 128, 4096
+    NL = a.attn_layers
+    pos_v = a.attn_pos
+    if not 0 <= pos_v < TM:
+        raise SystemExit(f"bench.py: --attn-pos must be in [0, {TM})")
+    gen = torch.Generator(device=dev).manual_seed(5)
+    kc = torch.randn((NL, 1, HK, TM, D), generator=gen, device=dev).to(torch.bfloat16)
+    vc = torch.randn((NL, 1, HK, TM, D), generator=gen, device=dev).to(torch.bfloat16)
+    qkv = torch.randn((NL, (HQ + 2 * HK) * D), generator=gen, device=dev).to(torch.bfloat16)
+    qn = (1 + 0.1 * torch.randn(D, generator=gen, device=dev)).to(torch.bfloat16)
+    kn = (1 + 0.1 * torch.randn(D, generator=gen, device=dev)).to(torch.bfloat16)
+    inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D))
+    ang = torch.arange(TM, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], -1).to(torch.bfloat16).contiguous()
+    sin = torch.cat([ang.sin(), ang.sin()], -1).to(torch.bfloat16).contiguous()
+    pos = torch.full((1,), pos_v, dtype=torch.int64, device=dev)
+    L = _lib.lib()
+    wsb = L.wisp_attn_ws_bytes(HQ, D, TM)
+    wstride = (wsb + 255) // 256 * 256
+    ws = torch.empty((NL, wstride), dtype=torch.uint8, device=dev)
+    out = torch.empty((NL, HQ * D), dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.Stream(dev)
+    sp = _lib.ptr
+    scale = D ** -0.5
+
+    def launch(l, st):
+        _lib.check(L.wisp_attn_decode_qk(sp(qkv[l]), sp(qn), sp(kn), 1e-6, sp(cos), sp(sin), sp(pos), HQ, HK, D,
+                                         sp(kc[l]), sp(vc[l]), kc.stride(2), TM, scale, sp(ws[l]), sp(out[l]), st),
+                   "attn_decode_qk")
+
+    ROT = 10  # rotations of the layer caches per graph (NL * ROT calls), so a replay's own latency is small
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        st = _lib.stream(dev)
+        for l in range(NL):
+            launch(l, st)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            st = _lib.stream(dev)
+            for _ in range(ROT):
+                for l in range(NL):
+                    launch(l, st)
+    torch.cuda.synchronize()
+
+    def run(reps):
+        with torch.cuda.stream(stream):
+            for _ in range(reps):
+                g.replay()
+
+    run(2)
+    reps = max(1, a.attn_reps)
+    times = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        run(reps)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e-3 / (reps * NL * ROT))
+    t = sorted(times)[2]
+    kv_bytes = 2 * (pos_v + 1) * D * 2 * HK  # K and V rows 0 .. pos of every KV head
+    byts = kv_bytes + qkv.shape[1] * 2 + HQ * D * 2  # + the qkv row in, the attention output out
+    gbs = byts / t / 1e9
+    return {
+        "metric": "us per decode attention call (C4 shape) + achieved HBM GB/s of its K/V bytes",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": reps * NL * ROT,
+        "warmup": 2 * NL * ROT,
+        "ms_per_step": round(t * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"decode attention, Hq {HQ} / Hk {HK} / d {D}, KV cache {TM}, position {pos_v}, "
+                               f"{NL} layer caches rotated",
+                   "path": "wisp_attn_decode_qk: q/k head norm + rope + K/V store folded into k_attn_mfma, then "
+                           "k_attn_merge (two launches)",
+                   "bytes_per_call": byts, "kv_bytes_per_call": kv_bytes,
+                   "timing": "median of 5 HIP-event timings of --attn-reps graph replays (each graph: 10 "
+                             "rotations of one call per layer cache) after 2 warm-up replays; per-call time "
+                             "includes the in-graph gap between launches"},
+        "us_per_call": round(t * 1e6, 3),
+        "pct_hbm_peak": round(gbs / PEAK_HBM_GBS * 100, 2),
+    }
+
+
 def _cpu_model() -> str:
     """The host CPU as /proc/cpuinfo and sysfs describe it (the baseline depends on it): model
     name, family/model/stepping, logical CPUs online and the L3 size of cpu0's cache."""
@@ -1034,9 +1216,18 @@ def main():
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write the PMC traffic summary under profiles/ from two counter_collection.csv files")
     ap.add_argument("--pmc-command", default="", help="command text recorded in the PMC summary")
-    ap.add_argument("--workload", default="c2", choices=["c2", "c4", "c5", "gptoss", "floor"],
+    ap.add_argument("--pmc-calib", action="store_true",
+                    help="after a c4 / c5 / gptoss / attn workload, three calibration copies for a --pmc pass")
+    ap.add_argument("--summarize-kernel-pmc", nargs="+", metavar="ARG",
+                    help="NAME TITLE FETCH_CSV WRITE_CSV SQ_A_CSV SQ_B_CSV KERNEL=BYTES...: write profiles/NAME.md "
+                         "from four rocprofv3 --pmc passes over one workload")
+    ap.add_argument("--workload", default="c2", choices=["c2", "c4", "c5", "gptoss", "attn", "floor"],
                     help="c2: one MoE layer (default); c4: full decode steps through the graph decoder and the "
-                    "expert cache; c5: grouped prefill; floor: empty-kernel and streaming-read probes beside C2")
+                    "expert cache; c5: grouped prefill; gptoss: the gpt-oss expert layer; attn: decode attention "
+                    "at the C4 shape; floor: empty-kernel and streaming-read probes beside C2")
+    ap.add_argument("--attn-layers", type=int, default=48)
+    ap.add_argument("--attn-pos", type=int, default=4090)
+    ap.add_argument("--attn-reps", type=int, default=4)
     ap.add_argument("--c5-tokens", default="64,256,512")
     ap.add_argument("--gptoss-pools", type=int, default=8, help="gpt-oss layer pools rotated (32 experts each)")
     ap.add_argument("--gptoss-reps", type=int, default=50, help="timed replays of the rotated layers")
@@ -1112,6 +1303,15 @@ def main():
         print(text)
         return
 
+    if a.summarize_kernel_pmc:
+        v = a.summarize_kernel_pmc
+        specs = [(sp.rsplit("=", 1)[0], int(sp.rsplit("=", 1)[1])) for sp in v[6:]]
+        text = summarize_kernel_pmc(v[1], a.pmc_command, v[2], v[3], v[4], v[5], specs)
+        with open(os.path.join(PROFILES, v[0] + ".md"), "w") as f:
+            f.write(text)
+        print(text)
+        return
+
     if a.summarize_pmc:
         text = summarize_pmc(a.summarize_pmc[0], a.summarize_pmc[1], a.bits, a.pmc_command)
         with open(pmc_profile_name(a.bits), "w") as f:
@@ -1134,14 +1334,11 @@ def main():
     if a.pmc_pass:
         pmc_pass(a.bits)
         return
-    if a.workload == "c4":
-        print(json.dumps(run_c4(a)))
-        return
-    if a.workload == "c5":
-        print(json.dumps(run_c5(a)))
-        return
-    if a.workload == "gptoss":
-        print(json.dumps(run_gptoss(a)))
+    if a.workload in ("c4", "c5", "gptoss", "attn"):
+        print(json.dumps({"c4": run_c4, "c5": run_c5, "gptoss": run_gptoss, "attn": run_attn}[a.workload](a)),
+              flush=True)
+        if a.pmc_calib:
+            calib_copies(dev)
         return
     if a.workload == "floor":
         print(json.dumps(run_floor(a)))

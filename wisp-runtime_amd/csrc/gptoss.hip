@@ -220,23 +220,41 @@ __device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int
     }
 }
 
-// grid (ceil(2I / kGoCols), S1 = ceil(H / (16 * go_pairs_gu(BITS))), k)
+// The workgroup's (column block bx, row block by, expert bz) of an nx x ny x nz grid launched
+// as T = nx ny nz workgroups in one dimension. Workgroup i runs on XCD i % 8; the logical
+// order (bx fastest) is dealt to the XCDs in contiguous runs (XCD x takes the x-th run of
+// about T / 8), so the nx column blocks of one row block and expert mostly share an XCD. They
+// read the same lines of the rows' fp16 scales and mins (a row's groups are contiguous in the
+// store, a block's 8 of them are 16 of a line's 128 bytes) and, in the down kernel, the same
+// gate_up partial sums: one XCD's L2 then fetches each line once instead of up to nx of them.
+__device__ __forceinline__ void go_block(int nx, int ny, int nz, int& bx, int& by, int& bz) {
+    const int T = nx * ny * nz, i = blockIdx.x;
+    const int q = T >> 3, r = T & 7, x = i & 7, j = i >> 3;
+    const int p = x * q + min(x, r) + j;
+    bx = p % nx;
+    by = (p / nx) % ny;
+    bz = p / (nx * ny);
+}
+
+// T = ceil(2I / kGoCols) x S1 x k workgroups, S1 = ceil(H / (16 * go_pairs_gu(BITS)))
 template <int BITS, bool POW2G>
 __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_gate_up(const GoLayer L) {
     __shared__ float red[2 * kGoWaves * kGoRedStride];
-    const int j = blockIdx.z;
+    constexpr int PAIRS = go_pairs_gu(BITS);
+    const int C = 2 * L.I;
+    int bx, by, j;
+    go_block((C + kGoCols - 1) / kGoCols, L.S1, L.k, bx, by, j);
     const int slot = go_slot(L, j);
     const uint8_t* base = L.pool + (int64_t)(slot >= 0 ? slot : 0) * L.slot_bytes;
-    constexpr int PAIRS = go_pairs_gu(BITS);
-    const int C = 2 * L.I, col0 = blockIdx.x * kGoCols, r0 = blockIdx.y * 16 * PAIRS;
+    const int col0 = bx * kGoCols, r0 = by * 16 * PAIRS;
     const uint32_t* xw = reinterpret_cast<const uint32_t*>(L.x);
     // (3-bit codes keep the operand loads after the weights: requested first they spilled there)
     go_colgemv<BITS, PAIRS, POW2G, BITS != 3>(base, 0, L.H, C, L.G, L.gsh, L.scale_off, L.NG, r0, col0,
                                    [&](int r) { return xw[r >> 1]; },
-                     [] {}, red, L.p1 + ((int64_t)j * L.S1 + blockIdx.y) * C + col0, slot < 0);
+                     [] {}, red, L.p1 + ((int64_t)j * L.S1 + by) * C + col0, slot < 0);
 }
 
-// grid (ceil(H / kGoCols), S2 = ceil(I / kGoRows), k)
+// T = ceil(H / kGoCols) x S2 x k workgroups, S2 = ceil(I / kGoRows)
 template <int BITS, bool POW2G>
 __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
     __shared__ float red[2 * kGoWaves * kGoRedStride];
@@ -244,9 +262,10 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
     __shared__ float half_sum[2][2 * kGoRows];
     __shared__ uint32_t actp[kGoRows / 2];
     static_assert(64 * kGoWaves == 4 * kGoRows, "two threads per gate_up column");
-    const int j = blockIdx.z;
+    int bx, by, j;
+    go_block((L.H + kGoCols - 1) / kGoCols, L.S2, L.k, bx, by, j);
     const int slot = go_slot(L, j), ex = go_expert(L, j);
-    const int I2 = 2 * L.I, i0 = blockIdx.y * kGoRows;
+    const int I2 = 2 * L.I, i0 = by * kGoRows;
     // gate_up outputs of activation rows i0 .. i0+kGoRows-1: gu = bf16(bf16(x . W) + bias). The S1 partial
     // sums of a column are split between two threads. The first kGoMaxPart of a thread's partials (all of
     // them at the gpt-oss shapes) and the column's bias are requested before the weight rows: vector loads
@@ -317,9 +336,9 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
     };
     const uint8_t* base = L.pool + (int64_t)(slot >= 0 ? slot : 0) * L.slot_bytes;
     go_colgemv<BITS, kGoPairsDN, POW2G, false>(base, 2 * L.n, L.I, L.H, L.G, L.gsh, L.scale_off, L.NG, i0,
-                                        blockIdx.x * kGoCols,
+                                        bx * kGoCols,
                      [&](int r) { return actp[(r - i0) >> 1]; }, prologue, red,
-                     L.p2 + ((int64_t)j * L.S2 + blockIdx.y) * L.H + blockIdx.x * kGoCols, slot < 0);
+                     L.p2 + ((int64_t)j * L.S2 + by) * L.H + bx * kGoCols, slot < 0);
 }
 
 // out[h] = bf16( sum_j bf16( w_j * bf16( bf16(sum_s p2[j][s][h]) + db[e_j][h] ) ) ), j ascending.
@@ -401,9 +420,9 @@ __global__ __launch_bounds__(kGoOutCols * kGoOutSlices) void k_go_out(const GoLa
 template <int BITS, bool POW2G>
 static void launch_go(const GoLayer& L, hipStream_t st) {
     const int C1 = 2 * L.I;
-    hipLaunchKernelGGL((k_go_gate_up<BITS, POW2G>), dim3((C1 + kGoCols - 1) / kGoCols, L.S1, L.k),
+    hipLaunchKernelGGL((k_go_gate_up<BITS, POW2G>), dim3((C1 + kGoCols - 1) / kGoCols * L.S1 * L.k),
                        dim3(64 * kGoWaves), 0, st, L);
-    hipLaunchKernelGGL((k_go_down<BITS, POW2G>), dim3((L.H + kGoCols - 1) / kGoCols, L.S2, L.k),
+    hipLaunchKernelGGL((k_go_down<BITS, POW2G>), dim3((L.H + kGoCols - 1) / kGoCols * L.S2 * L.k),
                        dim3(64 * kGoWaves), 0, st, L);
     hipLaunchKernelGGL(k_go_out, dim3((L.H + kGoOutCols - 1) / kGoOutCols), dim3(kGoOutCols * kGoOutSlices), 0, st, L);
 }
