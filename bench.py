@@ -409,7 +409,7 @@ SQ_PASS_B = ("SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT SQ_I
 def summarize_kernel_pmc(title: str, cmd: str, fetch_csv: str, write_csv: str, sq_a_csv: str, sq_b_csv: str,
                          specs) -> str:
     """Markdown summary of four rocprofv3 --pmc passes over one workload (FETCH_SIZE, WRITE_SIZE,
-    then the two SQ passes) for the kernels named in specs = [(name substring, algorithmic bytes
+    then the two SQ passes; "-" for the SQ files: traffic only) for the kernels named in specs = [(name substring, algorithmic bytes
     per dispatch)]: HBM traffic scaled by the run's own calibration copies, and the issue and
     wait shares (1,024 SIMDs at 2.4 GHz, 4 cycles per wave64 VALU instruction; durations include
     the profiler's per-dispatch overhead)."""
@@ -428,7 +428,7 @@ def summarize_kernel_pmc(title: str, cmd: str, fetch_csv: str, write_csv: str, s
     f_scale = cf * 1024 / CALIB_BYTES
     w_scale = cw * 1024 / CALIB_BYTES
     sq = collections.defaultdict(lambda: collections.defaultdict(list))
-    for path in (sq_a_csv, sq_b_csv):
+    for path in ((sq_a_csv, sq_b_csv) if sq_a_csv != "-" else ()):
         with open(path) as f:
             for r in _csv.DictReader(f):
                 for pat, _ in specs:
@@ -450,6 +450,8 @@ def summarize_kernel_pmc(title: str, cmd: str, fetch_csv: str, write_csv: str, s
         fb, wb = fk * 1024 / f_scale, wk * 1024 / w_scale
         lines.append(f"| `{pat}` | {nf}/{nw} | {fk:.1f} | {wk:.1f} | {fb:.0f} | {wb:.0f} | {alg} | {fb / alg:.3f} | "
                      f"{(fb + wb) / alg:.3f} |")
+    if sq_a_csv == "-":  # traffic passes only
+        return "\n".join(lines) + "\n"
     lines += ["", "SQ counters, averages per dispatch (VALU share = SQ_INSTS_VALU x 4 / (1,024 x cycles), cycles = "
               "dispatch duration x 2.4 GHz; MFMA share = SQ_VALU_MFMA_BUSY_CYCLES / (1,024 x cycles); SQ_INSTS_VALU "
               "counts the MFMA instructions too):", "",

@@ -220,22 +220,10 @@ __device__ __forceinline__ void go_colgemv(const uint8_t* __restrict__ base, int
     }
 }
 
-// The workgroup's (column block bx, row block by, expert bz) of an nx x ny x nz grid launched
-// as T = nx ny nz workgroups in one dimension. Workgroup i runs on XCD i % 8; the logical
-// order (bx fastest) is dealt to the XCDs in contiguous runs (XCD x takes the x-th run of
-// about T / 8), so the nx column blocks of one row block and expert mostly share an XCD. They
-// read the same lines of the rows' fp16 scales and mins (a row's groups are contiguous in the
-// store, a block's 8 of them are 16 of a line's 128 bytes) and, in the down kernel, the same
-// gate_up partial sums: one XCD's L2 then fetches each line once instead of up to nx of them.
-__device__ __forceinline__ void go_block(int nx, int ny, int nz, int& bx, int& by, int& bz) {
-    const int T = nx * ny * nz, i = blockIdx.x;
-    const int q = T >> 3, r = T & 7, x = i & 7, j = i >> 3;
-    const int p = x * q + min(x, r) + j;
-    bx = p % nx;
-    by = (p / nx) % ny;
-    bz = p / (nx * ny);
-}
-
+// Workgroups are launched in one dimension and placed by xcd_block: the column blocks of one
+// row block and expert read the same lines of the rows' fp16 scales and mins (a row's groups
+// are contiguous in the store; a block's 8 of them are 16 of a line's 128 bytes) and, in the
+// down kernel, the same gate_up partial sums, so they share an XCD and its L2.
 // T = ceil(2I / kGoCols) x S1 x k workgroups, S1 = ceil(H / (16 * go_pairs_gu(BITS)))
 template <int BITS, bool POW2G>
 __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_gate_up(const GoLayer L) {
@@ -243,7 +231,7 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_gate_up(const GoLayer L
     constexpr int PAIRS = go_pairs_gu(BITS);
     const int C = 2 * L.I;
     int bx, by, j;
-    go_block((C + kGoCols - 1) / kGoCols, L.S1, L.k, bx, by, j);
+    xcd_block((C + kGoCols - 1) / kGoCols, L.S1, L.k, bx, by, j);
     const int slot = go_slot(L, j);
     const uint8_t* base = L.pool + (int64_t)(slot >= 0 ? slot : 0) * L.slot_bytes;
     const int col0 = bx * kGoCols, r0 = by * 16 * PAIRS;
@@ -263,7 +251,7 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
     __shared__ uint32_t actp[kGoRows / 2];
     static_assert(64 * kGoWaves == 4 * kGoRows, "two threads per gate_up column");
     int bx, by, j;
-    go_block((L.H + kGoCols - 1) / kGoCols, L.S2, L.k, bx, by, j);
+    xcd_block((L.H + kGoCols - 1) / kGoCols, L.S2, L.k, bx, by, j);
     const int slot = go_slot(L, j), ex = go_expert(L, j);
     const int I2 = 2 * L.I, i0 = by * kGoRows;
     // gate_up outputs of activation rows i0 .. i0+kGoRows-1: gu = bf16(bf16(x . W) + bias). The S1 partial

@@ -68,6 +68,7 @@ struct Prefill {
     const uint16_t* x;      // [T, H]
     uint16_t* act;          // [P, I]
     float* y;               // [P, H]
+    int gy, gz;             // the LDS-DMA kernels' logical grid: work items, workgroups per item's passes
 };
 
 __device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
@@ -736,11 +737,11 @@ __device__ __forceinline__ void pf_gemm_dmag_h(const PfDma& R, const uint8_t* ab
 
 template <int MT, int NW, bool GATE_UP, class Epi>
 __device__ __forceinline__ void pf_dmag_passes(const Prefill& F, const PfDma& R, int p0, int cnt, uint8_t* ab,
-                                               uint8_t* ringw, int nk, Epi epi) {
+                                               uint8_t* ringw, int nk, int bz, int nz, Epi epi) {
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     constexpr int MB = MT * 16;
-    for (int mb = blockIdx.z * MB; mb < cnt; mb += gridDim.z * MB) {
+    for (int mb = bz * MB; mb < cnt; mb += nz * MB) {
         const int nt = min(MT, (cnt - mb + 15) / 16);
         auto pass = [&](auto NTc) {
             constexpr int NT = decltype(NTc)::value, RPTG = 4 * NT / NW;
@@ -816,7 +817,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     __shared__ uint4 ring[NW * kDmaSlot / 16];
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
-    const int c0 = blockIdx.x * HR + wv * CW, u = blockIdx.y;
+    // one-dimensional launch of (I / HR) x gy x gz workgroups: an item's row blocks share an
+    // XCD (items dealt round robin), so its token tile is fetched into one L2
+    int bx, u, bz;
+    xcd_rr_block(F.I / HR, F.gy, F.gz, bx, u, bz);
+    const int c0 = bx * HR + wv * CW;
     int slot, p0, cnt;
     const int gs = group_state(F, u, slot, p0, cnt);
     if (gs == 0) return;
@@ -838,7 +843,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
                        (lane & 15) * nk * 2);
     uint8_t* ringw = reinterpret_cast<uint8_t*>(ring) + wv * kDmaSlot;
     uint8_t* ab = reinterpret_cast<uint8_t*>(abuf);
-    pf_dmag_passes<MT, NW, true>(F, R, p0, cnt, ab, ringw, nk, [&](auto& acc, int mb) {
+    pf_dmag_passes<MT, NW, true>(F, R, p0, cnt, ab, ringw, nk, bz, F.gz, [&](auto& acc, int mb) {
         constexpr int NT = sizeof(acc) / sizeof(acc[0]);
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt)
@@ -857,7 +862,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     __shared__ uint4 ring[NW * kDmaSlot / 16];
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
-    const int h0 = blockIdx.x * RWG + wv * RW, u = blockIdx.y;
+    // one-dimensional launch of (H / RWG) x gy x gz workgroups: an item's row blocks share an
+    // XCD (items dealt round robin), so its activation tile is fetched into one L2
+    int bx, u, bz;
+    xcd_rr_block(F.H / RWG, F.gy, F.gz, bx, u, bz);
+    const int h0 = bx * RWG + wv * RW;
     int slot, p0, cnt;
     const int gs = group_state(F, u, slot, p0, cnt);
     if (gs == 0) return;
@@ -878,7 +887,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     R.vos = (uint32_t)((lane >= 32 ? 3 * (int64_t)F.NGM * 2 : 0) + (lane & 31) * nk * 2);
     uint8_t* ringw = reinterpret_cast<uint8_t*>(ring) + wv * kDmaSlot;
     uint8_t* ab = reinterpret_cast<uint8_t*>(abuf);
-    pf_dmag_passes<MT, NW, false>(F, R, p0, cnt, ab, ringw, nk, [&](auto& acc, int mb) {
+    pf_dmag_passes<MT, NW, false>(F, R, p0, cnt, ab, ringw, nk, bz, F.gz, [&](auto& acc, int mb) {
         constexpr int NT = sizeof(acc) / sizeof(acc[0]);
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt)
@@ -949,10 +958,13 @@ static void launch_pf_mt(const Prefill& F, int ngroups, int max_group, hipStream
             // workgroups share a CU (measured on C5 against 8-wave workgroups with the tile
             // staged per group pair, one per CU: T = 256 119.7 -> 114.3 us, 512 150.5 -> 142.3)
             if (F.I % 64 == 0 && F.H % 128 == 0) {
-                hipLaunchKernelGGL((k_pf_gate_up_dmag<MT, 4>), dim3((unsigned)(F.I / 64), (unsigned)ngroups, z),
-                                   dim3(256), 0, st, F);
-                hipLaunchKernelGGL((k_pf_down_dmag<MT, 4>), dim3((unsigned)(F.H / 128), (unsigned)ngroups, z),
-                                   dim3(256), 0, st, F);
+                Prefill G = F;
+                G.gy = ngroups;
+                G.gz = (int)z;
+                hipLaunchKernelGGL((k_pf_gate_up_dmag<MT, 4>), dim3((unsigned)(F.I / 64) * (unsigned)ngroups * z),
+                                   dim3(256), 0, st, G);
+                hipLaunchKernelGGL((k_pf_down_dmag<MT, 4>), dim3((unsigned)(F.H / 128) * (unsigned)ngroups * z),
+                                   dim3(256), 0, st, G);
                 return;
             }
         }
@@ -1032,6 +1044,7 @@ extern "C" int wisp_moe_prefill(const uint8_t* pool, int64_t slot_bytes, int64_t
     F.x = x;
     F.act = static_cast<uint16_t*>(ws);
     F.y = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + (pairs * I * 2 + 255) / 256 * 256);
+    F.gy = F.gz = 1;  // set per launch for the LDS-DMA kernels
     hipStream_t st = (hipStream_t)stream;
     max_group = std::max(1, std::min(max_group, T));  // a launch-shape hint; any value is correct
     switch (bits) {

@@ -70,6 +70,41 @@ __device__ __forceinline__ uint32_t alignbit(uint32_t hi, uint32_t lo, uint32_t 
     return __builtin_amdgcn_alignbit(hi, lo, s);
 }
 
+// The workgroup's (bx, by, bz) of a logical nx x ny x nz grid launched as T = nx ny nz
+// workgroups in one dimension. Workgroup i runs on XCD i % 8; the logical order (bx fastest)
+// is dealt to the XCDs in contiguous runs (XCD x takes the x-th run of about T / 8: logical
+// index (i % 8) floor(T / 8) + min(i % 8, T mod 8) + floor(i / 8), a bijection for every T),
+// so workgroups that differ only in bx mostly share an XCD, and lines they all read (a row's
+// quant-group scales, a token tile, partial sums) are fetched into one XCD's L2 once instead
+// of into up to nx of them.
+__device__ __forceinline__ void xcd_block(int nx, int ny, int nz, int& bx, int& by, int& bz) {
+    const int T = nx * ny * nz, i = blockIdx.x;
+    const int q = T >> 3, r = T & 7, x = i & 7, j = i >> 3;
+    const int p = x * q + min(x, r) + j;
+    bx = p % nx;
+    by = (p / nx) % ny;
+    bz = p / (nx * ny);
+}
+
+// As xcd_block, but the groups of nx workgroups (one (by, bz)) are dealt to the XCDs round
+// robin, group g to XCD g % 8, each group's nx workgroups on that XCD: for groups of unequal
+// work (work items of different token counts), which contiguous runs would pile onto a few
+// XCDs. The last (ny nz) mod 8 groups keep the plain order (no XCD in common).
+__device__ __forceinline__ void xcd_rr_block(int nx, int ny, int nz, int& bx, int& by, int& bz) {
+    const int i = blockIdx.x, ng = ny * nz, ng8 = ng & ~7, t8 = ng8 * nx;
+    int g;
+    if (i < t8) {
+        const int j = i >> 3;
+        g = (i & 7) + 8 * (j / nx);
+        bx = j % nx;
+    } else {
+        g = ng8 + (i - t8) / nx;
+        bx = (i - t8) % nx;
+    }
+    by = g % ny;
+    bz = g / ny;
+}
+
 // ---------------------------------------------------------------------------
 // Pair maps: for pair P of a chunk, the chunk-relative code index of its low
 // and high half and the power-of-two exponent e of each half (the code sits at
