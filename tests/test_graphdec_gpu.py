@@ -106,10 +106,12 @@ def test_graph_and_eager_decode_agree():
     rt.cache.free()
 
 
-def test_device_paging_with_partly_forced_routing_matches_host_steps():
+@pytest.mark.parametrize("policy", ["lru", "wsa"])
+def test_device_paging_with_partly_forced_routing_matches_host_steps(policy):
     """A decoder whose hook forces the experts of even layers only (None for the others: the
     router's choice): the graph with the paging points on the GPU gives the host-step
-    decoder's logits bit for bit and the same cache bookkeeping."""
+    decoder's logits bit for bit and the same cache state (slots, counters, free stack,
+    ticks, scores, the frequency table and inc), under the LRU and the WSA policy."""
     cfg, ref, gpu, rt = _models(seed=5)
     ids = torch.randint(0, 128, (1, 4), generator=torch.Generator().manual_seed(6))
     rng = np.random.default_rng(7)
@@ -122,7 +124,7 @@ def test_device_paging_with_partly_forced_routing_matches_host_steps():
     outs, cores = [], []
     for paging in (False, True):
         rt.cache.free()
-        rt.cache = ExpertCache(rt.store, 10)
+        rt.cache = ExpertCache(rt.store, 10, policy=policy)
         dec = Half(gpu, rt, tmax=64, device_paging=paging)
         with torch.no_grad():
             t = dec.prefill(ids[0].cuda()).argmax(-1)
@@ -134,7 +136,8 @@ def test_device_paging_with_partly_forced_routing_matches_host_steps():
         assert dec._dev == paging and len(dec.graphs) == (1 if paging else L + 1)
         outs.append(torch.stack(seq))
         core = rt.cache.core
-        cores.append((dict(core.key2slot), dict(core.stats), list(core.free)))
+        cores.append((dict(core.key2slot), dict(core.stats), list(core.free), list(core.last), list(core.score),
+                      list(core.freq.items()), core.inc))
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
     assert cores[0] == cores[1]
     rt.cache.free()
