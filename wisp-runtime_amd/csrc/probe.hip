@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kProbeThreads) void k_probe_read(const uint8_t* __r
 }
 
 // ---- the C2 layer's skeleton --------------------------------------------------------------
-constexpr int kSkelP = 768, kSkelC = 512, kSkelAct = 8 * 768, kSkelOut = 2048;
+constexpr int kSkelP = 768, kSkelC = 512, kSkelAct = 8 * 768;  // 4 outputs per consumer: 2,048
 constexpr int kSkelPerA = 8, kSkelPerB = 4;  // 16-byte loads per thread at most (bytes checked on the host)
 constexpr unsigned kSkelSpin = 1u << 22;
 
