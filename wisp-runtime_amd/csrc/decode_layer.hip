@@ -78,9 +78,9 @@ __global__ __launch_bounds__(256) void k_dl_gemv(const GemvArgs g) {
     const int K = CPL * 512;
     const int row0 = (blockIdx.x * 4 + wv) * R;
 
-    // The operand's inputs (and the residual) are requested before the weight rows: vector loads
-    // retire in issue order, so requested after them the RMSNorm below would start only once the
-    // wave's whole weight stream had arrived.
+    // The operand's inputs are requested before the weight rows: vector loads retire in issue
+    // order, so requested after them the RMSNorm below would start only once the wave's whole
+    // weight stream had arrived.
     const uint16_t* A = g.a + (g.a_row ? *g.a_row * (int64_t)K : 0);
     const uint4* a4 = reinterpret_cast<const uint4*>(A);
     constexpr int PT = (CPL * 64 + 255) / 256;  // 16-byte chunks per thread (NORM)
@@ -100,7 +100,10 @@ __global__ __launch_bounds__(256) void k_dl_gemv(const GemvArgs g) {
 #pragma unroll
         for (int c = 0; c < CPL; ++c) xv[c] = a4[c * 64 + lane];
     }
-    const uint16_t resv = g.res && lane < R ? g.res[min(row0 + lane, g.O - 1)] : (uint16_t)0;
+    // NORM: the residual (no caller of the decoder passes one) under a branch that is skipped when
+    // there is none
+    uint16_t resv = 0;
+    if constexpr (NORM) resv = g.res && lane < R ? g.res[min(row0 + lane, g.O - 1)] : (uint16_t)0;
 
     uint4 wr[R][CPL];
 #pragma unroll
@@ -117,6 +120,10 @@ __global__ __launch_bounds__(256) void k_dl_gemv(const GemvArgs g) {
             wr[r][c] = make_uint4(v.x, v.y, v.z, v.w);
         }
     }
+    // otherwise the residual, needed last, is requested last, by every lane (the input's first
+    // element when there is none): loaded under a branch, its value was needed at the branch's end,
+    // so the wave waited there for it and every earlier load before requesting the weight rows
+    if constexpr (!NORM) resv = (g.res ? g.res : A)[g.res ? min(row0 + lane, g.O - 1) : 0];
     __builtin_amdgcn_sched_barrier(0);  // the prologue's arithmetic stays behind every load
 
     if constexpr (NORM) {

@@ -242,6 +242,9 @@ __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __re
             sv[t][3 % (QSC ? 1 : 4)] = mn[L.NGM + gidx];
         }
     }
+    // every load above is issued before any arithmetic (else the fp32-x form started row 0's dot
+    // products, and waited for its codes, before requesting row 1's)
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t xp[16];
     float xs, bias = 0.f;
     if constexpr (XF) {
@@ -591,12 +594,25 @@ __global__ __launch_bounds__(64 * NWV) void k_down_rows(const float* meta, const
     if ((NB & 7) == 0) rb = (rb & 7) * (NB >> 3) + (rb >> 3);
     const int h0 = rb * ROWS_WG + wv * RPW;
 
-    // the activations of all k experts (k * 192 uint4) -> registers, then LDS
+    // Each lane reads the slot ids and weights of its three pairs' experts from meta
+    // itself (one round trip, no cross-lane broadcast between the slot ids' arrival and
+    // the code loads), slot ids first, then the activations of all k experts (k * 192
+    // uint4, staged in LDS below): waiting for the slot ids does not wait for the rest.
     constexpr int APT = (8 * SEG * 8 + 64 * NWV - 1) / (64 * NWV);
     const int na = k * SEG * 8;
-    // lane i < 2k holds meta[i] (slot ids, then weights); issued before the activation
-    // loads, so waiting for it does not wait for them
-    const float mv = meta[min(lane & 15, 2 * k - 1)];
+    int ec[NC], sg[NC];
+    bool on[NC], okc[NC];
+    float fs[NC], fw[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int combo = lane + 64 * c;
+        ec[c] = combo / SEG;
+        sg[c] = combo - ec[c] * SEG;
+        on[c] = ec[c] < k;
+        fs[c] = meta[on[c] ? ec[c] : 0];
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) fw[c] = meta[k + (on[c] ? ec[c] : 0)];
     const uint4* a4 = reinterpret_cast<const uint4*>(act);
     uint4 ap[APT];
 #pragma unroll
@@ -605,23 +621,12 @@ __global__ __launch_bounds__(64 * NWV) void k_down_rows(const float* meta, const
         ap[i] = a4[min(idx, na - 1)];
     }
     __builtin_amdgcn_sched_barrier(0);
-    int ec[NC], sg[NC];
-    bool on[NC], okc[NC];
     const uint8_t* bc[NC];
-    float wc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        const int combo = lane + 64 * c;
-        ec[c] = combo / SEG;
-        sg[c] = combo - ec[c] * SEG;
-        on[c] = ec[c] < k;
-        const int e = on[c] ? ec[c] : 0;
-        const float f = __shfl(mv, e, 64);
-        const int slot = slot_from(f, nslots);
+        const int slot = slot_from(fs[c], nslots);
         okc[c] = slot >= 0;
         bc[c] = pool + (int64_t)(okc[c] ? slot : 0) * slot_bytes;
-        const float w = __shfl(mv, k + e, 64);
-        wc[c] = on[c] ? w : 0.f;
     }
     uint32_t cd[RPW][NC][BITS];
     uint32_t sv[QS ? RPW / 2 : RPW][NC];
@@ -645,10 +650,13 @@ __global__ __launch_bounds__(64 * NWV) void k_down_rows(const float* meta, const
             }
         }
     }
+    // every code load is issued before the staging below: a register copy placed among them
+    // would wait for an activation load first
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
-        // every thread stores (clamped: duplicates rewrite the same value), halves swapped so the
-        // compiler cannot fold the load and this store into a copy placed here
+        // every thread stores (clamped: duplicates rewrite the same value), halves swapped: a plain
+        // copy would let the compiler sink the load past the code loads, next to this store
         const int idx = min((int)threadIdx.x + i * 64 * NWV, na - 1);
         const uint4 a = ap[i];
         stage[(idx >> 3) * CW + (idx & 7)] = make_uint4(a.z, a.w, a.x, a.y);
@@ -668,7 +676,11 @@ __global__ __launch_bounds__(64 * NWV) void k_down_rows(const float* meta, const
         }
         as[c] = chunk_sum_f32(A[c]);
     }
-    // everything above uses the staged activation only: keep it ahead of every wait for the codes
+    float wc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) wc[c] = on[c] ? fw[c] : 0.f;
+    // everything above uses the staged activation and meta only: keep it ahead of every wait for
+    // the codes
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < RPW; ++t) {
