@@ -242,9 +242,6 @@ __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __re
             sv[t][3 % (QSC ? 1 : 4)] = mn[L.NGM + gidx];
         }
     }
-    // every load above is issued before any arithmetic (else the fp32-x form started row 0's dot
-    // products, and waited for its codes, before requesting row 1's)
-    __builtin_amdgcn_sched_barrier(0);
     uint32_t xp[16];
     float xs, bias = 0.f;
     if constexpr (XF) {
