@@ -119,8 +119,10 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
             hnr_load<D>(qp.qkv + ((int64_t)hk * G + min(wv + 4 * j, G - 1)) * D, qp.qnw, cs, sn, lane, qin[j]);
         // Only the two waves that use them load the new K and V rows' inputs. The compiler
         // converts them at the branch's end, so those waves' K/V loads start one round trip
-        // late; loading them in every wave instead (no branch) measured slower (8.61 -> 8.86 us
-        // per call at 4,090 positions): every wave's K/V data then retires behind them.
+        // late. Measured slower at 4,090 positions: loading them in every wave (no branch),
+        // 8.61 -> 8.86 us per call (every wave's K/V data then retires behind them); requesting
+        // them after the K/V rows, 8.58 -> 9.38 us (that workgroup's head norm then starts only
+        // once all its K/V data is in, and it is the last workgroup to finish).
         if (own && wv == (G & 3)) hnr_load<D>(qp.qkv + ((int64_t)qp.hq + hk) * D, qp.knw, cs, sn, lane, kin);
         if (own && wv == ((G + 1) & 3)) {
             const uint16_t* xv = qp.qkv + ((int64_t)qp.hq + qp.hk + hk) * D;
