@@ -122,7 +122,9 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
         // late. Measured slower at 4,090 positions: loading them in every wave (no branch),
         // 8.61 -> 8.86 us per call (every wave's K/V data then retires behind them); requesting
         // them after the K/V rows, 8.58 -> 9.38 us (that workgroup's head norm then starts only
-        // once all its K/V data is in, and it is the last workgroup to finish).
+        // once all its K/V data is in, and it is the last workgroup to finish), or after them in
+        // every wave with the load order pinned, 8.61 -> 8.97 us (the new K row's head norm then
+        // still runs after all of that workgroup's data).
         if (own && wv == (G & 3)) hnr_load<D>(qp.qkv + ((int64_t)qp.hq + hk) * D, qp.knw, cs, sn, lane, kin);
         if (own && wv == ((G + 1) & 3)) {
             const uint16_t* xv = qp.qkv + ((int64_t)qp.hq + qp.hk + hk) * D;
