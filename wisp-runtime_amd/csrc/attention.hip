@@ -81,6 +81,17 @@ struct QkPrep {
     float eps;
     int hq, hk;
 };
+// The new row's inputs pass through here raw (no instruction): the compiler may not move their
+// conversions ahead of this point, into the branch that loads them, where converting them would
+// wait for those loads and every earlier one before the wave's K/V rows are requested.
+template <int D>
+__device__ __forceinline__ void opaque_raw(HnrIn<D>& in) {
+#pragma unroll
+    for (int t = 0; t < HnrIn<D>::NP; ++t)
+        asm volatile("" : "+v"(in.a[t]), "+v"(in.b[t]), "+v"(in.wa[t]), "+v"(in.wb[t]), "+v"(in.ca[t]),
+                     "+v"(in.cb[t]), "+v"(in.sa[t]), "+v"(in.sb[t]));
+}
+
 template <int G, int D, bool QK>
 __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ q, const uint16_t* kc,
                                                    const uint16_t* vc, int64_t head_stride,
@@ -110,21 +121,20 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
     constexpr int QPW = (G + 3) / 4;  // query heads this wave forms (QK)
     constexpr int VPL = (D + 63) / 64;
     HnrIn<D> qin[QPW], kin;
-    uint16_t vnew[VPL];
+    uint32_t vnew[VPL];  // 16-bit values, one per register (packed pairs were formed at the load)
     if constexpr (QK) {
         const uint16_t* cs = qp.cos_t + pos * D;
         const uint16_t* sn = qp.sin_t + pos * D;
 #pragma unroll
         for (int j = 0; j < QPW; ++j)
             hnr_load<D>(qp.qkv + ((int64_t)hk * G + min(wv + 4 * j, G - 1)) * D, qp.qnw, cs, sn, lane, qin[j]);
-        // Only the two waves that use them load the new K and V rows' inputs. The compiler
-        // converts them at the branch's end, so those waves' K/V loads start one round trip
-        // late. Measured slower at 4,090 positions: loading them in every wave (no branch),
-        // 8.61 -> 8.86 us per call (every wave's K/V data then retires behind them); requesting
-        // them after the K/V rows, 8.58 -> 9.38 us (that workgroup's head norm then starts only
-        // once all its K/V data is in, and it is the last workgroup to finish), or after them in
-        // every wave with the load order pinned, 8.61 -> 8.97 us (the new K row's head norm then
-        // still runs after all of that workgroup's data).
+        // Only the two waves that use them load the new K and V rows' inputs, and the values stay
+        // raw until their use (opaque_raw; the V row one value per register): converted at the
+        // branch's end, they made those waves wait for these loads before requesting their K/V
+        // rows (8.61 -> 8.42 us per call at 4,090 positions without that wait). Measured slower:
+        // loading them in every wave (8.86 us: every wave's K/V data retires behind them), and
+        // requesting them after the K/V rows (8.97-9.38 us: the new K row's head norm then runs
+        // after all of that workgroup's data, and that workgroup finishes last).
         if (own && wv == (G & 3)) hnr_load<D>(qp.qkv + ((int64_t)qp.hq + hk) * D, qp.knw, cs, sn, lane, kin);
         if (own && wv == ((G + 1) & 3)) {
             const uint16_t* xv = qp.qkv + ((int64_t)qp.hq + qp.hk + hk) * D;
@@ -163,14 +173,17 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
         if (own) {
             const int64_t at = hk * head_stride + pos * D;
             if (wv == (G & 3)) {  // a wave with the fewest q heads
+                opaque_raw(kin);
                 hnr_finish<D>(kin, qp.eps, &kv_l[0][0], qp.kc_w + at, lane);
             } else if (wv == ((G + 1) & 3)) {
+#pragma unroll
+                for (int t = 0; t < VPL; ++t) asm volatile("" : "+v"(vnew[t]));
 #pragma unroll
                 for (int t = 0; t < VPL; ++t) {
                     const int i = lane + 64 * t;
                     if (i < D) {
-                        kv_l[1][i] = vnew[t];
-                        qp.vc_w[at + i] = vnew[t];
+                        kv_l[1][i] = (uint16_t)vnew[t];
+                        qp.vc_w[at + i] = (uint16_t)vnew[t];
                     }
                 }
             }
