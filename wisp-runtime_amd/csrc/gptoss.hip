@@ -332,12 +332,18 @@ __global__ __launch_bounds__(64 * kGoWaves, 4) void k_go_down(const GoLayer L) {
 // out[h] = bf16( sum_j bf16( w_j * bf16( bf16(sum_s p2[j][s][h]) + db[e_j][h] ) ) ), j ascending.
 // A workgroup takes kGoOutCols columns and splits each column's S2 partial sums
 // into kGoOutSlices slices, one per wave. Every lane requests the partials of
-// up to kGoOutBatch experts before adding any (the sums are latency-bound);
-// the slice sums are added in slice order through LDS.
+// up to B experts before adding any (the sums are latency-bound); the slice sums
+// are added in slice order through LDS. B (experts per batch) and U (partials per
+// request round) are chosen at launch to fit k and the slice length, so no lane
+// requests a clamped duplicate: at the gpt-oss shapes B = 4 and U = 6, 24 requests per
+// lane where B = U = 8 made 64 (the layer 28.0-28.4 -> 27.0-27.4 us).
 // 32 columns per workgroup (90 workgroups at H = 2880): measured 33.4 us per layer against
-// 34.1 with 64 (45 workgroups), the same as 16
-constexpr int kGoOutCols = 32, kGoOutSlices = 8, kGoOutBatch = 8, kGoOutUnroll = 8;
+// 34.1 with 64 (45 workgroups), the same as 16; with B = 4, U = 6 also 16 columns (180
+// workgroups), 16 slices per column or 64 columns measured no faster.
+constexpr int kGoOutCols = 32, kGoOutSlices = 8;
+template <int B, int U>
 __global__ __launch_bounds__(kGoOutCols * kGoOutSlices) void k_go_out(const GoLayer L) {
+    constexpr int kGoOutBatch = B, kGoOutUnroll = U;
     __shared__ float part[kGoOutSlices][kGoOutBatch][kGoOutCols];
     const int c = threadIdx.x & (kGoOutCols - 1), sl = threadIdx.x / kGoOutCols;
     const int h = blockIdx.x * kGoOutCols + c, hh = min(h, L.H - 1);
@@ -412,7 +418,12 @@ static void launch_go(const GoLayer& L, hipStream_t st) {
                        dim3(64 * kGoWaves), 0, st, L);
     hipLaunchKernelGGL((k_go_down<BITS, POW2G>), dim3((L.H + kGoCols - 1) / kGoCols * L.S2 * L.k),
                        dim3(64 * kGoWaves), 0, st, L);
-    hipLaunchKernelGGL(k_go_out, dim3((L.H + kGoOutCols - 1) / kGoOutCols), dim3(kGoOutCols * kGoOutSlices), 0, st, L);
+    const dim3 og((L.H + kGoOutCols - 1) / kGoOutCols), ob(kGoOutCols * kGoOutSlices);
+    const int per = (L.S2 + kGoOutSlices - 1) / kGoOutSlices;
+    if (L.k <= 4 && per <= 6)
+        hipLaunchKernelGGL((k_go_out<4, 6>), og, ob, 0, st, L);
+    else
+        hipLaunchKernelGGL((k_go_out<8, 8>), og, ob, 0, st, L);
 }
 
 }  // namespace wisp
