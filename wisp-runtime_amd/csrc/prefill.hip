@@ -921,18 +921,25 @@ __global__ __launch_bounds__(256) void k_pf_combine(const float* __restrict__ y,
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= (int64_t)T * H) return;
     const int t = (int)(i / H), h = (int)(i - (int64_t)t * H);
+    // Every request unconditional and issued before any use: the token's k pair indices, then
+    // its k rows of y at clamped indices (a load under a per-lane condition was merged at the
+    // branch's end, so each pair's round trip waited for the previous one's). Pairs past k
+    // repeat the last (cached) and are skipped below; P >= 1 whenever this kernel runs.
     int pj[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) pj[j] = back[t * k + min(j, k - 1)];
+    __builtin_amdgcn_sched_barrier(0);
     float4 v[KMAX];
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {
-        pj[j] = j < k ? back[t * k + j] : -1;
-        const bool in = pj[j] >= 0 && pj[j] < P;
-        v[j] = in ? *reinterpret_cast<const float4*>(y + (int64_t)pj[j] * H + h) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int q = min(max(pj[j], 0), P - 1);
+        v[j] = *reinterpret_cast<const float4*>(y + (int64_t)q * H + h);
     }
+    __builtin_amdgcn_sched_barrier(0);
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {
-        if (pj[j] == -1) continue;
+        if (j >= k || pj[j] == -1) continue;
         if (pj[j] < 0 || pj[j] >= P) {
             const float nan = __builtin_nanf("");
             v[j] = make_float4(nan, nan, nan, nan);
