@@ -470,8 +470,10 @@ struct LruLane {
 // state. A launch while device paging is off (a captured step replayed after
 // wisp_cache_device_end) does no step and writes slot -1 into meta.
 // `resident` is key2slot[key] (-1 for key < 0), looked up by the caller.
+// have_pre: pfq / pfst are freq[key] / first[key], requested by the caller at the step's start.
 __device__ __forceinline__ LruLane lru_classify(const DevPaging& d, const LruCtr& st, int lane, int k, int key,
-                                                int resident, float w, LruShared& sh) {
+                                                int resident, float w, LruShared& sh, bool have_pre = false,
+                                                double pfq = 0.0, int64_t pfst = 0) {
     LruLane ln{};
     ln.key = key;
     ln.w = w;
@@ -489,13 +491,13 @@ __device__ __forceinline__ LruLane lru_classify(const DevPaging& d, const LruCtr
     ln.lead = lane;
     ln.mult = 0;
     for (int j = 0; j < k; ++j) {
-        const int kj = __shfl(key, j, 64);
+        const int kj = __builtin_amdgcn_readlane(key, j);  // j is uniform: no LDS round trip
         if (kj == key && j < ln.lead) ln.lead = j;
         ln.mult += kj == key ? 1 : 0;
     }
     if (key >= 0 && ln.lead == lane) {
-        ln.fq = d.freq[key];
-        ln.fst = d.first[key];
+        ln.fq = have_pre ? pfq : d.freq[key];
+        ln.fst = have_pre ? pfst : d.first[key];
     }
     const int64_t nf = st.nf;
     int slot = key >= 0 ? resident : -1;
@@ -680,7 +682,7 @@ __device__ __forceinline__ void lru_commit(const DevPaging& d, const LruCtr& st,
     // a key repeated later in the step: the later lane's slot is the one key2slot keeps
     bool later = false;
     for (int j = 0; j < k; ++j) {
-        const int kj = __shfl(key, j, 64);
+        const int kj = __builtin_amdgcn_readlane(key, j);
         later = later || (j > lane && kj == key);
     }
     const bool gets = ln.miss && slot >= 0;
@@ -810,13 +812,20 @@ __global__ __launch_bounds__(R == kLruSmall ? 64 : 1024) void k_route_lru(const 
     }
     const LruCtr st = lru_counters(d);
     int64_t forced = -1;
-    int32_t pre[EPL];  // key2slot[key_base + lane + 64 t], clamped into the table
+    // key2slot, freq and first of key_base + lane + 64 t (clamped into the table), requested
+    // at the start: the chosen keys' entries then need no round trip after the top-k
+    int32_t pre[EPL];
+    double pfq[EPL];
+    int64_t pfst[EPL];
     if (wave0) {
         forced = ids ? ids[lane < k ? lane : 0] : -1;
 #pragma unroll
         for (int t = 0; t < EPL; ++t) {
             const int64_t kq = key_base + lane + 64 * t;
-            pre[t] = d.key2slot[kq < 0 ? 0 : (kq < d.nkeys ? kq : d.nkeys - 1)];
+            const int64_t kc = kq < 0 ? 0 : (kq < d.nkeys ? kq : d.nkeys - 1);
+            pre[t] = d.key2slot[kc];
+            pfq[t] = d.freq[kc];
+            pfst[t] = d.first[kc];
         }
     }
     uint64_t key[R];
@@ -832,13 +841,25 @@ __global__ __launch_bounds__(R == kLruSmall ? 64 : 1024) void k_route_lru(const 
         const int64_t id = kk >= 0 ? (int64_t)kk - key_base : 0;
         const int src = (int)(id & 63), reg = (int)(id >> 6);
         int res = -1;
+        double fq = 0.0;
+        int64_t fst = 0;
 #pragma unroll
         for (int t = 0; t < EPL; ++t) {
             const int o = __shfl(pre[t], src, 64);
-            res = reg == t ? o : res;
+            const long long fb = __double_as_longlong(pfq[t]);
+            const uint32_t flo = (uint32_t)__shfl((int)(uint32_t)fb, src, 64);
+            const uint32_t fhi = (uint32_t)__shfl((int)(uint32_t)((uint64_t)fb >> 32), src, 64);
+            const uint32_t slo = (uint32_t)__shfl((int)(uint32_t)pfst[t], src, 64);
+            const uint32_t shi = (uint32_t)__shfl((int)(uint32_t)((uint64_t)pfst[t] >> 32), src, 64);
+            if (reg == t) {
+                res = o;
+                fq = __longlong_as_double((long long)(((uint64_t)fhi << 32) | flo));
+                fst = (int64_t)(((uint64_t)shi << 32) | slo);
+            }
         }
-        if (kk >= 0 && id >= 64 * EPL) res = d.key2slot[kk];
-        return lru_classify(d, st, lane, k, kk, kk >= 0 ? res : -1, w, sh);
+        const bool have = kk >= 0 && id < 64 * EPL;  // else read after the top-k
+        if (kk >= 0 && !have) res = d.key2slot[kk];
+        return lru_classify(d, st, lane, k, kk, kk >= 0 ? res : -1, w, sh, have, fq, fst);
     });
     __syncthreads();
     const int evicted = lru_evict<R, SC>(sh, key, ln, wave0, (int)d.n_static);
