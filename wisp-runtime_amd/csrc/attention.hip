@@ -219,8 +219,8 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
         sv[i] = ok ? sc[i] * scale : -INFINITY;
         m = fmaxf(m, sv[i]);
     }
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32));
+    m = max_xor16(m);
+    m = max_xor32(m);
     if (lane < 16) red_m[wv][n] = m;
     __syncthreads();
     // the workgroup's maximum (finite for n < G: position p0 <= pos is in wave 0)
@@ -231,8 +231,8 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
         pe[i] = sv[i] == -INFINITY ? 0.f : expf(sv[i] - m);
         l += pe[i];
     }
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = add_xor16(l);
+    l = add_xor32(l);
     if (lane < 16) red_l[wv][n] = l;
 
     uint2 phi, plo;

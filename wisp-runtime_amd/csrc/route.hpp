@@ -66,11 +66,7 @@ __device__ __forceinline__ float route_select(const uint16_t* __restrict__ logit
         v[t] = i < E ? expf(v[t] - mx) : 0.f;
         sum += v[t];
     }
-    // the xor butterfly's sum (xor 1, 2, 4, 8, 16, 32), bit for bit, without LDS round trips:
-    // xor 1 and 2 are the quad permutations; after them every lane of a quad holds the quad's
-    // sum, so the half-row and row mirrors pair the same values as xor 4 and 8; the rows' sums
-    // then combine as (R0 + R1) + (R2 + R3), as xor 16 and 32 do (addition commutes)
-    sum = wave_sum_dpp(sum);
+    sum = wave_sum(sum);
 #pragma unroll
     for (int t = 0; t < kRouteMaxPerLane; ++t) v[t] = lane + 64 * t < E ? v[t] / sum : -1.f;
     float sel_v[16];
@@ -96,8 +92,8 @@ __device__ __forceinline__ float route_select(const uint16_t* __restrict__ logit
     // The renormalising sum adds adjacent pairs level by level (an odd last entry carried
     // up), which is the order torch's sum over the last dim takes for k = 1, 2, 4, 8 and 16
     // (checked bit for bit on MI355X; for other k torch's order differs and the sum may
-    // differ in its last bit). The softmax above sums per lane in index order, then as the
-    // xor butterfly over the 64 lanes does, as torch's warp softmax does.
+    // differ in its last bit). The softmax above sums per lane in index order, then with the
+    // xor butterfly over the 64 lanes, as torch's warp softmax does.
     float tree[16];
     for (int r = 0; r < k; ++r) tree[r] = sel_v[r];
     for (int n = k; n > 1; n = (n + 1) >> 1) {

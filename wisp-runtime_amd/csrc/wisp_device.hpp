@@ -522,9 +522,40 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
 
 // Wave-wide sum (wave64) with xor shuffles: the butterfly order (every lane ends with the
 // same value), which torch's warp reductions also take.
+// The value of lane l ^ 16 (xor16) or l ^ 32 (xor32) combined with lane l's, in every lane,
+// without LDS: gfx950's permlane swaps exchange the odd rows (halves) of one copy of v with
+// the even rows (halves) of another, after which each lane holds its own value in one result
+// and its partner's in the other. Sums add the two in either order (addition commutes), so
+// they equal the xor butterfly's own + partner bit for bit.
+__device__ __forceinline__ float max_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float add_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// The xor butterfly's sum (partners l ^ 32, ^ 16, ^ 8, ^ 4, ^ 2, ^ 1 in that order, as
+// torch's warp reductions take them), bit for bit, without LDS: ^ 32 and ^ 16 by the permlane
+// swaps; ^ 8 is row_ror:8 exactly; after it every lane's value equals its ^ 8 partner's (the
+// two added the same pair), so row_ror:4 (lane (l + 4) % 16, which differs from l ^ 4 at most
+// in bit 3) reads the same value as l ^ 4, and likewise row_ror:2 and row_ror:1 after the
+// steps before them.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = add_xor32(v);
+    v = add_xor16(v);
+    v += dpp_f<0x128>(v);  // row_ror:8
+    v += dpp_f<0x124>(v);  // row_ror:4
+    v += dpp_f<0x122>(v);  // row_ror:2
+    v += dpp_f<0x121>(v);  // row_ror:1
     return v;
 }
 __device__ __forceinline__ float wave_min(float v) {
