@@ -148,17 +148,28 @@ __device__ __forceinline__ void wave_sync_lds() {
 // a[j, r] into the fp32 activation workspace
 __device__ __forceinline__ void write_act(float* act, int j, int I, int r, float a) { act[(int64_t)j * I + r] = a; }
 
-// dot of one chunk of codes against one bf16 operand in pair order, bias removed: sum q*v
+// dot of one chunk of codes against one bf16 operand in pair order, bias removed: sum q*v.
+// Even pairs accumulate from b0, odd pairs from b1. 3-bit: the operand scaled per half
+// (operand_pairs), b0 = -128 * (sum of its values), b1 = 0. 4- and 2-bit: the operand as
+// the x values are (operand_pairs<BITS, false>), each accumulator's pairs at one e in both
+// halves (4-bit 3; 2-bit 3 for even pairs, 5 for odd ones), so each accumulator's dot is
+// 2^e times the scaled form's and is scaled back here. 4-bit with b0 = -128 * (sum of the
+// values), b1 = 0: every product, partial sum and the bias are exactly 8 times the scaled
+// form's, so the result has the same bits. 2-bit: b0 and b1 = -128 * (sum of the values
+// of the even / odd pairs), each accumulator cancelling its own bias.
 template <int BITS>
-__device__ __forceinline__ float chunk_dot(const uint32_t* codes, const uint32_t* opr, float bias, uint32_t B) {
+__device__ __forceinline__ float chunk_dot(const uint32_t* codes, const uint32_t* opr, float b0, float b1,
+                                           uint32_t B) {
     uint32_t p[16];
     code_pairs<BITS>(codes, p, B);
-    float a0 = bias, a1 = 0.f;
+    float a0 = b0, a1 = b1;
 #pragma unroll
     for (int P = 0; P < 16; P += 2) {
         a0 = dot2(p[P], opr[P], a0);
         a1 = dot2(p[P + 1], opr[P + 1], a1);
     }
+    if constexpr (BITS == 4) return (a0 + a1) * 0.125f;
+    if constexpr (BITS == 2) return __builtin_fmaf(a1, 0.03125f, a0 * 0.125f);
     return a0 + a1;
 }
 
@@ -243,14 +254,30 @@ __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __re
         }
     }
     uint32_t xp[16];
-    float xs, bias = 0.f;
+    float xs, b0 = 0.f, b1 = 0.f;
     if constexpr (XF) {
         xs = chunk_sum_f32(xf);
-    } else {
+    } else if constexpr (BITS == 3) {
         float vs;
         operand_pairs<BITS>(xw, xp);
         operand_sums<BITS>(xp, vs, xs);
-        bias = -kBiasF * vs;
+        b0 = -kBiasF * vs;
+    } else {
+        // the x values as they are, one v_perm each; the biases as chunk_dot takes them
+        operand_pairs<BITS, false>(xw, xp);
+        float se = 0.f, so = 0.f;
+#pragma unroll
+        for (int P = 0; P < 16; P += 2) {
+            se = dot2(xp[P], kOnes2, se);
+            so = dot2(xp[P + 1], kOnes2, so);
+        }
+        xs = se + so;
+        if constexpr (BITS == 4) {
+            b0 = -kBiasF * xs;
+        } else {
+            b0 = -kBiasF * se;
+            b1 = -kBiasF * so;
+        }
     }
     const uint32_t B = bias_vgpr();
 #pragma unroll
@@ -261,8 +288,8 @@ __device__ __forceinline__ void gate_up_rows(const Layer& L, const uint8_t* __re
             dg = chunk_dot_f32<BITS>(cg[t], xf);
             du = chunk_dot_f32<BITS>(cu[t], xf);
         } else {
-            dg = chunk_dot<BITS>(cg[t], xp, bias, B);
-            du = chunk_dot<BITS>(cu[t], xp, bias, B);
+            dg = chunk_dot<BITS>(cg[t], xp, b0, b1, B);
+            du = chunk_dot<BITS>(cu[t], xp, b0, b1, B);
         }
         uint32_t s_g, m_g, s_u, m_u;
         if (QSC) {

@@ -436,18 +436,20 @@ constexpr uint32_t kOnes2 = 0x3F803F80u;  // bf16 pair (1, 1)
 
 // Operand pairs of one chunk from the 16 dwords w[] holding 32 consecutive
 // bf16 values (value c = half c&1 of w[c>>1]): pair P = (v[lo]*2^-elo,
-// v[hi]*2^-ehi). Exact for bf16 inputs.
-template <int BITS>
+// v[hi]*2^-ehi). Exact for bf16 inputs. SCALED false: the values as they are,
+// (v[lo], v[hi]) -- for a width whose pairs all share one e, the dots are then
+// 2^e times the scaled ones, with the same bits once multiplied by 2^-e.
+template <int BITS, bool SCALED = true>
 __device__ __forceinline__ void operand_pairs(const uint32_t* w, uint32_t* pr) {
 #pragma unroll
     for (int P = 0; P < 16; ++P) {
         const int lo = PairMap<BITS>::lo(P), hi = PairMap<BITS>::hi(P);
         const uint32_t wl = w[lo >> 1], wh = w[hi >> 1];
-        if (PairMap<BITS>::elo(P) == 0 && PairMap<BITS>::ehi(P) == 0) {
-            // pure 16-bit shuffle: v_perm_b32 / v_bfi_b32
-            const uint32_t l16 = (lo & 1) ? (wl >> 16) : (wl & 0xFFFFu);
-            const uint32_t h16 = (hi & 1) ? (wh & 0xFFFF0000u) : (wh << 16);
-            pr[P] = l16 | h16;
+        if (!SCALED || (PairMap<BITS>::elo(P) == 0 && PairMap<BITS>::ehi(P) == 0)) {
+            // pure 16-bit shuffle, one v_perm_b32: result bytes 0-1 from wl (selectors 0-3), 2-3 from
+            // wh (selectors 4-7), each the low or the high half
+            const uint32_t sl = (lo & 1) ? 0x0302u : 0x0100u, sh = (hi & 1) ? 0x0706u : 0x0504u;
+            pr[P] = __builtin_amdgcn_perm(wh, wl, (sh << 16) | sl);
         } else {
             const float fl = (lo & 1) ? bf16_hi(wl) : bf16_lo(wl);
             const float fh = (hi & 1) ? bf16_hi(wh) : bf16_lo(wh);
