@@ -310,39 +310,49 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float* __restrict__ pa
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // chunk indices in SGPRs
     const int h = blockIdx.x, hk = h / G, g = h - hk * G;
     const int64_t pos = *pos_ptr;
-    const int nv = (int)min<int64_t>(nsplit, pos / kChunk + 1);
     const float* base = part + ((int64_t)hk * nsplit * G + g) * (2 + D);
-    const int64_t stride = (int64_t)G * (2 + D);
+    const int stride = G * (2 + D);  // c * stride < nsplit * G * (2 + D): 32-bit offsets within one head's records
     float M = -INFINITY, L = 0.f, O[DPL];
 #pragma unroll
     for (int t = 0; t < DPL; ++t) O[t] = 0.f;
-    for (int c0 = 0; c0 < nv; c0 += 4 * B) {
+    // A batch's records are requested without waiting for the position: chunk indices are
+    // clamped to the workspace's nsplit chunks, and records past the position's last chunk
+    // (stale or never written) are masked once it has arrived -- never multiplied, so their
+    // bits cannot reach the sums. The first batch always exists (chunk 0).
+    int c0 = 0, nv;
+    do {
         float ov[B][DPL];
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const int c = min(c0 + wv + 4 * b, nv - 1);
+            const int c = min(c0 + wv + 4 * b, nsplit - 1);
 #pragma unroll
             for (int t = 0; t < DPL; ++t) ov[b][t] = base[c * stride + 2 + lane * DPL + t];
         }
         const int cl = c0 + wv + 4 * (lane & 15);
+        const int cc = min(cl, nsplit - 1);
+        float mr = base[cc * stride], lr = base[cc * stride + 1];
+        __builtin_amdgcn_sched_barrier(0);
+        int64_t pv = pos;
+        asm volatile("" : "+s"(pv));  // the position's first use stays here, after the batch's loads
+        nv = (int)min<int64_t>(nsplit, pv / kChunk + 1);
         const bool have = lane < 16 && cl < nv;
-        const int cc = min(cl, nv - 1);
-        const float mc = have ? base[cc * stride] : -INFINITY;
-        const float lc = base[cc * stride + 1];
+        const float mc = have ? mr : -INFINITY;
         const float Mn = fmaxf(M, row0_max(mc));
         const float f = M == -INFINITY ? 0.f : expf(M - Mn);  // rescale of the sums so far
         const float w = have ? expf(mc - Mn) : 0.f;
-        L = L * f + row0_sum(w * lc);
+        L = L * f + row0_sum(have ? w * lr : 0.f);
 #pragma unroll
         for (int t = 0; t < DPL; ++t) O[t] *= f;
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const float wb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), b));
+            const bool vb = c0 + wv + 4 * b < nv;  // the same in every lane
 #pragma unroll
-            for (int t = 0; t < DPL; ++t) O[t] += wb * ov[b][t];
+            for (int t = 0; t < DPL; ++t) O[t] += vb ? wb * ov[b][t] : 0.f;
         }
         M = Mn;
-    }
+        c0 += 4 * B;
+    } while (c0 < nv);
     if (lane == 0) {
         red_m[wv] = M;
         red_l[wv] = L;
