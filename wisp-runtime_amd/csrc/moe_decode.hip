@@ -155,7 +155,9 @@ __device__ __forceinline__ void write_act(float* act, int j, int I, int r, float
 // halves (4-bit 3; 2-bit 3 for even pairs, 5 for odd ones), so each accumulator's dot is
 // 2^e times the scaled form's and is scaled back here. 4-bit with b0 = -128 * (sum of the
 // values), b1 = 0: every product, partial sum and the bias are exactly 8 times the scaled
-// form's, so the result has the same bits. 2-bit: b0 and b1 = -128 * (sum of the values
+// form's, so the result has the same bits (for |x| between about 2^-120 and 2^120: past
+// those the scaled form's operands leave bf16's normal range, or the products fp32's, one
+// step earlier than the other form's). 2-bit: b0 and b1 = -128 * (sum of the values
 // of the even / odd pairs), each accumulator cancelling its own bias.
 template <int BITS>
 __device__ __forceinline__ float chunk_dot(const uint32_t* codes, const uint32_t* opr, float b0, float b1,
