@@ -522,8 +522,6 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
-// Wave-wide sum (wave64) with xor shuffles: the butterfly order (every lane ends with the
-// same value), which torch's warp reductions also take.
 // The value of lane l ^ 16 (xor16) or l ^ 32 (xor32) combined with lane l's, in every lane,
 // without LDS: gfx950's permlane swaps exchange the odd rows (halves) of one copy of v with
 // the even rows (halves) of another, after which each lane holds its own value in one result
